@@ -1,0 +1,208 @@
+/*
+ * pagelora.h — C ABI of the MI355X (gfx950) paged-decode + no-merge LoRA library.
+ *
+ * Every entry point is stream ordered: it enqueues work on `stream` (a
+ * hipStream_t passed as void*, NULL = the legacy default stream) and returns
+ * without synchronising.  None of them allocates device memory: scratch space
+ * is the caller's `workspace`.  Return value: PL_OK (0) or a pl_status code;
+ * pl_last_error() then holds a message for the calling thread.
+ *
+ * Pointers are device pointers unless a parameter name ends in `_h` (host).
+ * Strides are in elements, not bytes.
+ */
+#ifndef PAGELORA_H_
+#define PAGELORA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  PL_DTYPE_F32 = 0,
+  PL_DTYPE_F16 = 1,
+  PL_DTYPE_BF16 = 2,
+} pl_dtype;
+
+typedef enum {
+  PL_OK = 0,
+  PL_ERR_INVALID = 1,      /* bad argument (shape, stride, null pointer)     */
+  PL_ERR_UNSUPPORTED = 2,  /* valid but not built (head_dim, group, dtype)  */
+  PL_ERR_WORKSPACE = 3,    /* workspace too small for the requested plan    */
+  PL_ERR_HIP = 4,          /* a HIP runtime call failed                     */
+} pl_status;
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* pl_last_error(void);
+
+/* Library ABI version: (major << 16) | minor. */
+int pl_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Paged decode attention                                                    */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Bytes of workspace that pl_decode_plan / pl_decode_run need for `batch`
+ * rows, `target_items` split-KV work items, `num_qo_heads` query heads and
+ * `head_dim`.  The plan may create up to target_items + batch items.
+ *
+ * Replaces the workspace sizing of FlashInferAttentionBackend.__init__
+ * (model/flashinfer/attention_backend.py:42-43): the reference hands a fixed
+ * 128 MiB buffer to FlashInfer; here the caller can size it exactly.
+ */
+size_t pl_decode_workspace_size(int batch, int target_items, int num_qo_heads,
+                                int head_dim);
+
+/*
+ * Device-side split-KV planning for one decode step.  Reads the page-table
+ * row pointer `indptr` [batch+1] (int32, device) and writes into `workspace`
+ * a work list of (row, page range) items of near-equal size:
+ *   chunk_pages = max(min_chunk_pages, ceil(total_pages / target_items)).
+ * Page ranges are clamped to [0, indices_capacity], the length of the
+ * indices buffer the run will read.
+ * No host read-back: the plan runs on the stream, so it can sit inside a
+ * captured hipGraph and one graph replays across steps whatever the lengths.
+ *
+ * Replaces FlashInferAttentionBackend.plan_decode / _call_plan
+ * (model/flashinfer/attention_backend.py:63-118, 229-285), which call
+ * flashinfer.BatchDecodeWithPagedKVCacheWrapper.plan with a host read-back
+ * of indptr.
+ */
+int pl_decode_plan(const int32_t* indptr, int batch, int indices_capacity,
+                   int num_qo_heads, int head_dim, int target_items,
+                   int min_chunk_pages, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/*
+ * Batched single-token paged attention:
+ *   o[b, hq] = softmax(q[b, hq] . K_b[:, hq / g]^T * sm_scale) . V_b
+ * with g = num_qo_heads / num_kv_heads, K_b / V_b gathered from the pages
+ * indices[indptr[b] .. indptr[b+1]) (all full except the last, which holds
+ * last_page_len[b] tokens).  Token t of page p, kv head h, dim d lives at
+ *   k_cache[p * page_stride + t * token_stride + h * head_stride + d]
+ * (same for v_cache; page ids outside [0, num_pages) are clamped into the
+ * pool rather than read out of bounds), which covers the reference's NHD pool
+ * [P, 2, page, Hkv, D] (k_cache = pool, v_cache = pool + page*Hkv*D,
+ * page_stride = 2*page*Hkv*D) as well as split K/V tensors and HND pages.
+ * q is [batch, num_qo_heads, head_dim] with strides (q_stride_b,
+ * q_stride_h, 1); o likewise.  lse (nullable) receives the natural-log
+ * log-sum-exp of the scaled scores, [batch, num_qo_heads] fp32.
+ * q, caches and o share `dtype`; accumulation is fp32.
+ * Requires a pl_decode_plan on the same workspace earlier on the stream.
+ * head_dim: 64, 128 or 256.  num_qo_heads / num_kv_heads: 1..8.
+ * page_size: a multiple of 16.
+ *
+ * Replaces FlashInferAttentionBackend.run_decode / _call_run
+ * (model/flashinfer/attention_backend.py:120-131, 287-292), i.e.
+ * flashinfer.BatchDecodeWithPagedKVCacheWrapper.run(q / 16, cache) with
+ * sm_scale 16/sqrt(D) (attention_backend.py:97) — the same softmax.
+ */
+int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                  const void* k_cache, const void* v_cache,
+                  int64_t page_stride, int64_t token_stride,
+                  int64_t head_stride, int64_t num_pages,
+                  const int32_t* indices,
+                  const int32_t* last_page_len, void* o, int64_t o_stride_b,
+                  int64_t o_stride_h, float* lse, int batch, int num_qo_heads,
+                  int num_kv_heads, int head_dim, int page_size,
+                  float sm_scale, int dtype, int target_items,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Write one decode token per row into its page:
+ *   K[page_id[b], offset[b], h, :] = k[b, h, :]   (and V from v)
+ * with the cache addressed as in pl_decode_run.  k and v are
+ * [batch, num_kv_heads, head_dim] with strides (k_stride_b, k_stride_h, 1).
+ * page_id / offset are int64 (the graph-owned buffers of the reference);
+ * a row whose page_id is outside [0, num_pages) or whose offset is outside
+ * [0, page_size) is skipped rather than written out of bounds.
+ *
+ * Replaces _append_decode_kv_static (model/flashinfer/layer_runner.py:399-412),
+ * two torch index_put_ calls into the paged pool.
+ */
+int pl_kv_append(const void* k, const void* v, int64_t k_stride_b,
+                 int64_t k_stride_h, int64_t v_stride_b, int64_t v_stride_h,
+                 void* k_cache, void* v_cache, int64_t page_stride,
+                 int64_t token_stride, int64_t head_stride, int64_t num_pages,
+                 int page_size, const int64_t* page_id, const int64_t* offset,
+                 int batch, int num_kv_heads, int head_dim, int dtype,
+                 void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* No-merge multi-adapter LoRA delta                                         */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * One LoRA-wrapped linear module of a group that shares its input x
+ * (q/k/v, or gate/up, or a lone o_proj / down_proj).
+ *   A    : [num_adapters, rank, in_features]   (dtype of x)
+ *   B    : [num_adapters, out_features, rank]  (dtype of x)
+ *   out  : rows t of out[t * ldo + j], j < out_features, receive
+ *          out += scale * B[a_t] . (A[a_t] . x_t)
+ */
+typedef struct {
+  const void* A;
+  const void* B;
+  void* out;
+  int64_t ldo;
+  int out_features;
+  int rank;
+  float scale;
+} pl_lora_module;
+
+/* Most modules in one group (q, k, v). */
+#define PL_LORA_MAX_MODULES 4
+
+/* Workspace bytes for one pl_lora_* call (at most 256 adapters): per-adapter
+ * ticket words, fp32 partial sums [ceil(in/256)][num_tokens][sum(rank)
+ * rounded up to 32] and the rounded rank-r intermediate.  The workspace must
+ * be zero-filled once before its first use; every call leaves the ticket
+ * words zero again.  Calls that share a workspace must be stream ordered. */
+size_t pl_lora_workspace_size(int num_tokens, int in_features,
+                              const pl_lora_module* modules_h, int num_modules);
+
+/*
+ * out_m[t] += scale_m * B_m[a_t] . (A_m[a_t] . x[t]) for every module m of the
+ * group and every token t with adapter_ids[t] in [0, num_adapters); tokens
+ * with a negative id are left untouched.  x is [num_tokens, in_features]
+ * with row stride ldx.  `dtype` is that of x, A and B (F16 or BF16);
+ * `out_dtype` that of the outputs (F16, BF16 or F32).  The rank-r
+ * intermediate is rounded to `dtype` before the expand, as the reference's
+ * two chained F.linear calls do.
+ *
+ * Replaces the packed / per-module LoRA delta of the no-merge path:
+ * _packed_lora_delta + _cached_packed_lora_delta
+ * (model/flashinfer/packed_ops.py:314-384; A concatenated, B block-diagonal
+ * with the scale folded in), _lora_delta (packed_ops.py:534-553) and the
+ * delta term of LoRALinear.forward (multilora/linear.py:226-231).  Per-token
+ * adapter ids generalise the reference's single bound adapter
+ * (multilora/runtime.py:138-174).
+ */
+int pl_lora_delta(const void* x, int64_t ldx, int num_tokens, int in_features,
+                  const pl_lora_module* modules_h, int num_modules,
+                  const int32_t* adapter_ids, int num_adapters, int dtype,
+                  int out_dtype, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* The two stages of pl_lora_delta, for callers that overlap them with the
+ * base GEMM: shrink writes the fp32 partial sums into the workspace, expand
+ * reduces them and accumulates into the outputs. */
+int pl_lora_shrink(const void* x, int64_t ldx, int num_tokens,
+                   int in_features, const pl_lora_module* modules_h,
+                   int num_modules, const int32_t* adapter_ids,
+                   int num_adapters, int dtype, void* workspace,
+                   size_t workspace_bytes, void* stream);
+int pl_lora_expand(int num_tokens, int in_features,
+                   const pl_lora_module* modules_h, int num_modules,
+                   const int32_t* adapter_ids, int num_adapters, int dtype,
+                   int out_dtype, const void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGELORA_H_ */

@@ -1,0 +1,169 @@
+"""ctypes binding of libpagelora_amd.so (declarations: include/pagelora.h).
+
+Loading fails loudly when the library has not been built: there is no CPU
+or torch fallback behind any entry point of this package.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libpagelora_amd.so"
+
+PL_DTYPE_F32 = 0
+PL_DTYPE_F16 = 1
+PL_DTYPE_BF16 = 2
+
+PL_OK = 0
+PL_ERR_INVALID = 1
+PL_ERR_UNSUPPORTED = 2
+PL_ERR_WORKSPACE = 3
+PL_ERR_HIP = 4
+
+PL_LORA_MAX_MODULES = 4
+
+
+class ExtensionNotBuiltError(ImportError):
+    """libpagelora_amd.so is missing: run ``__graft_entry__.build()``."""
+
+
+class WorkspaceTooSmallError(RuntimeError):
+    """The caller's workspace cannot hold the requested plan."""
+
+
+class HipError(RuntimeError):
+    """A HIP runtime call inside the library failed."""
+
+
+class LoraModule(ctypes.Structure):
+    """Mirror of ``pl_lora_module``."""
+
+    _fields_ = [
+        ("A", ctypes.c_void_p),
+        ("B", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("ldo", ctypes.c_int64),
+        ("out_features", ctypes.c_int),
+        ("rank", ctypes.c_int),
+        ("scale", ctypes.c_float),
+    ]
+
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); the exact list of symbols the header declares.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "pl_last_error": (ctypes.c_char_p, []),
+    "pl_version": (_i32, []),
+    "pl_decode_workspace_size": (_sz, [_i32, _i32, _i32, _i32]),
+    "pl_decode_plan": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
+    "pl_decode_run": (
+        _i32,
+        [
+            _vp, _i64, _i64,            # q, strides
+            _vp, _vp, _i64, _i64, _i64,  # k/v cache, page/token/head strides
+            _i64,                        # num_pages
+            _vp, _vp,                    # indices, last_page_len
+            _vp, _i64, _i64,             # o, strides
+            _vp,                         # lse
+            _i32, _i32, _i32, _i32, _i32,  # batch, hq, hkv, head_dim, page_size
+            _f32, _i32, _i32,            # sm_scale, dtype, target_items
+            _vp, _sz, _vp,               # workspace, bytes, stream
+        ],
+    ),
+    "pl_kv_append": (
+        _i32,
+        [
+            _vp, _vp, _i64, _i64, _i64, _i64,  # k, v, strides
+            _vp, _vp, _i64, _i64, _i64,         # caches, page/token/head strides
+            _i64, _i32,                         # num_pages, page_size
+            _vp, _vp,                           # page_id, offset
+            _i32, _i32, _i32, _i32, _vp,        # batch, hkv, head_dim, dtype, stream
+        ],
+    ),
+    "pl_lora_workspace_size": (_sz, [_i32, _i32, ctypes.POINTER(LoraModule), _i32]),
+    "pl_lora_delta": (
+        _i32,
+        [_vp, _i64, _i32, _i32, ctypes.POINTER(LoraModule), _i32, _vp, _i32, _i32, _i32, _vp, _sz, _vp],
+    ),
+    "pl_lora_shrink": (
+        _i32,
+        [_vp, _i64, _i32, _i32, ctypes.POINTER(LoraModule), _i32, _vp, _i32, _i32, _vp, _sz, _vp],
+    ),
+    "pl_lora_expand": (
+        _i32,
+        [_i32, _i32, ctypes.POINTER(LoraModule), _i32, _vp, _i32, _i32, _i32, _vp, _sz, _vp],
+    ),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Return the loaded library, loading it on first use."""
+
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise ExtensionNotBuiltError(
+                f"{LIB_PATH} is missing; build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+            )
+        # torch first: its bundled HIP runtime then serves this library too
+        # (one runtime per process, so torch streams are valid handles here).
+        import torch  # noqa: F401
+
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    msg = load().pl_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(status: int, what: str) -> None:
+    """Map a pl_status to the Python exception the reference would raise."""
+
+    if status == PL_OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if status == PL_ERR_INVALID:
+        raise ValueError(msg)
+    if status == PL_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    if status == PL_ERR_WORKSPACE:
+        raise WorkspaceTooSmallError(msg)
+    raise HipError(msg)
+
+
+def dtype_code(dtype) -> int:
+    import torch
+
+    codes = {torch.float32: PL_DTYPE_F32, torch.float16: PL_DTYPE_F16, torch.bfloat16: PL_DTYPE_BF16}
+    if dtype not in codes:
+        raise NotImplementedError(f"dtype {dtype} is not supported (float32, float16, bfloat16)")
+    return codes[dtype]
+
+
+def stream_handle(device=None) -> int:
+    """Raw hipStream_t of torch's current stream on ``device``."""
+
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

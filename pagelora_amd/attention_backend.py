@@ -1,0 +1,359 @@
+"""Paged decode attention behind the reference's plan()/run() surface.
+
+``PagedDecodeAttention`` keeps the constructor, methods and attributes of the
+reference's ``FlashInferAttentionBackend`` (model/flashinfer/attention_backend.py:18-292)
+that its callers use -- ``plan_decode``, ``run_decode``, ``decode_graph_signature``,
+``workspace_buffer``, ``page_size``, ``query_rescale``, ``decode_use_tensor_cores``,
+``use_flashinfer_qk_norm`` -- and runs the gfx950 kernels of libpagelora_amd.so:
+
+* ``plan_decode`` copies the page table into persistent device buffers and
+  enqueues the device-side split-KV plan.  Nothing is read back to the host,
+  so the plan can also be captured into the decode graph.
+* ``run_decode`` launches the split-KV decode kernel (+ merge) on the
+  current stream.  Its grid depends only on the batch size, so one captured
+  hipGraph replays across steps while the rows grow
+  (``decode_graph_signature`` does not change with sequence length).
+
+Mathematics: ``o = softmax(q . K^T / sqrt(D)) . V`` per (row, q head), kv head
+``hq // (Hq / Hkv)``.  The reference divides q by 16 and multiplies the scale
+by 16 (attention_backend.py:37-41, 97, 128) to dodge FlashInfer's finite
+``-5e4`` mask sentinel; the kernels here mask with ``-inf`` selects, so that
+workaround is not needed and ``query_rescale`` is 1.0.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+from collections import deque
+from typing import Sequence
+
+import torch
+
+from . import _lib
+
+_DEFAULT_TARGET_WAVES = int(os.environ.get("PAGELORA_DECODE_TARGET_WAVES", "8192"))
+_DEFAULT_MIN_CHUNK_PAGES = int(os.environ.get("PAGELORA_DECODE_MIN_CHUNK_PAGES", "2"))
+
+
+def _validate_host_table(indptr: torch.Tensor, indices: torch.Tensor, last: torch.Tensor, page_size: int) -> int:
+    """Check a host-side page table; returns the largest page id (or -1)."""
+
+    ip = indptr.tolist()
+    if ip and ip[0] != 0:
+        raise ValueError("paged_kv_indptr must start at 0")
+    if any(b < a for a, b in zip(ip, ip[1:])):
+        raise ValueError("paged_kv_indptr must be non-decreasing")
+    if ip and ip[-1] > indices.numel():
+        raise ValueError(f"paged_kv_indptr[-1]={ip[-1]} exceeds paged_kv_indices length {indices.numel()}")
+    lens = last.tolist()
+    for b, (a, e) in enumerate(zip(ip, ip[1:])):
+        if e > a and not (1 <= lens[b] <= page_size):
+            raise ValueError(f"paged_kv_last_page_len[{b}]={lens[b]} outside [1, {page_size}]")
+    used = indices[: ip[-1]] if ip else indices[:0]
+    if used.numel() and int(used.min()) < 0:
+        raise ValueError("paged_kv_indices holds a negative page id")
+    return int(used.max()) if used.numel() else -1
+
+
+def _cache_geometry(cache, num_kv_heads: int, head_dim: int, page_size: int):
+    """(k_tensor, v_tensor_or_ptr_source, page_stride, token_stride, head_stride, num_pages)."""
+
+    if isinstance(cache, (tuple, list)):
+        k, v = cache
+        if k.shape != v.shape or k.stride() != v.stride() or k.dtype != v.dtype:
+            raise ValueError("K and V caches must have the same shape, strides and dtype")
+        if k.dim() != 4 or tuple(k.shape[1:]) != (page_size, num_kv_heads, head_dim):
+            raise ValueError(f"K/V caches must be [P, {page_size}, {num_kv_heads}, {head_dim}] (NHD), got {tuple(k.shape)}")
+        if k.stride(3) != 1:
+            raise ValueError("head_dim must be contiguous in the KV cache")
+        return k, v, k.stride(0), k.stride(1), k.stride(2), k.shape[0]
+    if cache.dim() != 5 or tuple(cache.shape[1:]) != (2, page_size, num_kv_heads, head_dim):
+        raise ValueError(
+            f"paged KV cache layer must be [P, 2, {page_size}, {num_kv_heads}, {head_dim}] (NHD), got {tuple(cache.shape)}"
+        )
+    if cache.stride(4) != 1:
+        raise ValueError("head_dim must be contiguous in the KV cache")
+    return cache[:, 0], cache[:, 1], cache.stride(0), cache.stride(2), cache.stride(3), cache.shape[0]
+
+
+class PagedDecodeAttention:
+    """gfx950 paged decode attention with the FlashInferAttentionBackend surface."""
+
+    def __init__(
+        self,
+        *,
+        device: torch.device | str,
+        workspace_mb: int,
+        num_qo_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        page_size: int,
+        target_waves: int | None = None,
+        min_chunk_pages: int | None = None,
+        max_pages: int = 0,
+    ) -> None:
+        self.device = torch.device(device)
+        self.workspace_mb = max(1, int(workspace_mb))
+        self.num_qo_heads = int(num_qo_heads)
+        self.num_kv_heads = int(num_kv_heads)
+        self.head_dim = int(head_dim)
+        self.page_size = int(page_size)
+        if self.num_kv_heads <= 0 or self.num_qo_heads % self.num_kv_heads:
+            raise ValueError("Q head count must be divisible by KV head count")
+        self.query_rescale = 1.0
+        self.sm_scale = 1.0 / math.sqrt(self.head_dim)
+        # One code path for every GQA ratio 1..8 (the reference switches to
+        # FlashInfer's tensor-core kernel for ratios outside {1,2,4,8}).
+        self.decode_use_tensor_cores = False
+        self.use_flashinfer_qk_norm = False
+        self.target_waves = int(target_waves or _DEFAULT_TARGET_WAVES)
+        self.min_chunk_pages = int(min_chunk_pages or _DEFAULT_MIN_CHUNK_PAGES)
+        if self.device.type == "cuda":
+            self._lib = _lib.load()  # fails loudly when the extension is not built
+        else:
+            self._lib = None
+        self.workspace_buffer = torch.empty(self.workspace_mb * 1024 * 1024, dtype=torch.uint8, device=self.device)
+        # Initial capacity of the persistent indices buffer.  A capacity that
+        # covers every page a batch can list (e.g. the pool size) means the
+        # buffers, and so decode_graph_signature(), never change as rows grow.
+        self.max_pages = int(max_pages)
+        self._decode_graph_buffers: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None
+        self._decode_host_uploads: deque = deque()
+        self._plan: dict | None = None
+
+    # ------------------------------------------------------------ planning
+    def plan_decode(
+        self,
+        *,
+        paged_kv_indptr: torch.Tensor,
+        paged_kv_indices: torch.Tensor,
+        paged_kv_last_page_len: torch.Tensor,
+        q_data_type: torch.dtype | None = None,
+        kv_data_type: torch.dtype | None = None,
+        non_blocking: bool | None = None,
+    ) -> None:
+        """Upload one step's page table and enqueue the device-side plan.
+
+        Shared by every decoder layer of the step (attention_backend.py:63-118).
+        Host tables are validated here; device tables are trusted (the kernels
+        still clamp every index into its buffer).
+        """
+
+        if paged_kv_indptr.dim() != 1 or paged_kv_last_page_len.dim() != 1 or paged_kv_indices.dim() != 1:
+            raise ValueError("page-table tensors must be 1-D")
+        batch = paged_kv_last_page_len.numel()
+        if paged_kv_indptr.numel() != batch + 1:
+            raise ValueError("paged_kv_indptr must have batch + 1 entries")
+        for t in (paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len):
+            if t.dtype != torch.int32:
+                raise ValueError("page-table tensors must be int32")
+        max_page = None
+        if paged_kv_indptr.device.type == "cpu":
+            max_page = _validate_host_table(paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len, self.page_size)
+        if self.device.type != "cuda":
+            raise RuntimeError("PagedDecodeAttention.plan_decode needs a ROCm device")
+
+        self._ensure_graph_safe_decode_buffers(paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len)
+        indptr_buf, indices_buf, last_buf = self._decode_graph_buffers
+        host = (paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len)
+        async_host = all(t.device.type == "cpu" and t.is_pinned() for t in host)
+        if async_host:
+            # A pinned source must stay alive until its upload has run; keep at
+            # most 8 in flight (attention_backend.py:79-88, 114-118).
+            while self._decode_host_uploads and self._decode_host_uploads[0][0].query():
+                self._decode_host_uploads.popleft()
+            if len(self._decode_host_uploads) >= 8:
+                self._decode_host_uploads[0][0].synchronize()
+                self._decode_host_uploads.popleft()
+        nb = bool(async_host if non_blocking is None else non_blocking)
+        indptr_buf[: batch + 1].copy_(paged_kv_indptr, non_blocking=nb)
+        if paged_kv_indices.numel():
+            indices_buf[: paged_kv_indices.numel()].copy_(paged_kv_indices, non_blocking=nb)
+        last_buf[:batch].copy_(paged_kv_last_page_len, non_blocking=nb)
+        if async_host:
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.device))
+            self._decode_host_uploads.append((ev, host))
+
+        target_items = self._target_items(batch)
+        self._launch_plan(batch, target_items)
+        self._plan = {
+            "batch": batch,
+            "target_items": target_items,
+            "q_data_type": q_data_type,
+            "kv_data_type": kv_data_type,
+            "max_page": max_page,
+        }
+
+    def replan_decode(self) -> None:
+        """Re-run the device-side plan on the current buffers (same batch).
+
+        For callers that update the persistent page-table buffers on the
+        device (e.g. inside a captured step) instead of calling plan_decode.
+        """
+
+        if self._plan is None:
+            raise RuntimeError("plan_decode has not been called")
+        self._launch_plan(self._plan["batch"], self._plan["target_items"])
+
+    def _launch_plan(self, batch: int, target_items: int) -> None:
+        indptr_buf, indices_buf, _ = self._decode_graph_buffers
+        status = self._lib.pl_decode_plan(
+            indptr_buf.data_ptr(),
+            batch,
+            indices_buf.numel(),
+            self.num_qo_heads,
+            self.head_dim,
+            target_items,
+            self.min_chunk_pages,
+            self.workspace_buffer.data_ptr(),
+            self.workspace_buffer.numel(),
+            _lib.stream_handle(self.device),
+        )
+        _lib.check(status, "pl_decode_plan")
+
+    def _target_items(self, batch: int) -> int:
+        """Work items per step: about target_waves wavefronts, within the workspace."""
+
+        t = max(1, self.target_waves // self.num_kv_heads)
+        cap = self.workspace_buffer.numel()
+        while t > 1 and self._lib.pl_decode_workspace_size(batch, t, self.num_qo_heads, self.head_dim) > cap:
+            t //= 2
+        if self._lib.pl_decode_workspace_size(batch, t, self.num_qo_heads, self.head_dim) > cap:
+            raise _lib.WorkspaceTooSmallError(
+                f"workspace of {self.workspace_mb} MiB cannot hold a decode plan for batch {batch}"
+            )
+        return t
+
+    def _ensure_graph_safe_decode_buffers(self, indptr, indices, last_page_len) -> None:
+        """Persistent device page-table buffers (attention_backend.py:198-221 policy):
+        rebuilt when the batch changes or the indices outgrow a power-of-two capacity."""
+
+        buffers = self._decode_graph_buffers
+        if buffers is not None and buffers[0].numel() == indptr.numel() and buffers[1].numel() >= indices.numel():
+            return
+        capacity = max(16, self.max_pages, 1 << max(0, indices.numel() - 1).bit_length())
+        self._decode_graph_buffers = (
+            torch.zeros(indptr.numel(), dtype=torch.int32, device=self.device),
+            torch.zeros(capacity, dtype=torch.int32, device=self.device),
+            torch.ones(last_page_len.numel(), dtype=torch.int32, device=self.device),
+        )
+
+    def decode_graph_signature(self):
+        """Everything a captured run_decode bakes in (attention_backend.py:223-227).
+
+        Sequence lengths are not part of it: the plan lives on the device.
+        """
+
+        bufs = self._decode_graph_buffers
+        ptrs = tuple(b.data_ptr() for b in bufs) if bufs is not None else ()
+        plan = self._plan or {}
+        return (id(self), plan.get("batch"), plan.get("target_items"), ptrs, self.workspace_buffer.data_ptr())
+
+    # ----------------------------------------------------------------- run
+    def run_decode(self, q: torch.Tensor, paged_kv_cache_layer) -> torch.Tensor:
+        """One layer of paged decode attention; returns ``[B, Hq, 1, D]``
+        (attention_backend.py:120-131)."""
+
+        q_nhd = q.squeeze(2) if q.dim() == 4 and q.size(2) == 1 else q
+        out = torch.empty(q_nhd.shape, dtype=q_nhd.dtype, device=q_nhd.device)
+        self.run_decode_into(q_nhd, paged_kv_cache_layer, out)
+        return out.unsqueeze(2) if out.dim() == 3 else out
+
+    def run_decode_into(
+        self,
+        q: torch.Tensor,
+        paged_kv_cache_layer,
+        out: torch.Tensor,
+        lse: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Allocation-free variant: writes ``out`` ([B, Hq, D]) and optionally
+        ``lse`` ([B, Hq] fp32, natural log)."""
+
+        plan = self._plan
+        if plan is None:
+            raise RuntimeError("plan_decode must be called before run_decode")
+        if q.dim() != 3 or tuple(q.shape[1:]) != (self.num_qo_heads, self.head_dim):
+            raise ValueError(f"q must be [B, {self.num_qo_heads}, {self.head_dim}], got {tuple(q.shape)}")
+        batch = q.shape[0]
+        if batch != plan["batch"]:
+            raise ValueError(f"q has batch {batch} but the plan has {plan['batch']}")
+        if q.stride(2) != 1 or out.stride(2) != 1 or tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype:
+            raise ValueError("q and out must match in shape/dtype with a contiguous head_dim")
+        if q.device.type != "cuda":
+            raise RuntimeError("run_decode needs tensors on a ROCm device")
+        k, v, page_stride, token_stride, head_stride, num_pages = _cache_geometry(
+            paged_kv_cache_layer, self.num_kv_heads, self.head_dim, self.page_size
+        )
+        if k.dtype != q.dtype:
+            raise ValueError(f"q dtype {q.dtype} != KV cache dtype {k.dtype}")
+        if plan["max_page"] is not None and plan["max_page"] >= num_pages:
+            raise ValueError(f"page id {plan['max_page']} is outside the {num_pages}-page KV pool")
+        if lse is not None and (lse.dtype != torch.float32 or tuple(lse.shape) != (batch, self.num_qo_heads) or not lse.is_contiguous()):
+            raise ValueError("lse must be a contiguous fp32 [B, Hq] tensor")
+        _, indices_buf, last_buf = self._decode_graph_buffers
+        status = self._lib.pl_decode_run(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            k.data_ptr(), v.data_ptr(), page_stride, token_stride, head_stride,
+            num_pages,
+            indices_buf.data_ptr(), last_buf.data_ptr(),
+            out.data_ptr(), out.stride(0), out.stride(1),
+            lse.data_ptr() if lse is not None else None,
+            batch, self.num_qo_heads, self.num_kv_heads, self.head_dim, self.page_size,
+            self.sm_scale, _lib.dtype_code(q.dtype), plan["target_items"],
+            self.workspace_buffer.data_ptr(), self.workspace_buffer.numel(),
+            _lib.stream_handle(q.device),
+        )
+        _lib.check(status, "pl_decode_run")
+        return out
+
+    # ------------------------------------------------------------- prefill
+    def plan_prefill(self, **kwargs) -> None:  # attention_backend.py:133-170
+        raise NotImplementedError("paged prefill attention is not part of this build; see run_prefill")
+
+    def run_prefill(self, q: torch.Tensor, paged_kv_cache_layer) -> torch.Tensor:  # :172-190
+        raise NotImplementedError("paged prefill attention is not part of this build")
+
+
+# The reference's class name, for drop-in imports.
+FlashInferAttentionBackend = PagedDecodeAttention
+
+
+def kv_append(
+    cache_layer,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    page_id: torch.Tensor,
+    page_offset: torch.Tensor,
+    *,
+    num_kv_heads: int,
+    head_dim: int,
+    page_size: int,
+) -> None:
+    """Write one decode token per row into its page: the graph-safe append
+    that replaces ``_append_decode_kv_static`` (layer_runner.py:399-412)."""
+
+    kc, vc, page_stride, token_stride, head_stride, num_pages = _cache_geometry(
+        cache_layer, num_kv_heads, head_dim, page_size
+    )
+    if k.dim() != 3 or k.shape != v.shape or tuple(k.shape[1:]) != (num_kv_heads, head_dim):
+        raise ValueError(f"k and v must be [B, {num_kv_heads}, {head_dim}]")
+    if k.stride(2) != 1 or v.stride(2) != 1:
+        raise ValueError("k and v need a contiguous head_dim")
+    if k.dtype != kc.dtype or v.dtype != kc.dtype:
+        raise ValueError("k/v dtype must match the cache")
+    batch = k.shape[0]
+    if page_id.dtype != torch.int64 or page_offset.dtype != torch.int64:
+        raise ValueError("page_id and page_offset must be int64")
+    if page_id.numel() != batch or page_offset.numel() != batch:
+        raise ValueError("page_id / page_offset must have one entry per row")
+    lib = _lib.load()
+    status = lib.pl_kv_append(
+        k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+        kc.data_ptr(), vc.data_ptr(), page_stride, token_stride, head_stride,
+        num_pages, page_size,
+        page_id.data_ptr(), page_offset.data_ptr(),
+        batch, num_kv_heads, head_dim, _lib.dtype_code(k.dtype), _lib.stream_handle(k.device),
+    )
+    _lib.check(status, "pl_kv_append")

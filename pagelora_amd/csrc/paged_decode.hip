@@ -1,0 +1,611 @@
+// Batched single-token paged attention for gfx950 (MI355X).
+//
+// Three kernels, all launched with a grid that depends only on the batch
+// size and the workspace plan, never on sequence lengths, so a captured
+// hipGraph replays across decode steps while rows grow:
+//
+//   plan_kernel    one workgroup; reads indptr[B+1] and cuts every row into
+//                  chunks of `chunk_pages` pages (chunk_pages chosen on the
+//                  device from the total page count) -> a work list of
+//                  (row, page range) items.
+//   decode_kernel  one wavefront per (item, kv head).  Streams the item's
+//                  pages 16 tokens at a time straight from HBM into VGPRs
+//                  (16 lanes x 16 B cover one 128-dim token row, so one
+//                  dwordx4 load instruction reads 4 token rows), scores them
+//                  against the g query heads of the kv head with v_dot2 and
+//                  DPP row reductions, and keeps an online softmax per lane
+//                  row in fp32.  Rows with one item write the output
+//                  directly; split rows write (o, lse) partials.
+//   merge_kernel   one wavefront per (row, q head) of split rows: LSE-weighted
+//                  sum of the partials.
+//
+// Mathematics: o = softmax(q . K^T * sm_scale) . V, as the reference's
+// FlashInferAttentionBackend.run_decode (model/flashinfer/attention_backend.py
+// :120-131) obtains from FlashInfer with q/16 and sm_scale 16/sqrt(D).
+#include "pl_common.h"
+
+namespace pl {
+namespace decode {
+
+constexpr int kWave = 64;
+constexpr int kBlockTokens = 16;   // tokens consumed per pipeline step
+constexpr int kWavesPerWG = 4;
+
+struct Item {   // one split-KV work item; lives in the workspace
+  int row;      // batch row, -1 = unused slot
+  int page_begin;  // absolute index into `indices`
+  int page_end;
+  int flags;    // bit0: row has a single item (write o directly)
+                // bit1: item holds the row's last (possibly partial) page
+};
+
+struct Layout {
+  size_t header, items, row_info, lse, partial_o, total;
+};
+
+inline Layout layout(int batch, int max_items, int hq, int d) {
+  Layout L;
+  L.header = 0;
+  L.items = 256;
+  L.row_info = align_up(L.items + (size_t)max_items * sizeof(Item), 256);
+  L.lse = align_up(L.row_info + (size_t)batch * 2 * sizeof(int), 256);
+  L.partial_o = align_up(L.lse + (size_t)max_items * hq * sizeof(float), 256);
+  L.total = align_up(L.partial_o + (size_t)max_items * hq * d * sizeof(float), 256);
+  return L;
+}
+
+// ------------------------------------------------------------------ plan ---
+constexpr int kPlanThreads = 1024;
+
+// Stamp written into header[2..3] by the plan and checked by the decode and
+// merge kernels, so a run on an unplanned or differently planned workspace
+// does no work instead of reading stale item ranges.
+__host__ __device__ inline int plan_stamp(int batch, int max_items) {
+  return (int)(0x51A70000u ^ ((unsigned)batch * 2654435761u) ^ (unsigned)max_items);
+}
+
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(
+    const int32_t* __restrict__ indptr, int batch, int indices_capacity, int target_items,
+    int min_chunk_pages, int max_items, Item* __restrict__ items,
+    int2* __restrict__ row_info, int* __restrict__ header) {
+  __shared__ int s_scan[kPlanThreads];
+  __shared__ int s_chunk;
+  const int tid = threadIdx.x;
+  // Page ranges are clamped to [0, indices_capacity] so a malformed indptr
+  // can never send a reader outside the indices buffer.
+  auto clampi = [&](int v) { return v < 0 ? 0 : (v > indices_capacity ? indices_capacity : v); };
+  if (tid == 0) {
+    const int total = clampi(indptr[batch]) - clampi(indptr[0]);
+    int c = (total + target_items - 1) / target_items;
+    c = c > min_chunk_pages ? c : min_chunk_pages;
+    s_chunk = c > 1 ? c : 1;
+  }
+  __syncthreads();
+  const int chunk = s_chunk;
+  const int per = (batch + kPlanThreads - 1) / kPlanThreads;
+  const int r0 = tid * per;
+  const int r1 = min(batch, r0 + per);
+  int local = 0;
+  for (int r = r0; r < r1; ++r) {
+    const int n = clampi(indptr[r + 1]) - clampi(indptr[r]);
+    const int nch = n > 0 ? (n + chunk - 1) / chunk : 1;
+    local += nch > 1 ? nch : 1;
+  }
+  s_scan[tid] = local;
+  __syncthreads();
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
+    const int v = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  int it = s_scan[tid] - local;
+  const int total_items = s_scan[kPlanThreads - 1];
+  for (int r = r0; r < r1; ++r) {
+    const int pb = clampi(indptr[r]);
+    const int pe = pb > clampi(indptr[r + 1]) ? pb : clampi(indptr[r + 1]);
+    int nch = (pe - pb + chunk - 1) / chunk;
+    nch = nch > 1 ? nch : 1;
+    const int room = max_items - it;
+    row_info[r] = make_int2(it < max_items ? it : max_items, nch < room ? nch : (room > 0 ? room : 0));
+    for (int j = 0; j < nch; ++j, ++it) {
+      if (it >= max_items) break;  // unreachable by construction; keeps writes in bounds
+      const int a = pb + j * chunk;
+      const int e = min(pe, a + chunk);
+      Item item;
+      item.row = r;
+      item.page_begin = a;
+      item.page_end = e;
+      item.flags = (nch == 1 ? 1 : 0) | (e == pe ? 2 : 0);
+      items[it] = item;
+    }
+  }
+  for (int i = total_items + tid; i < max_items; i += kPlanThreads) {
+    Item item;
+    item.row = -1;
+    item.page_begin = item.page_end = item.flags = 0;
+    items[i] = item;
+  }
+  if (tid == 0) {
+    header[0] = chunk;
+    header[1] = total_items;
+    header[2] = batch;
+    header[3] = plan_stamp(batch, max_items);
+  }
+}
+
+// ---------------------------------------------------------------- decode ---
+// Per-type traits: how one lane's 8 elements of a token row are loaded and
+// consumed.  16-bit types: one 16-byte load; fp32: two.
+template <typename T> struct Lane8;
+
+template <> struct Lane8<float> {
+  static constexpr int kWords = 8;
+  __device__ static void load(uint32_t (&w)[8], const float* p) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint4 b = *reinterpret_cast<const uint4*>(p + 4);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  }
+  __device__ static float dot(const uint32_t (&q)[8], const uint32_t (&k)[8]) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc = fmaf(__uint_as_float(q[i]), __uint_as_float(k[i]), acc);
+    return acc;
+  }
+  __device__ static void to_f32(const uint32_t (&w)[8], float (&f)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = __uint_as_float(w[i]);
+  }
+  __device__ static void store(float* p, const float (&f)[8]) {
+    *reinterpret_cast<float4*>(p) = make_float4(f[0], f[1], f[2], f[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(f[4], f[5], f[6], f[7]);
+  }
+};
+
+template <typename T> struct Lane8Half {
+  static constexpr int kWords = 4;
+  __device__ static void load(uint32_t (&w)[4], const T* p) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  }
+  __device__ static float dot(const uint32_t (&q)[4], const uint32_t (&k)[4]) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = dot2<T>(q[i], k[i], acc);
+    return acc;
+  }
+  __device__ static void to_f32(const uint32_t (&w)[4], float (&f)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) unpack2<T>(w[i], f[2 * i], f[2 * i + 1]);
+  }
+  __device__ static void store(T* p, const float (&f)[8]) {
+    uint4 a;
+    a.x = pack2<T>(f[0], f[1]);
+    a.y = pack2<T>(f[2], f[3]);
+    a.z = pack2<T>(f[4], f[5]);
+    a.w = pack2<T>(f[6], f[7]);
+    *reinterpret_cast<uint4*>(p) = a;
+  }
+};
+template <> struct Lane8<f16_t> : Lane8Half<f16_t> {};
+template <> struct Lane8<bf16_t> : Lane8Half<bf16_t> {};
+
+// Sum across the LPT lanes that share one token row.
+template <int LPT> __device__ __forceinline__ float row_sum(float x);
+template <> __device__ __forceinline__ float row_sum<8>(float x) { return row8_sum(x); }
+template <> __device__ __forceinline__ float row_sum<16>(float x) { return row16_sum(x); }
+template <> __device__ __forceinline__ float row_sum<32>(float x) { return row32_sum(x); }
+
+template <typename T, int D, int G>
+struct DecodeWave {
+  static constexpr int LPT = D / 8;             // lanes per token row
+  static constexpr int TPI = kWave / LPT;       // token rows per load instruction
+  static constexpr int NS = kBlockTokens / TPI; // loads per lane per block
+  static constexpr int W = Lane8<T>::kWords;
+  using L8 = Lane8<T>;
+
+  uint32_t q[G][W];   // this lane's 8 dims of the g query heads
+  float m[G], l[G];   // online-softmax state of this lane row (log2 domain)
+  float acc[G][8];    // unnormalised output, this lane's 8 dims
+
+  __device__ void init() {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = -INFINITY;
+      l[g] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+    }
+  }
+
+  // Consume one block of 16 tokens already in registers.  `valid` = number
+  // of tokens of the block that exist (16 for all blocks but the last).
+  template <bool MASK>
+  __device__ __forceinline__ void consume(const uint32_t (&kw)[NS][W], const uint32_t (&vw)[NS][W],
+                                          float scale_log2, int row, int valid) {
+    float sc[NS][G];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = L8::dot(q[g], kw[s]);
+        d = row_sum<LPT>(d) * scale_log2;
+        if (MASK) d = (row + s * TPI < valid) ? d : -INFINITY;
+        sc[s][g] = d;
+      }
+    }
+    float vf[NS][8];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      L8::to_f32(vw[s], vf[s]);
+      if (MASK) {
+        const bool ok = row + s * TPI < valid;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vf[s][i] = ok ? vf[s][i] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = sc[0][g];
+#pragma unroll
+      for (int s = 1; s < NS; ++s) mx = fmaxf(mx, sc[s][g]);
+      const float m_new = fmaxf(m[g], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // all masked so far
+      const float alpha = fast_exp2(m[g] - m_use);
+      m[g] = m_new;
+      float psum = 0.f;
+      float p[NS];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        p[s] = fast_exp2(sc[s][g] - m_use);
+        psum += p[s];
+      }
+      l[g] = l[g] * alpha + psum;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float a = acc[g][i] * alpha;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) a = fmaf(p[s], vf[s][i], a);
+        acc[g][i] = a;
+      }
+    }
+  }
+
+  // Fold the TPI lane rows together (xor over the row bits of the lane id).
+  // Afterwards every lane holds the wave's combined state for its 8 dims.
+  __device__ __forceinline__ void merge_rows() {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int off = LPT; off < kWave; off <<= 1) {
+        const float m_o = __shfl_xor(m[g], off);
+        const float l_o = __shfl_xor(l[g], off);
+        const float m_new = fmaxf(m[g], m_o);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float a_s = fast_exp2(m[g] - m_use);
+        const float a_o = fast_exp2(m_o - m_use);
+        l[g] = l[g] * a_s + l_o * a_o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float o_o = __shfl_xor(acc[g][i], off);
+          acc[g][i] = acc[g][i] * a_s + o_o * a_o;
+        }
+        m[g] = m_new;
+      }
+    }
+  }
+};
+
+template <typename T, int D, int G>
+__global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
+    const T* __restrict__ q, int64_t q_sb, int64_t q_sh, const T* __restrict__ kc,
+    const T* __restrict__ vc, int64_t page_stride, int64_t token_stride, int64_t head_stride,
+    const int32_t* __restrict__ indices, const int32_t* __restrict__ last_page_len,
+    T* __restrict__ o, int64_t o_sb, int64_t o_sh, float* __restrict__ lse, int num_qo_heads,
+    int num_kv_heads, int page_size, int64_t num_pages, float scale_log2,
+    const int* __restrict__ header, const Item* __restrict__ items, int batch, int max_items,
+    float* __restrict__ part_lse, float* __restrict__ part_o) {
+  using WaveT = DecodeWave<T, D, G>;
+  constexpr int LPT = WaveT::LPT, TPI = WaveT::TPI, NS = WaveT::NS, W = WaveT::W;
+  using L8 = Lane8<T>;
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = uniform(blockIdx.x * kWavesPerWG + threadIdx.x / kWave);
+  const int item_idx = wave / num_kv_heads;
+  const int h = wave - item_idx * num_kv_heads;
+  if (item_idx >= max_items) return;
+  if (uniform(header[2]) != batch || uniform(header[3]) != plan_stamp(batch, max_items)) return;
+  const Item it = items[item_idx];
+  const int b = uniform(it.row);
+  if (b < 0 || b >= batch) return;
+  const int pbeg = uniform(it.page_begin), pend = uniform(it.page_end), flags = uniform(it.flags);
+
+  const int row = lane / LPT;   // token row inside a load instruction
+  const int col = lane % LPT;   // 8-element slice of the head dim
+
+  WaveT st;
+  st.init();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const T* qp = q + (int64_t)b * q_sb + (int64_t)(h * G + g) * q_sh + col * 8;
+    L8::load(st.q[g], qp);
+  }
+
+  int ntok = 0;
+  if (pend > pbeg) {
+    ntok = (pend - pbeg) * page_size;
+    if (flags & 2) {
+      int last = last_page_len[b];
+      last = last < 1 ? 1 : (last > page_size ? page_size : last);
+      ntok -= page_size - last;
+    }
+  }
+  ntok = uniform(ntok);
+  const int nblk = (ntok + kBlockTokens - 1) / kBlockTokens;
+
+  const int64_t lane_off = (int64_t)row * token_stride + (int64_t)h * head_stride + col * 8;
+  auto load_block = [&](int blk, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
+    const int t0 = blk * kBlockTokens;
+    const int pg = t0 / page_size;
+    const int tip = t0 - pg * page_size;
+    int64_t page = uniform(indices[pbeg + pg]);
+    page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);  // stay inside the pool
+    const int64_t base = page * page_stride + (int64_t)tip * token_stride + lane_off;
+    const T* kp = kc + base;
+    const T* vp = vc + base;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) L8::load(kw[s], kp + (int64_t)s * TPI * token_stride);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) L8::load(vw[s], vp + (int64_t)s * TPI * token_stride);
+  };
+
+  if (nblk > 0) {
+    uint32_t ka[NS][W], va[NS][W], kb[NS][W], vb[NS][W];
+    load_block(0, ka, va);
+    for (int i = 0; i < nblk; i += 2) {
+      // Prefetch the next block before consuming this one.  The index is
+      // clamped instead of branched on so the load count is the same on
+      // every path (a re-load of the last block hits in cache).
+      load_block(min(i + 1, nblk - 1), kb, vb);
+      if ((i + 1) * kBlockTokens <= ntok)
+        st.template consume<false>(ka, va, scale_log2, row, kBlockTokens);
+      else
+        st.template consume<true>(ka, va, scale_log2, row, ntok - i * kBlockTokens);
+      if (i + 1 >= nblk) break;
+      load_block(min(i + 2, nblk - 1), ka, va);
+      if ((i + 2) * kBlockTokens <= ntok)
+        st.template consume<false>(kb, vb, scale_log2, row, kBlockTokens);
+      else
+        st.template consume<true>(kb, vb, scale_log2, row, ntok - (i + 1) * kBlockTokens);
+    }
+  }
+
+  st.merge_rows();
+  if (row != 0) return;
+
+  constexpr float kLn2 = 0.69314718055994530942f;
+  if (flags & 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int hq = h * G + g;
+      const float inv = st.l[g] > 0.f ? 1.f / st.l[g] : 0.f;
+      float out[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) out[i] = st.acc[g][i] * inv;
+      L8::store(o + (int64_t)b * o_sb + (int64_t)hq * o_sh + col * 8, out);
+      if (lse != nullptr && col == 0)
+        lse[(int64_t)b * num_qo_heads + hq] =
+            st.l[g] > 0.f ? (st.m[g] + __log2f(st.l[g])) * kLn2 : -INFINITY;
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int hq = h * G + g;
+      const float inv = st.l[g] > 0.f ? 1.f / st.l[g] : 0.f;
+      float out[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) out[i] = st.acc[g][i] * inv;
+      float* pp = part_o + ((int64_t)item_idx * num_qo_heads + hq) * D + col * 8;
+      Lane8<float>::store(pp, out);
+      if (col == 0)
+        part_lse[(int64_t)item_idx * num_qo_heads + hq] =
+            st.l[g] > 0.f ? st.m[g] + __log2f(st.l[g]) : -INFINITY;
+    }
+  }
+}
+
+// ----------------------------------------------------------------- merge ---
+template <typename T, int D>
+__global__ __launch_bounds__(kWave * kWavesPerWG) void merge_kernel(
+    const int2* __restrict__ row_info, const float* __restrict__ part_lse,
+    const float* __restrict__ part_o, T* __restrict__ o, int64_t o_sb, int64_t o_sh,
+    float* __restrict__ lse, const int* __restrict__ header, int batch, int num_qo_heads,
+    int max_items) {
+  constexpr int DPL = (D + kWave - 1) / kWave;  // dims per lane
+  const int lane = threadIdx.x % kWave;
+  const int wave = uniform(blockIdx.x * kWavesPerWG + threadIdx.x / kWave);
+  if (wave >= batch * num_qo_heads) return;
+  if (uniform(header[2]) != batch || uniform(header[3]) != plan_stamp(batch, max_items)) return;
+  const int b = wave / num_qo_heads;
+  const int hq = wave - b * num_qo_heads;
+  const int2 info = row_info[b];
+  const int first = uniform(info.x), n = uniform(info.y);
+  if (n <= 1 || first < 0 || first + n > max_items) return;
+
+  float mx = -INFINITY;
+  for (int c = 0; c < n; ++c) mx = fmaxf(mx, part_lse[(int64_t)(first + c) * num_qo_heads + hq]);
+  const float m_use = mx == -INFINITY ? 0.f : mx;
+  float acc[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+  float wsum = 0.f;
+  for (int c = 0; c < n; ++c) {
+    const int64_t slot = (int64_t)(first + c) * num_qo_heads + hq;
+    const float w = fast_exp2(part_lse[slot] - m_use);
+    wsum += w;
+    const float* pp = part_o + slot * D;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) {
+      const int d = lane + i * kWave;
+      if (d < D) acc[i] = fmaf(w, pp[d], acc[i]);
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  T* op = o + (int64_t)b * o_sb + (int64_t)hq * o_sh;
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) {
+    const int d = lane + i * kWave;
+    if (d < D) op[d] = from_float<T>(acc[i] * inv);
+  }
+  if (lse != nullptr && lane == 0) {
+    constexpr float kLn2 = 0.69314718055994530942f;
+    lse[(int64_t)b * num_qo_heads + hq] = wsum > 0.f ? (m_use + __log2f(wsum)) * kLn2 : -INFINITY;
+  }
+}
+
+// ------------------------------------------------------------- dispatch ---
+struct RunArgs {
+  const void* q; int64_t q_sb, q_sh;
+  const void* kc; const void* vc; int64_t page_stride, token_stride, head_stride;
+  const int32_t* indices; const int32_t* last;
+  void* o; int64_t o_sb, o_sh; float* lse;
+  int batch, hq, hkv, page_size; int64_t num_pages; float scale_log2;
+  const int* header; const Item* items; int max_items; const int2* row_info; float* part_lse; float* part_o;
+  hipStream_t stream;
+};
+
+template <typename T, int D, int G>
+int launch(const RunArgs& a) {
+  const int64_t waves = (int64_t)a.max_items * a.hkv;
+  const int grid = (int)((waves + kWavesPerWG - 1) / kWavesPerWG);
+  hipLaunchKernelGGL((decode_kernel<T, D, G>), dim3(grid), dim3(kWave * kWavesPerWG), 0, a.stream,
+                     (const T*)a.q, a.q_sb, a.q_sh, (const T*)a.kc, (const T*)a.vc, a.page_stride,
+                     a.token_stride, a.head_stride, a.indices, a.last, (T*)a.o, a.o_sb, a.o_sh,
+                     a.lse, a.hq, a.hkv, a.page_size, a.num_pages, a.scale_log2, a.header,
+                     a.items, a.batch, a.max_items, a.part_lse, a.part_o);
+  PL_LAUNCH_CHECK("decode_kernel");
+  const int mgrid = (a.batch * a.hq + kWavesPerWG - 1) / kWavesPerWG;
+  hipLaunchKernelGGL((merge_kernel<T, D>), dim3(mgrid), dim3(kWave * kWavesPerWG), 0, a.stream,
+                     a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
+                     a.batch, a.hq, a.max_items);
+  PL_LAUNCH_CHECK("merge_kernel");
+  return ok();
+}
+
+template <typename T, int D>
+int by_group(const RunArgs& a, int g) {
+  switch (g) {
+    case 1: return launch<T, D, 1>(a);
+    case 2: return launch<T, D, 2>(a);
+    case 3: return launch<T, D, 3>(a);
+    case 4: return launch<T, D, 4>(a);
+    case 5: return launch<T, D, 5>(a);
+    case 6: return launch<T, D, 6>(a);
+    case 7: return launch<T, D, 7>(a);
+    case 8: return launch<T, D, 8>(a);
+  }
+  return fail(PL_ERR_UNSUPPORTED, "GQA group size %d not built (1..8)", g);
+}
+
+template <typename T>
+int by_dim(const RunArgs& a, int d, int g) {
+  switch (d) {
+    case 64: return by_group<T, 64>(a, g);
+    case 128: return by_group<T, 128>(a, g);
+    case 256: return by_group<T, 256>(a, g);
+  }
+  return fail(PL_ERR_UNSUPPORTED, "head_dim %d not built (64, 128, 256)", d);
+}
+
+}  // namespace decode
+}  // namespace pl
+
+using namespace pl;
+using namespace pl::decode;
+
+extern "C" size_t pl_decode_workspace_size(int batch, int target_items, int num_qo_heads,
+                                           int head_dim) {
+  if (batch < 0 || target_items <= 0 || num_qo_heads <= 0 || head_dim <= 0) return 0;
+  return layout(batch, target_items + batch, num_qo_heads, head_dim).total;
+}
+
+extern "C" int pl_decode_plan(const int32_t* indptr, int batch, int indices_capacity,
+                              int num_qo_heads, int head_dim, int target_items,
+                              int min_chunk_pages, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0 (got %d)", batch);
+  if (target_items <= 0) return fail(PL_ERR_INVALID, "target_items must be > 0");
+  if (num_qo_heads <= 0 || head_dim <= 0) return fail(PL_ERR_INVALID, "bad head shape");
+  if (indices_capacity < 0) return fail(PL_ERR_INVALID, "indices_capacity must be >= 0");
+  if (batch == 0) return ok();
+  if (indptr == nullptr || workspace == nullptr) return fail(PL_ERR_INVALID, "null pointer");
+  if ((uintptr_t)workspace % 256) return fail(PL_ERR_INVALID, "workspace must be 256-byte aligned");
+  const int max_items = target_items + batch;
+  const Layout L = layout(batch, max_items, num_qo_heads, head_dim);
+  if (L.total > workspace_bytes)
+    return fail(PL_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, L.total);
+  char* ws = (char*)workspace;
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, indptr,
+                     batch, indices_capacity, target_items, min_chunk_pages < 1 ? 1 : min_chunk_pages, max_items,
+                     (Item*)(ws + L.items), (int2*)(ws + L.row_info), (int*)(ws + L.header));
+  PL_LAUNCH_CHECK("plan_kernel");
+  return ok();
+}
+
+extern "C" int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                             const void* k_cache, const void* v_cache, int64_t page_stride,
+                             int64_t token_stride, int64_t head_stride, int64_t num_pages,
+                             const int32_t* indices, const int32_t* last_page_len, void* o, int64_t o_stride_b,
+                             int64_t o_stride_h, float* lse, int batch, int num_qo_heads,
+                             int num_kv_heads, int head_dim, int page_size, float sm_scale,
+                             int dtype, int target_items, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0");
+  if (batch == 0) return ok();
+  if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads)
+    return fail(PL_ERR_INVALID, "num_qo_heads (%d) must be a positive multiple of num_kv_heads (%d)",
+                num_qo_heads, num_kv_heads);
+  if (page_size <= 0 || page_size % kBlockTokens)
+    return fail(PL_ERR_UNSUPPORTED, "page_size %d: must be a positive multiple of %d", page_size,
+                kBlockTokens);
+  if (target_items <= 0) return fail(PL_ERR_INVALID, "target_items must be > 0");
+  if (num_pages <= 0) return fail(PL_ERR_INVALID, "num_pages must be > 0");
+  if (!q || !k_cache || !v_cache || !indices || !last_page_len || !o || !workspace)
+    return fail(PL_ERR_INVALID, "null pointer argument");
+  if (dtype != PL_DTYPE_F32 && dtype != PL_DTYPE_F16 && dtype != PL_DTYPE_BF16)
+    return fail(PL_ERR_UNSUPPORTED, "dtype %d", dtype);
+  // Every lane issues 16-byte loads of 8 consecutive elements.
+  const int64_t strides[] = {q_stride_b, q_stride_h, page_stride, token_stride, head_stride,
+                             o_stride_b, o_stride_h};
+  for (int64_t s : strides)
+    if (s % 8) return fail(PL_ERR_INVALID, "every stride must be a multiple of 8 elements");
+  const void* ptrs[] = {q, k_cache, v_cache, o};
+  for (const void* p : ptrs)
+    if ((uintptr_t)p % 16) return fail(PL_ERR_INVALID, "q, caches and o must be 16-byte aligned");
+  const int max_items = target_items + batch;
+  const Layout L = layout(batch, max_items, num_qo_heads, head_dim);
+  if (L.total > workspace_bytes)
+    return fail(PL_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, L.total);
+  char* ws = (char*)workspace;
+  RunArgs a;
+  a.q = q; a.q_sb = q_stride_b; a.q_sh = q_stride_h;
+  a.kc = k_cache; a.vc = v_cache;
+  a.page_stride = page_stride; a.token_stride = token_stride; a.head_stride = head_stride;
+  a.indices = indices; a.last = last_page_len;
+  a.o = o; a.o_sb = o_stride_b; a.o_sh = o_stride_h; a.lse = lse;
+  a.batch = batch; a.hq = num_qo_heads; a.hkv = num_kv_heads; a.page_size = page_size;
+  a.num_pages = num_pages; a.header = (const int*)(ws + L.header);
+  a.scale_log2 = sm_scale * 1.44269504088896340736f;
+  a.items = (const Item*)(ws + L.items); a.max_items = max_items;
+  a.row_info = (const int2*)(ws + L.row_info);
+  a.part_lse = (float*)(ws + L.lse); a.part_o = (float*)(ws + L.partial_o);
+  a.stream = (hipStream_t)stream;
+  const int g = num_qo_heads / num_kv_heads;
+  switch (dtype) {
+    case PL_DTYPE_F32: return by_dim<float>(a, head_dim, g);
+    case PL_DTYPE_F16: return by_dim<f16_t>(a, head_dim, g);
+    case PL_DTYPE_BF16: return by_dim<bf16_t>(a, head_dim, g);
+  }
+  return fail(PL_ERR_UNSUPPORTED, "dtype %d", dtype);
+}

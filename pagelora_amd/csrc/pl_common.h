@@ -1,0 +1,186 @@
+// Shared helpers for the gfx950 kernels: status reporting, element types,
+// 16-byte vector loads and wave64 lane reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/pagelora.h"
+
+namespace pl {
+
+// ---------------------------------------------------------------- errors ---
+// The message buffer is per host thread, so concurrent callers on different
+// threads do not clobber each other's diagnostics.
+inline char* error_buffer() {
+  static thread_local char buf[512] = {0};
+  return buf;
+}
+
+inline int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(error_buffer(), 512, fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+inline int ok() {
+  error_buffer()[0] = 0;
+  return PL_OK;
+}
+
+#define PL_HIP_CHECK(expr)                                                  \
+  do {                                                                      \
+    hipError_t _e = (expr);                                                 \
+    if (_e != hipSuccess)                                                   \
+      return ::pl::fail(PL_ERR_HIP, "%s failed: %s", #expr,                 \
+                        hipGetErrorString(_e));                             \
+  } while (0)
+
+// After a kernel launch: report launch-configuration errors synchronously.
+#define PL_LAUNCH_CHECK(name)                                               \
+  do {                                                                      \
+    hipError_t _e = hipGetLastError();                                      \
+    if (_e != hipSuccess)                                                   \
+      return ::pl::fail(PL_ERR_HIP, "launch of %s failed: %s", name,        \
+                        hipGetErrorString(_e));                             \
+  } while (0)
+
+// --------------------------------------------------------- element types ---
+// Storage types.  bf16 is kept as raw 16-bit words: every conversion below is
+// written out so the rounding is explicit (round-to-nearest-even).
+struct bf16_t { uint16_t x; };
+typedef _Float16 f16_t;
+
+template <typename T> struct ElemBytes;
+template <> struct ElemBytes<float> { static constexpr int value = 4; };
+template <> struct ElemBytes<f16_t> { static constexpr int value = 2; };
+template <> struct ElemBytes<bf16_t> { static constexpr int value = 2; };
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) {
+  return __uint_as_float(w << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t w) {
+  return __uint_as_float(w & 0xffff0000u);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // NaN stays NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float h_lo(uint32_t w) {
+  half2_t h = __builtin_bit_cast(half2_t, w);
+  return (float)h.x;
+}
+__device__ __forceinline__ float h_hi(uint32_t w) {
+  half2_t h = __builtin_bit_cast(half2_t, w);
+  return (float)h.y;
+}
+
+// Unpack two packed 16-bit values of type T into floats.
+template <typename T> __device__ __forceinline__ void unpack2(uint32_t w, float& a, float& b);
+template <> __device__ __forceinline__ void unpack2<bf16_t>(uint32_t w, float& a, float& b) {
+  a = bf16_lo(w);
+  b = bf16_hi(w);
+}
+template <> __device__ __forceinline__ void unpack2<f16_t>(uint32_t w, float& a, float& b) {
+  a = h_lo(w);
+  b = h_hi(w);
+}
+
+// fp32 dot of two packed pairs plus c: v_dot2_f32_{f16,bf16}.
+template <typename T> __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c);
+template <> __device__ __forceinline__ float dot2<f16_t>(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a),
+                                __builtin_bit_cast(half2_t, b), c, false);
+}
+template <> __device__ __forceinline__ float dot2<bf16_t>(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// Store one float as T.
+template <typename T> __device__ __forceinline__ T from_float(float f);
+template <> __device__ __forceinline__ float from_float<float>(float f) { return f; }
+template <> __device__ __forceinline__ f16_t from_float<f16_t>(float f) { return (f16_t)f; }
+template <> __device__ __forceinline__ bf16_t from_float<bf16_t>(float f) {
+  bf16_t r;
+  r.x = f32_to_bf16_bits(f);
+  return r;
+}
+template <typename T> __device__ __forceinline__ float to_float(T v);
+template <> __device__ __forceinline__ float to_float<float>(float v) { return v; }
+template <> __device__ __forceinline__ float to_float<f16_t>(f16_t v) { return (float)v; }
+template <> __device__ __forceinline__ float to_float<bf16_t>(bf16_t v) {
+  return __uint_as_float(((uint32_t)v.x) << 16);
+}
+
+// Pack two floats into one 32-bit word of two T (16-bit types only).
+template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float a, float b) {
+  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+}
+template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
+  half2_t h;
+  h.x = (f16_t)a;
+  h.y = (f16_t)b;
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// ------------------------------------------------------- lane reductions ---
+// All-reduce across the 16 lanes of a DPP row with row rotations; every lane
+// of the row ends with the full result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_mov<0x128>(x);  // row_ror:8
+  x += dpp_mov<0x124>(x);  // row_ror:4
+  x += dpp_mov<0x122>(x);  // row_ror:2
+  x += dpp_mov<0x121>(x);  // row_ror:1
+  return x;
+}
+__device__ __forceinline__ float row8_sum(float x) {  // within aligned groups of 8 lanes
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 1);
+  return x;
+}
+__device__ __forceinline__ float row32_sum(float x) {  // within aligned groups of 32 lanes
+  x = row16_sum(x);
+  x += __shfl_xor(x, 16);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
+  return x;
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// exp2 on the hardware transcendental unit (v_exp_f32).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+inline int dtype_bytes(int dtype) {
+  return dtype == PL_DTYPE_F32 ? 4 : 2;
+}
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace pl

@@ -1,0 +1,126 @@
+"""No-merge LoRA delta on the gfx950 shrink/expand kernels.
+
+``lora_delta_`` adds ``scale_m * B_m[a_t] . (A_m[a_t] . x_t)`` to the output
+of every module m of a group sharing the input x, in place, for per-token
+adapter ids ``a_t`` -- the delta term of the reference's no-merge path:
+
+* packed q/k/v and gate/up: ``_packed_lora_delta`` / ``_cached_packed_lora_delta``
+  (model/flashinfer/packed_ops.py:314-384) build ``A_cat`` and a block-diagonal
+  ``B_bd`` with the scale folded in and run two ``F.linear``;
+* o_proj / down_proj: ``LoRALinear.forward`` (multilora/linear.py:200-231) and
+  ``_lora_delta`` (packed_ops.py:534-553).
+
+Here one shrink launch reads x once for the whole group and one expand
+launch accumulates every module's delta straight into its base output; the
+block-diagonal zeros are never stored or read.  Adapter selection is per
+token (the reference binds one adapter for the whole batch,
+multilora/runtime.py:138-174; a single adapter is the case ``ids == 0``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Sequence
+
+import torch
+
+from . import _lib
+
+_WS: dict[int, torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device zero-initialised workspace, grown (never shrunk) on demand.
+
+    The kernels return the ticket words to zero after every call, so the
+    buffer is zeroed only when it is (re)allocated -- never inside a
+    captured graph.
+    """
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("LoRA workspace must be sized before graph capture (call reserve_workspace)")
+        size = max(nbytes, 1 << 20)
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _WS[key] = ws
+    return ws
+
+
+def reserve_workspace(device: torch.device | str, num_tokens: int, in_features: int, ranks: Sequence[int]) -> None:
+    """Allocate the workspace a later (possibly captured) call will need."""
+    device = torch.device(device)
+    r_pad = (sum(ranks) + 31) // 32 * 32
+    ksplit = (in_features + 255) // 256
+    nbytes = 256 * 4 + ksplit * num_tokens * r_pad * 4 + num_tokens * r_pad * 2 + 4096
+    _workspace(device, nbytes)
+
+
+def _module_structs(modules, x: torch.Tensor):
+    """ctypes array of pl_lora_module for [(A, B, out, scale), ...]."""
+    n = len(modules)
+    if not 1 <= n <= _lib.PL_LORA_MAX_MODULES:
+        raise ValueError(f"a LoRA group holds 1..{_lib.PL_LORA_MAX_MODULES} modules, got {n}")
+    arr = (_lib.LoraModule * n)()
+    n_adapters = None
+    out_dtype = None
+    for i, (A, B, out, scale) in enumerate(modules):
+        if A.dim() == 2:
+            A = A.unsqueeze(0)
+        if B.dim() == 2:
+            B = B.unsqueeze(0)
+        if A.dim() != 3 or B.dim() != 3:
+            raise ValueError("A must be [adapters, rank, in] and B [adapters, out, rank]")
+        na, r, fin = A.shape
+        nb, fout, rb = B.shape
+        if na != nb or rb != r or fin != x.shape[1]:
+            raise ValueError(f"module {i}: A {tuple(A.shape)} / B {tuple(B.shape)} do not match x {tuple(x.shape)}")
+        if not (A.is_contiguous() and B.is_contiguous()):
+            raise ValueError(f"module {i}: A and B must be contiguous")
+        if A.dtype != x.dtype or B.dtype != x.dtype:
+            raise ValueError(f"module {i}: A/B dtype must equal x dtype {x.dtype}")
+        if out.dim() != 2 or out.shape[0] != x.shape[0] or out.shape[1] != fout or out.stride(1) != 1:
+            raise ValueError(f"module {i}: out must be [T, {fout}] with unit column stride")
+        if n_adapters is None:
+            n_adapters, out_dtype = na, out.dtype
+        elif na != n_adapters or out.dtype != out_dtype:
+            raise ValueError("all modules of a group need the same adapter count and output dtype")
+        for t in (A, B, out):
+            if t.device != x.device:
+                raise ValueError("x, A, B and out must be on one device")
+        arr[i].A, arr[i].B, arr[i].out = A.data_ptr(), B.data_ptr(), out.data_ptr()
+        arr[i].ldo, arr[i].out_features, arr[i].rank, arr[i].scale = out.stride(0), fout, r, float(scale)
+    return arr, n_adapters, out_dtype
+
+
+def lora_delta_(
+    x: torch.Tensor,
+    modules: Sequence[tuple[torch.Tensor, torch.Tensor, torch.Tensor, float]],
+    adapter_ids: torch.Tensor,
+) -> None:
+    """In place: ``out += scale * B[ids] . (A[ids] . x)`` for each ``(A, B, out, scale)``.
+
+    x: [T, in] (bf16 or fp16, unit column stride); A: [adapters, r, in] or
+    [r, in]; B: [adapters, out, r] or [out, r]; out: [T, out] view of the
+    base projection output (bf16, fp16 or fp32); adapter_ids: int32 [T] on
+    the device (negative = no adapter).
+    """
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be [T, in] with unit column stride")
+    if adapter_ids.dtype != torch.int32 or adapter_ids.numel() != x.shape[0] or adapter_ids.device != x.device:
+        raise ValueError("adapter_ids must be int32 [T] on x's device")
+    if x.shape[0] == 0:
+        return
+    arr, n_adapters, out_dtype = _module_structs(modules, x)
+    lib = _lib.load()
+    n = len(modules)
+    nbytes = lib.pl_lora_workspace_size(x.shape[0], x.shape[1], arr, n)
+    if nbytes == 0:
+        raise ValueError(f"invalid LoRA group: {_lib.last_error()}")
+    ws = _workspace(x.device, nbytes)
+    status = lib.pl_lora_delta(
+        x.data_ptr(), x.stride(0), x.shape[0], x.shape[1], arr, n,
+        adapter_ids.data_ptr(), n_adapters, _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype),
+        ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device),
+    )
+    _lib.check(status, "pl_lora_delta")

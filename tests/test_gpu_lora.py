@@ -1,0 +1,135 @@
+"""No-merge LoRA delta on the GPU vs the float64 oracle.
+
+The kernels round the rank-r intermediate x.A^T to the input dtype, as the
+reference's chained F.linear calls return it (packed_ops.py:324), so the
+oracle is evaluated with the same rounding (intermediate="bf16"/"f16").
+Bars: fp32 outputs 2e-3 max-abs; 16-bit outputs add one rounding of the
+result to the output type (2^-8 relative for bf16, 2^-11 for fp16).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import lora as ol
+from pagelora_amd.lora import lora_delta_
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(shape, std, gen, dtype=torch.bfloat16):
+    return (torch.randn(shape, generator=gen) * std).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("out_dtype", ["f32", "same"])
+def test_cfg4_qwen3_modules_4_adapters(gpu_device, dtype, out_dtype):
+    # hidden 4096, intermediate 12288, r=16, alpha 32 (s=2), 64 tokens over 4 adapters.
+    gen = torch.Generator().manual_seed(1237)
+    T, H, I, r, n = 64, 4096, 12288, 16, 4
+    ids = torch.randint(0, n, (T,), generator=gen, dtype=torch.int32)
+    groups = {
+        "qkv": (H, [4096, 1024, 1024]),
+        "o": (H, [4096]),
+        "gate_up": (H, [I, I]),
+        "down": (I, [H]),
+    }
+    for name, (fin, outs) in groups.items():
+        x = _rand((T, fin), 1.0, gen, dtype)
+        mods, host = [], []
+        for fout in outs:
+            A = _rand((n, r, fin), fin ** -0.5, gen, dtype)
+            B = _rand((n, fout, r), 0.01, gen, dtype)
+            out = torch.zeros((T, fout), dtype=torch.float32 if out_dtype == "f32" else dtype, device=gpu_device)
+            mods.append((A.to(gpu_device), B.to(gpu_device), out, 2.0))
+            host.append((A, B))
+        lora_delta_(x.to(gpu_device), mods, ids.to(gpu_device))
+        torch.cuda.synchronize()
+        for (A, B), (_, _, out, _) in zip(host, mods):
+            inter = "bf16" if dtype == torch.bfloat16 else "f16"
+            want = ol.multi_adapter_delta(x.float().numpy(), ids.tolist(), A.float().numpy(), B.float().numpy(), 2.0,
+                                          intermediate=inter)
+            got = out.float().cpu().numpy()
+            rtol = 0.0 if out_dtype == "f32" else (2.0**-8 if dtype == torch.bfloat16 else 2.0**-11)
+            err = np.abs(got - want)
+            assert (err <= 2e-3 + rtol * np.abs(want)).all(), f"{name}: max err {err.max():.3e}"
+
+
+def test_accumulates_into_base_and_matches_merged_weights(gpu_device):
+    # base + B(Ax) vs x (W + s B A)^T, both from the same bf16 inputs (a16).
+    gen = torch.Generator().manual_seed(3)
+    T, fin, fout, r = 16, 1024, 768, 16
+    x = _rand((T, fin), 1.0, gen)
+    W = _rand((fout, fin), 0.02, gen)
+    A = _rand((r, fin), fin ** -0.5, gen)
+    B = _rand((fout, r), 0.01, gen)
+    xd = x.to(gpu_device)
+    base = (xd.float() @ W.to(gpu_device).float().T)  # fp32 base output
+    lora_delta_(xd, [(A.to(gpu_device), B.to(gpu_device), base, 2.0)], torch.zeros(T, dtype=torch.int32, device=gpu_device))
+    torch.cuda.synchronize()
+    # The merged comparator has no intermediate rounding; the difference is
+    # the bf16 rounding of x.A^T times |B|*s (~1e-4 here), inside the bar.
+    want = ol.merged_linear(x.float().numpy(), W.float().numpy(), None, A.float().numpy(), B.float().numpy(), 2.0)
+    assert np.abs(base.cpu().numpy() - want).max() <= 2e-3
+
+
+def test_negative_ids_untouched_and_rank_not_multiple_of_8(gpu_device):
+    gen = torch.Generator().manual_seed(4)
+    T, fin = 20, 64
+    ids = torch.tensor([-1, 0, 1, 2, -5] * 4, dtype=torch.int32)
+    x = _rand((T, fin), 1.0, gen)
+    mods, host = [], []
+    for fout, r in ((40, 2), (24, 6), (8, 3)):   # ranks 2, 6, 3 (the reference's unit tests use rank 2)
+        A = _rand((3, r, fin), 0.2, gen)
+        B = _rand((3, fout, r), 0.2, gen)
+        base = torch.randn((T, fout), generator=gen)
+        mods.append((A.to(gpu_device), B.to(gpu_device), base.clone().to(gpu_device), 1.5))
+        host.append((A, B, base))
+    lora_delta_(x.to(gpu_device), mods, ids.to(gpu_device))
+    torch.cuda.synchronize()
+    for (A, B, base), (_, _, out, _) in zip(host, mods):
+        want = base.numpy() + ol.multi_adapter_delta(x.float().numpy(), ids.tolist(), A.float().numpy(),
+                                                     B.float().numpy(), 1.5, intermediate="bf16")
+        got = out.cpu().numpy()
+        assert np.abs(got - want).max() <= 2e-3
+        neg = (ids < 0).numpy()
+        assert np.array_equal(got[neg], base.numpy()[neg])
+
+
+def test_packed_group_equals_separate_calls(gpu_device):
+    gen = torch.Generator().manual_seed(5)
+    T, fin = 7, 256
+    x = _rand((T, fin), 1.0, gen).to(gpu_device)
+    ids = torch.zeros(T, dtype=torch.int32, device=gpu_device)
+    specs = [(128, 16), (32, 16), (32, 16)]
+    As = [_rand((1, r, fin), 0.1, gen).to(gpu_device) for _, r in specs]
+    Bs = [_rand((1, o, r), 0.1, gen).to(gpu_device) for o, r in specs]
+    packed_out = torch.zeros((T, sum(o for o, _ in specs)), dtype=torch.float32, device=gpu_device)
+    views, off = [], 0
+    for o, _ in specs:
+        views.append(packed_out[:, off:off + o])
+        off += o
+    lora_delta_(x, [(A, B, v, 2.0) for A, B, v in zip(As, Bs, views)], ids)
+    sep = [torch.zeros((T, o), dtype=torch.float32, device=gpu_device) for o, _ in specs]
+    for A, B, s in zip(As, Bs, sep):
+        lora_delta_(x, [(A, B, s, 2.0)], ids)
+    torch.cuda.synchronize()
+    assert torch.equal(packed_out, torch.cat(sep, dim=1))
+
+
+def test_repeated_calls_reuse_workspace(gpu_device):
+    # The per-adapter tickets must return to zero after every call.
+    gen = torch.Generator().manual_seed(6)
+    T, fin, fout, r = 33, 512, 64, 16
+    x = _rand((T, fin), 1.0, gen).to(gpu_device)
+    A = _rand((2, r, fin), 0.05, gen).to(gpu_device)
+    B = _rand((2, fout, r), 0.05, gen).to(gpu_device)
+    ids = (torch.arange(T, dtype=torch.int32) % 2).to(gpu_device)
+    outs = []
+    for _ in range(5):
+        o = torch.zeros((T, fout), dtype=torch.float32, device=gpu_device)
+        lora_delta_(x, [(A, B, o, 1.0)], ids)
+        outs.append(o)
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
