@@ -1,0 +1,299 @@
+"""Benchmark of the paged decode hot path on one MI355X.
+
+Headline workload: ragged batched decode, Llama-2-7B attention shape --
+64 rows with lengths U[128, 8192] (seed 1236), 32 q / 32 kv heads, head_dim
+128, fp16, 16-token pages scattered over a pool of (pages + 1024).  One step
+is one decode-attention pass over the batch: the device-side plan kernel and
+the decode kernel, inputs already resident in HBM.
+
+value = algorithmic bytes per step / measured step time (GB/s), where the
+algorithmic bytes are K+V of every valid token + q + o + page tables.  The
+roofline object reports the decode kernel alone (per-launch HIP events on
+the stream it runs on) against MI355X's 8 TB/s HBM peak.
+
+Also reported: the Qwen3-8B decode-layer latency (1 row x 2048 tokens, 32/8
+heads, bf16), the per-layer LoRA delta time of 64 tokens over 4 adapters,
+and the CPU baseline (the float64 numpy oracle on a bounded sample of rows,
+one thread).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode-attn achieved HBM GB/s (% peak); tok/s Qwen3-8B-shape LoRA decode"
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "decode_kernel_ragged64_mha_fp16.traffic.json"
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    p.add_argument("--no-extra", action="store_true", help="headline workload only")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="also run a 1 GiB device copy (for scaling rocprofv3 FETCH/WRITE_SIZE)")
+    return p.parse_args()
+
+
+def ragged_mha_workload(device, seed=1236):
+    import torch
+
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(128, 8193, size=64).tolist()
+    ps, h, d = 16, 32, 128
+    n_pages = [math.ceil(L / ps) for L in lens]
+    total = sum(n_pages)
+    pool = total + 1024
+    gen = torch.Generator(device=device).manual_seed(seed)
+    cache = torch.randn((pool, 2, ps, h, d), device=device, dtype=torch.float16, generator=gen)
+    q = (torch.randn((64, h, d), device=device, generator=gen) / math.sqrt(d)).to(torch.float16)
+    perm = torch.randperm(pool, generator=torch.Generator().manual_seed(seed))[:total].to(torch.int32)
+    indptr = torch.tensor(np.concatenate([[0], np.cumsum(n_pages)]), dtype=torch.int32)
+    last = torch.tensor([L - ps * (n - 1) for L, n in zip(lens, n_pages)], dtype=torch.int32)
+    return dict(name="ragged64_mha_fp16", q=q, cache=cache, indptr=indptr, indices=perm, last=last,
+                hq=h, hkv=h, d=d, ps=ps, lens=lens, dtype_bytes=2)
+
+
+def qwen3_layer_workload(device, seed=1235):
+    import torch
+
+    ps, hq, hkv, d, pool, L = 16, 32, 8, 128, 4096, 2048
+    gen = torch.Generator(device=device).manual_seed(seed)
+    cache = torch.randn((pool, 2, ps, hkv, d), device=device, dtype=torch.bfloat16, generator=gen)
+    q = torch.randn((1, hq, d), device=device, generator=gen).to(torch.bfloat16)
+    perm = torch.randperm(pool, generator=torch.Generator().manual_seed(seed))[: L // ps].to(torch.int32)
+    return dict(name="qwen3_layer_b1_2048_bf16", q=q, cache=cache,
+                indptr=torch.tensor([0, L // ps], dtype=torch.int32), indices=perm,
+                last=torch.tensor([ps], dtype=torch.int32), hq=hq, hkv=hkv, d=d, ps=ps, lens=[L], dtype_bytes=2)
+
+
+def algorithmic_bytes(w):
+    from oracle.paged_decode import algorithmic_bytes as ab
+
+    return ab(w["indptr"].tolist(), w["last"].tolist(), w["ps"], w["hq"], w["hkv"], w["d"], w["dtype_bytes"], w["dtype_bytes"])
+
+
+def time_decode(w, steps, warmup):
+    """(ms per step, per-launch decode-kernel ms, per-launch merge-kernel ms).
+
+    A step is the plan kernel, the decode kernel and the merge kernel; the
+    two run kernels are launched as two calls so HIP events on their stream
+    bracket each one.
+    """
+    import torch
+
+    from pagelora_amd import _lib
+    from pagelora_amd.attention_backend import PagedDecodeAttention
+
+    dev = w["q"].device
+    be = PagedDecodeAttention(device=dev, workspace_mb=256, num_qo_heads=w["hq"], num_kv_heads=w["hkv"],
+                              head_dim=w["d"], page_size=w["ps"])
+    be.plan_decode(paged_kv_indptr=w["indptr"], paged_kv_indices=w["indices"], paged_kv_last_page_len=w["last"])
+    out = torch.empty_like(w["q"])
+    for _ in range(warmup):
+        be.replan_decode()
+        be.run_decode_into(w["q"], w["cache"], out)
+    stream = torch.cuda.current_stream(dev)  # the stream every kernel is launched on
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    t0.record(stream)
+    for i in range(steps):
+        be.replan_decode()
+        ev[i][0].record(stream)
+        be.run_decode_into(w["q"], w["cache"], out, flags=_lib.PL_DECODE_SKIP_MERGE)
+        ev[i][1].record(stream)
+        be.run_decode_into(w["q"], w["cache"], out, flags=_lib.PL_DECODE_MERGE_ONLY)
+        ev[i][2].record(stream)
+    t1.record(stream)
+    torch.cuda.synchronize(dev)
+    decode = [e[0].elapsed_time(e[1]) for e in ev]
+    merge = [e[1].elapsed_time(e[2]) for e in ev]
+    return t0.elapsed_time(t1) / steps, decode, merge
+
+
+def time_lora(device, steps=20):
+    """Per-layer no-merge LoRA delta: 64 tokens over 4 adapters, r=16, the 7
+    Qwen3-8B modules in their 4 groups (q/k/v, o, gate/up, down)."""
+    import torch
+
+    from pagelora_amd.lora import lora_delta_
+
+    gen = torch.Generator(device=device).manual_seed(1237)
+    T, H, I, r, n = 64, 4096, 12288, 16, 4
+    ids = torch.randint(0, n, (T,), generator=gen, device=device, dtype=torch.int32)
+    groups = []
+    nbytes = 0
+    for fin, outs in ((H, [4096, 1024, 1024]), (H, [4096]), (H, [I, I]), (I, [H])):
+        x = torch.randn((T, fin), device=device, generator=gen).to(torch.bfloat16)
+        mods = []
+        for fout in outs:
+            A = (torch.randn((n, r, fin), device=device, generator=gen) / fin**0.5).to(torch.bfloat16)
+            B = (torch.randn((n, fout, r), device=device, generator=gen) * 0.01).to(torch.bfloat16)
+            out = torch.zeros((T, fout), device=device, dtype=torch.bfloat16)
+            mods.append((A, B, out, 2.0))
+            nbytes += (A.numel() + B.numel()) * 2 + out.numel() * 4
+        nbytes += x.numel() * 2
+        groups.append((x, mods))
+    for _ in range(3):
+        for x, mods in groups:
+            lora_delta_(x, mods, ids)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(device)
+    s.record()
+    for _ in range(steps):
+        for x, mods in groups:
+            lora_delta_(x, mods, ids)
+    e.record()
+    torch.cuda.synchronize(device)
+    ms = s.elapsed_time(e) / steps
+    return ms, nbytes
+
+
+def cpu_baseline(w, budget_s):
+    """Time the float64 numpy oracle on whole rows of the workload until the
+    budget is spent; report algorithmic GB/s of the rows it finished."""
+    import torch
+
+    from oracle import paged_decode as opd
+
+    q = w["q"].float().cpu().numpy()
+    indptr = w["indptr"].numpy()
+    last = w["last"].numpy()
+    order = list(range(len(last)))
+    done_bytes, spent, rows = 0, 0.0, 0
+    for b in order:
+        pages = w["indices"][indptr[b]: indptr[b + 1]].long()
+        sub = w["cache"][pages.to(w["cache"].device)].float().cpu().numpy()
+        n = len(pages)
+        t = time.perf_counter()
+        opd.paged_decode(q[b: b + 1], sub, [0, n], np.arange(n), [int(last[b])])
+        spent += time.perf_counter() - t
+        done_bytes += opd.algorithmic_bytes([0, n], [int(last[b])], w["ps"], w["hq"], w["hkv"], w["d"], 2, 2)
+        rows += 1
+        if spent >= budget_s:
+            break
+    return {
+        "value": round(done_bytes / spent / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"float64 numpy oracle, {rows} of 64 rows of the same workload ({sum(w['lens'][:rows])} tokens), "
+                  f"{spent:.1f} s, host has {os.cpu_count()} cores",
+    }
+
+
+def copy_calibration(device):
+    import torch
+
+    x = torch.ones(1 << 30, dtype=torch.uint8, device=device)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize(device)
+    print(f"[bench] copy calibration: 3 dispatches of a {1 << 30}-byte device copy", file=sys.stderr)
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every box here has one GPU)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        copy_calibration(dev)
+
+    w = ragged_mha_workload(dev)
+    nbytes = algorithmic_bytes(w)
+    ms_step, per_launch, merge_ms = time_decode(w, args.steps, args.warmup)
+    kern_ms = float(np.mean(per_launch))
+    value = nbytes / (ms_step * 1e-3) / 1e9
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    extra = {
+        "decode_kernel_us": round(kern_ms * 1e3, 2),
+        "decode_kernel_us_min": round(min(per_launch) * 1e3, 2),
+        "merge_kernel_us": round(float(np.mean(merge_ms)) * 1e3, 2),
+        "algorithmic_bytes_per_step": nbytes,
+        "tokens": int(sum(w["lens"])),
+    }
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(w, args.cpu_seconds)
+    del w
+    torch.cuda.empty_cache()
+    if not args.no_extra:
+        w2 = qwen3_layer_workload(dev)
+        ms2, per2, merge2 = time_decode(w2, max(args.steps, 100), args.warmup)
+        extra["qwen3_layer_b1_2048_bf16"] = {
+            "decode_kernel_us": round(float(np.mean(per2)) * 1e3, 2),
+            "merge_kernel_us": round(float(np.mean(merge2)) * 1e3, 2),
+            "step_us_incl_plan": round(ms2 * 1e3, 2),
+            "algorithmic_GBps": round(algorithmic_bytes(w2) / (float(np.mean(per2)) * 1e-3) / 1e9, 1),
+        }
+        del w2
+        torch.cuda.empty_cache()
+        lora_ms, lora_bytes = time_lora(dev)
+        extra["lora_delta_64tok_4adapters_7modules"] = {
+            "us_per_layer": round(lora_ms * 1e3, 2),
+            "algorithmic_GBps": round(lora_bytes / (lora_ms * 1e-3) / 1e9, 1),
+        }
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": "ragged batched paged decode attention, Llama-2-7B shape: batch 64, seq lens U[128,8192] "
+                        "(seed 1236), 32 q / 32 kv heads, head_dim 128, fp16, page_size 16, random pages in a "
+                        "pool of pages+1024",
+            "global_batch": 64,
+            "page_size": 16,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -108,8 +108,15 @@ int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                   const int32_t* last_page_len, void* o, int64_t o_stride_b,
                   int64_t o_stride_h, float* lse, int batch, int num_qo_heads,
                   int num_kv_heads, int head_dim, int page_size,
-                  float sm_scale, int dtype, int target_items,
+                  float sm_scale, int dtype, int target_items, int flags,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* pl_decode_run flags.  0 launches both of the run's kernels: the split-KV
+ * decode kernel and the merge of split rows.  A caller may launch them as
+ * two calls (SKIP_MERGE, then MERGE_ONLY with the same arguments) to place
+ * other work or timing events between them. */
+#define PL_DECODE_SKIP_MERGE 1
+#define PL_DECODE_MERGE_ONLY 2
 
 /*
  * Write one decode token per row into its page:

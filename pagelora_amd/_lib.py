@@ -24,6 +24,9 @@ PL_ERR_HIP = 4
 
 PL_LORA_MAX_MODULES = 4
 
+PL_DECODE_SKIP_MERGE = 1
+PL_DECODE_MERGE_ONLY = 2
+
 
 class ExtensionNotBuiltError(ImportError):
     """libpagelora_amd.so is missing: run ``__graft_entry__.build()``."""
@@ -73,7 +76,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _i64, _i64,             # o, strides
             _vp,                         # lse
             _i32, _i32, _i32, _i32, _i32,  # batch, hq, hkv, head_dim, page_size
-            _f32, _i32, _i32,            # sm_scale, dtype, target_items
+            _f32, _i32, _i32, _i32,      # sm_scale, dtype, target_items, flags
             _vp, _sz, _vp,               # workspace, bytes, stream
         ],
     ),

@@ -267,9 +267,12 @@ class PagedDecodeAttention:
         paged_kv_cache_layer,
         out: torch.Tensor,
         lse: torch.Tensor | None = None,
+        *,
+        flags: int = 0,
     ) -> torch.Tensor:
         """Allocation-free variant: writes ``out`` ([B, Hq, D]) and optionally
-        ``lse`` ([B, Hq] fp32, natural log)."""
+        ``lse`` ([B, Hq] fp32, natural log).  ``flags`` (PL_DECODE_SKIP_MERGE /
+        PL_DECODE_MERGE_ONLY) launches only one of the two run kernels."""
 
         plan = self._plan
         if plan is None:
@@ -301,7 +304,7 @@ class PagedDecodeAttention:
             out.data_ptr(), out.stride(0), out.stride(1),
             lse.data_ptr() if lse is not None else None,
             batch, self.num_qo_heads, self.num_kv_heads, self.head_dim, self.page_size,
-            self.sm_scale, _lib.dtype_code(q.dtype), plan["target_items"],
+            self.sm_scale, _lib.dtype_code(q.dtype), plan["target_items"], int(flags),
             self.workspace_buffer.data_ptr(), self.workspace_buffer.numel(),
             _lib.stream_handle(q.device),
         )

@@ -16,8 +16,10 @@
 //                  DPP row reductions, and keeps an online softmax per lane
 //                  row in fp32.  Rows with one item write the output
 //                  directly; split rows write (o, lse) partials.
-//   merge_kernel   one wavefront per (row, q head) of split rows: LSE-weighted
-//                  sum of the partials.
+//   merge_kernel   one wavefront per (row, q head) of a split row: the
+//                  LSE-weighted sum of its partials.  A separate launch, so
+//                  the kernel boundary orders the partials across the eight
+//                  XCD L2 caches without per-wave L2 write-back fences.
 //
 // Mathematics: o = softmax(q . K^T * sm_scale) . V, as the reference's
 // FlashInferAttentionBackend.run_decode (model/flashinfer/attention_backend.py
@@ -382,10 +384,10 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
   }
 
   st.merge_rows();
-  if (row != 0) return;
 
   constexpr float kLn2 = 0.69314718055994530942f;
-  if (flags & 1) {
+  if (flags & 1) {  // the row is one item: write the output directly
+    if (row != 0) return;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int hq = h * G + g;
@@ -398,31 +400,37 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
         lse[(int64_t)b * num_qo_heads + hq] =
             st.l[g] > 0.f ? (st.m[g] + __log2f(st.l[g])) * kLn2 : -INFINITY;
     }
-  } else {
+    return;
+  }
+
+  // Split row: publish this item's normalised partial and its log2-sum-exp;
+  // merge_kernel combines them after this kernel has finished.
+  if (row != 0) return;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int hq = h * G + g;
-      const float inv = st.l[g] > 0.f ? 1.f / st.l[g] : 0.f;
-      float out[8];
+  for (int g = 0; g < G; ++g) {
+    const int hq = h * G + g;
+    const float inv = st.l[g] > 0.f ? 1.f / st.l[g] : 0.f;
+    float out[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) out[i] = st.acc[g][i] * inv;
-      float* pp = part_o + ((int64_t)item_idx * num_qo_heads + hq) * D + col * 8;
-      Lane8<float>::store(pp, out);
-      if (col == 0)
-        part_lse[(int64_t)item_idx * num_qo_heads + hq] =
-            st.l[g] > 0.f ? st.m[g] + __log2f(st.l[g]) : -INFINITY;
-    }
+    for (int i = 0; i < 8; ++i) out[i] = st.acc[g][i] * inv;
+    Lane8<float>::store(part_o + ((int64_t)item_idx * num_qo_heads + hq) * D + col * 8, out);
+    if (col == 0)
+      part_lse[(int64_t)item_idx * num_qo_heads + hq] =
+          st.l[g] > 0.f ? st.m[g] + __log2f(st.l[g]) : -INFINITY;
   }
 }
 
 // ----------------------------------------------------------------- merge ---
+// One wavefront per (row, q head) of a split row.  LPT lanes cover one
+// partial row of D floats (32 bytes each), so a wave folds 64/LPT partials
+// per iteration; the lane rows are summed with xor shuffles at the end.
 template <typename T, int D>
 __global__ __launch_bounds__(kWave * kWavesPerWG) void merge_kernel(
     const int2* __restrict__ row_info, const float* __restrict__ part_lse,
     const float* __restrict__ part_o, T* __restrict__ o, int64_t o_sb, int64_t o_sh,
     float* __restrict__ lse, const int* __restrict__ header, int batch, int num_qo_heads,
     int max_items) {
-  constexpr int DPL = (D + kWave - 1) / kWave;  // dims per lane
+  constexpr int LPT = D / 8, CPI = kWave / LPT;
   const int lane = threadIdx.x % kWave;
   const int wave = uniform(blockIdx.x * kWavesPerWG + threadIdx.x / kWave);
   if (wave >= batch * num_qo_heads) return;
@@ -434,31 +442,38 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void merge_kernel(
   if (n <= 1 || first < 0 || first + n > max_items) return;
 
   float mx = -INFINITY;
-  for (int c = 0; c < n; ++c) mx = fmaxf(mx, part_lse[(int64_t)(first + c) * num_qo_heads + hq]);
+  for (int c = lane; c < n; c += kWave)
+    mx = fmaxf(mx, part_lse[(int64_t)(first + c) * num_qo_heads + hq]);
+  mx = wave_max(mx);
   const float m_use = mx == -INFINITY ? 0.f : mx;
-  float acc[DPL];
-#pragma unroll
-  for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+
+  const int row = lane / LPT, col = lane % LPT;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float wsum = 0.f;
-  for (int c = 0; c < n; ++c) {
+#pragma unroll 2
+  for (int c = row; c < n; c += CPI) {
     const int64_t slot = (int64_t)(first + c) * num_qo_heads + hq;
     const float w = fast_exp2(part_lse[slot] - m_use);
+    const float4 a = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8);
+    const float4 bq = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8 + 4);
     wsum += w;
-    const float* pp = part_o + slot * D;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) {
-      const int d = lane + i * kWave;
-      if (d < D) acc[i] = fmaf(w, pp[d], acc[i]);
-    }
+    acc[0] = fmaf(w, a.x, acc[0]); acc[1] = fmaf(w, a.y, acc[1]);
+    acc[2] = fmaf(w, a.z, acc[2]); acc[3] = fmaf(w, a.w, acc[3]);
+    acc[4] = fmaf(w, bq.x, acc[4]); acc[5] = fmaf(w, bq.y, acc[5]);
+    acc[6] = fmaf(w, bq.z, acc[6]); acc[7] = fmaf(w, bq.w, acc[7]);
   }
+#pragma unroll
+  for (int off = LPT; off < kWave; off <<= 1) {
+    wsum += __shfl_xor(wsum, off);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] += __shfl_xor(acc[i], off);
+  }
+  if (row != 0) return;
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  T* op = o + (int64_t)b * o_sb + (int64_t)hq * o_sh;
+  T* op = o + (int64_t)b * o_sb + (int64_t)hq * o_sh + col * 8;
 #pragma unroll
-  for (int i = 0; i < DPL; ++i) {
-    const int d = lane + i * kWave;
-    if (d < D) op[d] = from_float<T>(acc[i] * inv);
-  }
-  if (lse != nullptr && lane == 0) {
+  for (int i = 0; i < 8; ++i) op[i] = from_float<T>(acc[i] * inv);
+  if (lse != nullptr && col == 0) {
     constexpr float kLn2 = 0.69314718055994530942f;
     lse[(int64_t)b * num_qo_heads + hq] = wsum > 0.f ? (m_use + __log2f(wsum)) * kLn2 : -INFINITY;
   }
@@ -471,25 +486,30 @@ struct RunArgs {
   const int32_t* indices; const int32_t* last;
   void* o; int64_t o_sb, o_sh; float* lse;
   int batch, hq, hkv, page_size; int64_t num_pages; float scale_log2;
-  const int* header; const Item* items; int max_items; const int2* row_info; float* part_lse; float* part_o;
+  const int* header; const Item* items; int max_items; const int2* row_info;
+  float* part_lse; float* part_o; int flags;
   hipStream_t stream;
 };
 
 template <typename T, int D, int G>
 int launch(const RunArgs& a) {
-  const int64_t waves = (int64_t)a.max_items * a.hkv;
-  const int grid = (int)((waves + kWavesPerWG - 1) / kWavesPerWG);
-  hipLaunchKernelGGL((decode_kernel<T, D, G>), dim3(grid), dim3(kWave * kWavesPerWG), 0, a.stream,
-                     (const T*)a.q, a.q_sb, a.q_sh, (const T*)a.kc, (const T*)a.vc, a.page_stride,
-                     a.token_stride, a.head_stride, a.indices, a.last, (T*)a.o, a.o_sb, a.o_sh,
-                     a.lse, a.hq, a.hkv, a.page_size, a.num_pages, a.scale_log2, a.header,
-                     a.items, a.batch, a.max_items, a.part_lse, a.part_o);
-  PL_LAUNCH_CHECK("decode_kernel");
-  const int mgrid = (a.batch * a.hq + kWavesPerWG - 1) / kWavesPerWG;
-  hipLaunchKernelGGL((merge_kernel<T, D>), dim3(mgrid), dim3(kWave * kWavesPerWG), 0, a.stream,
-                     a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
-                     a.batch, a.hq, a.max_items);
-  PL_LAUNCH_CHECK("merge_kernel");
+  if (!(a.flags & PL_DECODE_MERGE_ONLY)) {
+    const int64_t waves = (int64_t)a.max_items * a.hkv;
+    const int grid = (int)((waves + kWavesPerWG - 1) / kWavesPerWG);
+    hipLaunchKernelGGL((decode_kernel<T, D, G>), dim3(grid), dim3(kWave * kWavesPerWG), 0, a.stream,
+                       (const T*)a.q, a.q_sb, a.q_sh, (const T*)a.kc, (const T*)a.vc, a.page_stride,
+                       a.token_stride, a.head_stride, a.indices, a.last, (T*)a.o, a.o_sb, a.o_sh,
+                       a.lse, a.hq, a.hkv, a.page_size, a.num_pages, a.scale_log2, a.header,
+                       a.items, a.batch, a.max_items, a.part_lse, a.part_o);
+    PL_LAUNCH_CHECK("decode_kernel");
+  }
+  if (!(a.flags & PL_DECODE_SKIP_MERGE)) {
+    const int mgrid = (a.batch * a.hq + kWavesPerWG - 1) / kWavesPerWG;
+    hipLaunchKernelGGL((merge_kernel<T, D>), dim3(mgrid), dim3(kWave * kWavesPerWG), 0, a.stream,
+                       a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
+                       a.batch, a.hq, a.max_items);
+    PL_LAUNCH_CHECK("merge_kernel");
+  }
   return ok();
 }
 
@@ -559,7 +579,7 @@ extern "C" int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride
                              const int32_t* indices, const int32_t* last_page_len, void* o, int64_t o_stride_b,
                              int64_t o_stride_h, float* lse, int batch, int num_qo_heads,
                              int num_kv_heads, int head_dim, int page_size, float sm_scale,
-                             int dtype, int target_items, void* workspace,
+                             int dtype, int target_items, int flags, void* workspace,
                              size_t workspace_bytes, void* stream) {
   if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0");
   if (batch == 0) return ok();
@@ -599,6 +619,7 @@ extern "C" int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride
   a.scale_log2 = sm_scale * 1.44269504088896340736f;
   a.items = (const Item*)(ws + L.items); a.max_items = max_items;
   a.row_info = (const int2*)(ws + L.row_info);
+  a.flags = flags;
   a.part_lse = (float*)(ws + L.lse); a.part_o = (float*)(ws + L.partial_o);
   a.stream = (hipStream_t)stream;
   const int g = num_qo_heads / num_kv_heads;
