@@ -163,11 +163,9 @@ typedef struct {
 /* Most modules in one group (q, k, v). */
 #define PL_LORA_MAX_MODULES 4
 
-/* Workspace bytes for one pl_lora_* call (at most 256 adapters): per-adapter
- * ticket words, fp32 partial sums [ceil(in/256)][num_tokens][sum(rank)
- * rounded up to 32] and the rounded rank-r intermediate.  The workspace must
- * be zero-filled once before its first use; every call leaves the ticket
- * words zero again.  Calls that share a workspace must be stream ordered. */
+/* Workspace bytes for one pl_lora_* call: the rank-r intermediate
+ * [num_tokens][sum(rank) rounded up to 32] in the input dtype.  Calls that
+ * share a workspace must be stream ordered; shrink writes it, expand reads it. */
 size_t pl_lora_workspace_size(int num_tokens, int in_features,
                               const pl_lora_module* modules_h, int num_modules);
 

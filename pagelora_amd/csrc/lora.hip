@@ -3,11 +3,11 @@
 // for the modules m of a group that share their input x (q/k/v, gate/up, or a
 // lone o_proj / down_proj) and per-token adapter ids a_t.
 //
-//   shrink_kernel  grid (k-slice, adapter).  Gathers the tokens of its adapter
-//                  (LDS list), multiplies their x slice by the adapter's
-//                  concatenated A rows on MFMA 16x16x32 tiles, writes fp32
-//                  partial sums; the last workgroup of each adapter (atomic
-//                  ticket) reduces the partials and rounds the rank-r
+//   shrink_kernel  grid (16 rank rows, adapter), 16 waves per workgroup.
+//                  Gathers the tokens of its adapter (LDS list), multiplies
+//                  their x by the adapter's concatenated A rows on MFMA
+//                  16x16x32 tiles with the k range split across the waves,
+//                  sums the waves' tiles in LDS and rounds the rank-r
 //                  intermediate to the input dtype.
 //   expand_kernel  grid (16-column tiles x 4, adapter).  Multiplies the
 //                  rounded intermediate by B^T on MFMA 16x16x32 tiles and
@@ -28,7 +28,6 @@ namespace lora {
 constexpr int kWave = 64;
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kSlice = 256;      // k elements per shrink workgroup
 constexpr int kMaxTokens = 4096; // tokens per call (LDS token list)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -62,27 +61,15 @@ template <> __device__ __forceinline__ f32x4 mfma32<f16_t>(uint4 a, uint4 b, f32
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// Workspace layout: per-adapter tickets, fp32 partials [ksplit][T][r_pad],
-// rounded intermediate [T][r_pad] of the input dtype.
-struct WsLayout {
-  size_t tickets, part, y, total;
-};
-inline int ksplit_for(int in_features) { return (in_features + kSlice - 1) / kSlice; }
-inline WsLayout ws_layout(int tokens, int in_features, int r_pad, int n_adapters) {
-  WsLayout L;
-  L.tickets = 0;
-  L.part = align_up((size_t)(n_adapters > 0 ? n_adapters : 1) * sizeof(int), 256);
-  L.y = align_up(L.part + (size_t)ksplit_for(in_features) * tokens * r_pad * sizeof(float), 256);
-  L.total = align_up(L.y + (size_t)tokens * r_pad * 2, 256);
-  return L;
-}
+// Workspace: the rank-r intermediate [T][r_pad], rounded to the input dtype.
+inline size_t ws_bytes_needed(int tokens, int r_pad) { return align_up((size_t)tokens * r_pad * 2, 256); }
 
 // Gather the tokens of adapter `a` into LDS; returns their count (all threads).
 __device__ __forceinline__ int gather_tokens(const int32_t* __restrict__ ids, int tokens, int a,
-                                             int* s_list, int* s_count) {
+                                             int* s_list, int* s_count, int nthreads) {
   if (threadIdx.x == 0) *s_count = 0;
   __syncthreads();
-  for (int t = threadIdx.x; t < tokens; t += kThreads) {
+  for (int t = threadIdx.x; t < tokens; t += nthreads) {
     if (ids[t] == a) {
       const int slot = atomicAdd(s_count, 1);
       s_list[slot] = t;
@@ -98,86 +85,88 @@ __device__ __forceinline__ uint4 load8(const void* p, bool ok) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
+// Shrink: one workgroup of kShrinkWaves waves per (16 rank rows, adapter).
+// The waves split the k range; each multiplies up to four 16-token tiles by
+// the 16 rank rows on MFMA 16x16x32, and the waves' partial tiles are summed
+// through LDS, so no global atomics, fences or partial buffers are needed.
+constexpr int kShrinkWaves = 16;
+constexpr int kShrinkThreads = kShrinkWaves * kWave;
+constexpr int kTilesPerPass = 4;
+
 template <typename T>
-__global__ __launch_bounds__(kThreads) void shrink_kernel(
+__global__ __launch_bounds__(kShrinkThreads) void shrink_kernel(
     const T* __restrict__ x, int64_t ldx, int tokens, int in_features, Group g,
-    const int32_t* __restrict__ ids, int ksplit, int* __restrict__ tickets,
-    float* __restrict__ part, uint16_t* __restrict__ y) {
+    const int32_t* __restrict__ ids, uint16_t* __restrict__ y) {
   __shared__ int s_list[kMaxTokens];
-  __shared__ int s_count, s_last;
-  const int ks = blockIdx.x;
+  __shared__ int s_count;
+  __shared__ float s_red[kShrinkWaves][kTilesPerPass][256];
+  const int jt = blockIdx.x;
   const int a = blockIdx.y;
-  const int n_a = gather_tokens(ids, tokens, a, s_list, &s_count);
+  const int n_a = gather_tokens(ids, tokens, a, s_list, &s_count, kShrinkThreads);
   if (n_a == 0) return;
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const int lr = lane % 16;       // MFMA row (token) / column (rank row)
   const int kq = (lane / 16) * 8; // this lane's 8-element k group
-  const int k0 = ks * kSlice;
-  const int n_tt = (n_a + 15) / 16;
-  const int n_jt = g.r_pad / 16;
+  // k range of this wave, in whole 32-element MFMA steps
+  const int steps_total = (in_features + 31) / 32;
+  const int steps_per_wave = (steps_total + kShrinkWaves - 1) / kShrinkWaves;
+  const int k_begin = wave * steps_per_wave * 32;
+  const int k_end = min(in_features, k_begin + steps_per_wave * 32);
 
-  for (int pair = wave; pair < n_tt * n_jt; pair += kWaves) {
-    const int tt = pair / n_jt, jt = pair - tt * n_jt;
-    const int ti = tt * 16 + lr;
-    const bool tok_ok = ti < n_a;
-    const T* xrow = x + (int64_t)(tok_ok ? s_list[ti] : 0) * ldx;
-    // rank row j -> module, local row
-    const int j = jt * 16 + lr;
-    const T* arow = x;  // placeholder address; never dereferenced unless a_ok
-    bool a_ok = false;
-    if (j < g.r_total) {
+  // rank row j -> module, local row
+  const int j = jt * 16 + lr;
+  const T* arow = x;  // placeholder address; never dereferenced unless a_ok
+  bool a_ok = false;
+  if (j < g.r_total) {
 #pragma unroll
-      for (int m = 0; m < PL_LORA_MAX_MODULES; ++m) {
-        if (m < g.n && j >= g.m[m].rank_offset && j < g.m[m].rank_offset + g.m[m].rank) {
-          const int jr = j - g.m[m].rank_offset;
-          arow = (const T*)g.m[m].A + ((int64_t)a * g.m[m].rank + jr) * in_features;
-          a_ok = true;
-        }
+    for (int m = 0; m < PL_LORA_MAX_MODULES; ++m) {
+      if (m < g.n && j >= g.m[m].rank_offset && j < g.m[m].rank_offset + g.m[m].rank) {
+        arow = (const T*)g.m[m].A + ((int64_t)a * g.m[m].rank + (j - g.m[m].rank_offset)) * in_features;
+        a_ok = true;
       }
     }
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int kk = 0; kk < kSlice; kk += 32) {
-      const int k = k0 + kk + kq;
-      const bool k_ok = k < in_features;  // in_features % 8 == 0: a group is all in or all out
-      const uint4 av = load8(xrow + k, tok_ok && k_ok);
-      const uint4 bv = load8(arow + k, a_ok && k_ok);
-      acc = mfma32<T>(av, bv, acc);
-    }
-    // D rows = tokens 4*(lane/16)+i, column = rank row jt*16 + lr.
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tr = tt * 16 + (lane / 16) * 4 + i;
-      if (tr < n_a)
-        part[((int64_t)ks * tokens + s_list[tr]) * g.r_pad + jt * 16 + lr] = acc[i];
-    }
   }
 
-  // Ticket: the last workgroup of this adapter reduces the k-slices.  Every
-  // thread publishes its partial stores at agent scope before the barrier.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(&tickets[a], 1, __ATOMIC_ACQ_REL,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == ksplit - 1;
+  const int n_tt = (n_a + 15) / 16;
+  for (int tt0 = 0; tt0 < n_tt; tt0 += kTilesPerPass) {
+    f32x4 acc[kTilesPerPass];
+    const T* xrow[kTilesPerPass];
+    bool tok_ok[kTilesPerPass];
+#pragma unroll
+    for (int u = 0; u < kTilesPerPass; ++u) {
+      acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int ti = (tt0 + u) * 16 + lr;
+      tok_ok[u] = ti < n_a;
+      xrow[u] = x + (int64_t)(tok_ok[u] ? s_list[ti] : 0) * ldx;
+    }
+    for (int k = k_begin + kq; k < k_end; k += 32) {
+      const uint4 bv = load8(arow + k, a_ok);  // in_features % 8 == 0: all 8 in range
+#pragma unroll
+      for (int u = 0; u < kTilesPerPass; ++u) {
+        if (tt0 + u < n_tt) acc[u] = mfma32<T>(load8(xrow[u] + k, tok_ok[u]), bv, acc[u]);
+      }
+    }
+    // D rows = tokens 4*(lane/16)+i of the tile, column = rank row lr.
+#pragma unroll
+    for (int u = 0; u < kTilesPerPass; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_red[wave][u][((lane / 16) * 4 + i) * 16 + lr] = acc[u][i];
+    __syncthreads();
+    for (int c = threadIdx.x; c < kTilesPerPass * 256; c += kShrinkThreads) {
+      const int u = c / 256, cell = c % 256;
+      const int tr = (tt0 + u) * 16 + cell / 16;
+      if (tt0 + u < n_tt && tr < n_a) {
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < kShrinkWaves; ++w) sum += s_red[w][u][cell];
+        const T v = from_float<T>(sum);
+        y[(int64_t)s_list[tr] * g.r_pad + jt * 16 + cell % 16] = __builtin_bit_cast(uint16_t, v);
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();  // acquire: the other slices' partials are visible from here on
-  const int cells = n_a * g.r_pad;
-  for (int c = threadIdx.x; c < cells; c += kThreads) {
-    const int ti = c / g.r_pad, jj = c - ti * g.r_pad;
-    const int t = s_list[ti];
-    float s = 0.f;
-    if (jj < g.r_total)
-      for (int q = 0; q < ksplit; ++q)
-        s += part[((int64_t)q * tokens + t) * g.r_pad + jj];
-    const T v = from_float<T>(s);
-    y[(int64_t)t * g.r_pad + jj] = __builtin_bit_cast(uint16_t, v);
-  }
-  if (threadIdx.x == 0) tickets[a] = 0;  // ready for the next call
 }
 
 template <typename OT> __device__ __forceinline__ void accumulate(OT* p, float v);
@@ -195,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(
   __shared__ int s_list[kMaxTokens];
   __shared__ int s_count;
   const int a = blockIdx.y;
-  const int n_a = gather_tokens(ids, tokens, a, s_list, &s_count);
+  const int n_a = gather_tokens(ids, tokens, a, s_list, &s_count, kThreads);
   if (n_a == 0) return;
 
   const int lane = threadIdx.x % kWave;
@@ -251,9 +240,9 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(
     const bool tok_ok = ti < n_a;
     const uint16_t* yrow = y + (int64_t)(tok_ok ? s_list[ti] : 0) * g.r_pad;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int kt = 0; kt < n_kt; ++kt) {
-      const uint4 av = load8(yrow + kt * 32 + kq, tok_ok);
-      acc = mfma32<T>(av, bop[kt], acc);
+#pragma unroll
+    for (int kt = 0; kt < kMaxKt; ++kt) {  // static indices keep bop[] in registers
+      if (kt < n_kt) acc = mfma32<T>(load8(yrow + kt * 32 + kq, tok_ok), bop[kt], acc);
     }
     if (out_col != nullptr) {
 #pragma unroll
@@ -324,31 +313,24 @@ extern "C" size_t pl_lora_workspace_size(int num_tokens, int in_features,
                                          const pl_lora_module* modules_h, int num_modules) {
   Group g;
   if (make_group(modules_h, num_modules, in_features, &g) != PL_OK || num_tokens < 0) return 0;
-  // Ticket slots for up to 65535 adapters would be wasteful; the layout is
-  // sized for the adapters actually passed at call time, so report the
-  // size for 256 adapter slots, the largest a single call accepts cheaply.
-  return ws_layout(num_tokens, in_features, g.r_pad, 256).total;
+  return ws_bytes_needed(num_tokens, g.r_pad);
 }
 
 static int lora_shrink_impl(const void* x, int64_t ldx, int tokens, int in_features,
                             const Group& g, const int32_t* ids, int n_adapters, int dtype,
                             void* ws, size_t ws_bytes, hipStream_t stream) {
-  const WsLayout L = ws_layout(tokens, in_features, g.r_pad, n_adapters);
-  if (n_adapters > 256) return fail(PL_ERR_UNSUPPORTED, "num_adapters %d > 256", n_adapters);
-  if (L.total > ws_bytes)
-    return fail(PL_ERR_WORKSPACE, "LoRA workspace of %zu bytes < %zu needed", ws_bytes, L.total);
+  (void)in_features;
+  const size_t need = ws_bytes_needed(tokens, g.r_pad);
+  if (need > ws_bytes)
+    return fail(PL_ERR_WORKSPACE, "LoRA workspace of %zu bytes < %zu needed", ws_bytes, need);
   if (ws == nullptr || (uintptr_t)ws % 256) return fail(PL_ERR_INVALID, "workspace must be 256-byte aligned");
-  char* w = (char*)ws;
-  const int ksplit = ksplit_for(in_features);
-  dim3 grid(ksplit, n_adapters);
+  dim3 grid(g.r_pad / 16, n_adapters);
   if (dtype == PL_DTYPE_BF16)
-    hipLaunchKernelGGL(shrink_kernel<bf16_t>, grid, dim3(kThreads), 0, stream, (const bf16_t*)x,
-                       ldx, tokens, in_features, g, ids, ksplit, (int*)(w + L.tickets),
-                       (float*)(w + L.part), (uint16_t*)(w + L.y));
+    hipLaunchKernelGGL(shrink_kernel<bf16_t>, grid, dim3(kShrinkThreads), 0, stream, (const bf16_t*)x,
+                       ldx, tokens, in_features, g, ids, (uint16_t*)ws);
   else
-    hipLaunchKernelGGL(shrink_kernel<f16_t>, grid, dim3(kThreads), 0, stream, (const f16_t*)x,
-                       ldx, tokens, in_features, g, ids, ksplit, (int*)(w + L.tickets),
-                       (float*)(w + L.part), (uint16_t*)(w + L.y));
+    hipLaunchKernelGGL(shrink_kernel<f16_t>, grid, dim3(kShrinkThreads), 0, stream, (const f16_t*)x,
+                       ldx, tokens, in_features, g, ids, (uint16_t*)ws);
   PL_LAUNCH_CHECK("lora shrink_kernel");
   return PL_OK;
 }
@@ -377,11 +359,11 @@ static int launch_expand(int tokens, const Group& g, const int32_t* ids, int n_a
 static int lora_expand_impl(int tokens, int in_features, const Group& g, const int32_t* ids,
                             int n_adapters, int dtype, int out_dtype, const void* ws,
                             size_t ws_bytes, hipStream_t stream) {
-  const WsLayout L = ws_layout(tokens, in_features, g.r_pad, n_adapters);
-  if (n_adapters > 256) return fail(PL_ERR_UNSUPPORTED, "num_adapters %d > 256", n_adapters);
-  if (L.total > ws_bytes)
-    return fail(PL_ERR_WORKSPACE, "LoRA workspace of %zu bytes < %zu needed", ws_bytes, L.total);
-  const uint16_t* y = (const uint16_t*)((const char*)ws + L.y);
+  (void)in_features;
+  const size_t need = ws_bytes_needed(tokens, g.r_pad);
+  if (need > ws_bytes)
+    return fail(PL_ERR_WORKSPACE, "LoRA workspace of %zu bytes < %zu needed", ws_bytes, need);
+  const uint16_t* y = (const uint16_t*)ws;
   return dtype == PL_DTYPE_BF16 ? launch_expand<bf16_t>(tokens, g, ids, n_adapters, out_dtype, y, stream)
                                 : launch_expand<f16_t>(tokens, g, ids, n_adapters, out_dtype, y, stream);
 }

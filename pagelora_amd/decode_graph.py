@@ -1,0 +1,117 @@
+"""hipGraph capture and replay of the batched decode step.
+
+Counterpart of the reference's ``FlashInferBatchDecodeCudaGraphRunner``
+(model/flashinfer/cuda_graph.py:307-543): graph-owned input buffers
+(tokens, positions, KV slot page/offset, adapter ids), one warmup on a
+side stream, then capture of embed -> layers -> final norm -> lm_head ->
+argmax (cuda_graph.py:222-234, 475-493); a capture failure disables graphs
+and the caller falls back to eager (cuda_graph.py:204-210, 420-426).
+
+The key (``DecodeGraphKey``, cuda_graph.py:76-93) differs on purpose: it has
+no ``page_table_pages`` and no host plan.  The decode plan lives on the
+device and the KV pool never moves, so a graph captured for a batch size
+replays for every later step while the rows grow; the reference recaptures
+on every new page.  torch's CUDAGraph is hipGraph on ROCm.
+"""
+
+from __future__ import annotations
+
+from collections import OrderedDict
+from dataclasses import dataclass
+
+import torch
+
+from .attention_backend import PagedDecodeAttention
+from .decoder import DecodeContext, DecoderWeights, decode_step_static
+from .kv_pool import PagedKVPool
+
+
+@dataclass(frozen=True)
+class DecodeGraphKey:
+    model_id: int
+    backend_signature: tuple
+    cache_data_ptr: int
+    cache_shape: tuple
+    cache_dtype: torch.dtype
+    batch: int
+    adapter_version: int
+
+
+@dataclass
+class DecodeGraphEntry:
+    graph: torch.cuda.CUDAGraph
+    ctx: DecodeContext
+    logits: torch.Tensor
+
+
+class BatchDecodeGraphRunner:
+    """Capture once per key, replay every step."""
+
+    def __init__(self, weights: DecoderWeights, pool: PagedKVPool, backend: PagedDecodeAttention,
+                 max_entries: int = 32) -> None:
+        self.weights = weights
+        self.pool = pool
+        self.backend = backend
+        self.max_entries = max_entries
+        self.adapter_version = 0
+        self.disabled_reason: str | None = None
+        self.capture_count = 0
+        self.replay_count = 0
+        self._graphs: OrderedDict[DecodeGraphKey, DecodeGraphEntry] = OrderedDict()
+
+    def key(self, batch: int) -> DecodeGraphKey:
+        cache = self.pool.cache
+        return DecodeGraphKey(
+            model_id=id(self.weights),
+            backend_signature=self.backend.decode_graph_signature(),
+            cache_data_ptr=cache.data_ptr(),
+            cache_shape=tuple(cache.shape),
+            cache_dtype=cache.dtype,
+            batch=batch,
+            adapter_version=self.adapter_version,
+        )
+
+    def entry(self, batch: int) -> DecodeGraphEntry | None:
+        """The graph for ``batch``: captured on first use (needs a current plan)."""
+        if self.disabled_reason is not None:
+            return None
+        k = self.key(batch)
+        e = self._graphs.get(k)
+        if e is not None:
+            self._graphs.move_to_end(k)
+            return e
+        try:
+            e = self._capture(batch)
+        except Exception as exc:  # capture failure: fall back to eager for good
+            self.disabled_reason = f"{type(exc).__name__}: {exc}"
+            self._graphs.clear()
+            return None
+        while len(self._graphs) >= self.max_entries:
+            self._graphs.popitem(last=False)
+        self._graphs[k] = e
+        self.capture_count += 1
+        return e
+
+    def _capture(self, batch: int) -> DecodeGraphEntry:
+        dev = self.pool.cache.device
+        ctx = DecodeContext(batch, dev)
+        # Warm up once on a side stream (allocator pools, library workspaces),
+        # writing to a slot nobody reads: page 0 of the pool is never handed out.
+        cur = torch.cuda.current_stream(dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            decode_step_static(self.weights, self.pool, self.backend, ctx)
+        cur.wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            logits = decode_step_static(self.weights, self.pool, self.backend, ctx)
+        return DecodeGraphEntry(graph=graph, ctx=ctx, logits=logits)
+
+    def replay(self, entry: DecodeGraphEntry) -> torch.Tensor:
+        entry.graph.replay()
+        self.replay_count += 1
+        return entry.logits
+
+    def clear(self) -> None:
+        self._graphs.clear()

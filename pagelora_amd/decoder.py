@@ -1,0 +1,285 @@
+"""Qwen3-shaped decoder around the paged-decode + LoRA hot path.
+
+This is the caller of the kernels, shaped like the reference's graph-static
+decode layer ``run_flashinfer_decode_layer_static_append_batch``
+(model/flashinfer/layer_runner.py:340-396):
+
+    rmsnorm -> packed q/k/v GEMM (+ no-merge LoRA delta, packed_ops.py:105-165)
+    -> per-head q/k RMSNorm (projection.py:248-260) -> RoPE (projection.py:155-190)
+    -> KV append into the page (layer_runner.py:399-412)
+    -> paged decode attention (attention_backend.py:120-131)
+    -> o_proj (+ LoRA, packed_ops.py:251-265 / linear.py:200-231) -> residual
+    -> rmsnorm -> packed gate/up GEMM (+ LoRA, packed_ops.py:168-203) -> SiLU*up
+    -> down_proj (+ LoRA) -> residual
+
+Base GEMMs are plain library GEMMs (torch -> hipBLASLt); the LoRA delta, KV
+append and attention are the library's HIP kernels.  Weights are random
+(no checkpoints are available); shapes follow Qwen3-8B.
+
+Prefill (``prefill``) is not on the decode path: it fills the paged KV pool
+for the prompt with plain torch math (float32 attention), so decode starts
+from a real context.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from .attention_backend import PagedDecodeAttention, kv_append
+from .kv_pool import PagedKVPool, Request
+from .lora import lora_delta_
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    num_layers: int = 36
+    hidden: int = 4096
+    num_qo_heads: int = 32
+    num_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 12288
+    vocab: int = 151936
+    rope_theta: float = 1_000_000.0
+    rms_eps: float = 1e-6
+    qk_norm: bool = True
+    lora_rank: int = 16
+    lora_alpha: float = 32.0
+
+    @property
+    def q_dim(self) -> int:
+        return self.num_qo_heads * self.head_dim
+
+    @property
+    def kv_dim(self) -> int:
+        return self.num_kv_heads * self.head_dim
+
+
+QWEN3_8B = DecoderConfig()
+
+
+class LayerWeights:
+    """One decoder layer: packed base weights plus stacked LoRA adapters.
+
+    Packed q/k/v and gate/up weights are the reference's packed layout
+    (``_cached_packed_linear``, packed_ops.py:268-311).  LoRA A/B of each
+    module are stacked over adapters: A [n, r, in], B [n, out, r].
+    """
+
+    def __init__(self, cfg: DecoderConfig, n_adapters: int, device, dtype, gen: torch.Generator) -> None:
+        h, qd, kd, i, r = cfg.hidden, cfg.q_dim, cfg.kv_dim, cfg.intermediate, cfg.lora_rank
+
+        def w(shape, std):
+            return (torch.randn(shape, device=device, dtype=torch.float32, generator=gen) * std).to(dtype)
+
+        self.input_norm = (1.0 + 0.1 * torch.randn(h, device=device, generator=gen)).to(dtype)
+        self.post_norm = (1.0 + 0.1 * torch.randn(h, device=device, generator=gen)).to(dtype)
+        self.q_norm = (1.0 + 0.1 * torch.randn(cfg.head_dim, device=device, generator=gen)).to(dtype)
+        self.k_norm = (1.0 + 0.1 * torch.randn(cfg.head_dim, device=device, generator=gen)).to(dtype)
+        self.w_qkv = w((qd + 2 * kd, h), 0.02)
+        self.w_o = w((h, qd), 0.02)
+        self.w_gate_up = w((2 * i, h), 0.02)
+        self.w_down = w((h, i), 0.02)
+        self.lora = {}
+        for name, fin, fout in (("q", h, qd), ("k", h, kd), ("v", h, kd), ("o", qd, h),
+                                ("gate", h, i), ("up", h, i), ("down", i, h)):
+            self.lora[name] = (w((n_adapters, r, fin), fin ** -0.5), w((n_adapters, fout, r), 0.01))
+
+
+class DecoderWeights:
+    def __init__(self, cfg: DecoderConfig, *, n_adapters: int = 1, device="cuda", dtype=torch.bfloat16, seed: int = 0):
+        gen = torch.Generator(device=device).manual_seed(seed)
+        self.cfg = cfg
+        self.dtype = dtype
+        self.n_adapters = n_adapters
+        self.embed = (torch.randn((cfg.vocab, cfg.hidden), device=device, generator=gen) * 0.02).to(dtype)
+        self.final_norm = (1.0 + 0.1 * torch.randn(cfg.hidden, device=device, generator=gen)).to(dtype)
+        self.lm_head = (torch.randn((cfg.vocab, cfg.hidden), device=device, generator=gen) * 0.02).to(dtype)
+        self.layers = [LayerWeights(cfg, n_adapters, device, dtype, gen) for _ in range(cfg.num_layers)]
+        self.lora_scale = cfg.lora_alpha / cfg.lora_rank  # linear.py:41, 71
+
+
+# ------------------------------------------------------------------ ops ---
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """Qwen3 RMSNorm: fp32 statistics, result cast back, then the weight."""
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return weight * xf.to(x.dtype)
+
+
+def rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float):
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=positions.device, dtype=torch.float32) / head_dim))
+    freqs = positions.float()[:, None] * inv[None, :]
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Non-interleaved (rotate-half) RoPE on [T, H, D] with cos/sin [T, D]."""
+    half = x.shape[-1] // 2
+    xf = x.float()
+    rot = torch.cat([-xf[..., half:], xf[..., :half]], dim=-1)
+    return (xf * cos[:, None, :] + rot * sin[:, None, :]).to(x.dtype)
+
+
+# ------------------------------------------------------- decode (static) ---
+class DecodeContext:
+    """Graph-owned per-step buffers of a batch (cuda_graph.py:307-464 analogue)."""
+
+    def __init__(self, batch: int, device) -> None:
+        self.batch = batch
+        self.tokens = torch.zeros(batch, dtype=torch.int64, device=device)
+        self.positions = torch.zeros(batch, dtype=torch.int64, device=device)
+        self.page_id = torch.zeros(batch, dtype=torch.int64, device=device)
+        self.page_offset = torch.zeros(batch, dtype=torch.int64, device=device)
+        self.adapter_ids = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.next_tokens = torch.zeros(batch, dtype=torch.int64, device=device)
+
+
+def decode_layer_static(
+    cfg: DecoderConfig,
+    lw: LayerWeights,
+    lora_scale: float,
+    hidden: torch.Tensor,
+    layer_cache: torch.Tensor,
+    backend: PagedDecodeAttention,
+    ctx: DecodeContext,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+) -> torch.Tensor:
+    """One single-token decode layer for the whole batch; graph-capturable."""
+    B = hidden.shape[0]
+    ids = ctx.adapter_ids
+    x = rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
+    qkv = F.linear(x, lw.w_qkv)
+    qd, kd = cfg.q_dim, cfg.kv_dim
+    (Aq, Bq), (Ak, Bk), (Av, Bv) = lw.lora["q"], lw.lora["k"], lw.lora["v"]
+    lora_delta_(x, [(Aq, Bq, qkv[:, :qd], lora_scale), (Ak, Bk, qkv[:, qd:qd + kd], lora_scale),
+                    (Av, Bv, qkv[:, qd + kd:], lora_scale)], ids)
+    q = qkv[:, :qd].view(B, cfg.num_qo_heads, cfg.head_dim)
+    k = qkv[:, qd:qd + kd].view(B, cfg.num_kv_heads, cfg.head_dim)
+    v = qkv[:, qd + kd:].view(B, cfg.num_kv_heads, cfg.head_dim)
+    if cfg.qk_norm:
+        q = rmsnorm(q, lw.q_norm, cfg.rms_eps)
+        k = rmsnorm(k, lw.k_norm, cfg.rms_eps)
+    q = apply_rope(q, cos, sin)
+    k = apply_rope(k, cos, sin)
+    kv_append(layer_cache, k, v, ctx.page_id, ctx.page_offset, num_kv_heads=cfg.num_kv_heads,
+              head_dim=cfg.head_dim, page_size=backend.page_size)
+    attn = torch.empty_like(q)
+    backend.run_decode_into(q, layer_cache, attn)
+    attn = attn.view(B, qd)
+    o = F.linear(attn, lw.w_o)
+    Ao, Bo = lw.lora["o"]
+    lora_delta_(attn, [(Ao, Bo, o, lora_scale)], ids)
+    hidden = hidden + o
+    x2 = rmsnorm(hidden, lw.post_norm, cfg.rms_eps)
+    gu = F.linear(x2, lw.w_gate_up)
+    I = cfg.intermediate
+    (Ag, Bg), (Au, Bu) = lw.lora["gate"], lw.lora["up"]
+    lora_delta_(x2, [(Ag, Bg, gu[:, :I], lora_scale), (Au, Bu, gu[:, I:], lora_scale)], ids)
+    act = F.silu(gu[:, :I]) * gu[:, I:]
+    d = F.linear(act, lw.w_down)
+    Ad, Bd = lw.lora["down"]
+    lora_delta_(act, [(Ad, Bd, d, lora_scale)], ids)
+    return hidden + d
+
+
+def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: PagedDecodeAttention,
+                       ctx: DecodeContext) -> torch.Tensor:
+    """embed -> layers -> final norm -> lm_head -> greedy argmax into ctx.next_tokens.
+
+    Returns the logits [B, vocab] (graph-owned under capture).
+    """
+    cfg = weights.cfg
+    hidden = F.embedding(ctx.tokens, weights.embed)
+    cos, sin = rope_cos_sin(ctx.positions, cfg.head_dim, cfg.rope_theta)
+    for li, lw in enumerate(weights.layers):
+        hidden = decode_layer_static(cfg, lw, weights.lora_scale, hidden, pool.layer_cache(li), backend, ctx, cos, sin)
+    x = rmsnorm(hidden, weights.final_norm, cfg.rms_eps)
+    logits = F.linear(x, weights.lm_head)
+    ctx.next_tokens.copy_(torch.argmax(logits, dim=-1))  # greedy, sampling.py:8-15
+    return logits
+
+
+# ------------------------------------------------------------- prefill ---
+def _attention_f32(q, k, v, causal_offset: int) -> torch.Tensor:
+    """softmax(q k^T / sqrt(D)) v over [T,Hq,D] x [S,Hkv,D] in float32, with
+    query t allowed to see keys < causal_offset + t + 1."""
+    T, hq, d = q.shape
+    S, hkv, _ = k.shape
+    g = hq // hkv
+    qf = q.float().permute(1, 0, 2).contiguous()                                   # [Hq, T, D]
+    kf = k.float().repeat_interleave(g, dim=1).permute(1, 2, 0).contiguous()     # [Hq, D, S]
+    vf = v.float().repeat_interleave(g, dim=1).permute(1, 0, 2).contiguous()     # [Hq, S, D]
+    s = torch.matmul(qf, kf) / math.sqrt(d)
+    t_idx = torch.arange(T, device=q.device)[:, None]
+    s_idx = torch.arange(S, device=q.device)[None, :]
+    s = s.masked_fill(s_idx > (causal_offset + t_idx), float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), vf).permute(1, 0, 2).contiguous()
+
+
+@torch.no_grad()
+def prefill(weights: DecoderWeights, pool: PagedKVPool, request: Request, tokens: torch.Tensor,
+            adapter: int = 0, chunk: int = 1024) -> torch.Tensor:
+    """Run ``tokens`` (appended after ``request.length``) through the model,
+    writing their K/V into the request's pages; returns the last hidden row's
+    logits.  Pages for the tokens must already be reserved."""
+    cfg = weights.cfg
+    ps = pool.page_size
+    start = request.length - tokens.numel()
+    assert start >= 0, "reserve pages for the prompt before prefill"
+    pages = torch.tensor(request.pages(), dtype=torch.int64, device=tokens.device)
+    last_logits = None
+    for c0 in range(0, tokens.numel(), chunk):
+        tok = tokens[c0:c0 + chunk]
+        T = tok.numel()
+        pos = torch.arange(start + c0, start + c0 + T, device=tokens.device)
+        cos, sin = rope_cos_sin(pos, cfg.head_dim, cfg.rope_theta)
+        page_of = pages[pos // ps]
+        off_of = pos % ps
+        hidden = F.embedding(tok, weights.embed)
+        ids = torch.full((T,), adapter, dtype=torch.int32, device=tokens.device)
+        for li, lw in enumerate(weights.layers):
+            cache = pool.layer_cache(li)
+            x = rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
+            qkv = F.linear(x, lw.w_qkv)
+            qd, kd = cfg.q_dim, cfg.kv_dim
+            (Aq, Bq), (Ak, Bk), (Av, Bv) = lw.lora["q"], lw.lora["k"], lw.lora["v"]
+            s = weights.lora_scale
+            lora_delta_(x, [(Aq, Bq, qkv[:, :qd], s), (Ak, Bk, qkv[:, qd:qd + kd], s), (Av, Bv, qkv[:, qd + kd:], s)], ids)
+            q = qkv[:, :qd].reshape(T, cfg.num_qo_heads, cfg.head_dim)
+            k = qkv[:, qd:qd + kd].reshape(T, cfg.num_kv_heads, cfg.head_dim)
+            v = qkv[:, qd + kd:].reshape(T, cfg.num_kv_heads, cfg.head_dim)
+            if cfg.qk_norm:
+                q = rmsnorm(q, lw.q_norm, cfg.rms_eps)
+                k = rmsnorm(k, lw.k_norm, cfg.rms_eps)
+            q = apply_rope(q, cos, sin)
+            k = apply_rope(k, cos, sin)
+            cache[page_of, 0, off_of] = k
+            cache[page_of, 1, off_of] = v
+            ctx_len = start + c0 + T
+            all_pos = torch.arange(ctx_len, device=tokens.device)
+            kk = cache[pages[all_pos // ps], 0, all_pos % ps]
+            vv = cache[pages[all_pos // ps], 1, all_pos % ps]
+            attn = _attention_f32(q, kk, vv, start + c0).to(hidden.dtype).reshape(T, qd)
+            o = F.linear(attn, lw.w_o)
+            Ao, Bo = lw.lora["o"]
+            lora_delta_(attn, [(Ao, Bo, o, s)], ids)
+            hidden = hidden + o
+            x2 = rmsnorm(hidden, lw.post_norm, cfg.rms_eps)
+            gu = F.linear(x2, lw.w_gate_up)
+            I = cfg.intermediate
+            (Ag, Bg), (Au, Bu) = lw.lora["gate"], lw.lora["up"]
+            lora_delta_(x2, [(Ag, Bg, gu[:, :I], s), (Au, Bu, gu[:, I:], s)], ids)
+            act = F.silu(gu[:, :I]) * gu[:, I:]
+            d = F.linear(act, lw.w_down)
+            Ad, Bd = lw.lora["down"]
+            lora_delta_(act, [(Ad, Bd, d, s)], ids)
+            hidden = hidden + d
+        x = rmsnorm(hidden[-1:], weights.final_norm, cfg.rms_eps)
+        last_logits = F.linear(x, weights.lm_head)
+    return last_logits

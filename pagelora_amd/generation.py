@@ -1,0 +1,194 @@
+"""Batched greedy decode loop with hipGraph replay.
+
+The driver of the decode path, after the reference's
+``generate_batch_with_flashinfer_kvcache`` (model/flashinfer/generation.py:872-1132):
+per step it reserves each row's KV slot (``reserve_chunk``), packs the page
+table and plans the decode (``_plan_decode_batch``, :221-247), copies the
+step inputs into the graph-owned buffers and replays the captured step
+(cuda_graph.py:350-418), falling back to eager when capture failed.
+
+Differences on MI355X: the next token never leaves the device (the graph
+writes the argmax into the buffer the next step reads), the page table goes
+up as one asynchronous copy from pinned memory with no read-back (the plan
+runs on the device), and the graph is not recaptured as rows grow.
+tok/s follows the reference's definition: generated tokens / decode seconds
+(test/inference/common.py:59-60).
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from .attention_backend import PagedDecodeAttention
+from .decode_graph import BatchDecodeGraphRunner
+from .decoder import DecodeContext, DecoderWeights, decode_step_static, prefill
+from .kv_pool import PagedKVPool, Request
+
+
+@dataclass
+class GenerateResult:
+    tokens: torch.Tensor             # [B, steps] generated ids (host)
+    decode_seconds: float
+    prefill_seconds: float
+    steps: int
+    batch: int
+    used_graph: bool
+    graph_captures: int = 0
+    graph_replays: int = 0
+    first_logits: torch.Tensor | None = None
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def decode_tokens_per_s(self) -> float:
+        return self.batch * self.steps / self.decode_seconds if self.decode_seconds > 0 else 0.0
+
+
+class _PinnedRing:
+    """Pinned host staging slots reused round-robin; a slot is rewritten only
+    after the copy that read it has run (event per slot)."""
+
+    def __init__(self, slots: int, shape, dtype) -> None:
+        self.bufs = [torch.empty(shape, dtype=dtype, pin_memory=True) for _ in range(slots)]
+        self.events: list[torch.cuda.Event | None] = [None] * slots
+        self.i = 0
+
+    def next(self) -> tuple[torch.Tensor, int]:
+        i = self.i
+        self.i = (self.i + 1) % len(self.bufs)
+        if self.events[i] is not None:
+            self.events[i].synchronize()
+        return self.bufs[i], i
+
+    def record(self, i: int) -> None:
+        ev = torch.cuda.Event()
+        ev.record()
+        self.events[i] = ev
+
+
+class BatchGenerator:
+    """Owns the backend, graph runner and pinned staging for one model + pool."""
+
+    def __init__(self, weights: DecoderWeights, pool: PagedKVPool, *, workspace_mb: int = 128,
+                 use_graph: bool = True) -> None:
+        cfg = weights.cfg
+        self.weights = weights
+        self.pool = pool
+        self.backend = PagedDecodeAttention(
+            device=pool.cache.device, workspace_mb=workspace_mb, num_qo_heads=cfg.num_qo_heads,
+            num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=pool.page_size,
+            max_pages=pool.capacity_pages,
+        )
+        self.use_graph = use_graph
+        self.graphs = BatchDecodeGraphRunner(weights, pool, self.backend)
+        cap = pool.capacity_pages
+        self._tables = _PinnedRing(4, (3, cap + 1), torch.int32)
+        self._inputs = _PinnedRing(4, (4, 4096), torch.int64)
+
+    def _plan(self, requests) -> None:
+        indptr, indices, last = self.pool.tables(requests)
+        buf, slot = self._tables.next()
+        B, n = len(requests), len(indices)
+        buf[0, : B + 1].numpy()[:] = indptr
+        buf[1, :n].numpy()[:] = indices
+        buf[2, :B].numpy()[:] = last
+        self.backend.plan_decode(paged_kv_indptr=buf[0, : B + 1], paged_kv_indices=buf[1, :n],
+                                 paged_kv_last_page_len=buf[2, :B])
+        self._tables.record(slot)
+
+    def _stage_inputs(self, ctx: DecodeContext, requests, adapters) -> None:
+        """Reserve each row's slot for its next token; upload position/slot/adapter."""
+        B = len(requests)
+        buf, slot = self._inputs.next()
+        ps = self.pool.page_size
+        for b, r in enumerate(requests):
+            pos = r.length
+            self.pool.reserve(r, 1)
+            page, off = r.slot(pos, ps)
+            buf[0, b], buf[1, b], buf[2, b], buf[3, b] = pos, page, off, adapters[b]
+        ctx.positions.copy_(buf[0, :B], non_blocking=True)
+        ctx.page_id.copy_(buf[1, :B], non_blocking=True)
+        ctx.page_offset.copy_(buf[2, :B], non_blocking=True)
+        ctx.adapter_ids.copy_(buf[3, :B], non_blocking=True)
+        self._inputs.record(slot)
+
+    @torch.no_grad()
+    def generate(self, requests: list[Request], first_tokens: torch.Tensor, steps: int,
+                 adapters: list[int] | None = None) -> GenerateResult:
+        """Decode ``steps`` greedy tokens for rows whose prompts are prefilled.
+
+        first_tokens: [B] int64 on the device, the token each row decodes
+        first (the greedy pick of the prefill logits).
+        """
+        B = len(requests)
+        dev = self.pool.cache.device
+        adapters = adapters or [0] * B
+        history = torch.empty((steps, B), dtype=torch.int64, device=dev)
+        entry = None
+        ctx = DecodeContext(B, dev)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        capture_s = 0.0
+        for step in range(steps):
+            if step == 0:
+                staging = ctx
+                self._stage_inputs(staging, requests, adapters)
+                self._plan(requests)
+                if self.use_graph:
+                    tc = time.perf_counter()
+                    n_before = self.graphs.capture_count
+                    entry = self.graphs.entry(B)
+                    if self.graphs.capture_count != n_before:
+                        torch.cuda.synchronize(dev)
+                        capture_s = time.perf_counter() - tc
+                if entry is not None:
+                    ctx = entry.ctx
+                    for name in ("positions", "page_id", "page_offset", "adapter_ids"):
+                        getattr(ctx, name).copy_(getattr(staging, name))
+                ctx.tokens.copy_(first_tokens)
+            else:
+                self._stage_inputs(ctx, requests, adapters)
+                self._plan(requests)
+                ctx.tokens.copy_(ctx.next_tokens)
+            if entry is not None:
+                self.graphs.replay(entry)
+            else:
+                decode_step_static(self.weights, self.pool, self.backend, ctx)
+            history[step].copy_(ctx.next_tokens)
+        torch.cuda.synchronize(dev)
+        dt = time.perf_counter() - t0 - capture_s
+        return GenerateResult(tokens=history.t().cpu(), decode_seconds=dt, prefill_seconds=0.0, steps=steps,
+                              batch=B, used_graph=entry is not None, graph_captures=self.graphs.capture_count,
+                              graph_replays=self.graphs.replay_count, extra={"capture_seconds": capture_s})
+
+
+def prefill_requests(weights: DecoderWeights, pool: PagedKVPool, prompts: list[torch.Tensor],
+                     shared_prefix: torch.Tensor | None = None, adapters: list[int] | None = None):
+    """Prefill rows (optionally behind one shared prefix held in shared pages).
+
+    Returns (requests, first_tokens [B] on the device, first-step logits [B, V]).
+    The shared prefix must fill whole pages so rows can list its pages
+    read-only (paged_kvcache_manager.py:324-333).
+    """
+    dev = pool.cache.device
+    ps = pool.page_size
+    adapters = adapters or [0] * len(prompts)
+    prefix_pages, prefix_len = [], 0
+    if shared_prefix is not None and shared_prefix.numel():
+        if shared_prefix.numel() % ps:
+            raise ValueError("a shared prefix must fill whole pages")
+        owner = Request()
+        pool.reserve(owner, shared_prefix.numel())
+        prefill(weights, pool, owner, shared_prefix.to(dev), adapter=adapters[0])
+        prefix_pages, prefix_len = list(owner.own_pages), owner.length
+    requests, logits = [], []
+    for p, a in zip(prompts, adapters):
+        r = Request(prefix_pages=list(prefix_pages), prefix_len=prefix_len, length=prefix_len)
+        pool.reserve(r, p.numel())
+        logits.append(prefill(weights, pool, r, p.to(dev), adapter=a))
+        requests.append(r)
+    logits = torch.cat(logits, dim=0)
+    return requests, torch.argmax(logits, dim=-1), logits

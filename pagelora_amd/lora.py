@@ -30,19 +30,15 @@ _WS: dict[int, torch.Tensor] = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device zero-initialised workspace, grown (never shrunk) on demand.
-
-    The kernels return the ticket words to zero after every call, so the
-    buffer is zeroed only when it is (re)allocated -- never inside a
-    captured graph.
-    """
+    """Per-device workspace for the rank-r intermediate, grown (never shrunk)
+    on demand -- never inside a captured graph."""
     key = device.index if device.index is not None else torch.cuda.current_device()
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("LoRA workspace must be sized before graph capture (call reserve_workspace)")
         size = max(nbytes, 1 << 20)
-        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        ws = torch.empty(size, dtype=torch.uint8, device=device)
         _WS[key] = ws
     return ws
 
@@ -51,9 +47,7 @@ def reserve_workspace(device: torch.device | str, num_tokens: int, in_features: 
     """Allocate the workspace a later (possibly captured) call will need."""
     device = torch.device(device)
     r_pad = (sum(ranks) + 31) // 32 * 32
-    ksplit = (in_features + 255) // 256
-    nbytes = 256 * 4 + ksplit * num_tokens * r_pad * 4 + num_tokens * r_pad * 2 + 4096
-    _workspace(device, nbytes)
+    _workspace(device, num_tokens * r_pad * 2 + 256)
 
 
 def _module_structs(modules, x: torch.Tensor):

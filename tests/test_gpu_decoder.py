@@ -1,0 +1,142 @@
+"""The decode step (caller of the kernels) on a small Qwen3-shaped model.
+
+(1) One eager decode step vs an independent torch implementation of the
+    reference's static decode layer (layer_runner.py:340-412): index_put_
+    append, float32 attention over the gathered pages, LoRA as chained
+    F.linear calls (packed_ops.py:534-553), greedy argmax.  Bar: the
+    reference's own logits gate (atol 0.1, rtol 0.01,
+    scripts/check_inference_correctness.py:26-37) and identical greedy tokens.
+(2) hipGraph replay vs eager over 12 steps: bit-identical tokens and logits.
+"""
+
+import copy
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from pagelora_amd.decoder import DecodeContext, DecoderConfig, DecoderWeights, decode_step_static
+from pagelora_amd.generation import BatchGenerator, prefill_requests
+from pagelora_amd.kv_pool import PagedKVPool
+
+pytestmark = pytest.mark.gpu
+
+SMALL = DecoderConfig(num_layers=2, hidden=256, num_qo_heads=8, num_kv_heads=2, head_dim=64, intermediate=512,
+                      vocab=1000, lora_rank=16, lora_alpha=32.0)
+
+
+def _setup(dev, seed=0):
+    w = DecoderWeights(SMALL, n_adapters=2, device=dev, seed=seed)
+    pool = PagedKVPool(num_layers=SMALL.num_layers, capacity_pages=64, page_size=16, num_kv_heads=2, head_dim=64,
+                       dtype=torch.bfloat16, device=dev)
+    g = torch.Generator().manual_seed(7)
+    prefix = torch.randint(0, SMALL.vocab, (32,), generator=g)
+    prompts = [torch.randint(0, SMALL.vocab, (n,), generator=g) for n in (5, 17, 1)]
+    reqs, first, logits = prefill_requests(w, pool, prompts, shared_prefix=prefix, adapters=[0, 1, 1])
+    return w, pool, reqs, first, logits
+
+
+def _rms(x, w, eps):
+    xf = x.float()
+    return w * (xf / torch.sqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
+
+
+def _rope(x, pos, d, theta):
+    inv = theta ** (-torch.arange(0, d, 2, device=x.device, dtype=torch.float64) / d)
+    ang = pos.double()[:, None] * inv[None]
+    c, s = torch.cos(ang).float(), torch.sin(ang).float()
+    x1, x2 = x.float()[..., : d // 2], x.float()[..., d // 2:]
+    c, s = c[:, None, :], s[:, None, :]
+    return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1).to(x.dtype)
+
+
+def _torch_reference_step(w, cache, reqs, tokens, adapters):
+    """Independent restatement of one batched static decode step."""
+    cfg = w.cfg
+    ps = 16
+    B = len(reqs)
+    pos = torch.tensor([r.length - 1 for r in reqs], device=cache.device)
+    slots = [r.slot(r.length - 1, ps) for r in reqs]
+    page_id = torch.tensor([p for p, _ in slots], device=cache.device)
+    off = torch.tensor([o for _, o in slots], device=cache.device)
+    hidden = w.embed[tokens]
+    s = w.lora_scale
+    for li, lw in enumerate(w.layers):
+        x = _rms(hidden, lw.input_norm, cfg.rms_eps)
+        outs = []
+        for name, W in (("q", lw.w_qkv[: cfg.q_dim]), ("k", lw.w_qkv[cfg.q_dim: cfg.q_dim + cfg.kv_dim]),
+                        ("v", lw.w_qkv[cfg.q_dim + cfg.kv_dim:])):
+            A, Bm = lw.lora[name]
+            base = F.linear(x, W)
+            delta = torch.stack([F.linear(F.linear(x[b], A[adapters[b]]), Bm[adapters[b]]) for b in range(B)]) * s
+            outs.append(base + delta)
+        q = outs[0].view(B, cfg.num_qo_heads, cfg.head_dim)
+        k = outs[1].view(B, cfg.num_kv_heads, cfg.head_dim)
+        v = outs[2].view(B, cfg.num_kv_heads, cfg.head_dim)
+        q = _rope(_rms(q, lw.q_norm, cfg.rms_eps), pos, cfg.head_dim, cfg.rope_theta)
+        k = _rope(_rms(k, lw.k_norm, cfg.rms_eps), pos, cfg.head_dim, cfg.rope_theta)
+        layer = cache[li]
+        layer.index_put_((page_id, torch.zeros_like(page_id), off), k)
+        layer.index_put_((page_id, torch.ones_like(page_id), off), v)
+        attn = []
+        for b, r in enumerate(reqs):
+            kk = torch.cat([layer[p, 0] for p in r.pages()])[: r.length].float()   # [L, Hkv, D]
+            vv = torch.cat([layer[p, 1] for p in r.pages()])[: r.length].float()
+            g = cfg.num_qo_heads // cfg.num_kv_heads
+            kk = kk.repeat_interleave(g, dim=1)
+            vv = vv.repeat_interleave(g, dim=1)
+            sc = torch.einsum("hd,lhd->hl", q[b].float(), kk) / math.sqrt(cfg.head_dim)
+            attn.append(torch.einsum("hl,lhd->hd", sc.softmax(-1), vv).to(hidden.dtype))
+        attn = torch.stack(attn).view(B, cfg.q_dim)
+        Ao, Bo = lw.lora["o"]
+        o = F.linear(attn, lw.w_o) + torch.stack(
+            [F.linear(F.linear(attn[b], Ao[adapters[b]]), Bo[adapters[b]]) for b in range(B)]) * s
+        hidden = hidden + o
+        x2 = _rms(hidden, lw.post_norm, cfg.rms_eps)
+        I = cfg.intermediate
+        gu = []
+        for name, W in (("gate", lw.w_gate_up[:I]), ("up", lw.w_gate_up[I:])):
+            A, Bm = lw.lora[name]
+            gu.append(F.linear(x2, W) + torch.stack(
+                [F.linear(F.linear(x2[b], A[adapters[b]]), Bm[adapters[b]]) for b in range(B)]) * s)
+        act = F.silu(gu[0]) * gu[1]
+        Ad, Bd = lw.lora["down"]
+        d = F.linear(act, lw.w_down) + torch.stack(
+            [F.linear(F.linear(act[b], Ad[adapters[b]]), Bd[adapters[b]]) for b in range(B)]) * s
+        hidden = hidden + d
+    logits = F.linear(_rms(hidden, w.final_norm, cfg.rms_eps), w.lm_head)
+    return logits.float(), logits.argmax(-1)
+
+
+def test_decode_step_matches_torch_reference(gpu_device):
+    w, pool, reqs, first, _ = _setup(gpu_device)
+    adapters = [0, 1, 1]
+    gen = BatchGenerator(w, pool, workspace_mb=8, use_graph=False)
+    ctx = DecodeContext(len(reqs), gpu_device)
+    gen._stage_inputs(ctx, reqs, adapters)
+    gen._plan(reqs)
+    ctx.tokens.copy_(first)
+    ref_cache = pool.cache.clone()
+    logits = decode_step_static(w, pool, gen.backend, ctx).float()
+    ref_logits, ref_tok = _torch_reference_step(w, ref_cache, reqs, first, adapters)
+    torch.cuda.synchronize()
+    assert torch.allclose(logits, ref_logits, atol=0.1, rtol=0.01), (logits - ref_logits).abs().max()
+    assert torch.equal(ctx.next_tokens, ref_tok)
+    # the appended K/V slot equals the reference's index_put_ (same rounded inputs)
+    for r in reqs:
+        p, o = r.slot(r.length - 1, 16)
+        diff = (pool.cache[:, p, :, o].float() - ref_cache[:, p, :, o].float()).abs().max()
+        assert diff <= 0.05, diff
+
+
+def test_graph_replay_matches_eager(gpu_device):
+    results = []
+    for use_graph in (False, True):
+        w, pool, reqs, first, _ = _setup(gpu_device)
+        gen = BatchGenerator(w, pool, workspace_mb=8, use_graph=use_graph)
+        res = gen.generate(reqs, first, steps=12, adapters=[0, 1, 1])
+        assert res.used_graph == use_graph
+        results.append(res)
+    assert torch.equal(results[0].tokens, results[1].tokens)
+    assert results[1].graph_captures == 1 and results[1].graph_replays == 12
