@@ -139,6 +139,62 @@ int pl_kv_append(const void* k, const void* v, int64_t k_stride_b,
                  void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Fused element-wise ops of the decode layer                                */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * out[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * weight, fp32 statistics, one
+ * rounding.  rows x hidden with row strides ldx / ldo; hidden % 8 == 0.
+ * Replaces apply_rmsnorm (model/flashinfer/norm.py:15-24, 60-65).
+ */
+int pl_rmsnorm(const void* x, int64_t ldx, const void* weight, void* out,
+               int64_t ldo, int rows, int hidden, float eps, int dtype,
+               void* stream);
+
+/*
+ * residual[r] += x[r] (stored in the storage type), then
+ * out[r] = rmsnorm(residual[r]) as pl_rmsnorm.
+ * Replaces add_residual_rmsnorm (model/flashinfer/norm.py:27-57).
+ */
+int pl_add_rmsnorm(void* residual, int64_t ldr, const void* x, int64_t ldx,
+                   const void* weight, void* out, int64_t ldo, int rows,
+                   int hidden, float eps, int dtype, void* stream);
+
+/*
+ * out[r, i] = silu(gate_up[r, i]) * gate_up[r, inter + i], fp32, one rounding.
+ * Replaces apply_gate_up_activation / flashinfer.silu_and_mul
+ * (model/flashinfer/packed_ops.py:230-239).
+ */
+int pl_silu_mul(const void* gate_up, int64_t ldg, void* out, int64_t ldo,
+                int rows, int inter, int dtype, void* stream);
+
+/*
+ * Per decode token b, from the packed projection row qkv[b] = [q | k | v]
+ * (num_qo_heads, num_kv_heads, num_kv_heads heads of head_dim):
+ *   q_out[b, h] = rope(rmsnorm(q[b, h]) * q_norm_weight)     (norm skipped if the weight is NULL)
+ *   K[page_id[b], offset[b], h] = rope(rmsnorm(k[b, h]) * k_norm_weight)
+ *   V[page_id[b], offset[b], h] = v[b, h]
+ * rope: non-interleaved rotate-half, angle(i) = positions[b] * inv_freq[i]
+ * in fp32, inv_freq[head_dim/2] (fp32, device) being the caller's table
+ * (1 / theta^(2i/head_dim), divided by a linear rope scale).  K/V addressed
+ * as in pl_decode_run; a slot outside the pool is skipped.  q_out is
+ * [batch, num_qo_heads, head_dim].
+ * Replaces project_qkv_with_optional_norm's head norm + apply_rope_pos_ids
+ * + _append_decode_kv_static (model/flashinfer/projection.py:155-190,
+ * 248-260; layer_runner.py:399-412).
+ */
+int pl_qk_norm_rope_append(const void* qkv, int64_t ld_qkv,
+                           const void* q_norm_weight, const void* k_norm_weight,
+                           const int64_t* positions, const int64_t* page_id,
+                           const int64_t* offset, void* q_out, void* k_cache,
+                           void* v_cache, int64_t page_stride,
+                           int64_t token_stride, int64_t head_stride,
+                           int64_t num_pages, int page_size, int batch,
+                           int num_qo_heads, int num_kv_heads, int head_dim,
+                           const float* inv_freq, float eps, int dtype,
+                           void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* No-merge multi-adapter LoRA delta                                         */
 /* ------------------------------------------------------------------------ */
 
@@ -163,9 +219,10 @@ typedef struct {
 /* Most modules in one group (q, k, v). */
 #define PL_LORA_MAX_MODULES 4
 
-/* Workspace bytes for one pl_lora_* call: the rank-r intermediate
- * [num_tokens][sum(rank) rounded up to 32] in the input dtype.  Calls that
- * share a workspace must be stream ordered; shrink writes it, expand reads it. */
+/* Workspace bytes for one pl_lora_* call: the shrink's fp32 partial sums,
+ * [k-slices][num_tokens][sum(rank) rounded up to 32], the slice count
+ * depending on num_tokens and in_features.  Calls that share a workspace
+ * must be stream ordered; shrink writes it, expand reads it. */
 size_t pl_lora_workspace_size(int num_tokens, int in_features,
                               const pl_lora_module* modules_h, int num_modules);
 

@@ -90,6 +90,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _i32, _i32, _i32, _i32, _vp,        # batch, hkv, head_dim, dtype, stream
         ],
     ),
+    "pl_rmsnorm": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _i32, _vp]),
+    "pl_add_rmsnorm": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _i32, _vp]),
+    "pl_silu_mul": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp]),
+    "pl_qk_norm_rope_append": (
+        _i32,
+        [
+            _vp, _i64, _vp, _vp,          # qkv, ld, q/k norm weights
+            _vp, _vp, _vp,                # positions, page_id, offset
+            _vp, _vp, _vp,                # q_out, k_cache, v_cache
+            _i64, _i64, _i64, _i64, _i32,  # page/token/head strides, num_pages, page_size
+            _i32, _i32, _i32, _i32,       # batch, hq, hkv, head_dim
+            _vp, _f32, _i32, _vp,         # inv_freq, eps, dtype, stream
+        ],
+    ),
     "pl_lora_workspace_size": (_sz, [_i32, _i32, ctypes.POINTER(LoraModule), _i32]),
     "pl_lora_delta": (
         _i32,

@@ -3,15 +3,15 @@
 // for the modules m of a group that share their input x (q/k/v, gate/up, or a
 // lone o_proj / down_proj) and per-token adapter ids a_t.
 //
-//   shrink_kernel  grid (16 rank rows, adapter), 16 waves per workgroup.
-//                  Gathers the tokens of its adapter (LDS list), multiplies
-//                  their x by the adapter's concatenated A rows on MFMA
-//                  16x16x32 tiles with the k range split across the waves,
-//                  sums the waves' tiles in LDS and rounds the rank-r
-//                  intermediate to the input dtype.
-//   expand_kernel  grid (16-column tiles x 4, adapter).  Multiplies the
-//                  rounded intermediate by B^T on MFMA 16x16x32 tiles and
-//                  accumulates scale * result into the outputs in place.
+//   shrink_kernel  grid (k-slice, 16 rank rows, adapter).  Gathers the
+//                  tokens of its adapter (LDS list), multiplies their x
+//                  slice by the adapter's concatenated A rows on MFMA
+//                  16x16x32 tiles and writes fp32 partial sums per slice.
+//   expand_kernel  grid (16-column tiles x 4, adapter).  Folds the slices
+//                  into the rank-r intermediate rounded to the input dtype
+//                  (as the reference's F.linear returns it), multiplies it
+//                  by B^T on MFMA 16x16x32 tiles and accumulates
+//                  scale * result into the outputs in place.
 //                  The contraction runs over the group's concatenated ranks,
 //                  with the B operand zero outside the column's own module,
 //                  i.e. the block-diagonal product of the reference without
@@ -61,8 +61,7 @@ template <> __device__ __forceinline__ f32x4 mfma32<f16_t>(uint4 a, uint4 b, f32
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// Workspace: the rank-r intermediate [T][r_pad], rounded to the input dtype.
-inline size_t ws_bytes_needed(int tokens, int r_pad) { return align_up((size_t)tokens * r_pad * 2, 256); }
+
 
 // Gather the tokens of adapter `a` into LDS; returns their count (all threads).
 __device__ __forceinline__ int gather_tokens(const int32_t* __restrict__ ids, int tokens, int a,
@@ -85,23 +84,37 @@ __device__ __forceinline__ uint4 load8(const void* p, bool ok) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
-// Shrink: one workgroup of kShrinkWaves waves per (16 rank rows, adapter).
-// The waves split the k range; each multiplies up to four 16-token tiles by
-// the 16 rank rows on MFMA 16x16x32, and the waves' partial tiles are summed
-// through LDS, so no global atomics, fences or partial buffers are needed.
-constexpr int kShrinkWaves = 16;
+// Shrink: split-K.  Workgroup (k-slice, 16 rank rows, adapter) multiplies the
+// adapter's tokens (up to four 16-token tiles per pass) by 16 rows of its
+// concatenated A over one k-slice on MFMA 16x16x32; its four waves split the
+// slice and are summed in LDS; the fp32 partial goes to part[slice][token][j].
+// The slice count grows as the token count shrinks (decode: many slices,
+// so the A rows stream from many CUs at once).
+constexpr int kShrinkWaves = 4;
 constexpr int kShrinkThreads = kShrinkWaves * kWave;
 constexpr int kTilesPerPass = 4;
+
+inline int ksplit_for(int tokens, int in_features) {
+  int by_k = in_features / 256;                   // at least 256 elements per slice
+  int by_t = 256 / (tokens > 0 ? tokens : 1);     // keep partial traffic ~ constant
+  int k = by_k < by_t ? by_k : by_t;
+  return k < 1 ? 1 : (k > 64 ? 64 : k);
+}
+inline int kslice_for(int in_features, int ksplit) {  // multiple of 32 * waves
+  const int step = 32 * kShrinkWaves;
+  return ((in_features + ksplit - 1) / ksplit + step - 1) / step * step;
+}
 
 template <typename T>
 __global__ __launch_bounds__(kShrinkThreads) void shrink_kernel(
     const T* __restrict__ x, int64_t ldx, int tokens, int in_features, Group g,
-    const int32_t* __restrict__ ids, uint16_t* __restrict__ y) {
+    const int32_t* __restrict__ ids, int kslice, float* __restrict__ part) {
   __shared__ int s_list[kMaxTokens];
   __shared__ int s_count;
   __shared__ float s_red[kShrinkWaves][kTilesPerPass][256];
-  const int jt = blockIdx.x;
-  const int a = blockIdx.y;
+  const int ks = blockIdx.x;
+  const int jt = blockIdx.y;
+  const int a = blockIdx.z;
   const int n_a = gather_tokens(ids, tokens, a, s_list, &s_count, kShrinkThreads);
   if (n_a == 0) return;
 
@@ -109,11 +122,9 @@ __global__ __launch_bounds__(kShrinkThreads) void shrink_kernel(
   const int wave = threadIdx.x / kWave;
   const int lr = lane % 16;       // MFMA row (token) / column (rank row)
   const int kq = (lane / 16) * 8; // this lane's 8-element k group
-  // k range of this wave, in whole 32-element MFMA steps
-  const int steps_total = (in_features + 31) / 32;
-  const int steps_per_wave = (steps_total + kShrinkWaves - 1) / kShrinkWaves;
-  const int k_begin = wave * steps_per_wave * 32;
-  const int k_end = min(in_features, k_begin + steps_per_wave * 32);
+  const int sub = kslice / kShrinkWaves;
+  const int k_begin = ks * kslice + wave * sub;
+  const int k_end = min(in_features, k_begin + sub);
 
   // rank row j -> module, local row
   const int j = jt * 16 + lr;
@@ -161,8 +172,7 @@ __global__ __launch_bounds__(kShrinkThreads) void shrink_kernel(
         float sum = 0.f;
 #pragma unroll
         for (int w = 0; w < kShrinkWaves; ++w) sum += s_red[w][u][cell];
-        const T v = from_float<T>(sum);
-        y[(int64_t)s_list[tr] * g.r_pad + jt * 16 + cell % 16] = __builtin_bit_cast(uint16_t, v);
+        part[((int64_t)ks * tokens + s_list[tr]) * g.r_pad + jt * 16 + cell % 16] = sum;
       }
     }
     __syncthreads();
@@ -178,11 +188,17 @@ template <> __device__ __forceinline__ void accumulate<bf16_t>(bf16_t* p, float 
   *p = from_float<bf16_t>(to_float<bf16_t>(*p) + v);
 }
 
+// Expand: workgroup (64 output columns, adapter).  Per 16-token tile the
+// workgroup first folds the shrink's k-slice partials into the rounded
+// rank-r intermediate (an LDS tile, the dtype of x), then each wave runs
+// MFMA 16x16x32 over the concatenated ranks for its 16 columns and adds
+// scale * result into the outputs.
 template <typename T, typename OT>
 __global__ __launch_bounds__(kThreads) void expand_kernel(
-    int tokens, Group g, const int32_t* __restrict__ ids, const uint16_t* __restrict__ y) {
+    int tokens, Group g, const int32_t* __restrict__ ids, int ksplit, const float* __restrict__ part) {
   __shared__ int s_list[kMaxTokens];
   __shared__ int s_count;
+  __shared__ __align__(16) uint16_t s_y[16][128 + 8];  // r_pad <= 128; +8 keeps rows 16-byte aligned
   const int a = blockIdx.y;
   const int n_a = gather_tokens(ids, tokens, a, s_list, &s_count, kThreads);
   if (n_a == 0) return;
@@ -193,7 +209,7 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(
   const int kq = (lane / 16) * 8;
   const int tile = blockIdx.x * kWaves + wave;
   const int o = tile * 16 + lr;  // this lane's output column (concatenated space)
-  if (tile * 16 >= g.out_total) return;
+  const bool tile_ok = tile * 16 < g.out_total;
 
   int mi = -1;
 #pragma unroll
@@ -236,21 +252,36 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(
   }
 
   for (int tt = 0; tt * 16 < n_a; ++tt) {
-    const int ti = tt * 16 + lr;
-    const bool tok_ok = ti < n_a;
-    const uint16_t* yrow = y + (int64_t)(tok_ok ? s_list[ti] : 0) * g.r_pad;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kt = 0; kt < kMaxKt; ++kt) {  // static indices keep bop[] in registers
-      if (kt < n_kt) acc = mfma32<T>(load8(yrow + kt * 32 + kq, tok_ok), bop[kt], acc);
+    // fold the partials of this token tile into the rounded intermediate
+    for (int c = threadIdx.x; c < 16 * g.r_pad; c += kThreads) {
+      const int i = c / g.r_pad, k = c - i * g.r_pad;
+      const int ti = tt * 16 + i;
+      float sum = 0.f;
+      if (ti < n_a && k < g.r_total) {
+        const float* pp = part + (int64_t)s_list[ti] * g.r_pad + k;
+        for (int q = 0; q < ksplit; ++q) sum += pp[(int64_t)q * tokens * g.r_pad];
+      }
+      s_y[i][k] = __builtin_bit_cast(uint16_t, from_float<T>(sum));
     }
-    if (out_col != nullptr) {
+    __syncthreads();
+    if (tile_ok) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tr = tt * 16 + (lane / 16) * 4 + i;
-        if (tr < n_a) accumulate<OT>(out_col + (int64_t)s_list[tr] * ldo, scale * acc[i]);
+      for (int kt = 0; kt < kMaxKt; ++kt) {  // static indices keep bop[] in registers
+        if (kt < n_kt) {
+          const uint4 av = *reinterpret_cast<const uint4*>(&s_y[lr][kt * 32 + kq]);
+          acc = mfma32<T>(av, bop[kt], acc);
+        }
+      }
+      if (out_col != nullptr) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tr = tt * 16 + (lane / 16) * 4 + i;
+          if (tr < n_a) accumulate<OT>(out_col + (int64_t)s_list[tr] * ldo, scale * acc[i]);
+        }
       }
     }
+    __syncthreads();
   }
 }
 
@@ -309,45 +340,53 @@ int check_common(const void* x, int64_t ldx, int tokens, int n_adapters, const i
 using namespace pl;
 using namespace pl::lora;
 
+// Workspace: the shrink's fp32 partials [ksplit][T][r_pad].
+static size_t ws_bytes_needed(int tokens, int in_features, int r_pad) {
+  return align_up((size_t)ksplit_for(tokens, in_features) * tokens * r_pad * sizeof(float), 256);
+}
+
 extern "C" size_t pl_lora_workspace_size(int num_tokens, int in_features,
                                          const pl_lora_module* modules_h, int num_modules) {
   Group g;
   if (make_group(modules_h, num_modules, in_features, &g) != PL_OK || num_tokens < 0) return 0;
-  return ws_bytes_needed(num_tokens, g.r_pad);
+  return ws_bytes_needed(num_tokens, in_features, g.r_pad);
 }
 
 static int lora_shrink_impl(const void* x, int64_t ldx, int tokens, int in_features,
                             const Group& g, const int32_t* ids, int n_adapters, int dtype,
                             void* ws, size_t ws_bytes, hipStream_t stream) {
-  (void)in_features;
-  const size_t need = ws_bytes_needed(tokens, g.r_pad);
+  const size_t need = ws_bytes_needed(tokens, in_features, g.r_pad);
   if (need > ws_bytes)
     return fail(PL_ERR_WORKSPACE, "LoRA workspace of %zu bytes < %zu needed", ws_bytes, need);
   if (ws == nullptr || (uintptr_t)ws % 256) return fail(PL_ERR_INVALID, "workspace must be 256-byte aligned");
-  dim3 grid(g.r_pad / 16, n_adapters);
+  if (n_adapters > 65535) return fail(PL_ERR_UNSUPPORTED, "num_adapters %d > 65535", n_adapters);
+  const int ksplit = ksplit_for(tokens, in_features);
+  const int kslice = kslice_for(in_features, ksplit);
+  dim3 grid(ksplit, g.r_pad / 16, n_adapters);
   if (dtype == PL_DTYPE_BF16)
     hipLaunchKernelGGL(shrink_kernel<bf16_t>, grid, dim3(kShrinkThreads), 0, stream, (const bf16_t*)x,
-                       ldx, tokens, in_features, g, ids, (uint16_t*)ws);
+                       ldx, tokens, in_features, g, ids, kslice, (float*)ws);
   else
     hipLaunchKernelGGL(shrink_kernel<f16_t>, grid, dim3(kShrinkThreads), 0, stream, (const f16_t*)x,
-                       ldx, tokens, in_features, g, ids, (uint16_t*)ws);
+                       ldx, tokens, in_features, g, ids, kslice, (float*)ws);
   PL_LAUNCH_CHECK("lora shrink_kernel");
   return PL_OK;
 }
 
 template <typename T>
-static int launch_expand(int tokens, const Group& g, const int32_t* ids, int n_adapters,
-                         int out_dtype, const uint16_t* y, hipStream_t stream) {
+static int launch_expand(int tokens, int in_features, const Group& g, const int32_t* ids, int n_adapters,
+                         int out_dtype, const float* part, hipStream_t stream) {
   dim3 grid((g.out_total + 16 * kWaves - 1) / (16 * kWaves), n_adapters);
+  const int ksplit = ksplit_for(tokens, in_features);
   switch (out_dtype) {
     case PL_DTYPE_F32:
-      hipLaunchKernelGGL((expand_kernel<T, float>), grid, dim3(kThreads), 0, stream, tokens, g, ids, y);
+      hipLaunchKernelGGL((expand_kernel<T, float>), grid, dim3(kThreads), 0, stream, tokens, g, ids, ksplit, part);
       break;
     case PL_DTYPE_F16:
-      hipLaunchKernelGGL((expand_kernel<T, f16_t>), grid, dim3(kThreads), 0, stream, tokens, g, ids, y);
+      hipLaunchKernelGGL((expand_kernel<T, f16_t>), grid, dim3(kThreads), 0, stream, tokens, g, ids, ksplit, part);
       break;
     case PL_DTYPE_BF16:
-      hipLaunchKernelGGL((expand_kernel<T, bf16_t>), grid, dim3(kThreads), 0, stream, tokens, g, ids, y);
+      hipLaunchKernelGGL((expand_kernel<T, bf16_t>), grid, dim3(kThreads), 0, stream, tokens, g, ids, ksplit, part);
       break;
     default:
       return fail(PL_ERR_UNSUPPORTED, "out_dtype %d", out_dtype);
@@ -359,13 +398,13 @@ static int launch_expand(int tokens, const Group& g, const int32_t* ids, int n_a
 static int lora_expand_impl(int tokens, int in_features, const Group& g, const int32_t* ids,
                             int n_adapters, int dtype, int out_dtype, const void* ws,
                             size_t ws_bytes, hipStream_t stream) {
-  (void)in_features;
-  const size_t need = ws_bytes_needed(tokens, g.r_pad);
+  const size_t need = ws_bytes_needed(tokens, in_features, g.r_pad);
   if (need > ws_bytes)
     return fail(PL_ERR_WORKSPACE, "LoRA workspace of %zu bytes < %zu needed", ws_bytes, need);
-  const uint16_t* y = (const uint16_t*)ws;
-  return dtype == PL_DTYPE_BF16 ? launch_expand<bf16_t>(tokens, g, ids, n_adapters, out_dtype, y, stream)
-                                : launch_expand<f16_t>(tokens, g, ids, n_adapters, out_dtype, y, stream);
+  if (n_adapters > 65535) return fail(PL_ERR_UNSUPPORTED, "num_adapters %d > 65535", n_adapters);
+  const float* part = (const float*)ws;
+  return dtype == PL_DTYPE_BF16 ? launch_expand<bf16_t>(tokens, in_features, g, ids, n_adapters, out_dtype, part, stream)
+                                : launch_expand<f16_t>(tokens, in_features, g, ids, n_adapters, out_dtype, part, stream);
 }
 
 extern "C" int pl_lora_shrink(const void* x, int64_t ldx, int num_tokens, int in_features,

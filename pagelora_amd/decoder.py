@@ -5,20 +5,22 @@ decode layer ``run_flashinfer_decode_layer_static_append_batch``
 (model/flashinfer/layer_runner.py:340-396):
 
     rmsnorm -> packed q/k/v GEMM (+ no-merge LoRA delta, packed_ops.py:105-165)
-    -> per-head q/k RMSNorm (projection.py:248-260) -> RoPE (projection.py:155-190)
-    -> KV append into the page (layer_runner.py:399-412)
+    -> per-head q/k RMSNorm (projection.py:248-260) + RoPE (projection.py:155-190)
+       + KV append into the page (layer_runner.py:399-412), one fused kernel
     -> paged decode attention (attention_backend.py:120-131)
     -> o_proj (+ LoRA, packed_ops.py:251-265 / linear.py:200-231) -> residual
     -> rmsnorm -> packed gate/up GEMM (+ LoRA, packed_ops.py:168-203) -> SiLU*up
     -> down_proj (+ LoRA) -> residual
 
-Base GEMMs are plain library GEMMs (torch -> hipBLASLt); the LoRA delta, KV
-append and attention are the library's HIP kernels.  Weights are random
+Base GEMMs are plain library GEMMs (torch -> hipBLASLt); everything else --
+norms (each residual add fused into the next norm), q/k-norm + RoPE + KV
+append, attention, SiLU*up and the LoRA delta -- runs on the library's HIP
+kernels.  Weights are random
 (no checkpoints are available); shapes follow Qwen3-8B.
 
 Prefill (``prefill``) is not on the decode path: it fills the paged KV pool
-for the prompt with plain torch math (float32 attention), so decode starts
-from a real context.
+for the prompt with the same kernels except attention, which is plain torch
+float32 math over the gathered pages, so decode starts from a real context.
 """
 
 from __future__ import annotations
@@ -29,7 +31,8 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from .attention_backend import PagedDecodeAttention, kv_append
+from . import fused_ops
+from .attention_backend import PagedDecodeAttention
 from .kv_pool import PagedKVPool, Request
 from .lora import lora_delta_
 
@@ -102,29 +105,6 @@ class DecoderWeights:
         self.lora_scale = cfg.lora_alpha / cfg.lora_rank  # linear.py:41, 71
 
 
-# ------------------------------------------------------------------ ops ---
-def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """Qwen3 RMSNorm: fp32 statistics, result cast back, then the weight."""
-    xf = x.float()
-    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return weight * xf.to(x.dtype)
-
-
-def rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float):
-    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=positions.device, dtype=torch.float32) / head_dim))
-    freqs = positions.float()[:, None] * inv[None, :]
-    emb = torch.cat([freqs, freqs], dim=-1)
-    return emb.cos(), emb.sin()
-
-
-def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """Non-interleaved (rotate-half) RoPE on [T, H, D] with cos/sin [T, D]."""
-    half = x.shape[-1] // 2
-    xf = x.float()
-    rot = torch.cat([-xf[..., half:], xf[..., :half]], dim=-1)
-    return (xf * cos[:, None, :] + rot * sin[:, None, :]).to(x.dtype)
-
-
 # ------------------------------------------------------- decode (static) ---
 class DecodeContext:
     """Graph-owned per-step buffers of a batch (cuda_graph.py:307-464 analogue)."""
@@ -139,53 +119,62 @@ class DecodeContext:
         self.next_tokens = torch.zeros(batch, dtype=torch.int64, device=device)
 
 
+def _lora_qkv(cfg: DecoderConfig, lw: LayerWeights, x, qkv, ids, scale: float) -> None:
+    qd, kd = cfg.q_dim, cfg.kv_dim
+    (Aq, Bq), (Ak, Bk), (Av, Bv) = lw.lora["q"], lw.lora["k"], lw.lora["v"]
+    lora_delta_(x, [(Aq, Bq, qkv[:, :qd], scale), (Ak, Bk, qkv[:, qd:qd + kd], scale),
+                    (Av, Bv, qkv[:, qd + kd:], scale)], ids)
+
+
+def _mlp(cfg: DecoderConfig, lw: LayerWeights, x2, ids, scale: float) -> torch.Tensor:
+    I = cfg.intermediate
+    gu = F.linear(x2, lw.w_gate_up)
+    (Ag, Bg), (Au, Bu) = lw.lora["gate"], lw.lora["up"]
+    lora_delta_(x2, [(Ag, Bg, gu[:, :I], scale), (Au, Bu, gu[:, I:], scale)], ids)
+    act = fused_ops.silu_mul(gu)
+    d = F.linear(act, lw.w_down)
+    Ad, Bd = lw.lora["down"]
+    lora_delta_(act, [(Ad, Bd, d, scale)], ids)
+    return d
+
+
 def decode_layer_static(
     cfg: DecoderConfig,
     lw: LayerWeights,
     lora_scale: float,
     hidden: torch.Tensor,
+    pending: torch.Tensor | None,
     layer_cache: torch.Tensor,
     backend: PagedDecodeAttention,
     ctx: DecodeContext,
-    cos: torch.Tensor,
-    sin: torch.Tensor,
 ) -> torch.Tensor:
-    """One single-token decode layer for the whole batch; graph-capturable."""
+    """One single-token decode layer for the whole batch; graph-capturable.
+
+    ``hidden`` is the residual stream, updated in place; ``pending`` is the
+    previous layer's MLP output, added to it by this layer's fused
+    add+RMSNorm.  Returns this layer's MLP output (pending for the next).
+    """
     B = hidden.shape[0]
     ids = ctx.adapter_ids
-    x = rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
+    if pending is None:
+        x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
+    else:
+        x = fused_ops.add_rmsnorm(hidden, pending, lw.input_norm, cfg.rms_eps)
     qkv = F.linear(x, lw.w_qkv)
-    qd, kd = cfg.q_dim, cfg.kv_dim
-    (Aq, Bq), (Ak, Bk), (Av, Bv) = lw.lora["q"], lw.lora["k"], lw.lora["v"]
-    lora_delta_(x, [(Aq, Bq, qkv[:, :qd], lora_scale), (Ak, Bk, qkv[:, qd:qd + kd], lora_scale),
-                    (Av, Bv, qkv[:, qd + kd:], lora_scale)], ids)
-    q = qkv[:, :qd].view(B, cfg.num_qo_heads, cfg.head_dim)
-    k = qkv[:, qd:qd + kd].view(B, cfg.num_kv_heads, cfg.head_dim)
-    v = qkv[:, qd + kd:].view(B, cfg.num_kv_heads, cfg.head_dim)
-    if cfg.qk_norm:
-        q = rmsnorm(q, lw.q_norm, cfg.rms_eps)
-        k = rmsnorm(k, lw.k_norm, cfg.rms_eps)
-    q = apply_rope(q, cos, sin)
-    k = apply_rope(k, cos, sin)
-    kv_append(layer_cache, k, v, ctx.page_id, ctx.page_offset, num_kv_heads=cfg.num_kv_heads,
-              head_dim=cfg.head_dim, page_size=backend.page_size)
+    _lora_qkv(cfg, lw, x, qkv, ids, lora_scale)
+    q = fused_ops.qk_norm_rope_append(
+        qkv, lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None,
+        ctx.positions, ctx.page_id, ctx.page_offset, layer_cache, num_qo_heads=cfg.num_qo_heads,
+        num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=backend.page_size,
+        rope_theta=cfg.rope_theta, eps=cfg.rms_eps)
     attn = torch.empty_like(q)
     backend.run_decode_into(q, layer_cache, attn)
-    attn = attn.view(B, qd)
+    attn = attn.view(B, cfg.q_dim)
     o = F.linear(attn, lw.w_o)
     Ao, Bo = lw.lora["o"]
     lora_delta_(attn, [(Ao, Bo, o, lora_scale)], ids)
-    hidden = hidden + o
-    x2 = rmsnorm(hidden, lw.post_norm, cfg.rms_eps)
-    gu = F.linear(x2, lw.w_gate_up)
-    I = cfg.intermediate
-    (Ag, Bg), (Au, Bu) = lw.lora["gate"], lw.lora["up"]
-    lora_delta_(x2, [(Ag, Bg, gu[:, :I], lora_scale), (Au, Bu, gu[:, I:], lora_scale)], ids)
-    act = F.silu(gu[:, :I]) * gu[:, I:]
-    d = F.linear(act, lw.w_down)
-    Ad, Bd = lw.lora["down"]
-    lora_delta_(act, [(Ad, Bd, d, lora_scale)], ids)
-    return hidden + d
+    x2 = fused_ops.add_rmsnorm(hidden, o, lw.post_norm, cfg.rms_eps)
+    return _mlp(cfg, lw, x2, ids, lora_scale)
 
 
 def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: PagedDecodeAttention,
@@ -196,10 +185,11 @@ def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: Page
     """
     cfg = weights.cfg
     hidden = F.embedding(ctx.tokens, weights.embed)
-    cos, sin = rope_cos_sin(ctx.positions, cfg.head_dim, cfg.rope_theta)
+    pending = None
     for li, lw in enumerate(weights.layers):
-        hidden = decode_layer_static(cfg, lw, weights.lora_scale, hidden, pool.layer_cache(li), backend, ctx, cos, sin)
-    x = rmsnorm(hidden, weights.final_norm, cfg.rms_eps)
+        pending = decode_layer_static(cfg, lw, weights.lora_scale, hidden, pending, pool.layer_cache(li),
+                                      backend, ctx)
+    x = fused_ops.add_rmsnorm(hidden, pending, weights.final_norm, cfg.rms_eps)
     logits = F.linear(x, weights.lm_head)
     ctx.next_tokens.copy_(torch.argmax(logits, dim=-1))  # greedy, sampling.py:8-15
     return logits
@@ -233,53 +223,39 @@ def prefill(weights: DecoderWeights, pool: PagedKVPool, request: Request, tokens
     start = request.length - tokens.numel()
     assert start >= 0, "reserve pages for the prompt before prefill"
     pages = torch.tensor(request.pages(), dtype=torch.int64, device=tokens.device)
+    s = weights.lora_scale
     last_logits = None
     for c0 in range(0, tokens.numel(), chunk):
         tok = tokens[c0:c0 + chunk]
         T = tok.numel()
         pos = torch.arange(start + c0, start + c0 + T, device=tokens.device)
-        cos, sin = rope_cos_sin(pos, cfg.head_dim, cfg.rope_theta)
         page_of = pages[pos // ps]
         off_of = pos % ps
         hidden = F.embedding(tok, weights.embed)
         ids = torch.full((T,), adapter, dtype=torch.int32, device=tokens.device)
+        pending = None
         for li, lw in enumerate(weights.layers):
             cache = pool.layer_cache(li)
-            x = rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
+            if pending is None:
+                x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
+            else:
+                x = fused_ops.add_rmsnorm(hidden, pending, lw.input_norm, cfg.rms_eps)
             qkv = F.linear(x, lw.w_qkv)
-            qd, kd = cfg.q_dim, cfg.kv_dim
-            (Aq, Bq), (Ak, Bk), (Av, Bv) = lw.lora["q"], lw.lora["k"], lw.lora["v"]
-            s = weights.lora_scale
-            lora_delta_(x, [(Aq, Bq, qkv[:, :qd], s), (Ak, Bk, qkv[:, qd:qd + kd], s), (Av, Bv, qkv[:, qd + kd:], s)], ids)
-            q = qkv[:, :qd].reshape(T, cfg.num_qo_heads, cfg.head_dim)
-            k = qkv[:, qd:qd + kd].reshape(T, cfg.num_kv_heads, cfg.head_dim)
-            v = qkv[:, qd + kd:].reshape(T, cfg.num_kv_heads, cfg.head_dim)
-            if cfg.qk_norm:
-                q = rmsnorm(q, lw.q_norm, cfg.rms_eps)
-                k = rmsnorm(k, lw.k_norm, cfg.rms_eps)
-            q = apply_rope(q, cos, sin)
-            k = apply_rope(k, cos, sin)
-            cache[page_of, 0, off_of] = k
-            cache[page_of, 1, off_of] = v
+            _lora_qkv(cfg, lw, x, qkv, ids, s)
+            q = fused_ops.qk_norm_rope_append(
+                qkv, lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None, pos, page_of,
+                off_of, cache, num_qo_heads=cfg.num_qo_heads, num_kv_heads=cfg.num_kv_heads,
+                head_dim=cfg.head_dim, page_size=ps, rope_theta=cfg.rope_theta, eps=cfg.rms_eps)
             ctx_len = start + c0 + T
             all_pos = torch.arange(ctx_len, device=tokens.device)
             kk = cache[pages[all_pos // ps], 0, all_pos % ps]
             vv = cache[pages[all_pos // ps], 1, all_pos % ps]
-            attn = _attention_f32(q, kk, vv, start + c0).to(hidden.dtype).reshape(T, qd)
+            attn = _attention_f32(q, kk, vv, start + c0).to(hidden.dtype).reshape(T, cfg.q_dim)
             o = F.linear(attn, lw.w_o)
             Ao, Bo = lw.lora["o"]
             lora_delta_(attn, [(Ao, Bo, o, s)], ids)
-            hidden = hidden + o
-            x2 = rmsnorm(hidden, lw.post_norm, cfg.rms_eps)
-            gu = F.linear(x2, lw.w_gate_up)
-            I = cfg.intermediate
-            (Ag, Bg), (Au, Bu) = lw.lora["gate"], lw.lora["up"]
-            lora_delta_(x2, [(Ag, Bg, gu[:, :I], s), (Au, Bu, gu[:, I:], s)], ids)
-            act = F.silu(gu[:, :I]) * gu[:, I:]
-            d = F.linear(act, lw.w_down)
-            Ad, Bd = lw.lora["down"]
-            lora_delta_(act, [(Ad, Bd, d, s)], ids)
-            hidden = hidden + d
-        x = rmsnorm(hidden[-1:], weights.final_norm, cfg.rms_eps)
-        last_logits = F.linear(x, weights.lm_head)
+            x2 = fused_ops.add_rmsnorm(hidden, o, lw.post_norm, cfg.rms_eps)
+            pending = _mlp(cfg, lw, x2, ids, s)
+        x = fused_ops.add_rmsnorm(hidden, pending, weights.final_norm, cfg.rms_eps)
+        last_logits = F.linear(x[-1:], weights.lm_head)
     return last_logits

@@ -1,0 +1,121 @@
+"""Python entry points of the fused element-wise decode kernels.
+
+``rmsnorm`` / ``add_rmsnorm`` replace the reference's ``apply_rmsnorm`` and
+``add_residual_rmsnorm`` (model/flashinfer/norm.py:15-65), ``silu_mul`` its
+``apply_gate_up_activation`` (packed_ops.py:230-239), and
+``qk_norm_rope_append`` fuses the q/k head norm and RoPE of
+``project_qkv_with_optional_norm`` (projection.py:34-190, 248-260) with the
+decode token's page append (layer_runner.py:399-412).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .attention_backend import _cache_geometry
+
+
+def _rows2d(t: torch.Tensor, name: str) -> None:
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be 2-D with unit column stride")
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    _rows2d(x, "x")
+    out = torch.empty_like(x) if out is None else out
+    _rows2d(out, "out")
+    if weight.numel() != x.shape[1] or weight.dtype != x.dtype or out.dtype != x.dtype:
+        raise ValueError("weight/out must match x")
+    lib = _lib.load()
+    _lib.check(lib.pl_rmsnorm(x.data_ptr(), x.stride(0), weight.data_ptr(), out.data_ptr(), out.stride(0),
+                              x.shape[0], x.shape[1], float(eps), _lib.dtype_code(x.dtype),
+                              _lib.stream_handle(x.device)), "pl_rmsnorm")
+    return out
+
+
+def add_rmsnorm(residual: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: float,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """In place ``residual += x``; returns ``rmsnorm(residual)``."""
+    _rows2d(residual, "residual")
+    _rows2d(x, "x")
+    if x.shape != residual.shape or x.dtype != residual.dtype:
+        raise ValueError("x must match residual")
+    out = torch.empty_like(residual) if out is None else out
+    lib = _lib.load()
+    _lib.check(lib.pl_add_rmsnorm(residual.data_ptr(), residual.stride(0), x.data_ptr(), x.stride(0),
+                                  weight.data_ptr(), out.data_ptr(), out.stride(0), residual.shape[0],
+                                  residual.shape[1], float(eps), _lib.dtype_code(x.dtype),
+                                  _lib.stream_handle(x.device)), "pl_add_rmsnorm")
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    _rows2d(gate_up, "gate_up")
+    inter = gate_up.shape[1] // 2
+    if gate_up.shape[1] != 2 * inter:
+        raise ValueError("gate_up must have an even number of columns")
+    out = torch.empty((gate_up.shape[0], inter), dtype=gate_up.dtype, device=gate_up.device) if out is None else out
+    lib = _lib.load()
+    _lib.check(lib.pl_silu_mul(gate_up.data_ptr(), gate_up.stride(0), out.data_ptr(), out.stride(0),
+                               gate_up.shape[0], inter, _lib.dtype_code(gate_up.dtype),
+                               _lib.stream_handle(gate_up.device)), "pl_silu_mul")
+    return out
+
+
+_INV_FREQ: dict = {}
+
+
+def rope_inv_freq(head_dim: int, theta: float, scale: float, device) -> torch.Tensor:
+    """fp32 inverse frequencies as the reference's RoPE forms them
+    (1 / theta^(arange(0, D, 2) / D), then / scale for linear scaling)."""
+    key = (head_dim, float(theta), float(scale), str(device))
+    t = _INV_FREQ.get(key)
+    if t is None:
+        t = 1.0 / (float(theta) ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
+        t = (t / float(scale)).to(device)
+        _INV_FREQ[key] = t
+    return t
+
+
+def qk_norm_rope_append(
+    qkv: torch.Tensor,
+    q_norm_weight: torch.Tensor | None,
+    k_norm_weight: torch.Tensor | None,
+    positions: torch.Tensor,
+    page_id: torch.Tensor,
+    page_offset: torch.Tensor,
+    cache_layer,
+    *,
+    num_qo_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    page_size: int,
+    rope_theta: float,
+    rope_scale: float = 1.0,
+    eps: float = 1e-6,
+    q_out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Returns the rotated q [B, Hq, D]; writes rotated k and v into the pages."""
+    _rows2d(qkv, "qkv")
+    B = qkv.shape[0]
+    kc, vc, page_stride, token_stride, head_stride, num_pages = _cache_geometry(
+        cache_layer, num_kv_heads, head_dim, page_size)
+    if kc.dtype != qkv.dtype:
+        raise ValueError("qkv dtype must match the KV cache")
+    for t, n in ((positions, "positions"), (page_id, "page_id"), (page_offset, "page_offset")):
+        if t.dtype != torch.int64 or t.numel() != B:
+            raise ValueError(f"{n} must be int64 [B]")
+    q_out = torch.empty((B, num_qo_heads, head_dim), dtype=qkv.dtype, device=qkv.device) if q_out is None else q_out
+    inv_freq = rope_inv_freq(head_dim, rope_theta, rope_scale, qkv.device)
+    lib = _lib.load()
+    _lib.check(lib.pl_qk_norm_rope_append(
+        qkv.data_ptr(), qkv.stride(0),
+        q_norm_weight.data_ptr() if q_norm_weight is not None else None,
+        k_norm_weight.data_ptr() if k_norm_weight is not None else None,
+        positions.data_ptr(), page_id.data_ptr(), page_offset.data_ptr(),
+        q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(), page_stride, token_stride, head_stride,
+        num_pages, page_size, B, num_qo_heads, num_kv_heads, head_dim,
+        inv_freq.data_ptr(), float(eps), _lib.dtype_code(qkv.dtype),
+        _lib.stream_handle(qkv.device)), "pl_qk_norm_rope_append")
+    return q_out

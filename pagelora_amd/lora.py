@@ -30,8 +30,8 @@ _WS: dict[int, torch.Tensor] = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device workspace for the rank-r intermediate, grown (never shrunk)
-    on demand -- never inside a captured graph."""
+    """Per-device workspace for the shrink's partial sums, grown (never
+    shrunk) on demand -- never inside a captured graph."""
     key = device.index if device.index is not None else torch.cuda.current_device()
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
@@ -43,11 +43,9 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
-def reserve_workspace(device: torch.device | str, num_tokens: int, in_features: int, ranks: Sequence[int]) -> None:
-    """Allocate the workspace a later (possibly captured) call will need."""
-    device = torch.device(device)
-    r_pad = (sum(ranks) + 31) // 32 * 32
-    _workspace(device, num_tokens * r_pad * 2 + 256)
+def reserve_workspace(device: torch.device | str, nbytes: int) -> None:
+    """Allocate ``nbytes`` of workspace ahead of a (possibly captured) call."""
+    _workspace(torch.device(device), nbytes)
 
 
 def _module_structs(modules, x: torch.Tensor):

@@ -37,7 +37,8 @@ def test_workspace_size_query_is_host_only():
     for m, out in zip(mods, (4096, 1024, 1024)):
         m.A = m.B = m.out = 256  # aligned dummy addresses: sizes only, never dereferenced
         m.ldo, m.out_features, m.rank, m.scale = 6144, out, 16, 2.0
-    assert lib.pl_lora_workspace_size(64, 4096, mods, 3) == 64 * 64 * 2  # [T][sum(rank) padded to 32] bf16
+    # fp32 partials [k-slices][T][sum(rank) padded to 32]: 64 tokens -> 4 slices of 4096
+    assert lib.pl_lora_workspace_size(64, 4096, mods, 3) == 4 * 64 * 64 * 4
 
 
 def test_lora_module_struct_layout():
