@@ -13,8 +13,10 @@ the stream it runs on) against MI355X's 8 TB/s HBM peak.
 
 Also reported: the Qwen3-8B decode-layer latency (1 row x 2048 tokens, 32/8
 heads, bf16), the per-layer LoRA delta time of 64 tokens over 4 adapters,
-and the CPU baseline (the float64 numpy oracle on a bounded sample of rows,
-one thread).
+end-to-end tok/s of a Qwen3-8B-shaped random-init decoder with rank-16
+no-merge LoRA under hipGraph replay (4 rows behind a 2048-token shared
+prefix; 1 row at 32768 tokens), and the CPU baseline (the float64 numpy
+oracle on a bounded sample of rows, one thread).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
 """
@@ -47,6 +49,7 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     p.add_argument("--no-extra", action="store_true", help="headline workload only")
+    p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Qwen3-8B-shaped decode legs")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a 1 GiB device copy (for scaling rocprofv3 FETCH/WRITE_SIZE)")
     return p.parse_args()
@@ -167,6 +170,50 @@ def time_lora(device, steps=20):
     return ms, nbytes
 
 
+def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_steps=2):
+    """Qwen3-8B-shaped random-init decoder (36 layers, hidden 4096, 32/8 heads,
+    head_dim 128, bf16) with rank-16 LoRA on all 7 modules: ``rows`` requests
+    behind a shared ``prefix_len``-token prefix in shared pages plus their own
+    ``suffix_len`` random-id tokens, then ``steps`` greedy steps under hipGraph
+    replay.  tok/s = generated tokens / decode seconds (the graph is captured
+    in a short warm-up call first, outside the timed region)."""
+    import torch
+
+    from pagelora_amd.decoder import QWEN3_8B, DecoderWeights
+    from pagelora_amd.generation import BatchGenerator, prefill_requests
+    from pagelora_amd.kv_pool import PagedKVPool
+
+    cfg = QWEN3_8B
+    w = DecoderWeights(cfg, n_adapters=1, device=device, seed=0)
+    ps = 16
+    pages = (prefix_len + rows * (suffix_len + steps + warm_steps + 16)) // ps + 8 * rows + 8
+    pool = PagedKVPool(num_layers=cfg.num_layers, capacity_pages=pages, page_size=ps, num_kv_heads=cfg.num_kv_heads,
+                       head_dim=cfg.head_dim, dtype=torch.bfloat16, device=device)
+    g = torch.Generator().manual_seed(seed)
+    prefix = torch.randint(0, cfg.vocab, (prefix_len,), generator=g) if prefix_len else None
+    prompts = [torch.randint(0, cfg.vocab, (suffix_len,), generator=g) for _ in range(rows)]
+    t = time.perf_counter()
+    reqs, first, _ = prefill_requests(w, pool, prompts, shared_prefix=prefix)
+    torch.cuda.synchronize(device)
+    prefill_s = time.perf_counter() - t
+    gen = BatchGenerator(w, pool, use_graph=True)
+    warm = gen.generate(reqs, first, steps=warm_steps)
+    res = gen.generate(reqs, warm.tokens[:, -1].to(device), steps=steps)
+    out = {
+        "tok_per_s": round(res.decode_tokens_per_s, 1),
+        "ms_per_step": round(res.decode_seconds / steps * 1e3, 3),
+        "rows": rows,
+        "context_at_start": prefix_len + suffix_len + warm_steps,
+        "steps": steps,
+        "hip_graph": res.used_graph,
+        "graph_captures": res.graph_captures,
+        "prefill_s": round(prefill_s, 2),
+    }
+    del w, pool, gen
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(w, budget_s):
     """Time the float64 numpy oracle on whole rows of the workload until the
     budget is spent; report algorithmic GB/s of the rows it finished."""
@@ -260,6 +307,11 @@ def main():
             "us_per_layer": round(lora_ms * 1e3, 2),
             "algorithmic_GBps": round(lora_bytes / (lora_ms * 1e-3) / 1e9, 1),
         }
+    if not args.no_extra and not args.no_e2e:
+        extra["e2e_qwen3_8b_lora_r16_4x(2048_shared+64)"] = e2e_decode(
+            dev, prefix_len=2048, suffix_len=64, rows=4, steps=128)
+        extra["e2e_qwen3_8b_lora_r16_1x32768"] = e2e_decode(
+            dev, prefix_len=0, suffix_len=32768, rows=1, steps=128)
     line = {
         "metric": METRIC,
         "value": round(value, 1),

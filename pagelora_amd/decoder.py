@@ -214,7 +214,7 @@ def _attention_f32(q, k, v, causal_offset: int) -> torch.Tensor:
 
 @torch.no_grad()
 def prefill(weights: DecoderWeights, pool: PagedKVPool, request: Request, tokens: torch.Tensor,
-            adapter: int = 0, chunk: int = 1024) -> torch.Tensor:
+            adapter: int = 0, chunk: int = 2048) -> torch.Tensor:
     """Run ``tokens`` (appended after ``request.length``) through the model,
     writing their K/V into the request's pages; returns the last hidden row's
     logits.  Pages for the tokens must already be reserved."""

@@ -77,19 +77,24 @@ class BatchGenerator:
         cfg = weights.cfg
         self.weights = weights
         self.pool = pool
+        # Rows that share prefix pages list them once each, so a batch's
+        # logical page count can exceed the pool; size the persistent table
+        # for that up front so the decode graph's buffers never move.
         self.backend = PagedDecodeAttention(
             device=pool.cache.device, workspace_mb=workspace_mb, num_qo_heads=cfg.num_qo_heads,
             num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=pool.page_size,
-            max_pages=pool.capacity_pages,
+            max_pages=4 * pool.capacity_pages,
         )
         self.use_graph = use_graph
         self.graphs = BatchDecodeGraphRunner(weights, pool, self.backend)
-        cap = pool.capacity_pages
-        self._tables = _PinnedRing(4, (3, cap + 1), torch.int32)
+        self._tables = _PinnedRing(4, (3, 4 * pool.capacity_pages + 1), torch.int32)
         self._inputs = _PinnedRing(4, (4, 4096), torch.int64)
 
     def _plan(self, requests) -> None:
         indptr, indices, last = self.pool.tables(requests)
+        if len(indices) + 1 > self._tables.bufs[0].shape[1]:
+            torch.cuda.synchronize(self.pool.cache.device)  # every staged copy has run
+            self._tables = _PinnedRing(4, (3, 2 * len(indices) + 1), torch.int32)
         buf, slot = self._tables.next()
         B, n = len(requests), len(indices)
         buf[0, : B + 1].numpy()[:] = indptr

@@ -1,0 +1,75 @@
+"""Host-side behaviour of the drop-in backend that needs no GPU: constructor
+checks and page-table validation (attention_backend.py:44-45 raises
+ValueError for a bad head ratio; flashinfer_page_table.py:205-218 for bad
+tables)."""
+
+import pytest
+import torch
+
+from pagelora_amd.attention_backend import FlashInferAttentionBackend, PagedDecodeAttention
+
+
+def _backend(**kw):
+    args = dict(device=torch.device("cpu"), workspace_mb=1, num_qo_heads=28, num_kv_heads=4, head_dim=128,
+                page_size=16)
+    args.update(kw)
+    return PagedDecodeAttention(**args)
+
+
+def test_alias_and_attributes():
+    assert FlashInferAttentionBackend is PagedDecodeAttention
+    be = _backend()
+    assert be.page_size == 16 and be.workspace_buffer.numel() == 1 << 20
+    assert be.query_rescale == 1.0 and be.sm_scale == pytest.approx(128 ** -0.5)
+    assert be.decode_use_tensor_cores is False and be.use_flashinfer_qk_norm is False
+
+
+def test_head_ratio_must_divide():
+    with pytest.raises(ValueError):
+        _backend(num_qo_heads=30, num_kv_heads=4)
+    with pytest.raises(ValueError):
+        _backend(num_kv_heads=0)
+
+
+@pytest.mark.parametrize(
+    "indptr,indices,last",
+    [
+        ([1, 2], [0, 0], [1]),        # indptr must start at 0
+        ([0, 2, 1], [0, 0], [1, 1]),  # non-decreasing
+        ([0, 3], [0, 0], [1]),        # points past indices
+        ([0, 1], [0], [17]),          # last_page_len > page_size
+        ([0, 1], [0], [0]),           # last_page_len < 1 on a non-empty row
+        ([0, 1], [-3], [4]),          # negative page id
+    ],
+)
+def test_bad_host_tables_raise_before_any_device_work(indptr, indices, last):
+    be = _backend()
+    with pytest.raises(ValueError):
+        be.plan_decode(paged_kv_indptr=torch.tensor(indptr, dtype=torch.int32),
+                       paged_kv_indices=torch.tensor(indices, dtype=torch.int32),
+                       paged_kv_last_page_len=torch.tensor(last, dtype=torch.int32))
+
+
+def test_wrong_dtype_or_shape_raises():
+    be = _backend()
+    with pytest.raises(ValueError):
+        be.plan_decode(paged_kv_indptr=torch.tensor([0, 1]), paged_kv_indices=torch.tensor([0]),
+                       paged_kv_last_page_len=torch.tensor([1]))  # int64, not int32
+    with pytest.raises(ValueError):
+        be.plan_decode(paged_kv_indptr=torch.tensor([0, 1, 2], dtype=torch.int32),
+                       paged_kv_indices=torch.tensor([0, 1], dtype=torch.int32),
+                       paged_kv_last_page_len=torch.tensor([1], dtype=torch.int32))  # B+1 mismatch
+
+
+def test_cpu_backend_refuses_to_plan_a_valid_table():
+    be = _backend()
+    with pytest.raises(RuntimeError):
+        be.plan_decode(paged_kv_indptr=torch.tensor([0, 1], dtype=torch.int32),
+                       paged_kv_indices=torch.tensor([3], dtype=torch.int32),
+                       paged_kv_last_page_len=torch.tensor([5], dtype=torch.int32))
+
+
+def test_prefill_is_not_part_of_this_build():
+    be = _backend()
+    with pytest.raises(NotImplementedError):
+        be.plan_prefill(qo_indptr=torch.tensor([0, 1]))
