@@ -95,8 +95,8 @@ constexpr int kShrinkThreads = kShrinkWaves * kWave;
 constexpr int kTilesPerPass = 4;
 
 inline int ksplit_for(int tokens, int in_features) {
-  int by_k = in_features / 256;                   // at least 256 elements per slice
-  int by_t = 256 / (tokens > 0 ? tokens : 1);     // keep partial traffic ~ constant
+  int by_k = in_features / 512;                   // at least 512 elements per slice
+  int by_t = 256 / (tokens > 0 ? tokens : 1);     // keep the expand's fold short
   int k = by_k < by_t ? by_k : by_t;
   return k < 1 ? 1 : (k > 64 ? 64 : k);
 }
@@ -252,14 +252,25 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(
   }
 
   for (int tt = 0; tt * 16 < n_a; ++tt) {
-    // fold the partials of this token tile into the rounded intermediate
+    // fold the partials of this token tile into the rounded intermediate:
+    // one thread per (valid token, rank) cell, eight independent loads in
+    // flight per step; rows of absent tokens are zero
+    const int valid = min(16, n_a - tt * 16);
     for (int c = threadIdx.x; c < 16 * g.r_pad; c += kThreads) {
       const int i = c / g.r_pad, k = c - i * g.r_pad;
-      const int ti = tt * 16 + i;
       float sum = 0.f;
-      if (ti < n_a && k < g.r_total) {
-        const float* pp = part + (int64_t)s_list[ti] * g.r_pad + k;
-        for (int q = 0; q < ksplit; ++q) sum += pp[(int64_t)q * tokens * g.r_pad];
+      if (i < valid && k < g.r_total) {
+        const float* pp = part + (int64_t)s_list[tt * 16 + i] * g.r_pad + k;
+        const int64_t stride = (int64_t)tokens * g.r_pad;
+        int q = 0;
+        for (; q + 8 <= ksplit; q += 8) {
+          float v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v[u] = pp[(q + u) * stride];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) sum += v[u];
+        }
+        for (; q < ksplit; ++q) sum += pp[q * stride];
       }
       s_y[i][k] = __builtin_bit_cast(uint16_t, from_float<T>(sum));
     }

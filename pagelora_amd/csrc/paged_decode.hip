@@ -165,11 +165,23 @@ template <> struct Lane8<float> {
   }
 };
 
+// K/V rows are read exactly once per call: non-temporal loads keep them from
+// displacing reusable lines in the L2 / infinity cache.
+#ifndef PL_DECODE_NT_LOADS
+#define PL_DECODE_NT_LOADS 1
+#endif
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 template <typename T> struct Lane8Half {
   static constexpr int kWords = 4;
   __device__ static void load(uint32_t (&w)[4], const T* p) {
+#if PL_DECODE_NT_LOADS
+    const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+#else
     const uint4 a = *reinterpret_cast<const uint4*>(p);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+#endif
   }
   __device__ static float dot(const uint32_t (&q)[4], const uint32_t (&k)[4]) {
     float acc = 0.f;

@@ -37,8 +37,9 @@ def test_workspace_size_query_is_host_only():
     for m, out in zip(mods, (4096, 1024, 1024)):
         m.A = m.B = m.out = 256  # aligned dummy addresses: sizes only, never dereferenced
         m.ldo, m.out_features, m.rank, m.scale = 6144, out, 16, 2.0
-    # fp32 partials [k-slices][T][sum(rank) padded to 32]: 64 tokens -> 4 slices of 4096
+    # fp32 partials [k-slices][T][sum(rank) padded to 32]: 64 tokens -> 4 slices, 4 tokens -> 8 slices
     assert lib.pl_lora_workspace_size(64, 4096, mods, 3) == 4 * 64 * 64 * 4
+    assert lib.pl_lora_workspace_size(4, 4096, mods, 3) == 8 * 4 * 64 * 4
 
 
 def test_lora_module_struct_layout():
