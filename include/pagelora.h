@@ -263,6 +263,46 @@ int pl_lora_expand(int num_tokens, int in_features,
                    int out_dtype, const void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Decode-sized linear layer with the fused LoRA expand                      */
+/* ------------------------------------------------------------------------ */
+
+/* Most tokens pl_linear takes (it re-reads W once per 16 tokens). */
+#define PL_LINEAR_MAX_TOKENS 64
+
+/* A LoRA module whose delta pl_linear adds to its output columns
+ * [col_offset, col_offset + out_features); B as in pl_lora_module. */
+typedef struct {
+  const void* B;
+  int col_offset;
+  int out_features;
+  int rank;
+  float scale;
+} pl_linear_lora;
+
+/*
+ * out[t, :] = x[t] . W^T (+ bias) (+ sum_m scale_m * B_m[a_t] . y_m[t])
+ * for num_tokens <= PL_LINEAR_MAX_TOKENS, W [out_features, in_features]
+ * (row stride ldw) streamed once, fp32 accumulation, one rounding.
+ * With num_lora > 0, y is the rank-r intermediate of the same group
+ * produced by pl_lora_shrink on lora_workspace just before (same x, same
+ * modules in the same order, same adapter_ids): the expand runs in this
+ * kernel's epilogue instead of a separate pl_lora_expand launch.
+ * dtype: F16 or BF16 for x, W, bias, B and out.
+ *
+ * Replaces the base F.linear of the packed / per-module projections
+ * (model/flashinfer/packed_ops.py:143, 179, 251-265) together with the
+ * LoRA up-projection of _packed_lora_delta / LoRALinear.forward
+ * (packed_ops.py:325; multilora/linear.py:230-231).
+ */
+int pl_linear(const void* x, int64_t ldx, int num_tokens, int in_features,
+              const void* weight, int64_t ldw, int out_features,
+              const void* bias, void* out, int64_t ldo,
+              const pl_linear_lora* lora_h, int num_lora,
+              const int32_t* adapter_ids, int num_adapters,
+              const void* lora_workspace, size_t lora_workspace_bytes,
+              int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

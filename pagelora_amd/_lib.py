@@ -54,6 +54,20 @@ class LoraModule(ctypes.Structure):
     ]
 
 
+class LinearLora(ctypes.Structure):
+    """Mirror of ``pl_linear_lora``."""
+
+    _fields_ = [
+        ("B", ctypes.c_void_p),
+        ("col_offset", ctypes.c_int),
+        ("out_features", ctypes.c_int),
+        ("rank", ctypes.c_int),
+        ("scale", ctypes.c_float),
+    ]
+
+
+PL_LINEAR_MAX_TOKENS = 64
+
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int
 _i64 = ctypes.c_int64
@@ -103,6 +117,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _i32, _i32, _i32, _i32,       # batch, hq, hkv, head_dim
             _vp, _f32, _i32, _vp,         # inv_freq, eps, dtype, stream
         ],
+    ),
+    "pl_linear": (
+        _i32,
+        [_vp, _i64, _i32, _i32, _vp, _i64, _i32, _vp, _vp, _i64, ctypes.POINTER(LinearLora), _i32, _vp, _i32,
+         _vp, _sz, _i32, _vp],
     ),
     "pl_lora_workspace_size": (_sz, [_i32, _i32, ctypes.POINTER(LoraModule), _i32]),
     "pl_lora_delta": (

@@ -94,12 +94,7 @@ constexpr int kShrinkWaves = 4;
 constexpr int kShrinkThreads = kShrinkWaves * kWave;
 constexpr int kTilesPerPass = 4;
 
-inline int ksplit_for(int tokens, int in_features) {
-  int by_k = in_features / 512;                   // at least 512 elements per slice
-  int by_t = 256 / (tokens > 0 ? tokens : 1);     // keep the expand's fold short
-  int k = by_k < by_t ? by_k : by_t;
-  return k < 1 ? 1 : (k > 64 ? 64 : k);
-}
+inline int ksplit_for(int tokens, int in_features) { return lora_ksplit(tokens, in_features); }
 inline int kslice_for(int in_features, int ksplit) {  // multiple of 32 * waves
   const int step = 32 * kShrinkWaves;
   return ((in_features + ksplit - 1) / ksplit + step - 1) / step * step;

@@ -183,4 +183,14 @@ inline int dtype_bytes(int dtype) {
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// k-slices of the LoRA shrink: at least 512 elements per slice, and fewer
+// slices as tokens grow so the expand's fold stays short.  Shared by the
+// shrink and by every consumer of its partials.
+inline int lora_ksplit(int tokens, int in_features) {
+  int by_k = in_features / 512;
+  int by_t = 256 / (tokens > 0 ? tokens : 1);
+  int k = by_k < by_t ? by_k : by_t;
+  return k < 1 ? 1 : (k > 64 ? 64 : k);
+}
+
 }  // namespace pl

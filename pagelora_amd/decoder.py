@@ -34,7 +34,7 @@ import torch.nn.functional as F
 from . import fused_ops
 from .attention_backend import PagedDecodeAttention
 from .kv_pool import PagedKVPool, Request
-from .lora import lora_delta_
+from .lora import lora_delta_, lora_linear
 
 
 @dataclass(frozen=True)
@@ -119,11 +119,31 @@ class DecodeContext:
         self.next_tokens = torch.zeros(batch, dtype=torch.int64, device=device)
 
 
-def _lora_qkv(cfg: DecoderConfig, lw: LayerWeights, x, qkv, ids, scale: float) -> None:
+# Projections with narrow outputs (q/k/v, o) run on the decode-sized linear
+# kernel with the LoRA expand in its epilogue; the wide MLP projections keep
+# the library GEMM plus the separate shrink/expand kernels, which is faster
+# for them.  Longer inputs (prefill) always take the library GEMM.
+FUSED_LINEAR_MAX_TOKENS = 16
+
+
+def _qkv_projection(cfg: DecoderConfig, lw: LayerWeights, x, ids, scale: float) -> torch.Tensor:
     qd, kd = cfg.q_dim, cfg.kv_dim
     (Aq, Bq), (Ak, Bk), (Av, Bv) = lw.lora["q"], lw.lora["k"], lw.lora["v"]
+    if x.shape[0] <= FUSED_LINEAR_MAX_TOKENS:
+        return lora_linear(x, lw.w_qkv, [(Aq, Bq, 0, scale), (Ak, Bk, qd, scale), (Av, Bv, qd + kd, scale)], ids)
+    qkv = F.linear(x, lw.w_qkv)
     lora_delta_(x, [(Aq, Bq, qkv[:, :qd], scale), (Ak, Bk, qkv[:, qd:qd + kd], scale),
                     (Av, Bv, qkv[:, qd + kd:], scale)], ids)
+    return qkv
+
+
+def _o_projection(lw: LayerWeights, attn, ids, scale: float) -> torch.Tensor:
+    Ao, Bo = lw.lora["o"]
+    if attn.shape[0] <= FUSED_LINEAR_MAX_TOKENS:
+        return lora_linear(attn, lw.w_o, [(Ao, Bo, 0, scale)], ids)
+    o = F.linear(attn, lw.w_o)
+    lora_delta_(attn, [(Ao, Bo, o, scale)], ids)
+    return o
 
 
 def _mlp(cfg: DecoderConfig, lw: LayerWeights, x2, ids, scale: float) -> torch.Tensor:
@@ -160,8 +180,7 @@ def decode_layer_static(
         x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
     else:
         x = fused_ops.add_rmsnorm(hidden, pending, lw.input_norm, cfg.rms_eps)
-    qkv = F.linear(x, lw.w_qkv)
-    _lora_qkv(cfg, lw, x, qkv, ids, lora_scale)
+    qkv = _qkv_projection(cfg, lw, x, ids, lora_scale)
     q = fused_ops.qk_norm_rope_append(
         qkv, lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None,
         ctx.positions, ctx.page_id, ctx.page_offset, layer_cache, num_qo_heads=cfg.num_qo_heads,
@@ -170,9 +189,7 @@ def decode_layer_static(
     attn = torch.empty_like(q)
     backend.run_decode_into(q, layer_cache, attn)
     attn = attn.view(B, cfg.q_dim)
-    o = F.linear(attn, lw.w_o)
-    Ao, Bo = lw.lora["o"]
-    lora_delta_(attn, [(Ao, Bo, o, lora_scale)], ids)
+    o = _o_projection(lw, attn, ids, lora_scale)
     x2 = fused_ops.add_rmsnorm(hidden, o, lw.post_norm, cfg.rms_eps)
     return _mlp(cfg, lw, x2, ids, lora_scale)
 
@@ -240,8 +257,7 @@ def prefill(weights: DecoderWeights, pool: PagedKVPool, request: Request, tokens
                 x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
             else:
                 x = fused_ops.add_rmsnorm(hidden, pending, lw.input_norm, cfg.rms_eps)
-            qkv = F.linear(x, lw.w_qkv)
-            _lora_qkv(cfg, lw, x, qkv, ids, s)
+            qkv = _qkv_projection(cfg, lw, x, ids, s)
             q = fused_ops.qk_norm_rope_append(
                 qkv, lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None, pos, page_of,
                 off_of, cache, num_qo_heads=cfg.num_qo_heads, num_kv_heads=cfg.num_kv_heads,
@@ -251,9 +267,7 @@ def prefill(weights: DecoderWeights, pool: PagedKVPool, request: Request, tokens
             kk = cache[pages[all_pos // ps], 0, all_pos % ps]
             vv = cache[pages[all_pos // ps], 1, all_pos % ps]
             attn = _attention_f32(q, kk, vv, start + c0).to(hidden.dtype).reshape(T, cfg.q_dim)
-            o = F.linear(attn, lw.w_o)
-            Ao, Bo = lw.lora["o"]
-            lora_delta_(attn, [(Ao, Bo, o, s)], ids)
+            o = _o_projection(lw, attn, ids, s)
             x2 = fused_ops.add_rmsnorm(hidden, o, lw.post_norm, cfg.rms_eps)
             pending = _mlp(cfg, lw, x2, ids, s)
         x = fused_ops.add_rmsnorm(hidden, pending, weights.final_norm, cfg.rms_eps)

@@ -116,3 +116,67 @@ def lora_delta_(
         ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device),
     )
     _lib.check(status, "pl_lora_delta")
+
+
+def lora_linear(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    lora_modules: Sequence[tuple[torch.Tensor, torch.Tensor, int, float]] | None,
+    adapter_ids: torch.Tensor | None,
+    *,
+    bias: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``x . W^T (+ bias) + sum_m scale_m * B_m[ids] . (A_m[ids] . x)`` for
+    decode-sized batches (T <= 64): the LoRA shrink, then one kernel that
+    streams W and adds the expand in its epilogue (``pl_linear``).
+
+    lora_modules: ``(A, B, col_offset, scale)`` per module, in rank order,
+    ``col_offset`` being the module's first output column of W's output.
+    """
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be [T, in] with unit column stride")
+    T, fin = x.shape
+    if T > _lib.PL_LINEAR_MAX_TOKENS:
+        raise ValueError(f"lora_linear takes at most {_lib.PL_LINEAR_MAX_TOKENS} tokens")
+    if weight.dim() != 2 or weight.shape[1] != fin or weight.stride(1) != 1 or weight.dtype != x.dtype:
+        raise ValueError("weight must be [out, in] matching x")
+    N = weight.shape[0]
+    out = torch.empty((T, N), dtype=x.dtype, device=x.device) if out is None else out
+    if out.shape != (T, N) or out.stride(1) != 1 or out.dtype != x.dtype:
+        raise ValueError("out must be [T, out] with unit column stride")
+    if bias is not None and (bias.numel() != N or bias.dtype != x.dtype):
+        raise ValueError("bias must be [out] of x's dtype")
+    lib = _lib.load()
+    stream = _lib.stream_handle(x.device)
+    n = 0
+    arr = None
+    ws = None
+    n_adapters = 1
+    if lora_modules:
+        n = len(lora_modules)
+        group = []
+        arr = (_lib.LinearLora * n)()
+        for i, (A, B, col, scale) in enumerate(lora_modules):
+            fout = B.shape[-2]
+            group.append((A, B, out[:, col:col + fout], scale))
+            Bc = B if B.dim() == 3 else B.unsqueeze(0)
+            arr[i].B, arr[i].col_offset, arr[i].out_features = Bc.data_ptr(), int(col), int(fout)
+            arr[i].rank, arr[i].scale = int(Bc.shape[2]), float(scale)
+        if adapter_ids is None or adapter_ids.dtype != torch.int32 or adapter_ids.numel() != T:
+            raise ValueError("adapter_ids must be int32 [T]")
+        mods, n_adapters, _ = _module_structs(group, x)
+        nbytes = lib.pl_lora_workspace_size(T, fin, mods, n)
+        if nbytes == 0:
+            raise ValueError(f"invalid LoRA group: {_lib.last_error()}")
+        ws = _workspace(x.device, nbytes)
+        _lib.check(lib.pl_lora_shrink(x.data_ptr(), x.stride(0), T, fin, mods, n, adapter_ids.data_ptr(),
+                                      n_adapters, _lib.dtype_code(x.dtype), ws.data_ptr(), ws.numel(), stream),
+                   "pl_lora_shrink")
+    _lib.check(lib.pl_linear(
+        x.data_ptr(), x.stride(0), T, fin, weight.data_ptr(), weight.stride(0), N,
+        bias.data_ptr() if bias is not None else None, out.data_ptr(), out.stride(0),
+        arr, n, adapter_ids.data_ptr() if n else None, n_adapters,
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+        _lib.dtype_code(x.dtype), stream), "pl_linear")
+    return out
