@@ -139,6 +139,60 @@ int pl_kv_append(const void* k, const void* v, int64_t k_stride_b,
                  void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Paged prefill attention                                                   */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Host-side plan of a paged prefill: validates the HOST tables qo_indptr
+ * [batch+1], kv_indptr [batch+1] and kv_last_page_len [batch] (int32) and
+ * writes the work list `items` (int32 pairs (request, first row), longest
+ * first) for pl_prefill_run.  *num_items receives the item count; with
+ * items == NULL only the count is computed.  A request's rows are its
+ * qo_len * (num_qo_heads / num_kv_heads) (position, group head) pairs, 64
+ * per item.  Under `causal` every request needs qo_len <= kv_len.
+ * PL_ERR_WORKSPACE if more than max_items items are needed.
+ *
+ * Replaces FlashInferAttentionBackend.plan_prefill
+ * (model/flashinfer/attention_backend.py:133-170), i.e.
+ * flashinfer.BatchPrefillWithPagedKVCacheWrapper.plan.
+ */
+int pl_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
+                    const int32_t* kv_last_page_len, int batch,
+                    int num_qo_heads, int num_kv_heads, int page_size,
+                    int causal, int32_t* items, int max_items,
+                    int* num_items);
+
+/*
+ * Multi-token paged attention over packed queries:
+ *   o[t, hq] = softmax(q[t, hq] . K_r[:, hq / g]^T * sm_scale [+ mask]) . V_r
+ * for the tokens t of request r, qo_indptr[r] <= t < qo_indptr[r+1], which
+ * are the LAST qo_len positions of the request's kv_len tokens (pages
+ * kv_indices[kv_indptr[r] ..], addressed as in pl_decode_run).  With
+ * `causal`, query j of a request sees kv positions <= kv_len - qo_len + j.
+ * q and o are [tokens, num_qo_heads, head_dim] with strides (stride_t,
+ * stride_h, 1); all tables and `items` (from pl_prefill_plan) are device
+ * arrays.  q, caches and o share `dtype` (F16 or BF16); accumulation is
+ * fp32.  head_dim: 64, 128 or 256.  Strides must be multiples of 8
+ * elements and q, o and the caches 16-byte aligned.
+ *
+ * Replaces FlashInferAttentionBackend.run_prefill
+ * (model/flashinfer/attention_backend.py:172-190), i.e.
+ * BatchPrefillWithPagedKVCacheWrapper.run(q / 16, cache) with sm_scale
+ * 16/sqrt(D) — the same softmax.
+ */
+int pl_prefill_run(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                   const void* k_cache, const void* v_cache,
+                   int64_t page_stride, int64_t token_stride,
+                   int64_t head_stride, int64_t num_pages,
+                   const int32_t* qo_indptr, const int32_t* kv_indptr,
+                   const int32_t* kv_indices,
+                   const int32_t* kv_last_page_len, const int32_t* items,
+                   int num_items, void* o, int64_t o_stride_t,
+                   int64_t o_stride_h, int batch, int num_qo_heads,
+                   int num_kv_heads, int head_dim, int page_size, int causal,
+                   float sm_scale, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Fused element-wise ops of the decode layer                                */
 /* ------------------------------------------------------------------------ */
 

@@ -104,6 +104,27 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _i32, _i32, _i32, _i32, _vp,        # batch, hkv, head_dim, dtype, stream
         ],
     ),
+    "pl_prefill_plan": (
+        _i32,
+        [
+            _vp, _vp, _vp, _i32,         # qo_indptr, kv_indptr, last_page_len (host), batch
+            _i32, _i32, _i32, _i32,      # hq, hkv, page_size, causal
+            _vp, _i32, ctypes.POINTER(_i32),  # items (host), max_items, num_items
+        ],
+    ),
+    "pl_prefill_run": (
+        _i32,
+        [
+            _vp, _i64, _i64,             # q, strides
+            _vp, _vp, _i64, _i64, _i64,  # k/v cache, page/token/head strides
+            _i64,                        # num_pages
+            _vp, _vp, _vp, _vp,          # qo_indptr, kv_indptr, kv_indices, last_page_len
+            _vp, _i32,                   # items, num_items
+            _vp, _i64, _i64,             # o, strides
+            _i32, _i32, _i32, _i32, _i32, _i32,  # batch, hq, hkv, head_dim, page_size, causal
+            _f32, _i32, _vp,             # sm_scale, dtype, stream
+        ],
+    ),
     "pl_rmsnorm": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _i32, _vp]),
     "pl_add_rmsnorm": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _i32, _vp]),
     "pl_silu_mul": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp]),

@@ -23,6 +23,7 @@ workaround is not needed and ``query_rescale`` is 1.0.
 
 from __future__ import annotations
 
+import ctypes
 import math
 import os
 from collections import deque
@@ -312,11 +313,110 @@ class PagedDecodeAttention:
         return out
 
     # ------------------------------------------------------------- prefill
-    def plan_prefill(self, **kwargs) -> None:  # attention_backend.py:133-170
-        raise NotImplementedError("paged prefill attention is not part of this build; see run_prefill")
+    def plan_prefill(
+        self,
+        *,
+        qo_indptr: torch.Tensor,
+        paged_kv_indptr: torch.Tensor,
+        paged_kv_indices: torch.Tensor,
+        paged_kv_last_page_len: torch.Tensor,
+        causal: bool = True,
+        q_data_type: torch.dtype | None = None,
+        kv_data_type: torch.dtype | None = None,
+    ) -> None:
+        """Plan packed multi-token attention (attention_backend.py:133-170).
 
-    def run_prefill(self, q: torch.Tensor, paged_kv_cache_layer) -> torch.Tensor:  # :172-190
-        raise NotImplementedError("paged prefill attention is not part of this build")
+        Request r owns query rows ``qo_indptr[r] .. qo_indptr[r+1]``, the last
+        ``qo_len`` positions of its paged sequence; with ``causal`` query j
+        sees kv positions ``<= kv_len - qo_len + j``.  The work list is built
+        on the host (the tables are read there, as FlashInfer's prefill plan
+        does), then tables and work list are uploaded on the current stream.
+        """
+
+        tables = (qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len)
+        if any(t.dim() != 1 for t in tables):
+            raise ValueError("prefill tables must be 1-D")
+        batch = paged_kv_last_page_len.numel()
+        if qo_indptr.numel() != batch + 1 or paged_kv_indptr.numel() != batch + 1:
+            raise ValueError("qo_indptr and paged_kv_indptr must have batch + 1 entries")
+        host = [t.detach().to("cpu", torch.int32).contiguous() for t in tables]
+        qo_h, kv_h, ind_h, last_h = host
+        max_page = _validate_host_table(kv_h, ind_h, last_h, self.page_size)
+        if self.device.type != "cuda":
+            raise RuntimeError("PagedDecodeAttention.plan_prefill needs a ROCm device")
+        n = ctypes.c_int(0)
+        args = (qo_h.data_ptr(), kv_h.data_ptr(), last_h.data_ptr(), batch, self.num_qo_heads, self.num_kv_heads,
+                self.page_size, int(bool(causal)))
+        _lib.check(self._lib.pl_prefill_plan(*args, None, 0, ctypes.byref(n)), "pl_prefill_plan")
+        items_h = torch.empty(max(1, 2 * n.value), dtype=torch.int32)
+        _lib.check(self._lib.pl_prefill_plan(*args, items_h.data_ptr(), n.value, ctypes.byref(n)), "pl_prefill_plan")
+        dev = [t.to(self.device, non_blocking=False) for t in (qo_h, kv_h, ind_h, last_h, items_h)]
+        self._prefill_plan = {
+            "batch": batch,
+            "tokens": int(qo_h[-1]) if batch else 0,
+            "num_items": n.value,
+            "causal": bool(causal),
+            "max_page": max_page,
+            "tables": dev,
+            "q_data_type": q_data_type,
+            "kv_data_type": kv_data_type,
+        }
+
+    def run_prefill(self, q: torch.Tensor, paged_kv_cache_layer) -> torch.Tensor:
+        """One layer of paged prefill attention (attention_backend.py:172-190).
+
+        ``q`` is packed ``[tokens, Hq, D]`` (returns the same shape) or
+        ``[B, Hq, S, D]`` with S tokens per request (returns ``[B, Hq, S, D]``).
+        """
+
+        if q.dim() == 4:
+            bsz, heads, seqlen, head_dim = q.shape
+            out4 = torch.empty((bsz, heads, seqlen, head_dim), dtype=q.dtype, device=q.device)
+            if bsz == 1:
+                # [1, H, S, D] seen as [S, H, D]: strided views, no copies
+                self.run_prefill_into(q[0].transpose(0, 1), paged_kv_cache_layer, out4[0].transpose(0, 1))
+                return out4
+            q_nhd = q.transpose(1, 2).reshape(bsz * seqlen, heads, head_dim)
+            out = self.run_prefill_into(q_nhd, paged_kv_cache_layer, torch.empty_like(q_nhd))
+            return out.reshape(bsz, seqlen, heads, head_dim).transpose(1, 2).contiguous()
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        return self.run_prefill_into(q, paged_kv_cache_layer, out)
+
+    def run_prefill_into(self, q: torch.Tensor, paged_kv_cache_layer, out: torch.Tensor) -> torch.Tensor:
+        """Writes ``out`` ([tokens, Hq, D], head_dim contiguous) for packed ``q``."""
+
+        plan = getattr(self, "_prefill_plan", None)
+        if plan is None:
+            raise RuntimeError("plan_prefill must be called before run_prefill")
+        if q.dim() != 3 or tuple(q.shape[1:]) != (self.num_qo_heads, self.head_dim):
+            raise ValueError(f"q must be [tokens, {self.num_qo_heads}, {self.head_dim}], got {tuple(q.shape)}")
+        if q.shape[0] != plan["tokens"]:
+            raise ValueError(f"q has {q.shape[0]} tokens but the plan has {plan['tokens']}")
+        if tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or q.stride(2) != 1 or out.stride(2) != 1:
+            raise ValueError("q and out must match in shape/dtype with a contiguous head_dim")
+        if q.device.type != "cuda":
+            raise RuntimeError("run_prefill needs tensors on a ROCm device")
+        k, v, page_stride, token_stride, head_stride, num_pages = _cache_geometry(
+            paged_kv_cache_layer, self.num_kv_heads, self.head_dim, self.page_size
+        )
+        if k.dtype != q.dtype:
+            raise ValueError(f"q dtype {q.dtype} != KV cache dtype {k.dtype}")
+        if plan["max_page"] >= num_pages:
+            raise ValueError(f"page id {plan['max_page']} is outside the {num_pages}-page KV pool")
+        qo_d, kv_d, ind_d, last_d, items_d = plan["tables"]
+        status = self._lib.pl_prefill_run(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            k.data_ptr(), v.data_ptr(), page_stride, token_stride, head_stride,
+            num_pages,
+            qo_d.data_ptr(), kv_d.data_ptr(), ind_d.data_ptr(), last_d.data_ptr(),
+            items_d.data_ptr(), plan["num_items"],
+            out.data_ptr(), out.stride(0), out.stride(1),
+            plan["batch"], self.num_qo_heads, self.num_kv_heads, self.head_dim, self.page_size,
+            int(plan["causal"]), self.sm_scale, _lib.dtype_code(q.dtype),
+            _lib.stream_handle(q.device),
+        )
+        _lib.check(status, "pl_prefill_run")
+        return out
 
 
 # The reference's class name, for drop-in imports.

@@ -1,0 +1,410 @@
+// Paged prefill (multi-query) attention for gfx950.
+//
+// For request r with query rows qo_indptr[r] .. qo_indptr[r+1] (qo_len of
+// them, the LAST qo_len positions of its kv_len-token sequence) and kv
+// pages kv_indices[kv_indptr[r] ..] (all full but the last, which holds
+// kv_last_page_len[r] tokens):
+//   o[t, h] = softmax(q[t, h] . K^T * sm_scale  [+ causal mask]) . V
+// With `causal`, query j of the request sees kv positions
+// p <= kv_len - qo_len + j (bottom-right aligned, as FlashInfer's
+// BatchPrefillWithPagedKVCacheWrapper); kv head = h / g, g = Hq / Hkv.
+//
+// Work decomposition.  A request's rows are (query position, head of the
+// GQA group) pairs, row = pos * g + hg, so one kv head's K/V tile serves
+// all g heads.  A work item is 64 consecutive rows of one request; the
+// host plan lists items longest first (causal items near the end of a
+// long prompt see the most tiles).  Grid = (items, kv heads), 4 waves of
+// 16 rows each.
+//
+// Per 32-token kv tile: K and V (both row-major) are staged in LDS
+// straight from the pages while the next tile's loads are already in
+// flight in registers; each wave computes S = Q K^T (MFMA 16x16x32, Q held
+// in registers), masks, runs an fp32 online softmax in the log2 domain,
+// moves P from the accumulator layout to the operand layout through LDS
+// and accumulates O += P V (MFMA).  For bf16, P (in [0, 1]) is split into
+// bf16 hi + lo parts and P V runs as two MFMAs, so P carries ~16 mantissa
+// bits instead of 8 (fp16's 11 bits are used as is).  The V operand pairs two adjacent
+// head-dim columns per lane: column tile 2a holds d = 32a + 2c and tile
+// 2a+1 holds d = 32a + 2c + 1, so a lane builds both B operands from eight
+// 32-bit LDS reads and byte permutes, and writes both outputs as one
+// 32-bit store.
+//
+// Reference: FlashInferAttentionBackend.plan_prefill / run_prefill
+// (model/flashinfer/attention_backend.py:133-190); q / query_rescale with
+// sm_scale * query_rescale there is the same softmax as here.
+#include <algorithm>
+#include <type_traits>
+#include <vector>
+
+#include "pl_common.h"
+
+namespace pl {
+namespace prefill {
+
+constexpr int kWave = 64;
+constexpr int kWaves = 4;
+constexpr int kThreads = kWave * kWaves;
+constexpr int kRows = 16 * kWaves;  // rows per work item
+constexpr int kTile = 32;           // kv tokens per tile
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+template <typename T> __device__ __forceinline__ f32x4 mfma32(u32x4 a, u32x4 b, f32x4 c);
+template <> __device__ __forceinline__ f32x4 mfma32<bf16_t>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+template <> __device__ __forceinline__ f32x4 mfma32<f16_t>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                0);
+}
+
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp_mov<0x128>(x));
+  x = fmaxf(x, dpp_mov<0x124>(x));
+  x = fmaxf(x, dpp_mov<0x122>(x));
+  x = fmaxf(x, dpp_mov<0x121>(x));
+  return x;
+}
+
+// Orders this wave's LDS stores before its later LDS loads (the compiler
+// may not move them across; the hardware drains lgkmcnt).
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+template <int D>
+struct Stage {
+  static constexpr int kChunks = D / 8;  // 16-byte chunks per token row
+  static constexpr int kPerThread = kTile * kChunks / kThreads;
+  static_assert(kTile * kChunks % kThreads == 0, "tile must split evenly");
+};
+
+// Loads this thread's K and V chunks of kv tile `tile` into registers.
+template <typename T, int D>
+__device__ __forceinline__ void load_tile(const T* __restrict__ kc, const T* __restrict__ vc,
+                                          const int32_t* __restrict__ ind, int tile, int kv_len, int page_size,
+                                          int64_t num_pages, int64_t page_stride, int64_t token_stride,
+                                          int64_t head_off, u32x4 (&kr)[Stage<D>::kPerThread],
+                                          u32x4 (&vr)[Stage<D>::kPerThread]) {
+  constexpr int CH = Stage<D>::kChunks;
+#pragma unroll
+  for (int j = 0; j < Stage<D>::kPerThread; ++j) {
+    const int c = threadIdx.x + j * kThreads;
+    const int tok = c / CH, ch = c % CH;
+    const int pos = tile * kTile + tok;
+    kr[j] = u32x4{0u, 0u, 0u, 0u};
+    vr[j] = u32x4{0u, 0u, 0u, 0u};
+    if (pos < kv_len) {
+      int64_t page = ind[pos / page_size];
+      page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);
+      const int64_t off = page * page_stride + (int64_t)(pos % page_size) * token_stride + head_off + ch * 8;
+      kr[j] = *reinterpret_cast<const u32x4*>(kc + off);
+      vr[j] = *reinterpret_cast<const u32x4*>(vc + off);
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) void prefill_kernel(
+    const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kc, const T* __restrict__ vc,
+    int64_t page_stride, int64_t token_stride, int64_t head_stride, int64_t num_pages,
+    const int32_t* __restrict__ qo_indptr, const int32_t* __restrict__ kv_indptr,
+    const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ kv_last, const int2* __restrict__ items,
+    int n_items, T* __restrict__ o, int64_t o_st, int64_t o_sh, int batch, int hq, int hkv, int page_size,
+    int causal, float scale_log2) {
+  constexpr int KSTEPS = D / 32;  // MFMA k-steps over the head dim for S
+  constexpr int NP = D / 32;      // column-tile pairs of O
+  constexpr int CH = Stage<D>::kChunks;
+  constexpr int PER = Stage<D>::kPerThread;
+  constexpr int KP = D + 8;       // K row pitch (elements): 16-byte aligned rows, conflict-free 16-byte reads
+  constexpr int VPW = D / 2 + 2;  // V row pitch in 32-bit words: rows 8 apart land 16 banks apart
+  constexpr int PP = kTile + 8;   // P row pitch (elements)
+  constexpr int NPP = std::is_same<T, bf16_t>::value ? 2 : 1;  // P planes: hi (+ lo)
+  __shared__ __align__(16) uint16_t s_k[kTile * KP];
+  __shared__ __align__(16) uint32_t s_v[kTile * VPW];
+  __shared__ __align__(16) uint16_t s_p[kWaves][NPP][16 * PP];
+
+  const int item = blockIdx.x;
+  const int h = blockIdx.y;  // kv head
+  if (item >= n_items || h >= hkv) return;
+  const int2 it = items[item];
+  const int r = uniform(it.x), row0 = uniform(it.y);
+  if (r < 0 || r >= batch) return;
+  const int g = hq / hkv;
+  const int qo_begin = uniform(qo_indptr[r]);
+  const int qo_len = uniform(qo_indptr[r + 1]) - qo_begin;
+  const int pb = uniform(kv_indptr[r]), pe = uniform(kv_indptr[r + 1]);
+  int last = uniform(kv_last[r]);
+  last = last < 1 ? 1 : (last > page_size ? page_size : last);
+  const int kv_len = pe > pb ? (pe - pb - 1) * page_size + last : 0;
+  const int n_rows = qo_len * g;
+  const int32_t* ind = kv_indices + pb;
+  const int64_t head_off = (int64_t)h * head_stride;
+
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lr = lane % 16, grp = lane / 16;
+
+  // rows this lane accumulates (accumulator layout: row 4*grp+i of the wave's 16)
+  int c_limit[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int crow = row0 + wave * 16 + grp * 4 + i;
+    const int pos = crow / g;
+    // last visible kv position; rows past the request stay fully masked
+    const int lim = crow >= n_rows ? -1 : (causal ? kv_len - qo_len + pos : kv_len - 1);
+    c_limit[i] = min(lim, kv_len - 1);
+  }
+
+  // Q as the A operand: row lr of the wave, head-dim 32*ks + 8*grp .. +8
+  u32x4 qa[KSTEPS];
+  {
+    const int arow = row0 + wave * 16 + lr;
+    const int a_pos = arow / g, a_hg = arow - a_pos * g;
+    const bool ok_row = arow < n_rows;
+    const T* qp = q + (int64_t)(qo_begin + a_pos) * q_st + (int64_t)(h * g + a_hg) * q_sh + grp * 8;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      qa[ks] = ok_row ? *reinterpret_cast<const u32x4*>(qp + ks * 32) : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  f32x4 acc[2 * NP];
+#pragma unroll
+  for (int nt = 0; nt < 2 * NP; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+  }
+
+  // kv tiles this item needs: up to the largest causal limit among its rows
+  const int last_row = min(row0 + kRows, n_rows) - 1;
+  const int max_pos = min(causal ? kv_len - qo_len + last_row / g : kv_len - 1, kv_len - 1);
+  const int n_tiles = uniform(max_pos < 0 ? 0 : max_pos / kTile + 1);
+
+  u32x4 kr[PER], vr[PER];
+  if (n_tiles > 0)
+    load_tile<T, D>(kc, vc, ind, 0, kv_len, page_size, num_pages, page_stride, token_stride, head_off, kr, vr);
+
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    // ---- registers -> LDS, then start the next tile's loads
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int c = threadIdx.x + j * kThreads;
+      const int tok = c / CH, ch = c % CH;
+      *reinterpret_cast<u32x4*>(&s_k[tok * KP + ch * 8]) = kr[j];
+      u32x2* vd = reinterpret_cast<u32x2*>(&s_v[tok * VPW + ch * 4]);
+      vd[0] = u32x2{vr[j].x, vr[j].y};
+      vd[1] = u32x2{vr[j].z, vr[j].w};
+    }
+    __syncthreads();
+    if (tile + 1 < n_tiles)
+      load_tile<T, D>(kc, vc, ind, tile + 1, kv_len, page_size, num_pages, page_stride, token_stride, head_off, kr,
+                      vr);
+
+    // ---- S = Q K^T for two 16-token blocks: lane holds rows 4*grp+i, token blk*16+lr
+    f32x4 s[2];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      s[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const u32x4 kb = *reinterpret_cast<const u32x4*>(&s_k[(blk * 16 + lr) * KP + ks * 32 + grp * 8]);
+        s[blk] = mfma32<T>(qa[ks], kb, s[blk]);
+      }
+    }
+    // ---- mask and online softmax; a row's 16 tokens of a block sit in one 16-lane DPP row
+    float alpha[4];
+    const int p0 = tile * kTile + lr, p1 = p0 + 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v0 = p0 <= c_limit[i] ? s[0][i] * scale_log2 : -INFINITY;
+      const float v1 = p1 <= c_limit[i] ? s[1][i] * scale_log2 : -INFINITY;
+      const float m_new = fmaxf(m[i], row16_max(fmaxf(v0, v1)));
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      alpha[i] = fast_exp2(m[i] - m_use);
+      const float e0 = fast_exp2(v0 - m_use), e1 = fast_exp2(v1 - m_use);
+      l[i] = l[i] * alpha[i] + row16_sum(e0 + e1);
+      m[i] = m_new;
+      s[0][i] = e0;
+      s[1][i] = e1;
+    }
+    // ---- P: accumulator layout -> LDS -> operand layout (row lr, tokens 8*grp .. +8)
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const T hi = from_float<T>(s[blk][i]);
+        s_p[wave][0][(grp * 4 + i) * PP + blk * 16 + lr] = __builtin_bit_cast(uint16_t, hi);
+        if constexpr (NPP == 2)
+          s_p[wave][NPP - 1][(grp * 4 + i) * PP + blk * 16 + lr] =
+              __builtin_bit_cast(uint16_t, from_float<T>(s[blk][i] - to_float<T>(hi)));
+      }
+    wave_lds_fence();
+    u32x4 pa[NPP];
+#pragma unroll
+    for (int pl = 0; pl < NPP; ++pl) pa[pl] = *reinterpret_cast<const u32x4*>(&s_p[wave][pl][lr * PP + grp * 8]);
+
+    // ---- O = O * alpha + P V; lane column lr of tile pair a covers d = 32a + 2lr (+1)
+#pragma unroll
+    for (int nt = 0; nt < 2 * NP; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[nt][i] *= alpha[i];
+#pragma unroll
+    for (int a = 0; a < NP; ++a) {
+      uint32_t w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = s_v[(grp * 8 + j) * VPW + 16 * a + lr];
+      u32x4 b_lo, b_hi;
+      b_lo.x = __builtin_amdgcn_perm(w[1], w[0], 0x05040100u);
+      b_hi.x = __builtin_amdgcn_perm(w[1], w[0], 0x07060302u);
+      b_lo.y = __builtin_amdgcn_perm(w[3], w[2], 0x05040100u);
+      b_hi.y = __builtin_amdgcn_perm(w[3], w[2], 0x07060302u);
+      b_lo.z = __builtin_amdgcn_perm(w[5], w[4], 0x05040100u);
+      b_hi.z = __builtin_amdgcn_perm(w[5], w[4], 0x07060302u);
+      b_lo.w = __builtin_amdgcn_perm(w[7], w[6], 0x05040100u);
+      b_hi.w = __builtin_amdgcn_perm(w[7], w[6], 0x07060302u);
+#pragma unroll
+      for (int pl = 0; pl < NPP; ++pl) {
+        acc[2 * a] = mfma32<T>(pa[pl], b_lo, acc[2 * a]);
+        acc[2 * a + 1] = mfma32<T>(pa[pl], b_hi, acc[2 * a + 1]);
+      }
+    }
+    __syncthreads();  // the next tile overwrites s_k / s_v
+  }
+
+  // ---- write: row 4*grp+i, d = 32a + 2lr and +1 as one 32-bit store
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int crow = row0 + wave * 16 + grp * 4 + i;
+    if (crow >= n_rows) continue;
+    const int pos = crow / g, hg = crow - pos * g;
+    const float inv = l[i] > 0.f ? 1.f / l[i] : 0.f;
+    T* op = o + (int64_t)(qo_begin + pos) * o_st + (int64_t)(h * g + hg) * o_sh;
+#pragma unroll
+    for (int a = 0; a < NP; ++a)
+      *reinterpret_cast<uint32_t*>(op + 32 * a + 2 * lr) = pack2<T>(acc[2 * a][i] * inv, acc[2 * a + 1][i] * inv);
+  }
+}
+
+template <typename T, int D>
+int launch(dim3 grid, hipStream_t s, const void* q, int64_t q_st, int64_t q_sh, const void* kc, const void* vc,
+           int64_t ps_, int64_t ts, int64_t hs, int64_t np, const int32_t* qo, const int32_t* kvi,
+           const int32_t* ind, const int32_t* last, const int2* items, int n_items, void* o, int64_t o_st,
+           int64_t o_sh, int batch, int hq, int hkv, int page_size, int causal, float sl2) {
+  hipLaunchKernelGGL((prefill_kernel<T, D>), grid, dim3(kThreads), 0, s, (const T*)q, q_st, q_sh, (const T*)kc,
+                     (const T*)vc, ps_, ts, hs, np, qo, kvi, ind, last, items, n_items, (T*)o, o_st, o_sh, batch,
+                     hq, hkv, page_size, causal, sl2);
+  PL_LAUNCH_CHECK("prefill_kernel");
+  return ok();
+}
+
+}  // namespace prefill
+}  // namespace pl
+
+using namespace pl;
+using namespace pl::prefill;
+
+extern "C" int pl_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
+                               const int32_t* kv_last_page_len, int batch, int num_qo_heads, int num_kv_heads,
+                               int page_size, int causal, int32_t* items, int max_items, int* num_items) {
+  if (!num_items) return fail(PL_ERR_INVALID, "num_items must not be null");
+  *num_items = 0;
+  if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0");
+  if (batch > 0 && (!qo_indptr || !kv_indptr || !kv_last_page_len))
+    return fail(PL_ERR_INVALID, "null table pointer");
+  if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads)
+    return fail(PL_ERR_INVALID, "num_qo_heads (%d) must be a multiple of num_kv_heads (%d)", num_qo_heads,
+                num_kv_heads);
+  if (page_size <= 0) return fail(PL_ERR_INVALID, "page_size must be > 0");
+  const int g = num_qo_heads / num_kv_heads;
+  if (batch > 0 && (qo_indptr[0] != 0 || kv_indptr[0] != 0))
+    return fail(PL_ERR_INVALID, "qo_indptr[0] and kv_indptr[0] must be 0");
+  struct Entry {
+    int64_t work;
+    int32_t r, row0;
+  };
+  std::vector<Entry> list;
+  for (int r = 0; r < batch; ++r) {
+    const int qo_len = qo_indptr[r + 1] - qo_indptr[r];
+    const int pages = kv_indptr[r + 1] - kv_indptr[r];
+    if (qo_len < 0) return fail(PL_ERR_INVALID, "qo_indptr must be non-decreasing (row %d)", r);
+    if (pages < 0) return fail(PL_ERR_INVALID, "kv_indptr must be non-decreasing (row %d)", r);
+    const int last = kv_last_page_len[r];
+    if (pages > 0 && (last < 1 || last > page_size))
+      return fail(PL_ERR_INVALID, "last_page_len[%d] = %d outside [1, %d]", r, last, page_size);
+    const int64_t kv_len = pages > 0 ? (int64_t)(pages - 1) * page_size + last : 0;
+    if (kv_len > INT32_MAX / 2) return fail(PL_ERR_INVALID, "row %d: kv_len %lld too large", r, (long long)kv_len);
+    if (causal && qo_len > kv_len)
+      return fail(PL_ERR_INVALID, "row %d: qo_len %d exceeds kv_len %lld under the causal mask", r, qo_len,
+                  (long long)kv_len);
+    if (qo_len > 0 && kv_len == 0) return fail(PL_ERR_INVALID, "row %d has queries but no kv", r);
+    const int64_t rows = (int64_t)qo_len * g;
+    if (rows > INT32_MAX / 2) return fail(PL_ERR_INVALID, "row %d: %lld query rows too many", r, (long long)rows);
+    for (int64_t r0 = 0; r0 < rows; r0 += kRows) {
+      const int64_t last_row = std::min<int64_t>(r0 + kRows, rows) - 1;
+      const int64_t max_pos = causal ? kv_len - qo_len + last_row / g : kv_len - 1;
+      list.push_back(Entry{max_pos / kTile + 1, r, (int32_t)r0});
+    }
+  }
+  if (list.size() > (size_t)INT32_MAX / 2) return fail(PL_ERR_INVALID, "too many prefill work items");
+  // longest first, so the causal tail of a long prompt does not finish last
+  std::stable_sort(list.begin(), list.end(), [](const Entry& a, const Entry& b) { return a.work > b.work; });
+  *num_items = (int)list.size();
+  if (items == nullptr) return ok();
+  if ((int)list.size() > max_items)
+    return fail(PL_ERR_WORKSPACE, "%zu prefill work items exceed the %d provided", list.size(), max_items);
+  for (size_t i = 0; i < list.size(); ++i) {
+    items[2 * i] = list[i].r;
+    items[2 * i + 1] = list[i].row0;
+  }
+  return ok();
+}
+
+extern "C" int pl_prefill_run(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                              const void* v_cache, int64_t page_stride, int64_t token_stride, int64_t head_stride,
+                              int64_t num_pages, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                              const int32_t* kv_indices, const int32_t* kv_last_page_len, const int32_t* items,
+                              int num_items, void* o, int64_t o_stride_t, int64_t o_stride_h, int batch,
+                              int num_qo_heads, int num_kv_heads, int head_dim, int page_size, int causal,
+                              float sm_scale, int dtype, void* stream) {
+  if (num_items < 0 || batch < 0) return fail(PL_ERR_INVALID, "num_items and batch must be >= 0");
+  if (num_items == 0 || batch == 0) return ok();
+  if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads)
+    return fail(PL_ERR_INVALID, "num_qo_heads (%d) must be a multiple of num_kv_heads (%d)", num_qo_heads,
+                num_kv_heads);
+  if (page_size <= 0 || num_pages <= 0) return fail(PL_ERR_INVALID, "page_size and num_pages must be > 0");
+  if (!q || !k_cache || !v_cache || !qo_indptr || !kv_indptr || !kv_indices || !kv_last_page_len || !items || !o)
+    return fail(PL_ERR_INVALID, "null pointer argument");
+  const int64_t strides[] = {q_stride_t, q_stride_h, o_stride_t, o_stride_h, page_stride, token_stride, head_stride};
+  for (int64_t st : strides)
+    if (st % 8) return fail(PL_ERR_INVALID, "strides must be multiples of 8 elements");
+  const void* ptrs[] = {q, k_cache, v_cache, o};
+  for (const void* p : ptrs)
+    if ((uintptr_t)p % 16) return fail(PL_ERR_INVALID, "q, o and the caches must be 16-byte aligned");
+  if (num_kv_heads > 65535) return fail(PL_ERR_INVALID, "num_kv_heads %d exceeds the grid limit", num_kv_heads);
+  if (dtype != PL_DTYPE_BF16 && dtype != PL_DTYPE_F16)
+    return fail(PL_ERR_UNSUPPORTED, "prefill dtype must be F16 or BF16 (got %d)", dtype);
+  const dim3 grid(num_items, num_kv_heads);
+  hipStream_t s = (hipStream_t)stream;
+  const float sl2 = sm_scale * 1.44269504088896340736f;
+  const int2* it = reinterpret_cast<const int2*>(items);
+  const bool bf = dtype == PL_DTYPE_BF16;
+#define PL_PREFILL_ARGS                                                                                            \
+  grid, s, q, q_stride_t, q_stride_h, k_cache, v_cache, page_stride, token_stride, head_stride, num_pages,         \
+      qo_indptr, kv_indptr, kv_indices, kv_last_page_len, it, num_items, o, o_stride_t, o_stride_h, batch,        \
+      num_qo_heads, num_kv_heads, page_size, causal, sl2
+  switch (head_dim) {
+    case 64: return bf ? launch<bf16_t, 64>(PL_PREFILL_ARGS) : launch<f16_t, 64>(PL_PREFILL_ARGS);
+    case 128: return bf ? launch<bf16_t, 128>(PL_PREFILL_ARGS) : launch<f16_t, 128>(PL_PREFILL_ARGS);
+    case 256: return bf ? launch<bf16_t, 256>(PL_PREFILL_ARGS) : launch<f16_t, 256>(PL_PREFILL_ARGS);
+  }
+#undef PL_PREFILL_ARGS
+  return fail(PL_ERR_UNSUPPORTED, "prefill head_dim %d not built (64, 128, 256)", head_dim);
+}

@@ -25,7 +25,6 @@ float32 math over the gathered pages, so decode starts from a real context.
 
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass
 
 import torch
@@ -213,43 +212,52 @@ def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: Page
 
 
 # ------------------------------------------------------------- prefill ---
-def _attention_f32(q, k, v, causal_offset: int) -> torch.Tensor:
-    """softmax(q k^T / sqrt(D)) v over [T,Hq,D] x [S,Hkv,D] in float32, with
-    query t allowed to see keys < causal_offset + t + 1."""
-    T, hq, d = q.shape
-    S, hkv, _ = k.shape
-    g = hq // hkv
-    qf = q.float().permute(1, 0, 2).contiguous()                                   # [Hq, T, D]
-    kf = k.float().repeat_interleave(g, dim=1).permute(1, 2, 0).contiguous()     # [Hq, D, S]
-    vf = v.float().repeat_interleave(g, dim=1).permute(1, 0, 2).contiguous()     # [Hq, S, D]
-    s = torch.matmul(qf, kf) / math.sqrt(d)
-    t_idx = torch.arange(T, device=q.device)[:, None]
-    s_idx = torch.arange(S, device=q.device)[None, :]
-    s = s.masked_fill(s_idx > (causal_offset + t_idx), float("-inf"))
-    return torch.matmul(torch.softmax(s, dim=-1), vf).permute(1, 0, 2).contiguous()
+def prefill_backend(cfg: DecoderConfig, page_size: int, device) -> PagedDecodeAttention:
+    """An attention backend for :func:`prefill` (the paged prefill kernel)."""
+    return PagedDecodeAttention(device=device, workspace_mb=1, num_qo_heads=cfg.num_qo_heads,
+                                num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=page_size)
 
 
 @torch.no_grad()
 def prefill(weights: DecoderWeights, pool: PagedKVPool, request: Request, tokens: torch.Tensor,
-            adapter: int = 0, chunk: int = 2048) -> torch.Tensor:
+            adapter: int = 0, chunk: int = 8192, backend: PagedDecodeAttention | None = None) -> torch.Tensor:
     """Run ``tokens`` (appended after ``request.length``) through the model,
     writing their K/V into the request's pages; returns the last hidden row's
-    logits.  Pages for the tokens must already be reserved."""
+    logits.  Pages for the tokens must already be reserved.
+
+    The reference's segment prefill (generation.py:250-275, layer_runner.py:40-102):
+    per chunk, one paged prefill plan (qo = the chunk, kv = prefix + chunk,
+    causal) shared by all layers; per layer q/k-norm + RoPE + KV append into
+    the pages, then causal paged attention over them.
+    """
     cfg = weights.cfg
     ps = pool.page_size
     start = request.length - tokens.numel()
     assert start >= 0, "reserve pages for the prompt before prefill"
-    pages = torch.tensor(request.pages(), dtype=torch.int64, device=tokens.device)
+    host_pages = request.pages()
+    pages = torch.tensor(host_pages, dtype=torch.int64, device=tokens.device)
+    if backend is None:
+        backend = prefill_backend(cfg, ps, tokens.device)
     s = weights.lora_scale
     last_logits = None
     for c0 in range(0, tokens.numel(), chunk):
         tok = tokens[c0:c0 + chunk]
         T = tok.numel()
-        pos = torch.arange(start + c0, start + c0 + T, device=tokens.device)
+        ctx_len = start + c0 + T
+        n_pages = -(-ctx_len // ps)
+        backend.plan_prefill(
+            qo_indptr=torch.tensor([0, T], dtype=torch.int32),
+            paged_kv_indptr=torch.tensor([0, n_pages], dtype=torch.int32),
+            paged_kv_indices=torch.tensor(host_pages[:n_pages], dtype=torch.int32),
+            paged_kv_last_page_len=torch.tensor([ctx_len - ps * (n_pages - 1)], dtype=torch.int32),
+            causal=True,
+        )
+        pos = torch.arange(start + c0, ctx_len, device=tokens.device)
         page_of = pages[pos // ps]
         off_of = pos % ps
         hidden = F.embedding(tok, weights.embed)
         ids = torch.full((T,), adapter, dtype=torch.int32, device=tokens.device)
+        attn = torch.empty((T, cfg.num_qo_heads, cfg.head_dim), dtype=hidden.dtype, device=tokens.device)
         pending = None
         for li, lw in enumerate(weights.layers):
             cache = pool.layer_cache(li)
@@ -262,12 +270,8 @@ def prefill(weights: DecoderWeights, pool: PagedKVPool, request: Request, tokens
                 qkv, lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None, pos, page_of,
                 off_of, cache, num_qo_heads=cfg.num_qo_heads, num_kv_heads=cfg.num_kv_heads,
                 head_dim=cfg.head_dim, page_size=ps, rope_theta=cfg.rope_theta, eps=cfg.rms_eps)
-            ctx_len = start + c0 + T
-            all_pos = torch.arange(ctx_len, device=tokens.device)
-            kk = cache[pages[all_pos // ps], 0, all_pos % ps]
-            vv = cache[pages[all_pos // ps], 1, all_pos % ps]
-            attn = _attention_f32(q, kk, vv, start + c0).to(hidden.dtype).reshape(T, cfg.q_dim)
-            o = _o_projection(lw, attn, ids, s)
+            backend.run_prefill_into(q, cache, attn)
+            o = _o_projection(lw, attn.view(T, cfg.q_dim), ids, s)
             x2 = fused_ops.add_rmsnorm(hidden, o, lw.post_norm, cfg.rms_eps)
             pending = _mlp(cfg, lw, x2, ids, s)
         x = fused_ops.add_rmsnorm(hidden, pending, weights.final_norm, cfg.rms_eps)

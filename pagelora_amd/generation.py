@@ -25,7 +25,7 @@ import torch
 
 from .attention_backend import PagedDecodeAttention
 from .decode_graph import BatchDecodeGraphRunner
-from .decoder import DecodeContext, DecoderWeights, decode_step_static, prefill
+from .decoder import DecodeContext, DecoderWeights, decode_step_static, prefill, prefill_backend
 from .kv_pool import PagedKVPool, Request
 
 
@@ -181,19 +181,20 @@ def prefill_requests(weights: DecoderWeights, pool: PagedKVPool, prompts: list[t
     dev = pool.cache.device
     ps = pool.page_size
     adapters = adapters or [0] * len(prompts)
+    backend = prefill_backend(weights.cfg, ps, dev)
     prefix_pages, prefix_len = [], 0
     if shared_prefix is not None and shared_prefix.numel():
         if shared_prefix.numel() % ps:
             raise ValueError("a shared prefix must fill whole pages")
         owner = Request()
         pool.reserve(owner, shared_prefix.numel())
-        prefill(weights, pool, owner, shared_prefix.to(dev), adapter=adapters[0])
+        prefill(weights, pool, owner, shared_prefix.to(dev), adapter=adapters[0], backend=backend)
         prefix_pages, prefix_len = list(owner.own_pages), owner.length
     requests, logits = [], []
     for p, a in zip(prompts, adapters):
         r = Request(prefix_pages=list(prefix_pages), prefix_len=prefix_len, length=prefix_len)
         pool.reserve(r, p.numel())
-        logits.append(prefill(weights, pool, r, p.to(dev), adapter=a))
+        logits.append(prefill(weights, pool, r, p.to(dev), adapter=a, backend=backend))
         requests.append(r)
     logits = torch.cat(logits, dim=0)
     return requests, torch.argmax(logits, dim=-1), logits

@@ -118,6 +118,21 @@ DECODE_CASES = [
     }
 ]
 
+# The same test in its own form: backend.plan_prefill(qo_indptr=[0, 2],
+# paged_kv_indptr=[0, 1], paged_kv_indices=[0], paged_kv_last_page_len=[2])
+# on a page of 2 tokens, causal (plan_prefill's default), then
+# run_prefill(q, kv) with q = -1000 for both tokens, k = 100, v = [1, 9]
+# -> [1, 5] (query 0 sees token 0 only, query 1 sees both).
+PREFILL_CASES = [
+    {
+        "source": "test/test_flashinfer_backend.py:157-177",
+        "page_size": 2, "head_dim": 1, "causal": True,
+        "qo_indptr": [0, 2], "kv_indptr": [0, 1], "kv_indices": [0], "kv_last_page_len": [2],
+        "q": [-1000.0, -1000.0], "k": [100.0, 100.0], "v": [1.0, 9.0],
+        "expected": [1.0, 5.0],
+    }
+]
+
 
 def main() -> None:
     data = {
@@ -125,6 +140,7 @@ def main() -> None:
         "page_table_rejects": PAGE_TABLE_REJECTS,
         "lora": LORA_CASES,
         "decode": DECODE_CASES,
+        "prefill": PREFILL_CASES,
     }
     OUT.write_text(json.dumps(data, indent=1, ensure_ascii=False) + "\n")
     print(f"wrote {OUT}")

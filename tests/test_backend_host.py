@@ -69,7 +69,30 @@ def test_cpu_backend_refuses_to_plan_a_valid_table():
                        paged_kv_last_page_len=torch.tensor([5], dtype=torch.int32))
 
 
-def test_prefill_is_not_part_of_this_build():
+def _i32(x):
+    return torch.tensor(x, dtype=torch.int32)
+
+
+@pytest.mark.parametrize(
+    "qo,indptr,indices,last",
+    [
+        ([0, 1], [0, 1, 2], [0, 0], [1]),  # qo_indptr / kv_indptr lengths differ from the batch
+        ([0, 1], [0, 3], [0, 0], [1]),     # kv_indptr points past indices
+        ([0, 1], [0, 1], [0], [17]),       # last_page_len > page_size
+        ([0, 1], [0, 1], [-3], [4]),       # negative page id
+    ],
+)
+def test_bad_prefill_tables_raise_before_any_device_work(qo, indptr, indices, last):
     be = _backend()
-    with pytest.raises(NotImplementedError):
-        be.plan_prefill(qo_indptr=torch.tensor([0, 1]))
+    with pytest.raises(ValueError):
+        be.plan_prefill(qo_indptr=_i32(qo), paged_kv_indptr=_i32(indptr), paged_kv_indices=_i32(indices),
+                        paged_kv_last_page_len=_i32(last))
+
+
+def test_cpu_backend_refuses_to_plan_or_run_prefill():
+    be = _backend()
+    with pytest.raises(RuntimeError):
+        be.plan_prefill(qo_indptr=_i32([0, 2]), paged_kv_indptr=_i32([0, 1]), paged_kv_indices=_i32([0]),
+                        paged_kv_last_page_len=_i32([2]))
+    with pytest.raises(RuntimeError, match="plan_prefill"):
+        be.run_prefill(torch.ones(2, 28, 128), torch.zeros(1, 2, 16, 4, 128))
