@@ -143,11 +143,12 @@ int pl_kv_append(const void* k, const void* v, int64_t k_stride_b,
 /* ------------------------------------------------------------------------ */
 
 /*
- * Host-side plan of a paged prefill: validates the HOST tables qo_indptr
- * [batch+1], kv_indptr [batch+1] and kv_last_page_len [batch] (int32) and
- * writes the work list `items` (int32 pairs (request, first row), longest
- * first) for pl_prefill_run.  *num_items receives the item count; with
- * items == NULL only the count is computed.  A request's rows are its
+ * Host-side plan of a paged prefill: validates the host tables qo_indptr_h
+ * [batch+1], kv_indptr_h [batch+1] and kv_last_page_len_h [batch] (int32)
+ * and writes the work list items_h (int32 pairs (request, first row),
+ * longest first) for pl_prefill_run, which reads it from device memory.
+ * *num_items_h receives the item count; with items_h == NULL only the count
+ * is computed.  A request's rows are its
  * qo_len * (num_qo_heads / num_kv_heads) (position, group head) pairs, 64
  * per item.  Under `causal` every request needs qo_len <= kv_len.
  * PL_ERR_WORKSPACE if more than max_items items are needed.
@@ -156,11 +157,11 @@ int pl_kv_append(const void* k, const void* v, int64_t k_stride_b,
  * (model/flashinfer/attention_backend.py:133-170), i.e.
  * flashinfer.BatchPrefillWithPagedKVCacheWrapper.plan.
  */
-int pl_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
-                    const int32_t* kv_last_page_len, int batch,
+int pl_prefill_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
+                    const int32_t* kv_last_page_len_h, int batch,
                     int num_qo_heads, int num_kv_heads, int page_size,
-                    int causal, int32_t* items, int max_items,
-                    int* num_items);
+                    int causal, int32_t* items_h, int max_items,
+                    int* num_items_h);
 
 /*
  * Multi-token paged attention over packed queries:
@@ -247,6 +248,80 @@ int pl_qk_norm_rope_append(const void* qkv, int64_t ld_qkv,
                            int num_qo_heads, int num_kv_heads, int head_dim,
                            const float* inv_freq, float eps, int dtype,
                            void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* The same ops with the LoRA up-projection of their input applied first     */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * The up-projection (expand) half of a no-merge LoRA module, applied by the
+ * kernel that consumes the module's output.  The producer GEMM ran on the
+ * base weight with the adapters' A rows stacked under it ([W; A_0; A_1 ..]),
+ * so its output row t holds, besides the base columns, the rank-space
+ * intermediate y[t, a] = x[t] . A_a^T of every adapter a (in the storage
+ * type, as the reference's F.linear(x, A) returns it) at columns
+ * y_offset + a * rank .. + rank of y (row stride ldy).  For the token's
+ * adapter a = adapter_ids[t] (0 <= a < num_adapters; other ids add nothing):
+ *   value[t, c] = round(base[t, c] + scale * sum_j y[t, a, j] * B[a][c][j])
+ * with B [num_adapters, out_features, rank] (rank % 8 == 0, <= 128).  That
+ * is LoRALinear.forward / _packed_lora_delta's module output
+ * (multilora/linear.py:226-231, model/flashinfer/packed_ops.py:314-325)
+ * without a separate expand kernel.
+ */
+typedef struct {
+  const void* y;
+  int64_t ldy;
+  int y_offset;
+  const void* B;
+  int out_features;
+  int rank;
+  float scale;
+} pl_lora_up;
+
+/*
+ * pl_add_rmsnorm with x = the o_proj / down_proj output whose module is
+ * lora_h: residual[r] += round(x[r] + delta[r]), then the norm.
+ * Replaces LoRALinear.forward's delta on project_linear's output followed
+ * by add_residual_rmsnorm (packed_ops.py:251-265, norm.py:27-57).
+ */
+int pl_add_rmsnorm_lora(void* residual, int64_t ldr, const void* x,
+                        int64_t ldx, const pl_lora_up* lora_h,
+                        const int32_t* adapter_ids, int num_adapters,
+                        const void* weight, void* out, int64_t ldo, int rows,
+                        int hidden, float eps, int dtype, void* stream);
+
+/*
+ * pl_silu_mul with the gate and up modules' deltas (lora_gate_up_h[0] for
+ * the gate columns, [1] for the up columns) added to gate_up first.
+ * Replaces project_gate_up_packed's delta + silu_and_mul
+ * (packed_ops.py:168-203, 230-239).
+ */
+int pl_silu_mul_lora(const void* gate_up, int64_t ldg,
+                     const pl_lora_up* lora_gate_up_h,
+                     const int32_t* adapter_ids, int num_adapters, void* out,
+                     int64_t ldo, int rows, int inter, int dtype,
+                     void* stream);
+
+/*
+ * pl_qk_norm_rope_append with the q, k and v modules' deltas
+ * (lora_qkv_h[0..2], columns head-major within each module) added to the
+ * packed row first.  Replaces project_qkv_packed's delta followed by the
+ * head norm, RoPE and append (packed_ops.py:105-165, projection.py:155-190).
+ */
+int pl_qk_norm_rope_append_lora(const void* qkv, int64_t ld_qkv,
+                                const pl_lora_up* lora_qkv_h,
+                                const int32_t* adapter_ids, int num_adapters,
+                                const void* q_norm_weight,
+                                const void* k_norm_weight,
+                                const int64_t* positions,
+                                const int64_t* page_id, const int64_t* offset,
+                                void* q_out, void* k_cache, void* v_cache,
+                                int64_t page_stride, int64_t token_stride,
+                                int64_t head_stride, int64_t num_pages,
+                                int page_size, int batch, int num_qo_heads,
+                                int num_kv_heads, int head_dim,
+                                const float* inv_freq, float eps, int dtype,
+                                void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* No-merge multi-adapter LoRA delta                                         */
@@ -356,6 +431,44 @@ int pl_linear(const void* x, int64_t ldx, int num_tokens, int in_features,
               const int32_t* adapter_ids, int num_adapters,
               const void* lora_workspace, size_t lora_workspace_bytes,
               int dtype, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Decode-sized linear layer on pre-shuffled weights                          */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Bytes of the shuffled copy of a [out_features, in_features] weight
+ * (rows padded to a multiple of 16); 0 when in_features is not a positive
+ * multiple of 32.
+ */
+size_t pl_weight_shuffled_bytes(int out_features, int in_features);
+
+/*
+ * Re-lays a row-major weight W [out_features, in_features] (row stride ldw,
+ * F16 or BF16) once, at load time, into 1 KiB blocks in the lane order of
+ * the MFMA B operand:
+ *   shuffled[((nb * in/32 + ks) * 64 + l) * 8 + e]
+ *     = W[nb*16 + l%16][ks*32 + (l/16)*8 + e]      (0 for rows >= out_features)
+ * so that pl_linear_shuffled reads every weight byte with fully coalesced
+ * 1 KiB wave loads.  shuffled_bytes >= pl_weight_shuffled_bytes(...).
+ * No counterpart in the reference: the weight layout of the decode GEMM.
+ */
+int pl_weight_shuffle(const void* weight, int64_t ldw, int out_features,
+                      int in_features, void* shuffled, size_t shuffled_bytes,
+                      int dtype, void* stream);
+
+/*
+ * out[t, n] = x[t] . W[n]^T (+ bias[n]) for t < num_tokens (<= 64) from the
+ * shuffled weight of pl_weight_shuffle (same out_features / in_features).
+ * x [num_tokens, in_features] with row stride ldx, out with ldo; fp32
+ * accumulation, one rounding.  Replaces the base F.linear of
+ * project_qkv_packed / project_gate_up_packed / project_linear
+ * (model/flashinfer/packed_ops.py:143, 179, 251-265) at decode batch sizes.
+ */
+int pl_linear_shuffled(const void* x, int64_t ldx, int num_tokens,
+                       int in_features, const void* shuffled,
+                       int out_features, const void* bias, void* out,
+                       int64_t ldo, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -66,6 +66,20 @@ class LinearLora(ctypes.Structure):
     ]
 
 
+class LoraUp(ctypes.Structure):
+    """Mirror of ``pl_lora_up``."""
+
+    _fields_ = [
+        ("y", ctypes.c_void_p),
+        ("ldy", ctypes.c_int64),
+        ("y_offset", ctypes.c_int),
+        ("B", ctypes.c_void_p),
+        ("out_features", ctypes.c_int),
+        ("rank", ctypes.c_int),
+        ("scale", ctypes.c_float),
+    ]
+
+
 PL_LINEAR_MAX_TOKENS = 64
 
 _vp = ctypes.c_void_p
@@ -126,6 +140,23 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ],
     ),
     "pl_rmsnorm": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _i32, _vp]),
+    "pl_add_rmsnorm_lora": (
+        _i32,
+        [_vp, _i64, _vp, _i64, ctypes.POINTER(LoraUp), _vp, _i32, _vp, _vp, _i64, _i32, _i32, _f32, _i32, _vp],
+    ),
+    "pl_silu_mul_lora": (_i32, [_vp, _i64, ctypes.POINTER(LoraUp), _vp, _i32, _vp, _i64, _i32, _i32, _i32, _vp]),
+    "pl_qk_norm_rope_append_lora": (
+        _i32,
+        [
+            _vp, _i64, ctypes.POINTER(LoraUp), _vp, _i32,  # qkv, ld, lora[3], ids, n_adapters
+            _vp, _vp,                     # q/k norm weights
+            _vp, _vp, _vp,                # positions, page_id, offset
+            _vp, _vp, _vp,                # q_out, k_cache, v_cache
+            _i64, _i64, _i64, _i64, _i32,  # page/token/head strides, num_pages, page_size
+            _i32, _i32, _i32, _i32,       # batch, hq, hkv, head_dim
+            _vp, _f32, _i32, _vp,         # inv_freq, eps, dtype, stream
+        ],
+    ),
     "pl_add_rmsnorm": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _i32, _vp]),
     "pl_silu_mul": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp]),
     "pl_qk_norm_rope_append": (
@@ -144,6 +175,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _i64, _i32, _i32, _vp, _i64, _i32, _vp, _vp, _i64, ctypes.POINTER(LinearLora), _i32, _vp, _i32,
          _vp, _sz, _i32, _vp],
     ),
+    "pl_weight_shuffled_bytes": (_sz, [_i32, _i32]),
+    "pl_weight_shuffle": (_i32, [_vp, _i64, _i32, _i32, _vp, _sz, _i32, _vp]),
+    "pl_linear_shuffled": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _vp, _vp, _i64, _i32, _vp]),
     "pl_lora_workspace_size": (_sz, [_i32, _i32, ctypes.POINTER(LoraModule), _i32]),
     "pl_lora_delta": (
         _i32,

@@ -9,6 +9,16 @@
 //                            half RoPE at the token's position, q written
 //                            out, k and v written straight into their page
 //
+// Each kernel can also apply the up-projection of the no-merge LoRA delta
+// to the columns it reads ("_lora" entry points): the producer GEMM ran on
+// [W; A] stacked, so its extra columns hold y = x . A^T (rounded to the
+// storage type, as the reference's F.linear(x, A) returns it); the kernel
+// stages the token's y in LDS and forms
+//   value[c] = round(base[c] + scale * sum_j y[j] * B[adapter][c][j])
+// before its own arithmetic -- the module output the reference's
+// LoRALinear.forward / _packed_lora_delta produce (multilora/linear.py:226-231,
+// packed_ops.py:314-325), without a separate expand kernel.
+//
 // Reference: norm.py:15-65 (FlashInfer rmsnorm / fused_add_rmsnorm, fp32
 // statistics, one rounding), packed_ops.py:230-239 (silu_and_mul),
 // projection.py:155-190, 248-260 (apply_rope_pos_ids non-interleaved, head
@@ -57,92 +67,226 @@ template <> __device__ __forceinline__ void store_row8<bf16_t>(bf16_t* p, const 
 // Round a float through the storage type T (what a store + reload would give).
 template <typename T> __device__ __forceinline__ float through(float v) { return to_float<T>(from_float<T>(v)); }
 
+// Device copy of pl_lora_up: adapter a's y columns are y_offset + a*rank ..
+struct LoraUp {
+  const void* y;
+  int64_t ldy;
+  int y_offset;
+  const void* B;  // [n_adapters, out_features, rank]
+  int out_features, rank;
+  float scale;
+};
+
+// One token's rank-space intermediate y[t, a, :], kept packed (R/8 x 16 B).
+template <int R>
+struct LoraRow {
+  uint4 v[R / 8];
+};
+
+// Loads y[t, a, :] (16-byte aligned: y, ldy and y_offset are checked on the host).
+template <typename T, int R>
+__device__ __forceinline__ void load_y(const LoraUp& m, int64_t t, int a, LoraRow<R>& y) {
+  const T* p = (const T*)m.y + t * m.ldy + m.y_offset + (int64_t)a * R;
+#pragma unroll
+  for (int v = 0; v < R / 8; ++v) y.v[v] = *reinterpret_cast<const uint4*>(p + v * 8);
+}
+
+template <typename T>
+__device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float acc) {
+  acc = dot2<T>(a.x, b.x, acc);
+  acc = dot2<T>(a.y, b.y, acc);
+  acc = dot2<T>(a.z, b.z, acc);
+  return dot2<T>(a.w, b.w, acc);
+}
+
+// d[i] = scale * y . B[a][c0 + i]^T for 8 consecutive output columns; the
+// rows' loads are issued together, 16 ranks at a time.
+template <typename T, int R>
+__device__ __forceinline__ void lora_delta8(const LoraUp& m, int a, int c0, const LoraRow<R>& y, float (&d)[8]) {
+  constexpr int KB = R >= 16 ? 2 : 1;  // 16-byte pieces of a B row per pass
+  const T* b0 = (const T*)m.B + ((int64_t)a * m.out_features + c0) * R;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) d[i] = 0.f;
+  // ranks above 16: one 16-rank pass in flight at a time (bounded registers)
+  constexpr int kPassUnroll = R <= 16 ? R / 8 : 1;
+#pragma unroll kPassUnroll
+  for (int kb = 0; kb < R / 8; kb += KB) {
+    uint4 b[8][KB];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int k = 0; k < KB; ++k) b[i][k] = *reinterpret_cast<const uint4*>(b0 + i * R + (kb + k) * 8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int k = 0; k < KB; ++k) d[i] = dot8<T>(y.v[kb + k], b[i][k], d[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) d[i] *= m.scale;
+}
+
+// scale * y . B[a][c]^T for one output column.
+template <typename T, int R>
+__device__ __forceinline__ float lora_delta1(const LoraUp& m, int a, int c, const LoraRow<R>& y) {
+  const T* b0 = (const T*)m.B + ((int64_t)a * m.out_features + c) * R;
+  uint4 b[R / 8];
+#pragma unroll
+  for (int v = 0; v < R / 8; ++v) b[v] = *reinterpret_cast<const uint4*>(b0 + v * 8);
+  float acc = 0.f;
+#pragma unroll
+  for (int v = 0; v < R / 8; ++v) acc = dot8<T>(y.v[v], b[v], acc);
+  return acc * m.scale;
+}
+
+template <int THREADS>
 __device__ __forceinline__ float block_sum(float v, float* s_red) {
   v = wave_sum(v);
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   if (lane == 0) s_red[wave] = v;
   __syncthreads();
   float t = 0.f;
-  for (int i = 0; i < kThreads / kWave; ++i) t += s_red[i];
-  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < THREADS / kWave; ++i) t += s_red[i];
   return t;
 }
 
 // One workgroup per row; each thread owns 8-element chunks (hidden % 8 == 0).
 // ADD: residual r (in/out) += x first (the sum is stored rounded, as a
 // separate bf16 add would leave it) and the norm reads the stored sum.
-template <typename T, bool ADD>
-__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(
+// R > 0 (with ADD): x is the base output of a LoRA module of rank R and gets
+// its up-projection first, rounded as the module output (the reference's
+// o_proj / down_proj output followed by `hidden + out`).
+// Every global load a thread needs is issued before the first use.
+template <typename T, bool ADD, int R, int THREADS>
+__global__ __launch_bounds__(THREADS) void rmsnorm_kernel(
     T* __restrict__ r, int64_t ldr, const T* __restrict__ x, int64_t ldx, const T* __restrict__ w,
-    T* __restrict__ out, int64_t ldo, int hidden, float eps) {
-  __shared__ float s_red[kThreads / kWave];
-  constexpr int kMaxChunks = 8;  // hidden <= 8 * 8 * 256 = 16384
+    T* __restrict__ out, int64_t ldo, int hidden, float eps, LoraUp lora, const int32_t* __restrict__ ids,
+    int n_adapters) {
+  __shared__ float s_red[THREADS / kWave];
+  constexpr int kMaxChunks = 16384 / 8 / THREADS;
   const int row = blockIdx.x;
   const int chunks = hidden / 8;
-  float v[kMaxChunks][8];
+  float v[kMaxChunks][8], xa[kMaxChunks][8], wf[kMaxChunks][8];
+  // every load that does not depend on the adapter id first
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c) {
+    const int idx = (threadIdx.x + c * THREADS) * 8;
+    if (threadIdx.x + c * THREADS < chunks) {
+      load_row8<T>(x + row * ldx + idx, xa[c]);
+      if (ADD) load_row8<T>(r + row * ldr + idx, v[c]);
+      load_row8<T>(w + idx, wf[c]);
+    }
+  }
+  if constexpr (R > 0) {
+    const int a = ids[row];
+    if (a >= 0 && a < n_adapters) {
+      LoraRow<R> y;
+      load_y<T, R>(lora, row, a, y);
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; ++c) {
+        const int idx = (threadIdx.x + c * THREADS) * 8;
+        if (threadIdx.x + c * THREADS < chunks) {
+          float d[8];
+          lora_delta8<T, R>(lora, a, idx, y, d);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) xa[c][i] = through<T>(xa[c][i] + d[i]);
+        }
+      }
+    }
+  }
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {
-    const int idx = (threadIdx.x + c * kThreads) * 8;
-    if (threadIdx.x + c * kThreads < chunks) {
+    const int idx = (threadIdx.x + c * THREADS) * 8;
+    if (threadIdx.x + c * THREADS < chunks) {
       if (ADD) {
-        float a[8];
-        load_row8<T>(r + row * ldr + idx, v[c]);
-        load_row8<T>(x + row * ldx + idx, a);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[c][i] = through<T>(v[c][i] + a[i]);
+        for (int i = 0; i < 8; ++i) v[c][i] = through<T>(v[c][i] + xa[c][i]);
         store_row8<T>(r + row * ldr + idx, v[c]);
       } else {
-        load_row8<T>(x + row * ldx + idx, v[c]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[c][i] = xa[c][i];
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss = fmaf(v[c][i], v[c][i], ss);
     }
   }
-  ss = block_sum(ss, s_red);
+  ss = block_sum<THREADS>(ss, s_red);
   const float rstd = rsqrtf(ss / (float)hidden + eps);
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {
-    const int idx = (threadIdx.x + c * kThreads) * 8;
-    if (threadIdx.x + c * kThreads < chunks) {
-      float wf[8];
-      load_row8<T>(w + idx, wf);
+    const int idx = (threadIdx.x + c * THREADS) * 8;
+    if (threadIdx.x + c * THREADS < chunks) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] * rstd * wf[i];
+      for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] * rstd * wf[c][i];
       store_row8<T>(out + row * ldo + idx, v[c]);
     }
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const T* __restrict__ gu, int64_t ldg,
-                                                            T* __restrict__ out, int64_t ldo,
-                                                            int inter) {
+// One 8-column chunk per thread.  R > 0: lg / lu are the gate and up
+// modules' up-projections (rank R), added to gate / up first.
+template <typename T, int R>
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const T* __restrict__ gu, int64_t ldg, T* __restrict__ out, int64_t ldo, int inter,
+                                LoraUp lg, LoraUp lu, const int32_t* __restrict__ ids, int n_adapters) {
   const int row = blockIdx.y;
-  const int chunk = blockIdx.x * kThreads + threadIdx.x;
+  const int chunk = blockIdx.x * blockDim.x + threadIdx.x;
   if (chunk * 8 >= inter) return;
   float g[8], u[8], o[8];
   load_row8<T>(gu + row * ldg + chunk * 8, g);
   load_row8<T>(gu + row * ldg + inter + chunk * 8, u);
+  if constexpr (R > 0) {
+    const int a = ids[row];
+    if (a >= 0 && a < n_adapters) {
+      LoraRow<R> yg, yu;
+      load_y<T, R>(lg, row, a, yg);
+      load_y<T, R>(lu, row, a, yu);
+      float dg[8], du[8];
+      lora_delta8<T, R>(lg, a, chunk * 8, yg, dg);
+      lora_delta8<T, R>(lu, a, chunk * 8, yu, du);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        g[i] = through<T>(g[i] + dg[i]);
+        u[i] = through<T>(u[i] + du[i]);
+      }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = g[i] / (1.f + expf(-g[i])) * u[i];
   store_row8<T>(out + row * ldo + chunk * 8, o);
 }
 
+// R > 0: the q, k and v modules' up-projections (rank R); their columns are
+// head-major within each module.
+struct QkvLora {
+  LoraUp m[3];
+};
+
 // Grid (token, group of 4 heads); a wave takes one head; lane l holds dims l
 // and l + D/2 (the rotate-half pair), i.e. D/128 pairs per lane.
-template <typename T, int D>
+template <typename T, int D, int R>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(
     const T* __restrict__ qkv, int64_t ld_qkv, const T* __restrict__ q_norm_w,
     const T* __restrict__ k_norm_w, const int64_t* __restrict__ positions,
     const int64_t* __restrict__ page_id, const int64_t* __restrict__ offset, T* __restrict__ q_out,
     T* __restrict__ k_cache, T* __restrict__ v_cache, int64_t page_stride, int64_t token_stride,
     int64_t head_stride, int64_t num_pages, int page_size, int hq, int hkv,
-    const float* __restrict__ inv_freq, float eps) {
+    const float* __restrict__ inv_freq, float eps, QkvLora lora, const int32_t* __restrict__ ids, int n_adapters) {
   constexpr int kPairs = D / 2;
   constexpr int kPPL = (kPairs + kWave - 1) / kWave;  // pairs per lane
+  constexpr int RR = R > 0 ? R : 8;
   const int b = blockIdx.x;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  int a = -1;
+  LoraRow<RR> y[3];
+  if constexpr (R > 0) {
+    a = ids[b];
+    if (a < 0 || a >= n_adapters) a = -1;
+    if (a >= 0) {
+#pragma unroll
+      for (int m = 0; m < 3; ++m) load_y<T, R>(lora.m[m], b, a, y[m]);
+    }
+  }
   const float pos = (float)positions[b];
   // rotation of pair i: angle = pos * inv_freq[i], the fp32 product the
   // reference forms (inv_freq is the caller's table, scaling folded in)
@@ -167,8 +311,24 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(
       const int i = lane + j * kWave;
       lo[j] = i < kPairs ? to_float<T>(src[i]) : 0.f;
       hi[j] = i < kPairs ? to_float<T>(src[i + kPairs]) : 0.f;
-      ss += lo[j] * lo[j] + hi[j] * hi[j];
     }
+    if constexpr (R > 0) {
+      if (a >= 0) {
+        const int mod = is_q ? 0 : (is_k ? 1 : 2);
+        const int mcol = (h - (is_q ? 0 : (is_k ? hq : hq + hkv))) * D;  // first column in its module
+        const LoraRow<RR>& ym = mod == 0 ? y[0] : (mod == 1 ? y[1] : y[2]);
+#pragma unroll
+        for (int j = 0; j < kPPL; ++j) {
+          const int i = lane + j * kWave;
+          if (i < kPairs) {
+            lo[j] = through<T>(lo[j] + lora_delta1<T, R>(lora.m[mod], a, mcol + i, ym));
+            hi[j] = through<T>(hi[j] + lora_delta1<T, R>(lora.m[mod], a, mcol + i + kPairs, ym));
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kPPL; ++j) ss += lo[j] * lo[j] + hi[j] * hi[j];
     T* dst;
     if (is_q) {
       dst = q_out + ((int64_t)b * hq + h) * D;
@@ -193,9 +353,9 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(
       }
 #pragma unroll
       for (int j = 0; j < kPPL; ++j) {
-        const float a = lo[j], c = hi[j];
-        lo[j] = a * cs[j] - c * sn[j];
-        hi[j] = c * cs[j] + a * sn[j];
+        const float a0 = lo[j], c = hi[j];
+        lo[j] = a0 * cs[j] - c * sn[j];
+        hi[j] = c * cs[j] + a0 * sn[j];
       }
     }
 #pragma unroll
@@ -215,19 +375,56 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(
 using namespace pl;
 using namespace pl::fused;
 
+// Host copy of a pl_lora_up into the device struct, with its checks.
+static int lora_up_from(const pl_lora_up* h, int need_out, LoraUp* d, const char* what) {
+  if (!h->y || !h->B) return fail(PL_ERR_INVALID, "%s: null y or B", what);
+  if (h->rank != 8 && h->rank != 16 && h->rank != 32 && h->rank != 64)
+    return fail(PL_ERR_UNSUPPORTED, "%s: rank %d not built (8, 16, 32, 64)", what, h->rank);
+  if (h->out_features < need_out)
+    return fail(PL_ERR_INVALID, "%s: B has %d output features, %d needed", what, h->out_features, need_out);
+  if (h->y_offset < 0 || h->ldy <= 0 || h->y_offset % 8 || h->ldy % 8 || (uintptr_t)h->y % 16)
+    return fail(PL_ERR_INVALID, "%s: y must be 16-byte aligned with ldy and y_offset multiples of 8", what);
+  if ((uintptr_t)h->B % 16) return fail(PL_ERR_INVALID, "%s: B must be 16-byte aligned", what);
+  *d = LoraUp{h->y, h->ldy, h->y_offset, h->B, h->out_features, h->rank, h->scale};
+  return ok();
+}
+
+constexpr int kNormThreads = 512;
+
+template <typename T, bool ADD, int R>
+static void launch_norm_t(void* r, int64_t ldr, const void* x, int64_t ldx, const void* w, void* out, int64_t ldo,
+                          int rows, int hidden, float eps, const LoraUp& lu, const int32_t* ids, int na,
+                          hipStream_t s) {
+  hipLaunchKernelGGL((rmsnorm_kernel<T, ADD, R, kNormThreads>), dim3(rows), dim3(kNormThreads), 0, s, (T*)r, ldr,
+                     (const T*)x, ldx, (const T*)w, (T*)out, ldo, hidden, eps, lu, ids, na);
+}
+
 template <typename T>
-static void launch_norm(bool add, void* r, int64_t ldr, const void* x, int64_t ldx, const void* w, void* out,
-                        int64_t ldo, int rows, int hidden, float eps, hipStream_t s) {
-  if (add)
-    hipLaunchKernelGGL((rmsnorm_kernel<T, true>), dim3(rows), dim3(kThreads), 0, s, (T*)r, ldr, (const T*)x, ldx,
-                       (const T*)w, (T*)out, ldo, hidden, eps);
-  else
-    hipLaunchKernelGGL((rmsnorm_kernel<T, false>), dim3(rows), dim3(kThreads), 0, s, (T*)r, ldr, (const T*)x, ldx,
-                       (const T*)w, (T*)out, ldo, hidden, eps);
+static int launch_norm(bool add, int rank, void* r, int64_t ldr, const void* x, int64_t ldx, const void* w,
+                       void* out, int64_t ldo, int rows, int hidden, float eps, const LoraUp& lu,
+                       const int32_t* ids, int na, hipStream_t s) {
+  if (rank == 0) {
+    if (add)
+      launch_norm_t<T, true, 0>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s);
+    else
+      launch_norm_t<T, false, 0>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s);
+  } else if constexpr (sizeof(T) == 2) {
+    switch (rank) {
+      case 8: launch_norm_t<T, true, 8>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s); break;
+      case 16: launch_norm_t<T, true, 16>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s); break;
+      case 32: launch_norm_t<T, true, 32>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s); break;
+      case 64: launch_norm_t<T, true, 64>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s); break;
+    }
+  } else {
+    return fail(PL_ERR_UNSUPPORTED, "LoRA prologue needs F16 or BF16");
+  }
+  PL_LAUNCH_CHECK("rmsnorm_kernel");
+  return ok();
 }
 
 static int norm_common(bool add, void* r, int64_t ldr, const void* x, int64_t ldx, const void* w, void* out,
-                       int64_t ldo, int rows, int hidden, float eps, int dtype, void* stream) {
+                       int64_t ldo, int rows, int hidden, float eps, int dtype, void* stream,
+                       const pl_lora_up* lora = nullptr, const int32_t* ids = nullptr, int n_adapters = 0) {
   if (rows < 0 || hidden <= 0 || hidden % 8 || hidden > 16384)
     return fail(PL_ERR_INVALID, "hidden must be a positive multiple of 8 up to 16384 (got %d)", hidden);
   if (rows == 0) return ok();
@@ -236,15 +433,20 @@ static int norm_common(bool add, void* r, int64_t ldr, const void* x, int64_t ld
   const void* ptrs[] = {x, w, out, add ? r : x};
   for (const void* p : ptrs)
     if ((uintptr_t)p % 16) return fail(PL_ERR_INVALID, "pointers must be 16-byte aligned");
+  LoraUp lu{};
+  int rank = 0;
+  if (lora) {
+    if (!ids || n_adapters < 1) return fail(PL_ERR_INVALID, "LoRA needs adapter ids and n_adapters >= 1");
+    if (const int st = lora_up_from(lora, hidden, &lu, "add_rmsnorm LoRA")) return st;
+    rank = lu.rank;
+  }
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case PL_DTYPE_F32: launch_norm<float>(add, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, s); break;
-    case PL_DTYPE_F16: launch_norm<f16_t>(add, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, s); break;
-    case PL_DTYPE_BF16: launch_norm<bf16_t>(add, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, s); break;
-    default: return fail(PL_ERR_UNSUPPORTED, "dtype %d", dtype);
+    case PL_DTYPE_F32: return launch_norm<float>(add, rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, n_adapters, s);
+    case PL_DTYPE_F16: return launch_norm<f16_t>(add, rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, n_adapters, s);
+    case PL_DTYPE_BF16: return launch_norm<bf16_t>(add, rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, n_adapters, s);
   }
-  PL_LAUNCH_CHECK("rmsnorm_kernel");
-  return ok();
+  return fail(PL_ERR_UNSUPPORTED, "dtype %d", dtype);
 }
 
 extern "C" int pl_rmsnorm(const void* x, int64_t ldx, const void* weight, void* out, int64_t ldo, int rows,
@@ -257,56 +459,170 @@ extern "C" int pl_add_rmsnorm(void* residual, int64_t ldr, const void* x, int64_
   return norm_common(true, residual, ldr, x, ldx, weight, out, ldo, rows, hidden, eps, dtype, stream);
 }
 
-extern "C" int pl_silu_mul(const void* gate_up, int64_t ldg, void* out, int64_t ldo, int rows, int inter,
-                           int dtype, void* stream) {
-  if (rows < 0 || inter <= 0 || inter % 8) return fail(PL_ERR_INVALID, "inter must be a positive multiple of 8");
-  if (rows == 0) return ok();
-  if (!gate_up || !out) return fail(PL_ERR_INVALID, "null pointer argument");
-  if (ldg % 8 || ldo % 8 || (uintptr_t)gate_up % 16 || (uintptr_t)out % 16)
-    return fail(PL_ERR_INVALID, "16-byte aligned rows required");
-  dim3 grid((inter / 8 + kThreads - 1) / kThreads, rows);
-  hipStream_t s = (hipStream_t)stream;
-  switch (dtype) {
-    case PL_DTYPE_F32:
-      hipLaunchKernelGGL(silu_mul_kernel<float>, grid, dim3(kThreads), 0, s, (const float*)gate_up, ldg, (float*)out, ldo, inter);
-      break;
-    case PL_DTYPE_F16:
-      hipLaunchKernelGGL(silu_mul_kernel<f16_t>, grid, dim3(kThreads), 0, s, (const f16_t*)gate_up, ldg, (f16_t*)out, ldo, inter);
-      break;
-    case PL_DTYPE_BF16:
-      hipLaunchKernelGGL(silu_mul_kernel<bf16_t>, grid, dim3(kThreads), 0, s, (const bf16_t*)gate_up, ldg, (bf16_t*)out, ldo, inter);
-      break;
-    default:
-      return fail(PL_ERR_UNSUPPORTED, "dtype %d", dtype);
+extern "C" int pl_add_rmsnorm_lora(void* residual, int64_t ldr, const void* x, int64_t ldx,
+                                   const pl_lora_up* lora_h, const int32_t* adapter_ids, int num_adapters,
+                                   const void* weight, void* out, int64_t ldo, int rows, int hidden, float eps,
+                                   int dtype, void* stream) {
+  if (!lora_h) return fail(PL_ERR_INVALID, "lora_h must not be null (use pl_add_rmsnorm)");
+  return norm_common(true, residual, ldr, x, ldx, weight, out, ldo, rows, hidden, eps, dtype, stream, lora_h,
+                     adapter_ids, num_adapters);
+}
+
+// Plain SiLU*up: 256 threads per workgroup; with the LoRA prologue every
+// thread also streams 8 B rows per module, so workgroups shrink to 64
+// threads to spread those reads over more CUs.
+template <typename T, int R>
+static void launch_silu_t(hipStream_t s, const void* gu, int64_t ldg, void* out, int64_t ldo, int rows, int inter,
+                          const LoraUp& lg, const LoraUp& lu, const int32_t* ids, int na) {
+  const int threads = R > 0 ? 64 : kThreads;
+  dim3 grid((inter / 8 + threads - 1) / threads, rows);
+  hipLaunchKernelGGL((silu_mul_kernel<T, R>), grid, dim3(threads), 0, s, (const T*)gu, ldg, (T*)out, ldo, inter, lg,
+                     lu, ids, na);
+}
+
+template <typename T>
+static int launch_silu(int rank, hipStream_t s, const void* gu, int64_t ldg, void* out, int64_t ldo, int rows,
+                       int inter, const LoraUp& lg, const LoraUp& lu, const int32_t* ids, int na) {
+  if (rank == 0) {
+    launch_silu_t<T, 0>(s, gu, ldg, out, ldo, rows, inter, lg, lu, ids, na);
+  } else if constexpr (sizeof(T) == 2) {
+    switch (rank) {
+      case 8: launch_silu_t<T, 8>(s, gu, ldg, out, ldo, rows, inter, lg, lu, ids, na); break;
+      case 16: launch_silu_t<T, 16>(s, gu, ldg, out, ldo, rows, inter, lg, lu, ids, na); break;
+      case 32: launch_silu_t<T, 32>(s, gu, ldg, out, ldo, rows, inter, lg, lu, ids, na); break;
+      case 64: launch_silu_t<T, 64>(s, gu, ldg, out, ldo, rows, inter, lg, lu, ids, na); break;
+    }
+  } else {
+    return fail(PL_ERR_UNSUPPORTED, "LoRA prologue needs F16 or BF16");
   }
   PL_LAUNCH_CHECK("silu_mul_kernel");
   return ok();
 }
 
-template <typename T, int D>
-static void launch_qkr(const void* qkv, int64_t ld, const void* qn, const void* kn, const int64_t* pos,
-                       const int64_t* pid, const int64_t* off, void* q_out, void* kc, void* vc, int64_t ps_,
-                       int64_t ts, int64_t hs, int64_t np, int page_size, int batch, int hq, int hkv,
-                       const float* invf, float eps, hipStream_t s) {
-  const int head_groups = (hq + 2 * hkv + kThreads / kWave - 1) / (kThreads / kWave);
-  hipLaunchKernelGGL((qk_norm_rope_append_kernel<T, D>), dim3(batch, head_groups), dim3(kThreads), 0, s, (const T*)qkv, ld,
-                     (const T*)qn, (const T*)kn, pos, pid, off, (T*)q_out, (T*)kc, (T*)vc, ps_, ts, hs, np,
-                     page_size, hq, hkv, invf, eps);
+static int silu_common(const void* gate_up, int64_t ldg, void* out, int64_t ldo, int rows, int inter, int dtype,
+                       void* stream, const pl_lora_up* lora, const int32_t* ids, int n_adapters) {
+  if (rows < 0 || inter <= 0 || inter % 8) return fail(PL_ERR_INVALID, "inter must be a positive multiple of 8");
+  if (rows == 0) return ok();
+  if (!gate_up || !out) return fail(PL_ERR_INVALID, "null pointer argument");
+  if (ldg % 8 || ldo % 8 || (uintptr_t)gate_up % 16 || (uintptr_t)out % 16)
+    return fail(PL_ERR_INVALID, "16-byte aligned rows required");
+  LoraUp lg{}, lu{};
+  int rank = 0;
+  if (lora) {
+    if (!ids || n_adapters < 1) return fail(PL_ERR_INVALID, "LoRA needs adapter ids and n_adapters >= 1");
+    if (const int st = lora_up_from(&lora[0], inter, &lg, "silu_mul gate LoRA")) return st;
+    if (const int st = lora_up_from(&lora[1], inter, &lu, "silu_mul up LoRA")) return st;
+    if (lg.rank != lu.rank) return fail(PL_ERR_UNSUPPORTED, "gate and up LoRA ranks differ (%d, %d)", lg.rank, lu.rank);
+    rank = lg.rank;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case PL_DTYPE_F32: return launch_silu<float>(rank, s, gate_up, ldg, out, ldo, rows, inter, lg, lu, ids, n_adapters);
+    case PL_DTYPE_F16: return launch_silu<f16_t>(rank, s, gate_up, ldg, out, ldo, rows, inter, lg, lu, ids, n_adapters);
+    case PL_DTYPE_BF16: return launch_silu<bf16_t>(rank, s, gate_up, ldg, out, ldo, rows, inter, lg, lu, ids, n_adapters);
+  }
+  return fail(PL_ERR_UNSUPPORTED, "dtype %d", dtype);
 }
 
-template <typename T>
-static int qkr_by_dim(int d, const void* qkv, int64_t ld, const void* qn, const void* kn, const int64_t* pos,
-                      const int64_t* pid, const int64_t* off, void* q_out, void* kc, void* vc, int64_t ps_,
-                      int64_t ts, int64_t hs, int64_t np, int page_size, int batch, int hq, int hkv,
-                      const float* invf, float eps, hipStream_t s) {
+extern "C" int pl_silu_mul(const void* gate_up, int64_t ldg, void* out, int64_t ldo, int rows, int inter,
+                           int dtype, void* stream) {
+  return silu_common(gate_up, ldg, out, ldo, rows, inter, dtype, stream, nullptr, nullptr, 0);
+}
+
+extern "C" int pl_silu_mul_lora(const void* gate_up, int64_t ldg, const pl_lora_up* lora_gate_up_h,
+                                const int32_t* adapter_ids, int num_adapters, void* out, int64_t ldo, int rows,
+                                int inter, int dtype, void* stream) {
+  if (!lora_gate_up_h) return fail(PL_ERR_INVALID, "lora_gate_up_h must not be null (use pl_silu_mul)");
+  return silu_common(gate_up, ldg, out, ldo, rows, inter, dtype, stream, lora_gate_up_h, adapter_ids, num_adapters);
+}
+
+struct QkrArgs {
+  const void *qkv, *qn, *kn;
+  int64_t ld;
+  const int64_t *pos, *pid, *off;
+  void *q_out, *kc, *vc;
+  int64_t ps_, ts, hs, np;
+  int page_size, batch, hq, hkv;
+  const float* invf;
+  float eps;
+  QkvLora lora;
+  const int32_t* ids;
+  int na;
+};
+
+template <typename T, int D, int R>
+static void launch_qkr(const QkrArgs& a, hipStream_t s) {
+  const int head_groups = (a.hq + 2 * a.hkv + kThreads / kWave - 1) / (kThreads / kWave);
+  hipLaunchKernelGGL((qk_norm_rope_append_kernel<T, D, R>), dim3(a.batch, head_groups), dim3(kThreads), 0, s,
+                     (const T*)a.qkv, a.ld, (const T*)a.qn, (const T*)a.kn, a.pos, a.pid, a.off, (T*)a.q_out,
+                     (T*)a.kc, (T*)a.vc, a.ps_, a.ts, a.hs, a.np, a.page_size, a.hq, a.hkv, a.invf, a.eps, a.lora,
+                     a.ids, a.na);
+}
+
+template <typename T, int R>
+static int qkr_by_dim(int d, const QkrArgs& a, hipStream_t s) {
   switch (d) {
-    case 64: launch_qkr<T, 64>(qkv, ld, qn, kn, pos, pid, off, q_out, kc, vc, ps_, ts, hs, np, page_size, batch, hq, hkv, invf, eps, s); break;
-    case 128: launch_qkr<T, 128>(qkv, ld, qn, kn, pos, pid, off, q_out, kc, vc, ps_, ts, hs, np, page_size, batch, hq, hkv, invf, eps, s); break;
-    case 256: launch_qkr<T, 256>(qkv, ld, qn, kn, pos, pid, off, q_out, kc, vc, ps_, ts, hs, np, page_size, batch, hq, hkv, invf, eps, s); break;
+    case 64: launch_qkr<T, 64, R>(a, s); break;
+    case 128: launch_qkr<T, 128, R>(a, s); break;
+    case 256: launch_qkr<T, 256, R>(a, s); break;
     default: return fail(PL_ERR_UNSUPPORTED, "head_dim %d not built (64, 128, 256)", d);
   }
   PL_LAUNCH_CHECK("qk_norm_rope_append_kernel");
   return ok();
+}
+
+template <typename T>
+static int qkr_by_rank(int rank, int d, const QkrArgs& a, hipStream_t s) {
+  if (rank == 0) return qkr_by_dim<T, 0>(d, a, s);
+  if constexpr (sizeof(T) == 2) {
+    switch (rank) {
+      case 8: return qkr_by_dim<T, 8>(d, a, s);
+      case 16: return qkr_by_dim<T, 16>(d, a, s);
+      case 32: return qkr_by_dim<T, 32>(d, a, s);
+      case 64: return qkr_by_dim<T, 64>(d, a, s);
+    }
+    return fail(PL_ERR_UNSUPPORTED, "rank %d", rank);
+  } else {
+    return fail(PL_ERR_UNSUPPORTED, "LoRA prologue needs F16 or BF16");
+  }
+}
+
+static int qkr_by_dtype(int dtype, int rank, int d, const QkrArgs& a, hipStream_t s) {
+  switch (dtype) {
+    case PL_DTYPE_F32: return qkr_by_rank<float>(rank, d, a, s);
+    case PL_DTYPE_F16: return qkr_by_rank<f16_t>(rank, d, a, s);
+    case PL_DTYPE_BF16: return qkr_by_rank<bf16_t>(rank, d, a, s);
+  }
+  return fail(PL_ERR_UNSUPPORTED, "dtype %d", dtype);
+}
+
+static int qkr_common(const void* qkv, int64_t ld_qkv, const void* q_norm_weight, const void* k_norm_weight,
+                      const int64_t* positions, const int64_t* page_id, const int64_t* offset, void* q_out,
+                      void* k_cache, void* v_cache, int64_t page_stride, int64_t token_stride, int64_t head_stride,
+                      int64_t num_pages, int page_size, int batch, int num_qo_heads, int num_kv_heads, int head_dim,
+                      const float* inv_freq, float eps, int dtype, void* stream, const pl_lora_up* lora,
+                      const int32_t* ids, int n_adapters) {
+  if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0) return fail(PL_ERR_INVALID, "bad shape");
+  if (batch == 0) return ok();
+  if (!qkv || !positions || !page_id || !offset || !q_out || !k_cache || !v_cache || !inv_freq)
+    return fail(PL_ERR_INVALID, "null pointer argument");
+  if (num_pages <= 0 || page_size <= 0) return fail(PL_ERR_INVALID, "num_pages and page_size must be > 0");
+  if (ld_qkv < (int64_t)(num_qo_heads + 2 * num_kv_heads) * head_dim)
+    return fail(PL_ERR_INVALID, "ld_qkv is shorter than the q|k|v row");
+  QkrArgs a{qkv, q_norm_weight, k_norm_weight, ld_qkv, positions, page_id, offset, q_out, k_cache, v_cache,
+            page_stride, token_stride, head_stride, num_pages, page_size, batch, num_qo_heads, num_kv_heads,
+            inv_freq, eps, QkvLora{}, ids, n_adapters};
+  if (lora) {
+    if (!ids || n_adapters < 1) return fail(PL_ERR_INVALID, "LoRA needs adapter ids and n_adapters >= 1");
+    const int need[3] = {num_qo_heads * head_dim, num_kv_heads * head_dim, num_kv_heads * head_dim};
+    const char* names[3] = {"q LoRA", "k LoRA", "v LoRA"};
+    for (int m = 0; m < 3; ++m)
+      if (const int st = lora_up_from(&lora[m], need[m], &a.lora.m[m], names[m])) return st;
+    if (a.lora.m[1].rank != a.lora.m[0].rank || a.lora.m[2].rank != a.lora.m[0].rank)
+      return fail(PL_ERR_UNSUPPORTED, "q, k and v LoRA ranks differ");
+    return qkr_by_dtype(dtype, a.lora.m[0].rank, head_dim, a, (hipStream_t)stream);
+  }
+  return qkr_by_dtype(dtype, 0, head_dim, a, (hipStream_t)stream);
 }
 
 extern "C" int pl_qk_norm_rope_append(const void* qkv, int64_t ld_qkv, const void* q_norm_weight,
@@ -316,27 +632,22 @@ extern "C" int pl_qk_norm_rope_append(const void* qkv, int64_t ld_qkv, const voi
                                       int64_t head_stride, int64_t num_pages, int page_size, int batch,
                                       int num_qo_heads, int num_kv_heads, int head_dim,
                                       const float* inv_freq, float eps, int dtype, void* stream) {
-  if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0) return fail(PL_ERR_INVALID, "bad shape");
-  if (batch == 0) return ok();
-  if (!qkv || !positions || !page_id || !offset || !q_out || !k_cache || !v_cache || !inv_freq)
-    return fail(PL_ERR_INVALID, "null pointer argument");
-  if (num_pages <= 0 || page_size <= 0) return fail(PL_ERR_INVALID, "num_pages and page_size must be > 0");
-  if (ld_qkv < (int64_t)(num_qo_heads + 2 * num_kv_heads) * head_dim)
-    return fail(PL_ERR_INVALID, "ld_qkv is shorter than the q|k|v row");
-  hipStream_t s = (hipStream_t)stream;
-  switch (dtype) {
-    case PL_DTYPE_F32:
-      return qkr_by_dim<float>(head_dim, qkv, ld_qkv, q_norm_weight, k_norm_weight, positions, page_id, offset, q_out,
-                               k_cache, v_cache, page_stride, token_stride, head_stride, num_pages, page_size, batch,
-                               num_qo_heads, num_kv_heads, inv_freq, eps, s);
-    case PL_DTYPE_F16:
-      return qkr_by_dim<f16_t>(head_dim, qkv, ld_qkv, q_norm_weight, k_norm_weight, positions, page_id, offset, q_out,
-                               k_cache, v_cache, page_stride, token_stride, head_stride, num_pages, page_size, batch,
-                               num_qo_heads, num_kv_heads, inv_freq, eps, s);
-    case PL_DTYPE_BF16:
-      return qkr_by_dim<bf16_t>(head_dim, qkv, ld_qkv, q_norm_weight, k_norm_weight, positions, page_id, offset, q_out,
-                                k_cache, v_cache, page_stride, token_stride, head_stride, num_pages, page_size, batch,
-                                num_qo_heads, num_kv_heads, inv_freq, eps, s);
-  }
-  return fail(PL_ERR_UNSUPPORTED, "dtype %d", dtype);
+  return qkr_common(qkv, ld_qkv, q_norm_weight, k_norm_weight, positions, page_id, offset, q_out, k_cache, v_cache,
+                    page_stride, token_stride, head_stride, num_pages, page_size, batch, num_qo_heads, num_kv_heads,
+                    head_dim, inv_freq, eps, dtype, stream, nullptr, nullptr, 0);
+}
+
+extern "C" int pl_qk_norm_rope_append_lora(const void* qkv, int64_t ld_qkv, const pl_lora_up* lora_qkv_h,
+                                           const int32_t* adapter_ids, int num_adapters, const void* q_norm_weight,
+                                           const void* k_norm_weight, const int64_t* positions,
+                                           const int64_t* page_id, const int64_t* offset, void* q_out,
+                                           void* k_cache, void* v_cache, int64_t page_stride,
+                                           int64_t token_stride, int64_t head_stride, int64_t num_pages,
+                                           int page_size, int batch, int num_qo_heads, int num_kv_heads,
+                                           int head_dim, const float* inv_freq, float eps, int dtype,
+                                           void* stream) {
+  if (!lora_qkv_h) return fail(PL_ERR_INVALID, "lora_qkv_h must not be null (use pl_qk_norm_rope_append)");
+  return qkr_common(qkv, ld_qkv, q_norm_weight, k_norm_weight, positions, page_id, offset, q_out, k_cache, v_cache,
+                    page_stride, token_stride, head_stride, num_pages, page_size, batch, num_qo_heads, num_kv_heads,
+                    head_dim, inv_freq, eps, dtype, stream, lora_qkv_h, adapter_ids, num_adapters);
 }

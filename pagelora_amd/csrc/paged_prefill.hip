@@ -311,32 +311,32 @@ int launch(dim3 grid, hipStream_t s, const void* q, int64_t q_st, int64_t q_sh, 
 using namespace pl;
 using namespace pl::prefill;
 
-extern "C" int pl_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
-                               const int32_t* kv_last_page_len, int batch, int num_qo_heads, int num_kv_heads,
-                               int page_size, int causal, int32_t* items, int max_items, int* num_items) {
-  if (!num_items) return fail(PL_ERR_INVALID, "num_items must not be null");
-  *num_items = 0;
+extern "C" int pl_prefill_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
+                               const int32_t* kv_last_page_len_h, int batch, int num_qo_heads, int num_kv_heads,
+                               int page_size, int causal, int32_t* items_h, int max_items, int* num_items_h) {
+  if (!num_items_h) return fail(PL_ERR_INVALID, "num_items_h must not be null");
+  *num_items_h = 0;
   if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0");
-  if (batch > 0 && (!qo_indptr || !kv_indptr || !kv_last_page_len))
+  if (batch > 0 && (!qo_indptr_h || !kv_indptr_h || !kv_last_page_len_h))
     return fail(PL_ERR_INVALID, "null table pointer");
   if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads)
     return fail(PL_ERR_INVALID, "num_qo_heads (%d) must be a multiple of num_kv_heads (%d)", num_qo_heads,
                 num_kv_heads);
   if (page_size <= 0) return fail(PL_ERR_INVALID, "page_size must be > 0");
   const int g = num_qo_heads / num_kv_heads;
-  if (batch > 0 && (qo_indptr[0] != 0 || kv_indptr[0] != 0))
-    return fail(PL_ERR_INVALID, "qo_indptr[0] and kv_indptr[0] must be 0");
+  if (batch > 0 && (qo_indptr_h[0] != 0 || kv_indptr_h[0] != 0))
+    return fail(PL_ERR_INVALID, "qo_indptr_h[0] and kv_indptr_h[0] must be 0");
   struct Entry {
     int64_t work;
     int32_t r, row0;
   };
   std::vector<Entry> list;
   for (int r = 0; r < batch; ++r) {
-    const int qo_len = qo_indptr[r + 1] - qo_indptr[r];
-    const int pages = kv_indptr[r + 1] - kv_indptr[r];
-    if (qo_len < 0) return fail(PL_ERR_INVALID, "qo_indptr must be non-decreasing (row %d)", r);
-    if (pages < 0) return fail(PL_ERR_INVALID, "kv_indptr must be non-decreasing (row %d)", r);
-    const int last = kv_last_page_len[r];
+    const int qo_len = qo_indptr_h[r + 1] - qo_indptr_h[r];
+    const int pages = kv_indptr_h[r + 1] - kv_indptr_h[r];
+    if (qo_len < 0) return fail(PL_ERR_INVALID, "qo_indptr_h must be non-decreasing (row %d)", r);
+    if (pages < 0) return fail(PL_ERR_INVALID, "kv_indptr_h must be non-decreasing (row %d)", r);
+    const int last = kv_last_page_len_h[r];
     if (pages > 0 && (last < 1 || last > page_size))
       return fail(PL_ERR_INVALID, "last_page_len[%d] = %d outside [1, %d]", r, last, page_size);
     const int64_t kv_len = pages > 0 ? (int64_t)(pages - 1) * page_size + last : 0;
@@ -356,13 +356,13 @@ extern "C" int pl_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indpt
   if (list.size() > (size_t)INT32_MAX / 2) return fail(PL_ERR_INVALID, "too many prefill work items");
   // longest first, so the causal tail of a long prompt does not finish last
   std::stable_sort(list.begin(), list.end(), [](const Entry& a, const Entry& b) { return a.work > b.work; });
-  *num_items = (int)list.size();
-  if (items == nullptr) return ok();
+  *num_items_h = (int)list.size();
+  if (items_h == nullptr) return ok();
   if ((int)list.size() > max_items)
     return fail(PL_ERR_WORKSPACE, "%zu prefill work items exceed the %d provided", list.size(), max_items);
   for (size_t i = 0; i < list.size(); ++i) {
-    items[2 * i] = list[i].r;
-    items[2 * i + 1] = list[i].row0;
+    items_h[2 * i] = list[i].r;
+    items_h[2 * i + 1] = list[i].row0;
   }
   return ok();
 }

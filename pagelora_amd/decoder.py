@@ -2,27 +2,29 @@
 
 This is the caller of the kernels, shaped like the reference's graph-static
 decode layer ``run_flashinfer_decode_layer_static_append_batch``
-(model/flashinfer/layer_runner.py:340-396):
+(model/flashinfer/layer_runner.py:340-396), no-merge LoRA on all seven
+modules (packed_ops.py:105-265, multilora/linear.py:200-231):
 
-    rmsnorm -> packed q/k/v GEMM (+ no-merge LoRA delta, packed_ops.py:105-165)
-    -> per-head q/k RMSNorm (projection.py:248-260) + RoPE (projection.py:155-190)
-       + KV append into the page (layer_runner.py:399-412), one fused kernel
+    [+ previous down_proj output, its LoRA delta] add+RMSNorm
+    -> GEMM on [W_qkv; A_q; A_k; A_v]
+    -> q/k/v LoRA up-projection + per-head q/k RMSNorm (projection.py:248-260)
+       + RoPE (projection.py:155-190) + KV append (layer_runner.py:399-412)
     -> paged decode attention (attention_backend.py:120-131)
-    -> o_proj (+ LoRA, packed_ops.py:251-265 / linear.py:200-231) -> residual
-    -> rmsnorm -> packed gate/up GEMM (+ LoRA, packed_ops.py:168-203) -> SiLU*up
-    -> down_proj (+ LoRA) -> residual
+    -> GEMM on [W_o; A_o] -> o LoRA up-projection + residual add + RMSNorm
+    -> GEMM on [W_gate_up; A_gate; A_up] -> LoRA up-projections + SiLU*up
+    -> GEMM on [W_down; A_down] (its delta lands in the next layer's norm)
 
-Base GEMMs are plain library GEMMs (torch -> hipBLASLt); everything else --
-norms (each residual add fused into the next norm), q/k-norm + RoPE + KV
-append, attention, SiLU*up and the LoRA delta -- runs on the library's HIP
-kernels.  Weights are random
-(no checkpoints are available); shapes follow Qwen3-8B.
+Ten kernels per layer: the LoRA shrink rides in the base GEMM (the adapters'
+A rows stacked under W) and the expand in the kernel that consumes the
+module output, so no separate LoRA launches remain.  GEMMs are the
+decode-sized linear kernel (q/k/v, o at decode batch sizes) or the library
+GEMM (torch -> hipBLASLt); everything else runs on the library's HIP
+kernels.  Weights are random (no checkpoints are available); shapes follow
+Qwen3-8B.
 
-Prefill (``prefill``) is not on the decode path: it fills the paged KV pool
-for the prompt with the same kernels except attention, which is plain torch
-float32 math over the gathered pages, so decode starts from a real context.
+``prefill`` runs the same layer over a prompt segment with the paged
+prefill attention kernel.
 """
-
 from __future__ import annotations
 
 from dataclasses import dataclass
@@ -33,7 +35,8 @@ import torch.nn.functional as F
 from . import fused_ops
 from .attention_backend import PagedDecodeAttention
 from .kv_pool import PagedKVPool, Request
-from .lora import lora_delta_, lora_linear
+from .linear import ShuffledWeight, linear_shuffled
+from .lora import lora_linear
 
 
 @dataclass(frozen=True)
@@ -67,12 +70,20 @@ class LayerWeights:
     """One decoder layer: packed base weights plus stacked LoRA adapters.
 
     Packed q/k/v and gate/up weights are the reference's packed layout
-    (``_cached_packed_linear``, packed_ops.py:268-311).  LoRA A/B of each
-    module are stacked over adapters: A [n, r, in], B [n, out, r].
+    (``_cached_packed_linear``, packed_ops.py:268-311).  Each projection's
+    weight is stored with its modules' LoRA A rows stacked under it, for
+    every adapter (``w_*_ext`` = [W; A_m0[0..n); A_m1[0..n); ..]), the
+    row-concatenated A_cat of ``_cached_packed_lora_delta`` (packed_ops.py:
+    328-384) extended over adapters: one GEMM then yields the base output and
+    every adapter's rank-space intermediate.  ``w_*`` and the A of
+    ``lora[name] = (A [n, r, in], B [n, out, r])`` are views into those
+    buffers; ``y_offset[name]`` is the first intermediate column of a module
+    in its projection's output.
     """
 
     def __init__(self, cfg: DecoderConfig, n_adapters: int, device, dtype, gen: torch.Generator) -> None:
         h, qd, kd, i, r = cfg.hidden, cfg.q_dim, cfg.kv_dim, cfg.intermediate, cfg.lora_rank
+        n = n_adapters
 
         def w(shape, std):
             return (torch.randn(shape, device=device, dtype=torch.float32, generator=gen) * std).to(dtype)
@@ -81,18 +92,49 @@ class LayerWeights:
         self.post_norm = (1.0 + 0.1 * torch.randn(h, device=device, generator=gen)).to(dtype)
         self.q_norm = (1.0 + 0.1 * torch.randn(cfg.head_dim, device=device, generator=gen)).to(dtype)
         self.k_norm = (1.0 + 0.1 * torch.randn(cfg.head_dim, device=device, generator=gen)).to(dtype)
-        self.w_qkv = w((qd + 2 * kd, h), 0.02)
-        self.w_o = w((h, qd), 0.02)
-        self.w_gate_up = w((2 * i, h), 0.02)
-        self.w_down = w((h, i), 0.02)
         self.lora = {}
-        for name, fin, fout in (("q", h, qd), ("k", h, kd), ("v", h, kd), ("o", qd, h),
-                                ("gate", h, i), ("up", h, i), ("down", i, h)):
-            self.lora[name] = (w((n_adapters, r, fin), fin ** -0.5), w((n_adapters, fout, r), 0.01))
+        self.y_offset = {}
+
+        def projection(out_features, fin, modules):
+            ext = torch.empty((out_features + len(modules) * n * r, fin), device=device, dtype=dtype)
+            ext[:out_features] = w((out_features, fin), 0.02)
+            for j, (name, fout) in enumerate(modules):
+                row = out_features + j * n * r
+                A = ext[row:row + n * r].view(n, r, fin)
+                A.copy_(w((n, r, fin), fin ** -0.5))
+                self.lora[name] = (A, w((n, fout, r), 0.01))
+                self.y_offset[name] = row
+            return ext
+
+        self.w_qkv_ext = projection(qd + 2 * kd, h, (("q", qd), ("k", kd), ("v", kd)))
+        self.w_o_ext = projection(h, qd, (("o", h),))
+        self.w_gate_up_ext = projection(2 * i, h, (("gate", i), ("up", i)))
+        self.w_down_ext = projection(h, i, (("down", h),))
+        self.w_qkv = self.w_qkv_ext[: qd + 2 * kd]
+        self.w_o = self.w_o_ext[:h]
+        self.w_gate_up = self.w_gate_up_ext[: 2 * i]
+        self.w_down = self.w_down_ext[:h]
+        self.shuffled: dict[str, ShuffledWeight] = {}
+
+    def shuffle(self) -> None:
+        """Shuffled copies of the four [W; A] weights for the decode GEMM.
+        The row-major weights stay for prefill's library GEMM (and for the
+        reference-facing LoRA path); the copies double the layer's weight
+        memory in exchange for fully coalesced decode weight streaming."""
+        for name in ("qkv", "o", "gate_up", "down"):
+            self.shuffled[name] = ShuffledWeight(getattr(self, f"w_{name}_ext"))
+
+    def up(self, name: str, y: torch.Tensor, scale: float) -> fused_ops.LoraUp:
+        """The up-projection of module ``name`` reading its intermediate from ``y``."""
+        return fused_ops.LoraUp(y, self.y_offset[name], self.lora[name][1], scale)
 
 
 class DecoderWeights:
-    def __init__(self, cfg: DecoderConfig, *, n_adapters: int = 1, device="cuda", dtype=torch.bfloat16, seed: int = 0):
+    """Random weights of the decoder.  ``shuffle`` (default) also builds the
+    shuffled decode-GEMM copies of every projection and of the lm_head."""
+
+    def __init__(self, cfg: DecoderConfig, *, n_adapters: int = 1, device="cuda", dtype=torch.bfloat16, seed: int = 0,
+                 shuffle: bool = True):
         gen = torch.Generator(device=device).manual_seed(seed)
         self.cfg = cfg
         self.dtype = dtype
@@ -102,6 +144,11 @@ class DecoderWeights:
         self.lm_head = (torch.randn((cfg.vocab, cfg.hidden), device=device, generator=gen) * 0.02).to(dtype)
         self.layers = [LayerWeights(cfg, n_adapters, device, dtype, gen) for _ in range(cfg.num_layers)]
         self.lora_scale = cfg.lora_alpha / cfg.lora_rank  # linear.py:41, 71
+        self.lm_head_shuffled: ShuffledWeight | None = None
+        if shuffle:
+            for lw in self.layers:
+                lw.shuffle()
+            self.lm_head_shuffled = ShuffledWeight(self.lm_head)
 
 
 # ------------------------------------------------------- decode (static) ---
@@ -118,43 +165,68 @@ class DecodeContext:
         self.next_tokens = torch.zeros(batch, dtype=torch.int64, device=device)
 
 
-# Projections with narrow outputs (q/k/v, o) run on the decode-sized linear
-# kernel with the LoRA expand in its epilogue; the wide MLP projections keep
-# the library GEMM plus the separate shrink/expand kernels, which is faster
-# for them.  Longer inputs (prefill) always take the library GEMM.
-FUSED_LINEAR_MAX_TOKENS = 16
+# Decode-sized inputs (up to 16 tokens) take the GEMM on shuffled weights
+# when the layer has them, else the row-major decode-sized linear kernel for
+# the narrow projections (q/k/v, o); the wide MLP projections and longer
+# inputs (prefill) take the library GEMM (torch -> hipBLASLt).
+DECODE_GEMM_MAX_TOKENS = 16
 
 
-def _qkv_projection(cfg: DecoderConfig, lw: LayerWeights, x, ids, scale: float) -> torch.Tensor:
-    qd, kd = cfg.q_dim, cfg.kv_dim
-    (Aq, Bq), (Ak, Bk), (Av, Bv) = lw.lora["q"], lw.lora["k"], lw.lora["v"]
-    if x.shape[0] <= FUSED_LINEAR_MAX_TOKENS:
-        return lora_linear(x, lw.w_qkv, [(Aq, Bq, 0, scale), (Ak, Bk, qd, scale), (Av, Bv, qd + kd, scale)], ids)
-    qkv = F.linear(x, lw.w_qkv)
-    lora_delta_(x, [(Aq, Bq, qkv[:, :qd], scale), (Ak, Bk, qkv[:, qd:qd + kd], scale),
-                    (Av, Bv, qkv[:, qd + kd:], scale)], ids)
-    return qkv
+def _project(x: torch.Tensor, lw: LayerWeights, name: str) -> torch.Tensor:
+    """x . [W; A]^T: the base output and every adapter's LoRA intermediate."""
+    if x.shape[0] <= DECODE_GEMM_MAX_TOKENS:
+        sw = lw.shuffled.get(name)
+        if sw is not None:
+            return linear_shuffled(x, sw)
+        if name in ("qkv", "o"):
+            return lora_linear(x, getattr(lw, f"w_{name}_ext"), None, None)
+    return F.linear(x, getattr(lw, f"w_{name}_ext"))
 
 
-def _o_projection(lw: LayerWeights, attn, ids, scale: float) -> torch.Tensor:
-    Ao, Bo = lw.lora["o"]
-    if attn.shape[0] <= FUSED_LINEAR_MAX_TOKENS:
-        return lora_linear(attn, lw.w_o, [(Ao, Bo, 0, scale)], ids)
-    o = F.linear(attn, lw.w_o)
-    lora_delta_(attn, [(Ao, Bo, o, scale)], ids)
-    return o
+def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Tensor, pending, ids: torch.Tensor,
+           positions: torch.Tensor, page_id: torch.Tensor, page_offset: torch.Tensor, layer_cache: torch.Tensor,
+           page_size: int, attend):
+    """One decoder layer over T tokens (decode or prefill), no-merge LoRA on
+    all seven modules.  ``hidden`` is the residual stream, updated in place;
+    ``pending`` = (previous layer's down_proj output, its LoRA up-projection)
+    or None, folded into this layer's input add+RMSNorm.  ``attend(q)``
+    returns attention over the pages as [T, Hq, D].  Returns this layer's
+    pending pair.
+
+    Per projection, one GEMM on [W; A] yields base output + LoRA intermediate
+    and the consumer kernel applies the up-projection: the q/k/v deltas in
+    the head-norm/RoPE/append kernel, o's and down's in the next
+    add+RMSNorm, gate's and up's in SiLU*up.
+    """
+    h, qd, kd, I = cfg.hidden, cfg.q_dim, cfg.kv_dim, cfg.intermediate
+    if pending is None:
+        x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
+    else:
+        prev_out, prev_up = pending
+        x = fused_ops.add_rmsnorm(hidden, prev_out[:, :h], lw.input_norm, cfg.rms_eps, lora=prev_up,
+                                  adapter_ids=ids)
+    qkv = _project(x, lw, "qkv")
+    q = fused_ops.qk_norm_rope_append(
+        qkv[:, : qd + 2 * kd], lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None,
+        positions, page_id, page_offset, layer_cache, num_qo_heads=cfg.num_qo_heads,
+        num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=page_size,
+        rope_theta=cfg.rope_theta, eps=cfg.rms_eps,
+        lora=(lw.up("q", qkv, scale), lw.up("k", qkv, scale), lw.up("v", qkv, scale)), adapter_ids=ids)
+    attn = attend(q).view(q.shape[0], qd)
+    o = _project(attn, lw, "o")
+    x2 = fused_ops.add_rmsnorm(hidden, o[:, :h], lw.post_norm, cfg.rms_eps, lora=lw.up("o", o, scale),
+                               adapter_ids=ids)
+    gu = _project(x2, lw, "gate_up")
+    act = fused_ops.silu_mul(gu[:, : 2 * I], lora=(lw.up("gate", gu, scale), lw.up("up", gu, scale)),
+                             adapter_ids=ids)
+    d = _project(act, lw, "down")
+    return d, lw.up("down", d, scale)
 
 
-def _mlp(cfg: DecoderConfig, lw: LayerWeights, x2, ids, scale: float) -> torch.Tensor:
-    I = cfg.intermediate
-    gu = F.linear(x2, lw.w_gate_up)
-    (Ag, Bg), (Au, Bu) = lw.lora["gate"], lw.lora["up"]
-    lora_delta_(x2, [(Ag, Bg, gu[:, :I], scale), (Au, Bu, gu[:, I:], scale)], ids)
-    act = fused_ops.silu_mul(gu)
-    d = F.linear(act, lw.w_down)
-    Ad, Bd = lw.lora["down"]
-    lora_delta_(act, [(Ad, Bd, d, scale)], ids)
-    return d
+def _final_norm(weights: "DecoderWeights", hidden: torch.Tensor, pending, ids: torch.Tensor) -> torch.Tensor:
+    prev_out, prev_up = pending
+    return fused_ops.add_rmsnorm(hidden, prev_out[:, : weights.cfg.hidden], weights.final_norm, weights.cfg.rms_eps,
+                                 lora=prev_up, adapter_ids=ids)
 
 
 def decode_layer_static(
@@ -162,35 +234,22 @@ def decode_layer_static(
     lw: LayerWeights,
     lora_scale: float,
     hidden: torch.Tensor,
-    pending: torch.Tensor | None,
+    pending,
     layer_cache: torch.Tensor,
     backend: PagedDecodeAttention,
     ctx: DecodeContext,
-) -> torch.Tensor:
-    """One single-token decode layer for the whole batch; graph-capturable.
+):
+    """One single-token decode layer for the whole batch; graph-capturable
+    (the reference's run_flashinfer_decode_layer_static_append_batch,
+    layer_runner.py:340-396).  See :func:`_layer` for ``pending``."""
 
-    ``hidden`` is the residual stream, updated in place; ``pending`` is the
-    previous layer's MLP output, added to it by this layer's fused
-    add+RMSNorm.  Returns this layer's MLP output (pending for the next).
-    """
-    B = hidden.shape[0]
-    ids = ctx.adapter_ids
-    if pending is None:
-        x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
-    else:
-        x = fused_ops.add_rmsnorm(hidden, pending, lw.input_norm, cfg.rms_eps)
-    qkv = _qkv_projection(cfg, lw, x, ids, lora_scale)
-    q = fused_ops.qk_norm_rope_append(
-        qkv, lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None,
-        ctx.positions, ctx.page_id, ctx.page_offset, layer_cache, num_qo_heads=cfg.num_qo_heads,
-        num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=backend.page_size,
-        rope_theta=cfg.rope_theta, eps=cfg.rms_eps)
-    attn = torch.empty_like(q)
-    backend.run_decode_into(q, layer_cache, attn)
-    attn = attn.view(B, cfg.q_dim)
-    o = _o_projection(lw, attn, ids, lora_scale)
-    x2 = fused_ops.add_rmsnorm(hidden, o, lw.post_norm, cfg.rms_eps)
-    return _mlp(cfg, lw, x2, ids, lora_scale)
+    def attend(q):
+        out = torch.empty_like(q)
+        backend.run_decode_into(q, layer_cache, out)
+        return out
+
+    return _layer(cfg, lw, lora_scale, hidden, pending, ctx.adapter_ids, ctx.positions, ctx.page_id,
+                  ctx.page_offset, layer_cache, backend.page_size, attend)
 
 
 def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: PagedDecodeAttention,
@@ -205,8 +264,11 @@ def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: Page
     for li, lw in enumerate(weights.layers):
         pending = decode_layer_static(cfg, lw, weights.lora_scale, hidden, pending, pool.layer_cache(li),
                                       backend, ctx)
-    x = fused_ops.add_rmsnorm(hidden, pending, weights.final_norm, cfg.rms_eps)
-    logits = F.linear(x, weights.lm_head)
+    x = _final_norm(weights, hidden, pending, ctx.adapter_ids)
+    if weights.lm_head_shuffled is not None and x.shape[0] <= DECODE_GEMM_MAX_TOKENS:
+        logits = linear_shuffled(x, weights.lm_head_shuffled)
+    else:
+        logits = F.linear(x, weights.lm_head)
     ctx.next_tokens.copy_(torch.argmax(logits, dim=-1))  # greedy, sampling.py:8-15
     return logits
 
@@ -261,19 +323,11 @@ def prefill(weights: DecoderWeights, pool: PagedKVPool, request: Request, tokens
         pending = None
         for li, lw in enumerate(weights.layers):
             cache = pool.layer_cache(li)
-            if pending is None:
-                x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
-            else:
-                x = fused_ops.add_rmsnorm(hidden, pending, lw.input_norm, cfg.rms_eps)
-            qkv = _qkv_projection(cfg, lw, x, ids, s)
-            q = fused_ops.qk_norm_rope_append(
-                qkv, lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None, pos, page_of,
-                off_of, cache, num_qo_heads=cfg.num_qo_heads, num_kv_heads=cfg.num_kv_heads,
-                head_dim=cfg.head_dim, page_size=ps, rope_theta=cfg.rope_theta, eps=cfg.rms_eps)
-            backend.run_prefill_into(q, cache, attn)
-            o = _o_projection(lw, attn.view(T, cfg.q_dim), ids, s)
-            x2 = fused_ops.add_rmsnorm(hidden, o, lw.post_norm, cfg.rms_eps)
-            pending = _mlp(cfg, lw, x2, ids, s)
-        x = fused_ops.add_rmsnorm(hidden, pending, weights.final_norm, cfg.rms_eps)
+
+            def attend(q, cache=cache):
+                return backend.run_prefill_into(q, cache, attn)
+
+            pending = _layer(cfg, lw, s, hidden, pending, ids, pos, page_of, off_of, cache, ps, attend)
+        x = _final_norm(weights, hidden, pending, ids)
         last_logits = F.linear(x[-1:], weights.lm_head)
     return last_logits

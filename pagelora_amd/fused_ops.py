@@ -10,6 +10,9 @@ decode token's page append (layer_runner.py:399-412).
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+from typing import Sequence
+
 import torch
 
 from . import _lib
@@ -19,6 +22,53 @@ from .attention_backend import _cache_geometry
 def _rows2d(t: torch.Tensor, name: str) -> None:
     if t.dim() != 2 or t.stride(1) != 1:
         raise ValueError(f"{name} must be 2-D with unit column stride")
+
+
+@dataclass
+class LoraUp:
+    """The up-projection half of a no-merge LoRA module, applied by the kernel
+    that consumes the module's output (``pl_lora_up``).
+
+    ``y`` is the producer GEMM's output row block ``[T, *]`` (a GEMM on the
+    base weight with the adapters' A rows stacked under it); adapter a's
+    rank-space intermediate sits at columns ``y_offset + a*r .. + r``.  ``B``
+    is ``[n_adapters, out, r]``.  The module output is
+    ``round(base + scale * y[a] . B[a]^T)`` (multilora/linear.py:226-231).
+    """
+
+    y: torch.Tensor
+    y_offset: int
+    B: torch.Tensor
+    scale: float
+
+    def struct(self) -> "_lib.LoraUp":
+        if self.y.dim() != 2 or self.y.stride(1) != 1:
+            raise ValueError("LoraUp.y must be 2-D with unit column stride")
+        B = self.B if self.B.dim() == 3 else self.B.unsqueeze(0)
+        if not B.is_contiguous() or B.dtype != self.y.dtype:
+            raise ValueError("LoraUp.B must be contiguous [n, out, r] of y's dtype")
+        n, _, r = B.shape
+        if self.y_offset < 0 or self.y_offset + n * r > self.y.shape[1]:
+            raise ValueError("LoraUp: y columns out of range")
+        return _lib.LoraUp(self.y.data_ptr(), self.y.stride(0), int(self.y_offset), B.data_ptr(), int(B.shape[1]),
+                           int(r), float(self.scale))
+
+    @property
+    def n_adapters(self) -> int:
+        return self.B.shape[0] if self.B.dim() == 3 else 1
+
+
+def _lora_args(lora: Sequence[LoraUp], adapter_ids: torch.Tensor | None, rows: int):
+    n = lora[0].n_adapters
+    if any(m.n_adapters != n for m in lora):
+        raise ValueError("every LoRA module of a call must stack the same adapters")
+    if adapter_ids is None or adapter_ids.dtype != torch.int32 or adapter_ids.numel() != rows:
+        raise ValueError("adapter_ids must be int32 [rows]")
+    for m in lora:
+        if m.y.shape[0] != rows:
+            raise ValueError("LoraUp.y must have one row per token")
+    arr = (_lib.LoraUp * len(lora))(*[m.struct() for m in lora])
+    return arr, adapter_ids.data_ptr(), n
 
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -35,30 +85,54 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor
 
 
 def add_rmsnorm(residual: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: float,
-                out: torch.Tensor | None = None) -> torch.Tensor:
-    """In place ``residual += x``; returns ``rmsnorm(residual)``."""
+                out: torch.Tensor | None = None, *, lora: LoraUp | None = None,
+                adapter_ids: torch.Tensor | None = None) -> torch.Tensor:
+    """In place ``residual += x``; returns ``rmsnorm(residual)``.
+
+    With ``lora``, x is the base output of the module whose up-projection
+    ``lora`` describes: ``residual += round(x + delta)`` (pl_add_rmsnorm_lora).
+    """
     _rows2d(residual, "residual")
     _rows2d(x, "x")
     if x.shape != residual.shape or x.dtype != residual.dtype:
         raise ValueError("x must match residual")
     out = torch.empty_like(residual) if out is None else out
     lib = _lib.load()
+    rows, hidden = residual.shape
+    if lora is not None:
+        arr, ids, n = _lora_args([lora], adapter_ids, rows)
+        _lib.check(lib.pl_add_rmsnorm_lora(residual.data_ptr(), residual.stride(0), x.data_ptr(), x.stride(0),
+                                           arr, ids, n, weight.data_ptr(), out.data_ptr(), out.stride(0), rows,
+                                           hidden, float(eps), _lib.dtype_code(x.dtype),
+                                           _lib.stream_handle(x.device)), "pl_add_rmsnorm_lora")
+        return out
     _lib.check(lib.pl_add_rmsnorm(residual.data_ptr(), residual.stride(0), x.data_ptr(), x.stride(0),
-                                  weight.data_ptr(), out.data_ptr(), out.stride(0), residual.shape[0],
-                                  residual.shape[1], float(eps), _lib.dtype_code(x.dtype),
-                                  _lib.stream_handle(x.device)), "pl_add_rmsnorm")
+                                  weight.data_ptr(), out.data_ptr(), out.stride(0), rows, hidden, float(eps),
+                                  _lib.dtype_code(x.dtype), _lib.stream_handle(x.device)), "pl_add_rmsnorm")
     return out
 
 
-def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None, *,
+             lora: Sequence[LoraUp] | None = None, adapter_ids: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(gate) * up`` of a packed ``[T, 2*inter]`` row block; with ``lora``
+    (gate, up) the modules' LoRA deltas are added first (pl_silu_mul_lora)."""
     _rows2d(gate_up, "gate_up")
     inter = gate_up.shape[1] // 2
     if gate_up.shape[1] != 2 * inter:
         raise ValueError("gate_up must have an even number of columns")
     out = torch.empty((gate_up.shape[0], inter), dtype=gate_up.dtype, device=gate_up.device) if out is None else out
     lib = _lib.load()
+    rows = gate_up.shape[0]
+    if lora is not None:
+        if len(lora) != 2:
+            raise ValueError("lora must be (gate, up)")
+        arr, ids, n = _lora_args(lora, adapter_ids, rows)
+        _lib.check(lib.pl_silu_mul_lora(gate_up.data_ptr(), gate_up.stride(0), arr, ids, n, out.data_ptr(),
+                                        out.stride(0), rows, inter, _lib.dtype_code(gate_up.dtype),
+                                        _lib.stream_handle(gate_up.device)), "pl_silu_mul_lora")
+        return out
     _lib.check(lib.pl_silu_mul(gate_up.data_ptr(), gate_up.stride(0), out.data_ptr(), out.stride(0),
-                               gate_up.shape[0], inter, _lib.dtype_code(gate_up.dtype),
+                               rows, inter, _lib.dtype_code(gate_up.dtype),
                                _lib.stream_handle(gate_up.device)), "pl_silu_mul")
     return out
 
@@ -95,8 +169,14 @@ def qk_norm_rope_append(
     rope_scale: float = 1.0,
     eps: float = 1e-6,
     q_out: torch.Tensor | None = None,
+    lora: Sequence[LoraUp] | None = None,
+    adapter_ids: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Returns the rotated q [B, Hq, D]; writes rotated k and v into the pages."""
+    """Returns the rotated q [B, Hq, D]; writes rotated k and v into the pages.
+
+    With ``lora`` (q, k, v) the modules' LoRA deltas are added to the packed
+    row first (pl_qk_norm_rope_append_lora).
+    """
     _rows2d(qkv, "qkv")
     B = qkv.shape[0]
     kc, vc, page_stride, token_stride, head_stride, num_pages = _cache_geometry(
@@ -109,6 +189,20 @@ def qk_norm_rope_append(
     q_out = torch.empty((B, num_qo_heads, head_dim), dtype=qkv.dtype, device=qkv.device) if q_out is None else q_out
     inv_freq = rope_inv_freq(head_dim, rope_theta, rope_scale, qkv.device)
     lib = _lib.load()
+    if lora is not None:
+        if len(lora) != 3:
+            raise ValueError("lora must be (q, k, v)")
+        arr, ids, n = _lora_args(lora, adapter_ids, B)
+        _lib.check(lib.pl_qk_norm_rope_append_lora(
+            qkv.data_ptr(), qkv.stride(0), arr, ids, n,
+            q_norm_weight.data_ptr() if q_norm_weight is not None else None,
+            k_norm_weight.data_ptr() if k_norm_weight is not None else None,
+            positions.data_ptr(), page_id.data_ptr(), page_offset.data_ptr(),
+            q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(), page_stride, token_stride, head_stride,
+            num_pages, page_size, B, num_qo_heads, num_kv_heads, head_dim,
+            inv_freq.data_ptr(), float(eps), _lib.dtype_code(qkv.dtype),
+            _lib.stream_handle(qkv.device)), "pl_qk_norm_rope_append_lora")
+        return q_out
     _lib.check(lib.pl_qk_norm_rope_append(
         qkv.data_ptr(), qkv.stride(0),
         q_norm_weight.data_ptr() if q_norm_weight is not None else None,

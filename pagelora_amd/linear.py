@@ -1,0 +1,59 @@
+"""Decode-sized linear layer on pre-shuffled weights (``pl_linear_shuffled``).
+
+``ShuffledWeight`` re-lays a row-major ``[out, in]`` weight once into the
+lane order of the MFMA B operand (1 KiB blocks of 16 rows x 32 k), so the
+decode GEMM reads every weight byte with fully coalesced 1 KiB loads; it
+replaces the base ``F.linear`` of the reference's projections
+(model/flashinfer/packed_ops.py:143, 179, 251-265) at decode batch sizes.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+class ShuffledWeight:
+    """The shuffled copy of a ``[out_features, in_features]`` F16/BF16 weight."""
+
+    def __init__(self, weight: torch.Tensor) -> None:
+        if weight.dim() != 2 or weight.stride(1) != 1:
+            raise ValueError("weight must be [out, in] with unit column stride")
+        if weight.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("shuffled weights are bf16 or fp16")
+        lib = _lib.load()
+        n, k = weight.shape
+        nbytes = lib.pl_weight_shuffled_bytes(n, k)
+        if nbytes == 0:
+            raise ValueError(f"in_features must be a positive multiple of 32 (got {k})")
+        self.data = torch.empty(nbytes // weight.element_size(), dtype=weight.dtype, device=weight.device)
+        _lib.check(lib.pl_weight_shuffle(weight.data_ptr(), weight.stride(0), n, k, self.data.data_ptr(), nbytes,
+                                         _lib.dtype_code(weight.dtype), _lib.stream_handle(weight.device)),
+                   "pl_weight_shuffle")
+        self.out_features, self.in_features, self.dtype = n, k, weight.dtype
+
+    @property
+    def nbytes(self) -> int:
+        return self.data.numel() * self.data.element_size()
+
+
+def linear_shuffled(x: torch.Tensor, weight: ShuffledWeight, bias: torch.Tensor | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """``x . W^T (+ bias)`` for up to 64 tokens from a :class:`ShuffledWeight`."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] != weight.in_features or x.dtype != weight.dtype:
+        raise ValueError(f"x must be [T, {weight.in_features}] of {weight.dtype} with unit column stride")
+    T, N = x.shape[0], weight.out_features
+    if T > _lib.PL_LINEAR_MAX_TOKENS:
+        raise ValueError(f"linear_shuffled takes at most {_lib.PL_LINEAR_MAX_TOKENS} tokens")
+    out = torch.empty((T, N), dtype=x.dtype, device=x.device) if out is None else out
+    if out.shape != (T, N) or out.stride(1) != 1 or out.dtype != x.dtype:
+        raise ValueError("out must be [T, out] with unit column stride")
+    if bias is not None and (bias.numel() != N or bias.dtype != x.dtype):
+        raise ValueError("bias must be [out] of x's dtype")
+    lib = _lib.load()
+    _lib.check(lib.pl_linear_shuffled(x.data_ptr(), x.stride(0), T, weight.in_features, weight.data.data_ptr(), N,
+                                      bias.data_ptr() if bias is not None else None, out.data_ptr(), out.stride(0),
+                                      _lib.dtype_code(x.dtype), _lib.stream_handle(x.device)),
+               "pl_linear_shuffled")
+    return out

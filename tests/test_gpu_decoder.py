@@ -109,6 +109,21 @@ def _torch_reference_step(w, cache, reqs, tokens, adapters):
     return logits.float(), logits.argmax(-1)
 
 
+def _assert_same_greedy(tokens, ref_logits, logits):
+    """The greedy pick must equal the reference's wherever the reference's
+    top-1 / top-2 margin exceeds twice the largest logit difference (a near
+    tie inside the numerical error may go either way)."""
+    err = (logits - ref_logits).abs().max().item()
+    top2 = ref_logits.topk(2, dim=-1).values
+    margin = (top2[..., 0] - top2[..., 1]).reshape(-1)
+    ref_tok = ref_logits.argmax(-1).reshape(-1)
+    tokens = tokens.reshape(-1)
+    decided = margin > 2 * err
+    assert decided.any(), f"every row is a near tie (margins {margin.tolist()}, err {err:.4f})"
+    assert torch.equal(tokens[decided], ref_tok[decided]), (
+        f"tokens {tokens.tolist()} vs {ref_tok.tolist()}, margins {margin.tolist()}, err {err:.4f}")
+
+
 def test_decode_step_matches_torch_reference(gpu_device):
     w, pool, reqs, first, _ = _setup(gpu_device)
     adapters = [0, 1, 1]
@@ -122,7 +137,7 @@ def test_decode_step_matches_torch_reference(gpu_device):
     ref_logits, ref_tok = _torch_reference_step(w, ref_cache, reqs, first, adapters)
     torch.cuda.synchronize()
     assert torch.allclose(logits, ref_logits, atol=0.1, rtol=0.01), (logits - ref_logits).abs().max()
-    assert torch.equal(ctx.next_tokens, ref_tok)
+    _assert_same_greedy(ctx.next_tokens, ref_logits, logits)
     # the appended K/V slot equals the reference's index_put_ (same rounded inputs)
     for r in reqs:
         p, o = r.slot(r.length - 1, 16)
@@ -199,4 +214,4 @@ def test_prefill_matches_torch_reference(gpu_device, chunk):
     ref = _torch_reference_prefill(w, tokens, adapter=1)
     torch.cuda.synchronize()
     assert torch.allclose(got, ref, atol=0.1, rtol=0.01), f"max diff {(got - ref).abs().max().item():.4f}"
-    assert got.argmax().item() == ref.argmax().item()
+    _assert_same_greedy(got.argmax(-1), ref, got)

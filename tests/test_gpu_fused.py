@@ -92,3 +92,136 @@ def test_qk_norm_rope_append(gpu_device, dtype, head_dim):
     mask = torch.ones((pool, ps), dtype=torch.bool)
     mask[page_id, offset] = False
     assert (got[:, :, :][mask.nonzero(as_tuple=True)[0], :, mask.nonzero(as_tuple=True)[1]] == 0).all()
+
+
+# ---- the same kernels with the LoRA up-projection of their input applied first
+# The producer GEMM's output row holds the base columns followed by every
+# adapter's rank-space intermediate y; the module output is
+# round(base + scale * y[a] . B[a]^T), restated here through the LoRA oracle
+# (lora_delta with A = identity is exactly scale * y . B^T).  Token 3 carries
+# an id outside [0, n_adapters): it gets no delta.  Bound: two roundings of
+# the result (the module output's and the kernel's own).
+
+IDS = [0, 2, 1, -1, 2]
+N_ADAPTERS, RANK, SCALE = 3, 16, 2.0
+
+
+def _lora_inputs(g, rows, base_cols, modules, dtype):
+    """(full producer output [rows, base + n*r*len(modules)], {name: B}, {name: y_offset})."""
+    full = torch.randn((rows, base_cols + N_ADAPTERS * RANK * len(modules)), generator=g).to(dtype)
+    Bs, offs = {}, {}
+    for j, (name, fout) in enumerate(modules):
+        Bs[name] = (torch.randn((N_ADAPTERS, fout, RANK), generator=g) * 0.05).to(dtype)
+        offs[name] = base_cols + j * N_ADAPTERS * RANK
+    return full, Bs, offs
+
+
+def _module_out(full, base_lo, base_hi, B, y_off, dtype):
+    """Oracle of round(base + scale * y[a] . B[a]^T) for columns [base_lo, base_hi)."""
+    f = full.double().numpy()
+    base = f[:, base_lo:base_hi].copy()
+    eye = np.eye(RANK)
+    for t, a in enumerate(IDS):
+        if 0 <= a < N_ADAPTERS:
+            y = f[t:t + 1, y_off + a * RANK: y_off + (a + 1) * RANK]
+            base[t] += ol.lora_delta(y, eye, B[a].double().numpy(), SCALE)[0]
+    return _round(dtype)(base)
+
+
+def _check2(got, want, dtype, extra_abs=1e-5):
+    got = got.float().cpu().numpy() if isinstance(got, torch.Tensor) else got
+    err = np.abs(got - want)
+    bound = extra_abs + 2 * REL[dtype] * np.maximum(np.abs(want), 1e-3)
+    assert np.isfinite(got).all()
+    assert (err <= bound).all(), f"max err {err.max():.3e}, worst ratio {(err / bound).max():.2f}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hidden", [256, 4096])
+def test_add_rmsnorm_lora(gpu_device, dtype, hidden):
+    g = torch.Generator().manual_seed(100 + hidden)
+    rows = len(IDS)
+    full, Bs, offs = _lora_inputs(g, rows, hidden, [("o", hidden)], dtype)
+    r = torch.randn((rows, hidden), generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(dtype)
+    fd, rd = full.to(gpu_device), r.to(gpu_device)
+    ids = torch.tensor(IDS, dtype=torch.int32, device=gpu_device)
+    up = fused_ops.LoraUp(fd, offs["o"], Bs["o"].to(gpu_device), SCALE)
+    out = fused_ops.add_rmsnorm(rd, fd[:, :hidden], w.to(gpu_device), 1e-6, lora=up, adapter_ids=ids)
+    torch.cuda.synchronize()
+    x_eff = _module_out(full, 0, hidden, Bs["o"], offs["o"], dtype)
+    new_r, want = of.add_rmsnorm(r.double().numpy(), x_eff, w.double().numpy(), 1e-6, round_sum=_round(dtype))
+    _check2(rd, new_r, dtype)
+    _check2(out, want, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_silu_mul_lora(gpu_device, dtype):
+    inter = 1024
+    g = torch.Generator().manual_seed(7)
+    rows = len(IDS)
+    full, Bs, offs = _lora_inputs(g, rows, 2 * inter, [("gate", inter), ("up", inter)], dtype)
+    fd = full.to(gpu_device)
+    ids = torch.tensor(IDS, dtype=torch.int32, device=gpu_device)
+    ups = (fused_ops.LoraUp(fd, offs["gate"], Bs["gate"].to(gpu_device), SCALE),
+           fused_ops.LoraUp(fd, offs["up"], Bs["up"].to(gpu_device), SCALE))
+    out = fused_ops.silu_mul(fd[:, : 2 * inter], lora=ups, adapter_ids=ids)
+    torch.cuda.synchronize()
+    gate = _module_out(full, 0, inter, Bs["gate"], offs["gate"], dtype)
+    up = _module_out(full, inter, 2 * inter, Bs["up"], offs["up"], dtype)
+    _check2(out, of.silu_mul(np.concatenate([gate, up], axis=1)), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_qk_norm_rope_append_lora(gpu_device, dtype, head_dim):
+    hq, hkv, ps, pool = 8, 2, 16, 10
+    rows = len(IDS)
+    qd, kd = hq * head_dim, hkv * head_dim
+    g = torch.Generator().manual_seed(head_dim + 1)
+    full, Bs, offs = _lora_inputs(g, rows, qd + 2 * kd, [("q", qd), ("k", kd), ("v", kd)], dtype)
+    qw = (1 + 0.1 * torch.randn(head_dim, generator=g)).to(dtype)
+    kw = (1 + 0.1 * torch.randn(head_dim, generator=g)).to(dtype)
+    positions = torch.tensor([0, 17, 4095, 40000, 5])
+    page_id = torch.tensor([3, 9, 0, 5, 7])
+    offset = torch.tensor([0, 15, 7, 1, 2])
+    dev = gpu_device
+    cd = torch.zeros((pool, 2, ps, hkv, head_dim), dtype=dtype, device=dev)
+    fd = full.to(dev)
+    ids = torch.tensor(IDS, dtype=torch.int32, device=dev)
+    ups = tuple(fused_ops.LoraUp(fd, offs[m], Bs[m].to(dev), SCALE) for m in ("q", "k", "v"))
+    q = fused_ops.qk_norm_rope_append(fd[:, : qd + 2 * kd], qw.to(dev), kw.to(dev), positions.to(dev),
+                                      page_id.to(dev), offset.to(dev), cd, num_qo_heads=hq, num_kv_heads=hkv,
+                                      head_dim=head_dim, page_size=ps, rope_theta=1e6, eps=1e-6, lora=ups,
+                                      adapter_ids=ids)
+    torch.cuda.synchronize()
+    qkv_eff = np.concatenate([_module_out(full, 0, qd, Bs["q"], offs["q"], dtype),
+                              _module_out(full, qd, qd + kd, Bs["k"], offs["k"], dtype),
+                              _module_out(full, qd + kd, qd + 2 * kd, Bs["v"], offs["v"], dtype)], axis=1)
+    table = fused_ops.rope_inv_freq(head_dim, 1e6, 1.0, dev).cpu().numpy()
+    wq, wk, wv = of.qk_norm_rope_append(qkv_eff, hq, hkv, head_dim, qw.double().numpy(), kw.double().numpy(),
+                                        positions.numpy(), 1e-6, 1e6, inv_freq=table)
+    _check2(q, wq, dtype, extra_abs=2e-5)
+    got = cd.cpu()
+    for b in range(rows):
+        _check2(got[page_id[b], 0, offset[b]], wk[b], dtype, extra_abs=2e-5)
+        _check2(got[page_id[b], 1, offset[b]], wv[b], dtype)
+
+
+def test_lora_up_rejects_bad_layouts(gpu_device):
+    x = torch.zeros((2, 64 + 16), dtype=torch.bfloat16, device=gpu_device)
+    r = torch.zeros((2, 64), dtype=torch.bfloat16, device=gpu_device)
+    w = torch.ones(64, dtype=torch.bfloat16, device=gpu_device)
+    ids = torch.zeros(2, dtype=torch.int32, device=gpu_device)
+    with pytest.raises(ValueError, match="out of range"):
+        fused_ops.add_rmsnorm(r, x[:, :64], w, 1e-6,
+                              lora=fused_ops.LoraUp(x, 72, torch.zeros((1, 64, 16), dtype=torch.bfloat16,
+                                                                       device=gpu_device), 1.0), adapter_ids=ids)
+    with pytest.raises(NotImplementedError, match="rank"):
+        fused_ops.add_rmsnorm(r, x[:, :64], w, 1e-6,
+                              lora=fused_ops.LoraUp(x, 64, torch.zeros((1, 64, 12), dtype=torch.bfloat16,
+                                                                       device=gpu_device), 1.0), adapter_ids=ids)
+    with pytest.raises(ValueError, match="output features"):
+        fused_ops.add_rmsnorm(r, x[:, :64], w, 1e-6,
+                              lora=fused_ops.LoraUp(x, 64, torch.zeros((1, 32, 16), dtype=torch.bfloat16,
+                                                                       device=gpu_device), 1.0), adapter_ids=ids)

@@ -1,0 +1,90 @@
+"""Pre-shuffled decode GEMM (pl_weight_shuffle + pl_linear_shuffled) vs the oracle.
+
+The shuffle is data movement: checked bit-exactly against the documented
+index map.  The GEMM is checked against the oracle's linear term (the LoRA
+oracle at scale 0: x . W^T + bias in float64) with one rounding of the
+output (2^-8 relative for bf16, 2^-11 for fp16) plus the fp32
+accumulation's error, 2e-3 max-abs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import lora as ol
+from pagelora_amd import _lib
+from pagelora_amd.linear import ShuffledWeight, linear_shuffled
+
+pytestmark = pytest.mark.gpu
+
+REL = {torch.bfloat16: 2.0**-8, torch.float16: 2.0**-11}
+
+
+def _oracle_linear(x, w, bias):
+    zero_a = np.zeros((1, x.shape[1]))
+    zero_b = np.zeros((w.shape[0], 1))
+    return ol.lora_linear(x, w, bias, zero_a, zero_b, 0.0)
+
+
+def test_shuffle_layout_matches_the_index_map(gpu_device):
+    n, k = 37, 96  # rows padded to 48
+    w = torch.arange(n * k, dtype=torch.int32).remainder(30000).to(torch.float32).to(torch.bfloat16).reshape(n, k)
+    sw = ShuffledWeight(w.to(gpu_device))
+    got = sw.data.cpu().view(torch.int16).numpy()
+    wi = w.view(torch.int16).numpy()
+    assert got.size == 48 * k
+    ks = k // 32
+    want = np.zeros(48 * k, dtype=np.int16)
+    for nb in range(3):
+        for s in range(ks):
+            for lane in range(64):
+                row, col = nb * 16 + lane % 16, s * 32 + (lane // 16) * 8
+                base = ((nb * ks + s) * 64 + lane) * 8
+                if row < n:
+                    want[base:base + 8] = wi[row, col:col + 8]
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("tokens", [1, 4, 16, 17, 64])
+@pytest.mark.parametrize("shape", [(6192, 4096), (4112, 12288), (1000, 256), (16, 32)])
+def test_linear_shuffled_vs_oracle(gpu_device, dtype, tokens, shape):
+    n, k = shape
+    g = torch.Generator().manual_seed(n + k + tokens)
+    x = torch.randn((tokens, k), generator=g).to(dtype)
+    w = (torch.randn((n, k), generator=g) * k ** -0.5).to(dtype)
+    bias = (torch.randn(n, generator=g) * 0.1).to(dtype) if n == 1000 else None
+    sw = ShuffledWeight(w.to(gpu_device))
+    out = linear_shuffled(x.to(gpu_device), sw, bias.to(gpu_device) if bias is not None else None)
+    torch.cuda.synchronize()
+    want = _oracle_linear(x.double().numpy(), w.double().numpy(), bias.double().numpy() if bias is not None else None)
+    got = out.float().cpu().numpy()
+    err = np.abs(got - want)
+    bound = 2e-3 + REL[dtype] * np.abs(want)
+    assert (err <= bound).all(), f"max err {err.max():.3e}"
+
+
+def test_strided_x_and_out(gpu_device):
+    """x and out as column slices of wider buffers (the decoder's views)."""
+    g = torch.Generator().manual_seed(3)
+    xs = torch.randn((4, 4096 + 64), generator=g).to(torch.bfloat16)
+    w = (torch.randn((512, 4096), generator=g) * 0.02).to(torch.bfloat16)
+    sw = ShuffledWeight(w.to(gpu_device))
+    xd = xs.to(gpu_device)
+    big = torch.full((4, 512 + 32), 7.0, dtype=torch.bfloat16, device=gpu_device)
+    linear_shuffled(xd[:, :4096], sw, out=big[:, :512])
+    ref = linear_shuffled(xd[:, :4096].contiguous(), sw)
+    torch.cuda.synchronize()
+    assert torch.equal(big[:, :512], ref)
+    assert (big[:, 512:] == 7.0).all()
+
+
+def test_bad_inputs_raise(gpu_device):
+    w = torch.zeros((16, 48), dtype=torch.bfloat16, device=gpu_device)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        ShuffledWeight(w)
+    sw = ShuffledWeight(torch.zeros((16, 64), dtype=torch.bfloat16, device=gpu_device))
+    with pytest.raises(ValueError):
+        linear_shuffled(torch.zeros((4, 32), dtype=torch.bfloat16, device=gpu_device), sw)
+    with pytest.raises(ValueError, match="at most"):
+        linear_shuffled(torch.zeros((_lib.PL_LINEAR_MAX_TOKENS + 1, 64), dtype=torch.bfloat16, device=gpu_device), sw)
