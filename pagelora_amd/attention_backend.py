@@ -33,8 +33,19 @@ import torch
 
 from . import _lib
 
-_DEFAULT_TARGET_WAVES = int(os.environ.get("PAGELORA_DECODE_TARGET_WAVES", "8192"))
-_DEFAULT_MIN_CHUNK_PAGES = int(os.environ.get("PAGELORA_DECODE_MIN_CHUNK_PAGES", "2"))
+# Split-KV sizing.  The decode grid is (target_items + batch) x kv heads
+# waves whatever the lengths (so one captured graph replays as rows grow), and
+# the device plan cuts rows into chunks of max(min_chunk, total/target_items)
+# pages.  Unset, target waves scale with the batch: 256 per row, at least
+# 1024 and at most 8192 (about 32 waves per CU on MI355X's 256 CUs).
+_ENV_TARGET_WAVES = os.environ.get("PAGELORA_DECODE_TARGET_WAVES")
+_DEFAULT_MIN_CHUNK_PAGES = int(os.environ.get("PAGELORA_DECODE_MIN_CHUNK_PAGES", "4"))
+
+
+def default_target_waves(batch: int) -> int:
+    if _ENV_TARGET_WAVES:
+        return int(_ENV_TARGET_WAVES)
+    return max(1024, min(8192, 256 * batch))
 
 
 def _validate_host_table(indptr: torch.Tensor, indices: torch.Tensor, last: torch.Tensor, page_size: int) -> int:
@@ -108,7 +119,7 @@ class PagedDecodeAttention:
         # FlashInfer's tensor-core kernel for ratios outside {1,2,4,8}).
         self.decode_use_tensor_cores = False
         self.use_flashinfer_qk_norm = False
-        self.target_waves = int(target_waves or _DEFAULT_TARGET_WAVES)
+        self.target_waves = int(target_waves) if target_waves else None  # None: default_target_waves(batch)
         self.min_chunk_pages = int(min_chunk_pages or _DEFAULT_MIN_CHUNK_PAGES)
         if self.device.type == "cuda":
             self._lib = _lib.load()  # fails loudly when the extension is not built
@@ -217,7 +228,8 @@ class PagedDecodeAttention:
     def _target_items(self, batch: int) -> int:
         """Work items per step: about target_waves wavefronts, within the workspace."""
 
-        t = max(1, self.target_waves // self.num_kv_heads)
+        waves = self.target_waves if self.target_waves else default_target_waves(batch)
+        t = max(1, waves // self.num_kv_heads)
         cap = self.workspace_buffer.numel()
         while t > 1 and self._lib.pl_decode_workspace_size(batch, t, self.num_qo_heads, self.head_dim) > cap:
             t //= 2
