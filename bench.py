@@ -41,6 +41,13 @@ HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = ROOT / "profiles" / "decode_kernel_ragged64_mha_fp16.traffic.json"
 
 
+# End-to-end legs: Qwen3-8B-shaped decode with rank-16 LoRA on all 7 modules.
+E2E_LEGS = {
+    "shared": ("e2e_qwen3_8b_lora_r16_4x(2048_shared+64)", dict(prefix_len=2048, suffix_len=64, rows=4, steps=128)),
+    "long": ("e2e_qwen3_8b_lora_r16_1x32768", dict(prefix_len=0, suffix_len=32768, rows=1, steps=128)),
+}
+
+
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
@@ -52,6 +59,8 @@ def parse_args():
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Qwen3-8B-shaped decode legs")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a 1 GiB device copy (for scaling rocprofv3 FETCH/WRITE_SIZE)")
+    p.add_argument("--e2e-only", choices=sorted(E2E_LEGS),
+                   help="run only this end-to-end decode leg and print its result (for profiling)")
     return p.parse_args()
 
 
@@ -267,6 +276,10 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
+    if args.e2e_only:
+        name, kw = E2E_LEGS[args.e2e_only]
+        print(json.dumps({"leg": name, **e2e_decode(dev, **kw)}), flush=True)
+        return
     if args.copy_calibration:
         copy_calibration(dev)
 
@@ -308,10 +321,8 @@ def main():
             "algorithmic_GBps": round(lora_bytes / (lora_ms * 1e-3) / 1e9, 1),
         }
     if not args.no_extra and not args.no_e2e:
-        extra["e2e_qwen3_8b_lora_r16_4x(2048_shared+64)"] = e2e_decode(
-            dev, prefix_len=2048, suffix_len=64, rows=4, steps=128)
-        extra["e2e_qwen3_8b_lora_r16_1x32768"] = e2e_decode(
-            dev, prefix_len=0, suffix_len=32768, rows=1, steps=128)
+        for name, kw in E2E_LEGS.values():
+            extra[name] = e2e_decode(dev, **kw)
     line = {
         "metric": METRIC,
         "value": round(value, 1),
