@@ -279,13 +279,30 @@ typedef struct {
 } pl_lora_up;
 
 /*
+ * A GEMM output given as split-K partial sums (pl_linear_shuffled_split):
+ * element (t, c) is the fp32 sum over planes s = 0, 1, .. splits-1, in that
+ * order, of partials[s * plane_stride + t * ld + c], rounded to the storage
+ * type -- the value the unsplit GEMM's output would hold.  ld and
+ * plane_stride are multiples of 8; partials is 16-byte aligned.
+ */
+typedef struct {
+  const float* partials;
+  int splits;
+  int64_t ld;
+  int64_t plane_stride;
+} pl_split_out;
+
+/*
  * pl_add_rmsnorm with x = the o_proj / down_proj output whose module is
- * lora_h: residual[r] += round(x[r] + delta[r]), then the norm.
+ * lora_h: residual[r] += round(x[r] + delta[r]), then the norm.  With
+ * x_split_h (nullable) x and the module's y are read from the split-K
+ * partial planes instead (x and lora_h->y are then ignored).
  * Replaces LoRALinear.forward's delta on project_linear's output followed
  * by add_residual_rmsnorm (packed_ops.py:251-265, norm.py:27-57).
  */
 int pl_add_rmsnorm_lora(void* residual, int64_t ldr, const void* x,
-                        int64_t ldx, const pl_lora_up* lora_h,
+                        int64_t ldx, const pl_split_out* x_split_h,
+                        const pl_lora_up* lora_h,
                         const int32_t* adapter_ids, int num_adapters,
                         const void* weight, void* out, int64_t ldo, int rows,
                         int hidden, float eps, int dtype, void* stream);
@@ -305,10 +322,13 @@ int pl_silu_mul_lora(const void* gate_up, int64_t ldg,
 /*
  * pl_qk_norm_rope_append with the q, k and v modules' deltas
  * (lora_qkv_h[0..2], columns head-major within each module) added to the
- * packed row first.  Replaces project_qkv_packed's delta followed by the
- * head norm, RoPE and append (packed_ops.py:105-165, projection.py:155-190).
+ * packed row first.  With qkv_split_h (nullable) the packed rows and the
+ * modules' y come from split-K partial planes (qkv and the y pointers are
+ * then ignored).  Replaces project_qkv_packed's delta followed by the head
+ * norm, RoPE and append (packed_ops.py:105-165, projection.py:155-190).
  */
 int pl_qk_norm_rope_append_lora(const void* qkv, int64_t ld_qkv,
+                                const pl_split_out* qkv_split_h,
                                 const pl_lora_up* lora_qkv_h,
                                 const int32_t* adapter_ids, int num_adapters,
                                 const void* q_norm_weight,
@@ -469,6 +489,21 @@ int pl_linear_shuffled(const void* x, int64_t ldx, int num_tokens,
                        int in_features, const void* shuffled,
                        int out_features, const void* bias, void* out,
                        int64_t ldo, int dtype, void* stream);
+
+/*
+ * pl_linear_shuffled with K split over `splits` workgroups per 16-column
+ * block: workgroup s sums k in [s*K/splits, (s+1)*K/splits) (whole 32-wide
+ * steps) and writes fp32 plane s of partials (row t at t * ld, planes
+ * plane_stride >= num_tokens * ld apart), no bias.  The consumer sums the
+ * planes in order (pl_split_out).  More workgroups for narrow projections
+ * (o_proj, down_proj: 257 row blocks for 4096 outputs) without a
+ * cross-workgroup reduction inside the kernel.
+ */
+int pl_linear_shuffled_split(const void* x, int64_t ldx, int num_tokens,
+                             int in_features, const void* shuffled,
+                             int out_features, int splits, float* partials,
+                             int64_t ld, int64_t plane_stride, int dtype,
+                             void* stream);
 
 #ifdef __cplusplus
 }

@@ -66,6 +66,17 @@ class LinearLora(ctypes.Structure):
     ]
 
 
+class SplitOut(ctypes.Structure):
+    """Mirror of ``pl_split_out``."""
+
+    _fields_ = [
+        ("partials", ctypes.c_void_p),
+        ("splits", ctypes.c_int),
+        ("ld", ctypes.c_int64),
+        ("plane_stride", ctypes.c_int64),
+    ]
+
+
 class LoraUp(ctypes.Structure):
     """Mirror of ``pl_lora_up``."""
 
@@ -142,13 +153,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pl_rmsnorm": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _i32, _vp]),
     "pl_add_rmsnorm_lora": (
         _i32,
-        [_vp, _i64, _vp, _i64, ctypes.POINTER(LoraUp), _vp, _i32, _vp, _vp, _i64, _i32, _i32, _f32, _i32, _vp],
+        [_vp, _i64, _vp, _i64, ctypes.POINTER(SplitOut), ctypes.POINTER(LoraUp), _vp, _i32, _vp, _vp, _i64, _i32,
+         _i32, _f32, _i32, _vp],
     ),
     "pl_silu_mul_lora": (_i32, [_vp, _i64, ctypes.POINTER(LoraUp), _vp, _i32, _vp, _i64, _i32, _i32, _i32, _vp]),
     "pl_qk_norm_rope_append_lora": (
         _i32,
         [
-            _vp, _i64, ctypes.POINTER(LoraUp), _vp, _i32,  # qkv, ld, lora[3], ids, n_adapters
+            _vp, _i64, ctypes.POINTER(SplitOut),  # qkv, ld, split planes
+            ctypes.POINTER(LoraUp), _vp, _i32,  # lora[3], ids, n_adapters
             _vp, _vp,                     # q/k norm weights
             _vp, _vp, _vp,                # positions, page_id, offset
             _vp, _vp, _vp,                # q_out, k_cache, v_cache
@@ -178,6 +191,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pl_weight_shuffled_bytes": (_sz, [_i32, _i32]),
     "pl_weight_shuffle": (_i32, [_vp, _i64, _i32, _i32, _vp, _sz, _i32, _vp]),
     "pl_linear_shuffled": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _vp, _vp, _i64, _i32, _vp]),
+    "pl_linear_shuffled_split": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _i64, _i64, _i32, _vp]),
     "pl_lora_workspace_size": (_sz, [_i32, _i32, ctypes.POINTER(LoraModule), _i32]),
     "pl_lora_delta": (
         _i32,

@@ -91,6 +91,49 @@ __device__ __forceinline__ void load_y(const LoraUp& m, int64_t t, int a, LoraRo
   for (int v = 0; v < R / 8; ++v) y.v[v] = *reinterpret_cast<const uint4*>(p + v * 8);
 }
 
+// A GEMM output given as split-K partial planes: element (t, c) is the fp32
+// sum over planes s = 0, 1, .. of p[s * plane + t * ld + c], rounded through
+// the storage type (what the GEMM's own output would hold).  splits == 0:
+// not in use.
+struct SplitIn {
+  const float* p;
+  int splits;
+  int64_t ld, plane;
+};
+
+// 8 consecutive elements (c % 8 == 0; ld, plane multiples of 8, p 16-byte aligned).
+template <typename T>
+__device__ __forceinline__ void load8_split(const SplitIn& sp, int64_t t, int c, float (&f)[8]) {
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < sp.splits; ++z) {
+    const float* q = sp.p + z * sp.plane + t * sp.ld + c;
+    const float4 a = *reinterpret_cast<const float4*>(q);
+    const float4 b = *reinterpret_cast<const float4*>(q + 4);
+    acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+    acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = through<T>(acc[i]);
+}
+
+template <typename T>
+__device__ __forceinline__ float load1_split(const SplitIn& sp, int64_t t, int c) {
+  float acc = 0.f;
+  for (int z = 0; z < sp.splits; ++z) acc += sp.p[z * sp.plane + t * sp.ld + c];
+  return through<T>(acc);
+}
+
+// y[t, a, :] of module m read from the partial planes (columns y_offset + a*R ..).
+template <typename T, int R>
+__device__ __forceinline__ void load_y_split(const SplitIn& sp, const LoraUp& m, int64_t t, int a, LoraRow<R>& y) {
+#pragma unroll
+  for (int v = 0; v < R / 8; ++v) {
+    float f[8];
+    load8_split<T>(sp, t, m.y_offset + a * R + v * 8, f);
+    y.v[v] = make_uint4(pack2<T>(f[0], f[1]), pack2<T>(f[2], f[3]), pack2<T>(f[4], f[5]), pack2<T>(f[6], f[7]));
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float acc) {
   acc = dot2<T>(a.x, b.x, acc);
@@ -161,7 +204,7 @@ template <typename T, bool ADD, int R, int THREADS>
 __global__ __launch_bounds__(THREADS) void rmsnorm_kernel(
     T* __restrict__ r, int64_t ldr, const T* __restrict__ x, int64_t ldx, const T* __restrict__ w,
     T* __restrict__ out, int64_t ldo, int hidden, float eps, LoraUp lora, const int32_t* __restrict__ ids,
-    int n_adapters) {
+    int n_adapters, SplitIn xs) {
   __shared__ float s_red[THREADS / kWave];
   constexpr int kMaxChunks = 16384 / 8 / THREADS;
   const int row = blockIdx.x;
@@ -172,7 +215,10 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_kernel(
   for (int c = 0; c < kMaxChunks; ++c) {
     const int idx = (threadIdx.x + c * THREADS) * 8;
     if (threadIdx.x + c * THREADS < chunks) {
-      load_row8<T>(x + row * ldx + idx, xa[c]);
+      if (xs.splits > 0)
+        load8_split<T>(xs, row, idx, xa[c]);
+      else
+        load_row8<T>(x + row * ldx + idx, xa[c]);
       if (ADD) load_row8<T>(r + row * ldr + idx, v[c]);
       load_row8<T>(w + idx, wf[c]);
     }
@@ -181,7 +227,10 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_kernel(
     const int a = ids[row];
     if (a >= 0 && a < n_adapters) {
       LoraRow<R> y;
-      load_y<T, R>(lora, row, a, y);
+      if (xs.splits > 0)
+        load_y_split<T, R>(xs, lora, row, a, y);
+      else
+        load_y<T, R>(lora, row, a, y);
 #pragma unroll
       for (int c = 0; c < kMaxChunks; ++c) {
         const int idx = (threadIdx.x + c * THREADS) * 8;
@@ -271,7 +320,8 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(
     const int64_t* __restrict__ page_id, const int64_t* __restrict__ offset, T* __restrict__ q_out,
     T* __restrict__ k_cache, T* __restrict__ v_cache, int64_t page_stride, int64_t token_stride,
     int64_t head_stride, int64_t num_pages, int page_size, int hq, int hkv,
-    const float* __restrict__ inv_freq, float eps, QkvLora lora, const int32_t* __restrict__ ids, int n_adapters) {
+    const float* __restrict__ inv_freq, float eps, QkvLora lora, const int32_t* __restrict__ ids, int n_adapters,
+    SplitIn xs) {
   constexpr int kPairs = D / 2;
   constexpr int kPPL = (kPairs + kWave - 1) / kWave;  // pairs per lane
   constexpr int RR = R > 0 ? R : 8;
@@ -284,7 +334,12 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(
     if (a < 0 || a >= n_adapters) a = -1;
     if (a >= 0) {
 #pragma unroll
-      for (int m = 0; m < 3; ++m) load_y<T, R>(lora.m[m], b, a, y[m]);
+      for (int m = 0; m < 3; ++m) {
+        if (xs.splits > 0)
+          load_y_split<T, R>(xs, lora.m[m], b, a, y[m]);
+        else
+          load_y<T, R>(lora.m[m], b, a, y[m]);
+      }
     }
   }
   const float pos = (float)positions[b];
@@ -309,8 +364,13 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(
 #pragma unroll
     for (int j = 0; j < kPPL; ++j) {
       const int i = lane + j * kWave;
-      lo[j] = i < kPairs ? to_float<T>(src[i]) : 0.f;
-      hi[j] = i < kPairs ? to_float<T>(src[i + kPairs]) : 0.f;
+      if (xs.splits > 0) {
+        lo[j] = i < kPairs ? load1_split<T>(xs, b, h * D + i) : 0.f;
+        hi[j] = i < kPairs ? load1_split<T>(xs, b, h * D + i + kPairs) : 0.f;
+      } else {
+        lo[j] = i < kPairs ? to_float<T>(src[i]) : 0.f;
+        hi[j] = i < kPairs ? to_float<T>(src[i + kPairs]) : 0.f;
+      }
     }
     if constexpr (R > 0) {
       if (a >= 0) {
@@ -376,7 +436,22 @@ using namespace pl;
 using namespace pl::fused;
 
 // Host copy of a pl_lora_up into the device struct, with its checks.
-static int lora_up_from(const pl_lora_up* h, int need_out, LoraUp* d, const char* what) {
+// With `split`, y is read from the split-K planes (h->y may be NULL) and its
+// columns y_offset + n_adapters*rank must fit the planes' row.
+static int lora_up_from(const pl_lora_up* h, int need_out, LoraUp* d, const char* what,
+                        const SplitIn* split = nullptr, int n_adapters = 0) {
+  if (split != nullptr) {
+    if (!h->B) return fail(PL_ERR_INVALID, "%s: null B", what);
+    if (h->rank != 8 && h->rank != 16 && h->rank != 32 && h->rank != 64)
+      return fail(PL_ERR_UNSUPPORTED, "%s: rank %d not built (8, 16, 32, 64)", what, h->rank);
+    if (h->out_features < need_out)
+      return fail(PL_ERR_INVALID, "%s: B has %d output features, %d needed", what, h->out_features, need_out);
+    if (h->y_offset < 0 || h->y_offset % 8 || (int64_t)h->y_offset + (int64_t)n_adapters * h->rank > split->ld)
+      return fail(PL_ERR_INVALID, "%s: y columns outside the split planes' rows", what);
+    if ((uintptr_t)h->B % 16) return fail(PL_ERR_INVALID, "%s: B must be 16-byte aligned", what);
+    *d = LoraUp{nullptr, 0, h->y_offset, h->B, h->out_features, h->rank, h->scale};
+    return ok();
+  }
   if (!h->y || !h->B) return fail(PL_ERR_INVALID, "%s: null y or B", what);
   if (h->rank != 8 && h->rank != 16 && h->rank != 32 && h->rank != 64)
     return fail(PL_ERR_UNSUPPORTED, "%s: rank %d not built (8, 16, 32, 64)", what, h->rank);
@@ -389,31 +464,42 @@ static int lora_up_from(const pl_lora_up* h, int need_out, LoraUp* d, const char
   return ok();
 }
 
+// Host copy of a pl_split_out with its checks (need_cols: columns read per row).
+static int split_from(const pl_split_out* h, int need_cols, SplitIn* d, const char* what) {
+  if (!h->partials) return fail(PL_ERR_INVALID, "%s: null partials", what);
+  if (h->splits < 1 || h->splits > 16) return fail(PL_ERR_INVALID, "%s: splits must be 1..16", what);
+  if (h->ld < need_cols || h->ld % 8 || h->plane_stride % 8 || (uintptr_t)h->partials % 16)
+    return fail(PL_ERR_INVALID, "%s: partial planes need ld >= %d, ld and plane stride multiples of 8, "
+                "16-byte alignment", what, need_cols);
+  *d = SplitIn{h->partials, h->splits, h->ld, h->plane_stride};
+  return ok();
+}
+
 constexpr int kNormThreads = 512;
 
 template <typename T, bool ADD, int R>
 static void launch_norm_t(void* r, int64_t ldr, const void* x, int64_t ldx, const void* w, void* out, int64_t ldo,
                           int rows, int hidden, float eps, const LoraUp& lu, const int32_t* ids, int na,
-                          hipStream_t s) {
+                          const SplitIn& xs, hipStream_t s) {
   hipLaunchKernelGGL((rmsnorm_kernel<T, ADD, R, kNormThreads>), dim3(rows), dim3(kNormThreads), 0, s, (T*)r, ldr,
-                     (const T*)x, ldx, (const T*)w, (T*)out, ldo, hidden, eps, lu, ids, na);
+                     (const T*)x, ldx, (const T*)w, (T*)out, ldo, hidden, eps, lu, ids, na, xs);
 }
 
 template <typename T>
 static int launch_norm(bool add, int rank, void* r, int64_t ldr, const void* x, int64_t ldx, const void* w,
                        void* out, int64_t ldo, int rows, int hidden, float eps, const LoraUp& lu,
-                       const int32_t* ids, int na, hipStream_t s) {
+                       const int32_t* ids, int na, const SplitIn& xs, hipStream_t s) {
   if (rank == 0) {
     if (add)
-      launch_norm_t<T, true, 0>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s);
+      launch_norm_t<T, true, 0>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s);
     else
-      launch_norm_t<T, false, 0>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s);
+      launch_norm_t<T, false, 0>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s);
   } else if constexpr (sizeof(T) == 2) {
     switch (rank) {
-      case 8: launch_norm_t<T, true, 8>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s); break;
-      case 16: launch_norm_t<T, true, 16>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s); break;
-      case 32: launch_norm_t<T, true, 32>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s); break;
-      case 64: launch_norm_t<T, true, 64>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, s); break;
+      case 8: launch_norm_t<T, true, 8>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+      case 16: launch_norm_t<T, true, 16>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+      case 32: launch_norm_t<T, true, 32>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+      case 64: launch_norm_t<T, true, 64>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
     }
   } else {
     return fail(PL_ERR_UNSUPPORTED, "LoRA prologue needs F16 or BF16");
@@ -424,10 +510,17 @@ static int launch_norm(bool add, int rank, void* r, int64_t ldr, const void* x, 
 
 static int norm_common(bool add, void* r, int64_t ldr, const void* x, int64_t ldx, const void* w, void* out,
                        int64_t ldo, int rows, int hidden, float eps, int dtype, void* stream,
-                       const pl_lora_up* lora = nullptr, const int32_t* ids = nullptr, int n_adapters = 0) {
+                       const pl_lora_up* lora = nullptr, const int32_t* ids = nullptr, int n_adapters = 0,
+                       const pl_split_out* x_split = nullptr) {
   if (rows < 0 || hidden <= 0 || hidden % 8 || hidden > 16384)
     return fail(PL_ERR_INVALID, "hidden must be a positive multiple of 8 up to 16384 (got %d)", hidden);
   if (rows == 0) return ok();
+  SplitIn xs{nullptr, 0, 0, 0};
+  if (x_split) {
+    if (const int st = split_from(x_split, hidden, &xs, "add_rmsnorm input")) return st;
+    x = w;  // unused: the input comes from the partial planes
+    ldx = 0;
+  }
   if (!x || !w || !out || (add && !r)) return fail(PL_ERR_INVALID, "null pointer argument");
   if (ldx % 8 || ldo % 8 || (add && ldr % 8)) return fail(PL_ERR_INVALID, "row strides must be multiples of 8");
   const void* ptrs[] = {x, w, out, add ? r : x};
@@ -437,14 +530,15 @@ static int norm_common(bool add, void* r, int64_t ldr, const void* x, int64_t ld
   int rank = 0;
   if (lora) {
     if (!ids || n_adapters < 1) return fail(PL_ERR_INVALID, "LoRA needs adapter ids and n_adapters >= 1");
-    if (const int st = lora_up_from(lora, hidden, &lu, "add_rmsnorm LoRA")) return st;
+    if (const int st = lora_up_from(lora, hidden, &lu, "add_rmsnorm LoRA", x_split ? &xs : nullptr, n_adapters))
+      return st;
     rank = lu.rank;
   }
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case PL_DTYPE_F32: return launch_norm<float>(add, rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, n_adapters, s);
-    case PL_DTYPE_F16: return launch_norm<f16_t>(add, rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, n_adapters, s);
-    case PL_DTYPE_BF16: return launch_norm<bf16_t>(add, rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, n_adapters, s);
+    case PL_DTYPE_F32: return launch_norm<float>(add, rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, n_adapters, xs, s);
+    case PL_DTYPE_F16: return launch_norm<f16_t>(add, rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, n_adapters, xs, s);
+    case PL_DTYPE_BF16: return launch_norm<bf16_t>(add, rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, n_adapters, xs, s);
   }
   return fail(PL_ERR_UNSUPPORTED, "dtype %d", dtype);
 }
@@ -460,12 +554,12 @@ extern "C" int pl_add_rmsnorm(void* residual, int64_t ldr, const void* x, int64_
 }
 
 extern "C" int pl_add_rmsnorm_lora(void* residual, int64_t ldr, const void* x, int64_t ldx,
-                                   const pl_lora_up* lora_h, const int32_t* adapter_ids, int num_adapters,
-                                   const void* weight, void* out, int64_t ldo, int rows, int hidden, float eps,
-                                   int dtype, void* stream) {
+                                   const pl_split_out* x_split_h, const pl_lora_up* lora_h,
+                                   const int32_t* adapter_ids, int num_adapters, const void* weight, void* out,
+                                   int64_t ldo, int rows, int hidden, float eps, int dtype, void* stream) {
   if (!lora_h) return fail(PL_ERR_INVALID, "lora_h must not be null (use pl_add_rmsnorm)");
   return norm_common(true, residual, ldr, x, ldx, weight, out, ldo, rows, hidden, eps, dtype, stream, lora_h,
-                     adapter_ids, num_adapters);
+                     adapter_ids, num_adapters, x_split_h);
 }
 
 // Plain SiLU*up: 256 threads per workgroup; with the LoRA prologue every
@@ -548,6 +642,7 @@ struct QkrArgs {
   QkvLora lora;
   const int32_t* ids;
   int na;
+  SplitIn xs;
 };
 
 template <typename T, int D, int R>
@@ -556,7 +651,7 @@ static void launch_qkr(const QkrArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((qk_norm_rope_append_kernel<T, D, R>), dim3(a.batch, head_groups), dim3(kThreads), 0, s,
                      (const T*)a.qkv, a.ld, (const T*)a.qn, (const T*)a.kn, a.pos, a.pid, a.off, (T*)a.q_out,
                      (T*)a.kc, (T*)a.vc, a.ps_, a.ts, a.hs, a.np, a.page_size, a.hq, a.hkv, a.invf, a.eps, a.lora,
-                     a.ids, a.na);
+                     a.ids, a.na, a.xs);
 }
 
 template <typename T, int R>
@@ -601,23 +696,31 @@ static int qkr_common(const void* qkv, int64_t ld_qkv, const void* q_norm_weight
                       void* k_cache, void* v_cache, int64_t page_stride, int64_t token_stride, int64_t head_stride,
                       int64_t num_pages, int page_size, int batch, int num_qo_heads, int num_kv_heads, int head_dim,
                       const float* inv_freq, float eps, int dtype, void* stream, const pl_lora_up* lora,
-                      const int32_t* ids, int n_adapters) {
+                      const int32_t* ids, int n_adapters, const pl_split_out* qkv_split = nullptr) {
   if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0) return fail(PL_ERR_INVALID, "bad shape");
   if (batch == 0) return ok();
+  const int row_cols = (num_qo_heads + 2 * num_kv_heads) * head_dim;
+  SplitIn xs{nullptr, 0, 0, 0};
+  if (qkv_split) {
+    if (const int st = split_from(qkv_split, row_cols, &xs, "qkv input")) return st;
+    qkv = inv_freq;  // unused: the row comes from the partial planes
+    ld_qkv = row_cols;
+  }
   if (!qkv || !positions || !page_id || !offset || !q_out || !k_cache || !v_cache || !inv_freq)
     return fail(PL_ERR_INVALID, "null pointer argument");
   if (num_pages <= 0 || page_size <= 0) return fail(PL_ERR_INVALID, "num_pages and page_size must be > 0");
-  if (ld_qkv < (int64_t)(num_qo_heads + 2 * num_kv_heads) * head_dim)
-    return fail(PL_ERR_INVALID, "ld_qkv is shorter than the q|k|v row");
+  if (ld_qkv < (int64_t)row_cols) return fail(PL_ERR_INVALID, "ld_qkv is shorter than the q|k|v row");
   QkrArgs a{qkv, q_norm_weight, k_norm_weight, ld_qkv, positions, page_id, offset, q_out, k_cache, v_cache,
             page_stride, token_stride, head_stride, num_pages, page_size, batch, num_qo_heads, num_kv_heads,
-            inv_freq, eps, QkvLora{}, ids, n_adapters};
+            inv_freq, eps, QkvLora{}, ids, n_adapters, xs};
   if (lora) {
     if (!ids || n_adapters < 1) return fail(PL_ERR_INVALID, "LoRA needs adapter ids and n_adapters >= 1");
     const int need[3] = {num_qo_heads * head_dim, num_kv_heads * head_dim, num_kv_heads * head_dim};
     const char* names[3] = {"q LoRA", "k LoRA", "v LoRA"};
     for (int m = 0; m < 3; ++m)
-      if (const int st = lora_up_from(&lora[m], need[m], &a.lora.m[m], names[m])) return st;
+      if (const int st = lora_up_from(&lora[m], need[m], &a.lora.m[m], names[m], qkv_split ? &xs : nullptr,
+                                      n_adapters))
+        return st;
     if (a.lora.m[1].rank != a.lora.m[0].rank || a.lora.m[2].rank != a.lora.m[0].rank)
       return fail(PL_ERR_UNSUPPORTED, "q, k and v LoRA ranks differ");
     return qkr_by_dtype(dtype, a.lora.m[0].rank, head_dim, a, (hipStream_t)stream);
@@ -637,7 +740,8 @@ extern "C" int pl_qk_norm_rope_append(const void* qkv, int64_t ld_qkv, const voi
                     head_dim, inv_freq, eps, dtype, stream, nullptr, nullptr, 0);
 }
 
-extern "C" int pl_qk_norm_rope_append_lora(const void* qkv, int64_t ld_qkv, const pl_lora_up* lora_qkv_h,
+extern "C" int pl_qk_norm_rope_append_lora(const void* qkv, int64_t ld_qkv, const pl_split_out* qkv_split_h,
+                                           const pl_lora_up* lora_qkv_h,
                                            const int32_t* adapter_ids, int num_adapters, const void* q_norm_weight,
                                            const void* k_norm_weight, const int64_t* positions,
                                            const int64_t* page_id, const int64_t* offset, void* q_out,
@@ -649,5 +753,5 @@ extern "C" int pl_qk_norm_rope_append_lora(const void* qkv, int64_t ld_qkv, cons
   if (!lora_qkv_h) return fail(PL_ERR_INVALID, "lora_qkv_h must not be null (use pl_qk_norm_rope_append)");
   return qkr_common(qkv, ld_qkv, q_norm_weight, k_norm_weight, positions, page_id, offset, q_out, k_cache, v_cache,
                     page_stride, token_stride, head_stride, num_pages, page_size, batch, num_qo_heads, num_kv_heads,
-                    head_dim, inv_freq, eps, dtype, stream, lora_qkv_h, adapter_ids, num_adapters);
+                    head_dim, inv_freq, eps, dtype, stream, lora_qkv_h, adapter_ids, num_adapters, qkv_split_h);
 }

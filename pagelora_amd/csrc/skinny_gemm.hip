@@ -67,11 +67,15 @@ __global__ void shuffle_kernel(const uint16_t* __restrict__ W, int64_t ldw, int 
   }
 }
 
-template <typename T>
+// PARTIAL: split-K over gridDim.z workgroups per row block; workgroup z sums
+// k-steps [z*K/32/splits, ..) and writes its fp32 tile to plane z of
+// `partial` (row t at t * ldp, planes plane_stride apart) instead of `out`.
+template <typename T, bool PARTIAL>
 __global__ __launch_bounds__(kThreads) void shuffled_gemm_kernel(const T* __restrict__ x, int64_t ldx, int tokens,
                                                                  int K, const T* __restrict__ Ws, int N,
                                                                  const T* __restrict__ bias, T* __restrict__ out,
-                                                                 int64_t ldo) {
+                                                                 int64_t ldo, float* __restrict__ partial,
+                                                                 int64_t ldp, int64_t plane_stride) {
   __shared__ float s_red[kWaves][256];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int lr = lane % 16, kq = (lane / 16) * 8;
@@ -79,8 +83,10 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_kernel(const T* __rest
   const int t = t0 + lr;
   const bool t_ok = t < tokens;
   const int ksteps = K / 32;
-  const int per = (ksteps + kWaves - 1) / kWaves;
-  const int sb = min(ksteps, wave * per), se = min(ksteps, sb + per);
+  const int chunk = (ksteps + gridDim.z - 1) / gridDim.z;
+  const int kb0 = min(ksteps, (int)blockIdx.z * chunk), ke0 = min(ksteps, kb0 + chunk);
+  const int per = (ke0 - kb0 + kWaves - 1) / kWaves;
+  const int sb = min(ke0, kb0 + wave * per), se = min(ke0, sb + per);
   const u32x4* wb = reinterpret_cast<const u32x4*>(Ws + (int64_t)nb * ksteps * kBlockElems) + lane;
   const T* xr = x + (int64_t)(t_ok ? t : 0) * ldx + kq;
 
@@ -106,7 +112,7 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_kernel(const T* __rest
   __syncthreads();
   if (wave == 0) {
     const int n = nb * 16 + lr;
-    const float bv = (bias != nullptr && n < N) ? to_float<T>(bias[n]) : 0.f;
+    const float bv = (!PARTIAL && bias != nullptr && n < N) ? to_float<T>(bias[n]) : 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int cell = ((lane / 16) * 4 + i) * 16 + lr;
@@ -114,7 +120,12 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_kernel(const T* __rest
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) sum += s_red[w][cell];
       const int tr = t0 + (lane / 16) * 4 + i;
-      if (n < N && tr < tokens) out[(int64_t)tr * ldo + n] = from_float<T>(sum + bv);
+      if (n < N && tr < tokens) {
+        if (PARTIAL)
+          partial[(int64_t)blockIdx.z * plane_stride + (int64_t)tr * ldp + n] = sum;
+        else
+          out[(int64_t)tr * ldo + n] = from_float<T>(sum + bv);
+      }
     }
   }
 }
@@ -167,11 +178,45 @@ extern "C" int pl_linear_shuffled(const void* x, int64_t ldx, int num_tokens, in
   const dim3 grid((out_features + 15) / 16, (num_tokens + 15) / 16);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == PL_DTYPE_BF16)
-    hipLaunchKernelGGL(shuffled_gemm_kernel<bf16_t>, grid, dim3(kThreads), 0, s, (const bf16_t*)x, ldx, num_tokens,
-                       in_features, (const bf16_t*)shuffled, out_features, (const bf16_t*)bias, (bf16_t*)out, ldo);
+    hipLaunchKernelGGL((shuffled_gemm_kernel<bf16_t, false>), grid, dim3(kThreads), 0, s, (const bf16_t*)x, ldx,
+                       num_tokens, in_features, (const bf16_t*)shuffled, out_features, (const bf16_t*)bias,
+                       (bf16_t*)out, ldo, nullptr, 0, 0);
   else
-    hipLaunchKernelGGL(shuffled_gemm_kernel<f16_t>, grid, dim3(kThreads), 0, s, (const f16_t*)x, ldx, num_tokens,
-                       in_features, (const f16_t*)shuffled, out_features, (const f16_t*)bias, (f16_t*)out, ldo);
+    hipLaunchKernelGGL((shuffled_gemm_kernel<f16_t, false>), grid, dim3(kThreads), 0, s, (const f16_t*)x, ldx,
+                       num_tokens, in_features, (const f16_t*)shuffled, out_features, (const f16_t*)bias,
+                       (f16_t*)out, ldo, nullptr, 0, 0);
+  PL_LAUNCH_CHECK("shuffled_gemm_kernel");
+  return ok();
+}
+
+extern "C" int pl_linear_shuffled_split(const void* x, int64_t ldx, int num_tokens, int in_features,
+                                        const void* shuffled, int out_features, int splits, float* partials,
+                                        int64_t ld, int64_t plane_stride, int dtype, void* stream) {
+  if (num_tokens < 0 || num_tokens > PL_LINEAR_MAX_TOKENS)
+    return fail(PL_ERR_INVALID, "num_tokens must be 0..%d (got %d)", PL_LINEAR_MAX_TOKENS, num_tokens);
+  if (num_tokens == 0) return ok();
+  if (in_features <= 0 || in_features % 32 || out_features <= 0)
+    return fail(PL_ERR_INVALID, "in_features must be a positive multiple of 32 and out_features > 0");
+  if (splits < 1 || splits > 16 || splits > in_features / 32)
+    return fail(PL_ERR_INVALID, "splits must be 1..min(16, in_features/32) (got %d)", splits);
+  if (!x || !shuffled || !partials) return fail(PL_ERR_INVALID, "null pointer argument");
+  if (ldx < in_features || ldx % 8 || (uintptr_t)x % 16 || (uintptr_t)shuffled % 16)
+    return fail(PL_ERR_INVALID, "x rows and the shuffled weight must be 16-byte aligned");
+  if (ld < out_features || plane_stride < ld * num_tokens)
+    return fail(PL_ERR_INVALID, "partial planes overlap (ld %lld, plane_stride %lld)", (long long)ld,
+                (long long)plane_stride);
+  if (dtype != PL_DTYPE_BF16 && dtype != PL_DTYPE_F16)
+    return fail(PL_ERR_UNSUPPORTED, "pl_linear_shuffled_split dtype must be F16 or BF16 (got %d)", dtype);
+  const dim3 grid((out_features + 15) / 16, (num_tokens + 15) / 16, splits);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == PL_DTYPE_BF16)
+    hipLaunchKernelGGL((shuffled_gemm_kernel<bf16_t, true>), grid, dim3(kThreads), 0, s, (const bf16_t*)x, ldx,
+                       num_tokens, in_features, (const bf16_t*)shuffled, out_features, nullptr, nullptr, 0,
+                       partials, ld, plane_stride);
+  else
+    hipLaunchKernelGGL((shuffled_gemm_kernel<f16_t, true>), grid, dim3(kThreads), 0, s, (const f16_t*)x, ldx,
+                       num_tokens, in_features, (const f16_t*)shuffled, out_features, nullptr, nullptr, 0,
+                       partials, ld, plane_stride);
   PL_LAUNCH_CHECK("shuffled_gemm_kernel");
   return ok();
 }

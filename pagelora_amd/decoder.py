@@ -35,7 +35,7 @@ import torch.nn.functional as F
 from . import fused_ops
 from .attention_backend import PagedDecodeAttention
 from .kv_pool import PagedKVPool, Request
-from .linear import ShuffledWeight, linear_shuffled
+from .linear import ShuffledWeight, SplitOutput, linear_shuffled, linear_shuffled_split
 from .lora import lora_linear
 
 
@@ -170,17 +170,33 @@ class DecodeContext:
 # the narrow projections (q/k/v, o); the wide MLP projections and longer
 # inputs (prefill) take the library GEMM (torch -> hipBLASLt).
 DECODE_GEMM_MAX_TOKENS = 16
+# Split-K ways of the decode GEMM per projection.  down_proj (257 blocks of
+# 16 output columns over K = 12288) keeps too few workgroups streaming: split
+# 3 ways it drops from 25.9 to 19.4 us at 4 tokens, and the next add+RMSNorm
+# sums the fp32 planes for ~1.7 us more.  Splitting o_proj (257 blocks, K =
+# 4096) or qkv saves less than its consumer then pays; gate_up (1538 blocks)
+# does not need it.
+DECODE_SPLITS = {"down": 3}
 
 
-def _project(x: torch.Tensor, lw: LayerWeights, name: str) -> torch.Tensor:
-    """x . [W; A]^T: the base output and every adapter's LoRA intermediate."""
+def _project(x: torch.Tensor, lw: LayerWeights, name: str) -> "torch.Tensor | SplitOutput":
+    """x . [W; A]^T: the base output and every adapter's LoRA intermediate
+    (as split-K planes for the narrow projections at decode batch sizes)."""
     if x.shape[0] <= DECODE_GEMM_MAX_TOKENS:
         sw = lw.shuffled.get(name)
         if sw is not None:
+            splits = DECODE_SPLITS.get(name, 1)
+            if splits > 1:
+                return linear_shuffled_split(x, sw, splits)
             return linear_shuffled(x, sw)
         if name in ("qkv", "o"):
             return lora_linear(x, getattr(lw, f"w_{name}_ext"), None, None)
     return F.linear(x, getattr(lw, f"w_{name}_ext"))
+
+
+def _cols(out, n: int):
+    """The first n columns of a projection output (split planes are passed whole)."""
+    return out if isinstance(out, SplitOutput) else out[:, :n]
 
 
 def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Tensor, pending, ids: torch.Tensor,
@@ -203,18 +219,18 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
         x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
     else:
         prev_out, prev_up = pending
-        x = fused_ops.add_rmsnorm(hidden, prev_out[:, :h], lw.input_norm, cfg.rms_eps, lora=prev_up,
+        x = fused_ops.add_rmsnorm(hidden, _cols(prev_out, h), lw.input_norm, cfg.rms_eps, lora=prev_up,
                                   adapter_ids=ids)
     qkv = _project(x, lw, "qkv")
     q = fused_ops.qk_norm_rope_append(
-        qkv[:, : qd + 2 * kd], lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None,
+        _cols(qkv, qd + 2 * kd), lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None,
         positions, page_id, page_offset, layer_cache, num_qo_heads=cfg.num_qo_heads,
         num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=page_size,
         rope_theta=cfg.rope_theta, eps=cfg.rms_eps,
         lora=(lw.up("q", qkv, scale), lw.up("k", qkv, scale), lw.up("v", qkv, scale)), adapter_ids=ids)
     attn = attend(q).view(q.shape[0], qd)
     o = _project(attn, lw, "o")
-    x2 = fused_ops.add_rmsnorm(hidden, o[:, :h], lw.post_norm, cfg.rms_eps, lora=lw.up("o", o, scale),
+    x2 = fused_ops.add_rmsnorm(hidden, _cols(o, h), lw.post_norm, cfg.rms_eps, lora=lw.up("o", o, scale),
                                adapter_ids=ids)
     gu = _project(x2, lw, "gate_up")
     act = fused_ops.silu_mul(gu[:, : 2 * I], lora=(lw.up("gate", gu, scale), lw.up("up", gu, scale)),
@@ -225,8 +241,8 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
 
 def _final_norm(weights: "DecoderWeights", hidden: torch.Tensor, pending, ids: torch.Tensor) -> torch.Tensor:
     prev_out, prev_up = pending
-    return fused_ops.add_rmsnorm(hidden, prev_out[:, : weights.cfg.hidden], weights.final_norm, weights.cfg.rms_eps,
-                                 lora=prev_up, adapter_ids=ids)
+    return fused_ops.add_rmsnorm(hidden, _cols(prev_out, weights.cfg.hidden), weights.final_norm,
+                                 weights.cfg.rms_eps, lora=prev_up, adapter_ids=ids)
 
 
 def decode_layer_static(

@@ -10,6 +10,7 @@ decode token's page append (layer_runner.py:399-412).
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import Sequence
 
@@ -17,6 +18,7 @@ import torch
 
 from . import _lib
 from .attention_backend import _cache_geometry
+from .linear import SplitOutput
 
 
 def _rows2d(t: torch.Tensor, name: str) -> None:
@@ -36,18 +38,24 @@ class LoraUp:
     ``round(base + scale * y[a] . B[a]^T)`` (multilora/linear.py:226-231).
     """
 
-    y: torch.Tensor
+    y: "torch.Tensor | SplitOutput"
     y_offset: int
     B: torch.Tensor
     scale: float
 
     def struct(self) -> "_lib.LoraUp":
+        B = self.B if self.B.dim() == 3 else self.B.unsqueeze(0)
+        n, _, r = B.shape
+        if isinstance(self.y, SplitOutput):  # read from the split planes by the kernel
+            if not B.is_contiguous() or B.dtype != self.y.dtype:
+                raise ValueError("LoraUp.B must be contiguous [n, out, r] of the model dtype")
+            if self.y_offset < 0 or self.y_offset + n * r > self.y.ld:
+                raise ValueError("LoraUp: y columns out of range")
+            return _lib.LoraUp(None, 0, int(self.y_offset), B.data_ptr(), int(B.shape[1]), int(r), float(self.scale))
         if self.y.dim() != 2 or self.y.stride(1) != 1:
             raise ValueError("LoraUp.y must be 2-D with unit column stride")
-        B = self.B if self.B.dim() == 3 else self.B.unsqueeze(0)
         if not B.is_contiguous() or B.dtype != self.y.dtype:
             raise ValueError("LoraUp.B must be contiguous [n, out, r] of y's dtype")
-        n, _, r = B.shape
         if self.y_offset < 0 or self.y_offset + n * r > self.y.shape[1]:
             raise ValueError("LoraUp: y columns out of range")
         return _lib.LoraUp(self.y.data_ptr(), self.y.stride(0), int(self.y_offset), B.data_ptr(), int(B.shape[1]),
@@ -65,7 +73,8 @@ def _lora_args(lora: Sequence[LoraUp], adapter_ids: torch.Tensor | None, rows: i
     if adapter_ids is None or adapter_ids.dtype != torch.int32 or adapter_ids.numel() != rows:
         raise ValueError("adapter_ids must be int32 [rows]")
     for m in lora:
-        if m.y.shape[0] != rows:
+        y_rows = m.y.rows if isinstance(m.y, SplitOutput) else m.y.shape[0]
+        if y_rows != rows:
             raise ValueError("LoraUp.y must have one row per token")
     arr = (_lib.LoraUp * len(lora))(*[m.struct() for m in lora])
     return arr, adapter_ids.data_ptr(), n
@@ -84,27 +93,37 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor
     return out
 
 
-def add_rmsnorm(residual: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: float,
+def add_rmsnorm(residual: torch.Tensor, x: "torch.Tensor | SplitOutput", weight: torch.Tensor, eps: float,
                 out: torch.Tensor | None = None, *, lora: LoraUp | None = None,
                 adapter_ids: torch.Tensor | None = None) -> torch.Tensor:
     """In place ``residual += x``; returns ``rmsnorm(residual)``.
 
     With ``lora``, x is the base output of the module whose up-projection
     ``lora`` describes: ``residual += round(x + delta)`` (pl_add_rmsnorm_lora).
+    x may then also be a :class:`SplitOutput` (split-K planes summed here).
     """
     _rows2d(residual, "residual")
-    _rows2d(x, "x")
-    if x.shape != residual.shape or x.dtype != residual.dtype:
-        raise ValueError("x must match residual")
+    rows, hidden = residual.shape
+    split = isinstance(x, SplitOutput)
+    if split:
+        if lora is None:
+            raise ValueError("a split-K input needs the module's lora")
+        if x.rows != rows or x.out_features < hidden or x.dtype != residual.dtype:
+            raise ValueError("x must match residual")
+    else:
+        _rows2d(x, "x")
+        if x.shape != residual.shape or x.dtype != residual.dtype:
+            raise ValueError("x must match residual")
     out = torch.empty_like(residual) if out is None else out
     lib = _lib.load()
-    rows, hidden = residual.shape
     if lora is not None:
         arr, ids, n = _lora_args([lora], adapter_ids, rows)
-        _lib.check(lib.pl_add_rmsnorm_lora(residual.data_ptr(), residual.stride(0), x.data_ptr(), x.stride(0),
-                                           arr, ids, n, weight.data_ptr(), out.data_ptr(), out.stride(0), rows,
-                                           hidden, float(eps), _lib.dtype_code(x.dtype),
-                                           _lib.stream_handle(x.device)), "pl_add_rmsnorm_lora")
+        xs = ctypes.byref(x.struct()) if split else None
+        _lib.check(lib.pl_add_rmsnorm_lora(residual.data_ptr(), residual.stride(0), None if split else x.data_ptr(),
+                                           0 if split else x.stride(0), xs, arr, ids, n, weight.data_ptr(),
+                                           out.data_ptr(), out.stride(0), rows, hidden, float(eps),
+                                           _lib.dtype_code(residual.dtype), _lib.stream_handle(residual.device)),
+                   "pl_add_rmsnorm_lora")
         return out
     _lib.check(lib.pl_add_rmsnorm(residual.data_ptr(), residual.stride(0), x.data_ptr(), x.stride(0),
                                   weight.data_ptr(), out.data_ptr(), out.stride(0), rows, hidden, float(eps),
@@ -175,14 +194,23 @@ def qk_norm_rope_append(
     """Returns the rotated q [B, Hq, D]; writes rotated k and v into the pages.
 
     With ``lora`` (q, k, v) the modules' LoRA deltas are added to the packed
-    row first (pl_qk_norm_rope_append_lora).
+    row first (pl_qk_norm_rope_append_lora); qkv may then also be a
+    :class:`SplitOutput` (split-K planes summed here).
     """
-    _rows2d(qkv, "qkv")
-    B = qkv.shape[0]
+    split = isinstance(qkv, SplitOutput)
+    if split:
+        if lora is None:
+            raise ValueError("a split-K input needs the modules' lora")
+        B = qkv.rows
+    else:
+        _rows2d(qkv, "qkv")
+        B = qkv.shape[0]
     kc, vc, page_stride, token_stride, head_stride, num_pages = _cache_geometry(
         cache_layer, num_kv_heads, head_dim, page_size)
     if kc.dtype != qkv.dtype:
         raise ValueError("qkv dtype must match the KV cache")
+    if split and qkv.out_features < (num_qo_heads + 2 * num_kv_heads) * head_dim:
+        raise ValueError("qkv has fewer columns than q|k|v")
     for t, n in ((positions, "positions"), (page_id, "page_id"), (page_offset, "page_offset")):
         if t.dtype != torch.int64 or t.numel() != B:
             raise ValueError(f"{n} must be int64 [B]")
@@ -194,7 +222,8 @@ def qk_norm_rope_append(
             raise ValueError("lora must be (q, k, v)")
         arr, ids, n = _lora_args(lora, adapter_ids, B)
         _lib.check(lib.pl_qk_norm_rope_append_lora(
-            qkv.data_ptr(), qkv.stride(0), arr, ids, n,
+            None if split else qkv.data_ptr(), 0 if split else qkv.stride(0),
+            ctypes.byref(qkv.struct()) if split else None, arr, ids, n,
             q_norm_weight.data_ptr() if q_norm_weight is not None else None,
             k_norm_weight.data_ptr() if k_norm_weight is not None else None,
             positions.data_ptr(), page_id.data_ptr(), page_offset.data_ptr(),

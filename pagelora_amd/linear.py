@@ -57,3 +57,61 @@ def linear_shuffled(x: torch.Tensor, weight: ShuffledWeight, bias: torch.Tensor 
                                       _lib.dtype_code(x.dtype), _lib.stream_handle(x.device)),
                "pl_linear_shuffled")
     return out
+
+
+class SplitOutput:
+    """A decode GEMM output held as split-K partial planes ``[splits, T, ld]``
+    (fp32).  Element (t, c) is the in-order sum over the planes, rounded to
+    the model dtype: the value the unsplit GEMM would have written.  The
+    kernels that consume the projection (``fused_ops.add_rmsnorm``,
+    ``fused_ops.qk_norm_rope_append``) read it directly (``pl_split_out``)."""
+
+    def __init__(self, partials: torch.Tensor, out_features: int, dtype: torch.dtype) -> None:
+        self.partials = partials
+        self.out_features = out_features
+        self.dtype = dtype
+
+    @property
+    def splits(self) -> int:
+        return self.partials.shape[0]
+
+    @property
+    def rows(self) -> int:
+        return self.partials.shape[1]
+
+    @property
+    def ld(self) -> int:
+        return self.partials.shape[2]
+
+    @property
+    def device(self) -> torch.device:
+        return self.partials.device
+
+    def struct(self) -> "_lib.SplitOut":
+        p = self.partials
+        return _lib.SplitOut(p.data_ptr(), p.shape[0], p.stride(1), p.stride(0))
+
+    def sum(self) -> torch.Tensor:
+        """The rounded output as a tensor (planes added in order, as the kernels do)."""
+        acc = torch.zeros_like(self.partials[0])
+        for s in range(self.splits):
+            acc = acc + self.partials[s]
+        return acc[:, : self.out_features].to(self.dtype)
+
+
+def linear_shuffled_split(x: torch.Tensor, weight: ShuffledWeight, splits: int) -> SplitOutput:
+    """``x . W^T`` with K split over ``splits`` workgroups per 16 output
+    columns, returned as fp32 partial planes for a consuming kernel to sum."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] != weight.in_features or x.dtype != weight.dtype:
+        raise ValueError(f"x must be [T, {weight.in_features}] of {weight.dtype} with unit column stride")
+    T, N = x.shape[0], weight.out_features
+    if T > _lib.PL_LINEAR_MAX_TOKENS:
+        raise ValueError(f"linear_shuffled_split takes at most {_lib.PL_LINEAR_MAX_TOKENS} tokens")
+    ld = (N + 7) // 8 * 8
+    partials = torch.empty((splits, T, ld), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    _lib.check(lib.pl_linear_shuffled_split(x.data_ptr(), x.stride(0), T, weight.in_features, weight.data.data_ptr(),
+                                            N, int(splits), partials.data_ptr(), ld, partials.stride(0),
+                                            _lib.dtype_code(x.dtype), _lib.stream_handle(x.device)),
+               "pl_linear_shuffled_split")
+    return SplitOutput(partials, N, x.dtype)

@@ -225,3 +225,62 @@ def test_lora_up_rejects_bad_layouts(gpu_device):
         fused_ops.add_rmsnorm(r, x[:, :64], w, 1e-6,
                               lora=fused_ops.LoraUp(x, 64, torch.zeros((1, 32, 16), dtype=torch.bfloat16,
                                                                        device=gpu_device), 1.0), adapter_ids=ids)
+
+
+# ---- split-K inputs: a consumer fed fp32 partial planes equals the same
+# consumer fed their in-order, rounded sum (bit-exact).
+
+def _random_split(g, splits, rows, cols, dtype, device):
+    from pagelora_amd.linear import SplitOutput
+
+    ld = (cols + 7) // 8 * 8 + 8
+    parts = (torch.randn((splits, rows, ld), generator=g) * 0.7).to(device)
+    return SplitOutput(parts, cols, dtype)
+
+
+@pytest.mark.parametrize("splits", [1, 3, 4])
+def test_add_rmsnorm_lora_split_input_matches_summed_input(gpu_device, splits):
+    hidden, rows = 4096, len(IDS)
+    g = torch.Generator().manual_seed(splits)
+    so = _random_split(g, splits, rows, hidden + N_ADAPTERS * RANK, torch.bfloat16, gpu_device)
+    B = (torch.randn((N_ADAPTERS, hidden, RANK), generator=g) * 0.05).to(torch.bfloat16).to(gpu_device)
+    r0 = torch.randn((rows, hidden), generator=g).to(torch.bfloat16).to(gpu_device)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(gpu_device)
+    ids = torch.tensor(IDS, dtype=torch.int32, device=gpu_device)
+    dense = so.sum()
+    r1, r2 = r0.clone(), r0.clone()
+    out1 = fused_ops.add_rmsnorm(r1, so, w, 1e-6, lora=fused_ops.LoraUp(so, hidden, B, SCALE), adapter_ids=ids)
+    out2 = fused_ops.add_rmsnorm(r2, dense[:, :hidden], w, 1e-6, lora=fused_ops.LoraUp(dense, hidden, B, SCALE),
+                                 adapter_ids=ids)
+    torch.cuda.synchronize()
+    assert torch.equal(r1, r2) and torch.equal(out1, out2)
+
+
+@pytest.mark.parametrize("splits", [2, 4])
+def test_qk_norm_rope_append_lora_split_input_matches_summed_input(gpu_device, splits):
+    hq, hkv, d, ps, pool = 8, 2, 128, 16, 10
+    rows = len(IDS)
+    qd, kd = hq * d, hkv * d
+    g = torch.Generator().manual_seed(10 + splits)
+    so = _random_split(g, splits, rows, qd + 2 * kd + 3 * N_ADAPTERS * RANK, torch.bfloat16, gpu_device)
+    dense = so.sum()
+    Bs = [(torch.randn((N_ADAPTERS, f, RANK), generator=g) * 0.05).to(torch.bfloat16).to(gpu_device)
+          for f in (qd, kd, kd)]
+    offs = [qd + 2 * kd + j * N_ADAPTERS * RANK for j in range(3)]
+    qw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(gpu_device)
+    kw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(gpu_device)
+    pos = torch.tensor([0, 17, 4095, 40000, 5], device=gpu_device)
+    pid = torch.tensor([3, 9, 0, 5, 7], device=gpu_device)
+    off = torch.tensor([0, 15, 7, 1, 2], device=gpu_device)
+    ids = torch.tensor(IDS, dtype=torch.int32, device=gpu_device)
+    outs = []
+    for src in (so, dense):
+        cache = torch.zeros((pool, 2, ps, hkv, d), dtype=torch.bfloat16, device=gpu_device)
+        ups = tuple(fused_ops.LoraUp(src, o, B, SCALE) for o, B in zip(offs, Bs))
+        inp = src if src is so else dense[:, : qd + 2 * kd]
+        q = fused_ops.qk_norm_rope_append(inp, qw, kw, pos, pid, off, cache, num_qo_heads=hq, num_kv_heads=hkv,
+                                          head_dim=d, page_size=ps, rope_theta=1e6, eps=1e-6, lora=ups,
+                                          adapter_ids=ids)
+        outs.append((q, cache))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])

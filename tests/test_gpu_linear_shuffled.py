@@ -88,3 +88,31 @@ def test_bad_inputs_raise(gpu_device):
         linear_shuffled(torch.zeros((4, 32), dtype=torch.bfloat16, device=gpu_device), sw)
     with pytest.raises(ValueError, match="at most"):
         linear_shuffled(torch.zeros((_lib.PL_LINEAR_MAX_TOKENS + 1, 64), dtype=torch.bfloat16, device=gpu_device), sw)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 4])
+@pytest.mark.parametrize("shape", [(4112, 4096), (4112, 12288), (6192, 4096), (48, 96)])
+@pytest.mark.parametrize("tokens", [1, 4, 17])
+def test_split_planes_sum_to_the_linear(gpu_device, splits, shape, tokens):
+    """pl_linear_shuffled_split: the in-order sum of the planes, rounded, is the
+    oracle's linear (same bar), and for one split it is pl_linear_shuffled."""
+    from pagelora_amd.linear import linear_shuffled_split
+
+    n, k = shape
+    g = torch.Generator().manual_seed(n * 7 + k + tokens + splits)
+    x = torch.randn((tokens, k), generator=g).to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=g) * k ** -0.5).to(torch.bfloat16)
+    sw = ShuffledWeight(w.to(gpu_device))
+    if splits > k // 32:  # fewer 32-wide k-steps than splits
+        with pytest.raises(ValueError, match="splits"):
+            linear_shuffled_split(x.to(gpu_device), sw, splits)
+        return
+    so = linear_shuffled_split(x.to(gpu_device), sw, splits)
+    got = so.sum()
+    torch.cuda.synchronize()
+    assert so.partials.shape == (splits, tokens, (n + 7) // 8 * 8)
+    want = _oracle_linear(x.double().numpy(), w.double().numpy(), None)
+    err = np.abs(got.float().cpu().numpy() - want)
+    assert (err <= 2e-3 + REL[torch.bfloat16] * np.abs(want)).all(), f"max err {err.max():.3e}"
+    if splits == 1:
+        assert torch.equal(got, linear_shuffled(x.to(gpu_device), sw))
