@@ -505,6 +505,40 @@ int pl_linear_shuffled_split(const void* x, int64_t ldx, int num_tokens,
                              int64_t ld, int64_t plane_stride, int dtype,
                              void* stream);
 
+/*
+ * Advance every row of a batched page table by one decode token, in place
+ * on the device (one kernel, no host table, safe to capture in a graph).
+ * indptr [batch+1], indices (capacity indices_capacity entries) and
+ * last_page_len [batch] are int32 device buffers in the layout pl_decode_plan
+ * reads.  A row whose last page has room grows its fill by one; a row whose
+ * last page is full, or that has no page, takes page
+ * reserve[b * reserve_slots + reserve_head[b] % reserve_slots] (int32), sets
+ * that slot to -1 and increments reserve_head[b]; its new page starts with
+ * fill 1.  Entries of later rows move right to make room.  The kernel
+ * writes each row's decode inputs (int64): positions[b] = the token's
+ * position, page_id[b] / page_offset[b] = the slot its K/V row goes to.
+ *
+ * Errors found on the device leave the table unchanged, set page_id[b] =
+ * page_offset[b] = -1 for every row (the append entry points skip such
+ * rows) and OR a bit into status[0]: 1 = a row needed a page and its
+ * reserve slot held -1, 2 = the table would outgrow indices_capacity,
+ * 4 = a malformed table (indptr decreasing or outside [0, capacity],
+ * last_page_len outside [1, page_size] on a row with pages).  batch is at
+ * most 4096.
+ *
+ * Replaces the per-step host bookkeeping of the batched decode loop
+ * (model/flashinfer/generation.py:1011-1035): reserve_chunk(request, 1) per
+ * row (model/kvcache/paged_kvcache_manager.py:195-213 ->
+ * model/kvcache/paged_kv_store.py:113-190) and the repack of all rows into
+ * the reusable table (model/kvcache/flashinfer_page_table.py:89-121).
+ */
+int pl_page_table_advance(int32_t* indptr, int32_t* indices,
+                          int64_t indices_capacity, int32_t* last_page_len,
+                          int batch, int page_size, int32_t* reserve,
+                          int reserve_slots, int32_t* reserve_head,
+                          int64_t* positions, int64_t* page_id,
+                          int64_t* page_offset, int32_t* status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

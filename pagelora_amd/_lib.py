@@ -129,6 +129,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _i32, _i32, _i32, _i32, _vp,        # batch, hkv, head_dim, dtype, stream
         ],
     ),
+    "pl_page_table_advance": (
+        _i32,
+        [
+            _vp, _vp, _i64, _vp,          # indptr, indices, capacity, last_page_len
+            _i32, _i32,                   # batch, page_size
+            _vp, _i32, _vp,               # reserve, slots, reserve_head
+            _vp, _vp, _vp, _vp, _vp,      # positions, page_id, page_offset, status, stream
+        ],
+    ),
     "pl_prefill_plan": (
         _i32,
         [

@@ -209,6 +209,30 @@ class PagedDecodeAttention:
             raise RuntimeError("plan_decode has not been called")
         self._launch_plan(self._plan["batch"], self._plan["target_items"])
 
+    def advance_decode(self, reserve, positions: torch.Tensor, page_id: torch.Tensor,
+                       page_offset: torch.Tensor) -> None:
+        """Grow every planned row by one decode token on the device, then re-plan.
+
+        ``reserve`` is a :class:`~pagelora_amd.page_table.PageReserve` of the
+        plan's batch; the token positions and KV slots land in ``positions`` /
+        ``page_id`` / ``page_offset``.  Two kernels, no host table and no
+        read-back, so a captured decode step can start with it
+        (generation.py:1011-1035 does this on the host every step).
+        """
+
+        from .page_table import page_table_advance
+
+        if self._plan is None:
+            raise RuntimeError("plan_decode has not been called")
+        batch = self._plan["batch"]
+        if reserve.batch != batch:
+            raise ValueError(f"reserve holds {reserve.batch} rows but the plan has {batch}")
+        indptr_buf, indices_buf, last_buf = self._decode_graph_buffers
+        page_table_advance(indptr_buf, indices_buf, last_buf[:batch], self.page_size, reserve.reserve,
+                           reserve.head, positions, page_id, page_offset, reserve.status)
+        self._plan["max_page"] = None  # pages now come from the reserve; the kernels clamp them
+        self._launch_plan(batch, self._plan["target_items"])
+
     def _launch_plan(self, batch: int, target_items: int) -> None:
         indptr_buf, indices_buf, _ = self._decode_graph_buffers
         status = self._lib.pl_decode_plan(

@@ -35,6 +35,7 @@ class DecodeGraphKey:
     cache_dtype: torch.dtype
     batch: int
     adapter_version: int
+    reserve_ptrs: tuple = ()  # device page-table advance captured in (its ring buffers)
 
 
 @dataclass
@@ -59,8 +60,10 @@ class BatchDecodeGraphRunner:
         self.replay_count = 0
         self._graphs: OrderedDict[DecodeGraphKey, DecodeGraphEntry] = OrderedDict()
 
-    def key(self, batch: int) -> DecodeGraphKey:
+    def key(self, batch: int, reserve=None) -> DecodeGraphKey:
         cache = self.pool.cache
+        ptrs = () if reserve is None else (reserve.reserve.data_ptr(), reserve.head.data_ptr(),
+                                           reserve.status.data_ptr())
         return DecodeGraphKey(
             model_id=id(self.weights),
             backend_signature=self.backend.decode_graph_signature(),
@@ -69,19 +72,24 @@ class BatchDecodeGraphRunner:
             cache_dtype=cache.dtype,
             batch=batch,
             adapter_version=self.adapter_version,
+            reserve_ptrs=ptrs,
         )
 
-    def entry(self, batch: int) -> DecodeGraphEntry | None:
-        """The graph for ``batch``: captured on first use (needs a current plan)."""
+    def entry(self, batch: int, reserve=None) -> DecodeGraphEntry | None:
+        """The graph for ``batch``: captured on first use (needs a current plan).
+
+        With a :class:`PageReserve` the graph starts with the device-side
+        page-table advance and re-plan, so a replay needs no host input.
+        """
         if self.disabled_reason is not None:
             return None
-        k = self.key(batch)
+        k = self.key(batch, reserve)
         e = self._graphs.get(k)
         if e is not None:
             self._graphs.move_to_end(k)
             return e
         try:
-            e = self._capture(batch)
+            e = self._capture(batch, reserve)
         except Exception as exc:  # capture failure: fall back to eager for good
             self.disabled_reason = f"{type(exc).__name__}: {exc}"
             self._graphs.clear()
@@ -92,7 +100,7 @@ class BatchDecodeGraphRunner:
         self.capture_count += 1
         return e
 
-    def _capture(self, batch: int) -> DecodeGraphEntry:
+    def _capture(self, batch: int, reserve=None) -> DecodeGraphEntry:
         dev = self.pool.cache.device
         ctx = DecodeContext(batch, dev)
         # Warm up once on a side stream (allocator pools, library workspaces),
@@ -105,6 +113,8 @@ class BatchDecodeGraphRunner:
         cur.wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
+            if reserve is not None:  # not in the warm-up: it would grow the rows
+                self.backend.advance_decode(reserve, ctx.positions, ctx.page_id, ctx.page_offset)
             logits = decode_step_static(self.weights, self.pool, self.backend, ctx)
         return DecodeGraphEntry(graph=graph, ctx=ctx, logits=logits)
 

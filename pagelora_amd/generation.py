@@ -27,6 +27,7 @@ from .attention_backend import PagedDecodeAttention
 from .decode_graph import BatchDecodeGraphRunner
 from .decoder import DecodeContext, DecoderWeights, decode_step_static, prefill, prefill_backend
 from .kv_pool import PagedKVPool, Request
+from .page_table import PageReserve
 
 
 @dataclass
@@ -69,6 +70,54 @@ class _PinnedRing:
         self.events[i] = ev
 
 
+class _ReserveFeeder:
+    """Keeps each row's reserve ring a window of steps ahead of the device.
+
+    Rows grow by exactly one token per step, so the host knows without a
+    read-back which step makes row b take its k-th new page: with L0 tokens
+    and n0 pages at the start, the pages taken by steps < s number
+    ``max(0, ceil((L0 + s) / ps) - n0)``.  Every refill reserves the tokens
+    of the next ``window`` steps in the pool (allocating pages as needed)
+    and uploads one snapshot of the rings: pages taken earlier are gone from
+    the device ring, the rest sit at slot ``k % slots``.  A window of
+    ``(slots - 1) * ps`` steps holds at most ``slots - 1`` new pages per row,
+    so a snapshot never overwrites a page the device has not taken yet.
+    """
+
+    def __init__(self, pool: PagedKVPool, requests: list[Request], reserve: PageReserve, steps: int) -> None:
+        self.pool, self.requests, self.reserve, self.steps = pool, requests, reserve, steps
+        ps = pool.page_size
+        self.ps = ps
+        self.L0 = [r.length for r in requests]
+        self.n0 = [-(-L // ps) for L in self.L0]
+        self.window = (reserve.slots - 1) * ps
+        self.reserved_until = 0  # steps whose tokens are reserved in the pool
+        self.uploads = 0
+
+    def taken_before(self, b: int, s: int) -> int:
+        return max(0, -(-(self.L0[b] + s) // self.ps) - self.n0[b])
+
+    def before_step(self, s: int) -> None:
+        """Refill (enqueued before step ``s``) when a row's window runs short."""
+        if s >= self.reserved_until or any(
+                self.taken_before(b, min(self.steps, s + self.ps)) > self.taken_before(b, self.reserved_until)
+                for b in range(len(self.requests))):
+            self._refill(s)
+
+    def _refill(self, s: int) -> None:
+        end = min(self.steps, s + self.window)
+        ring = np.full((len(self.requests), self.reserve.slots), -1, dtype=np.int32)
+        for b, r in enumerate(self.requests):
+            if end > self.reserved_until:
+                self.pool.reserve(r, end - self.reserved_until)
+            pages = r.pages()
+            for k in range(self.taken_before(b, s), self.taken_before(b, end)):
+                ring[b, k % self.reserve.slots] = pages[self.n0[b] + k]
+        self.reserved_until = max(self.reserved_until, end)
+        self.reserve.upload(ring)
+        self.uploads += 1
+
+
 class BatchGenerator:
     """Owns the backend, graph runner and pinned staging for one model + pool."""
 
@@ -89,6 +138,8 @@ class BatchGenerator:
         self.graphs = BatchDecodeGraphRunner(weights, pool, self.backend)
         self._tables = _PinnedRing(4, (3, 4 * pool.capacity_pages + 1), torch.int32)
         self._inputs = _PinnedRing(4, (4, 4096), torch.int64)
+        self._reserves: dict[int, PageReserve] = {}  # batch -> rings (their pointers are in the graphs)
+        self.reserve_slots = 3
 
     def _plan(self, requests) -> None:
         indptr, indices, last = self.pool.tables(requests)
@@ -122,12 +173,17 @@ class BatchGenerator:
 
     @torch.no_grad()
     def generate(self, requests: list[Request], first_tokens: torch.Tensor, steps: int,
-                 adapters: list[int] | None = None) -> GenerateResult:
+                 adapters: list[int] | None = None, device_tables: bool = False) -> GenerateResult:
         """Decode ``steps`` greedy tokens for rows whose prompts are prefilled.
 
         first_tokens: [B] int64 on the device, the token each row decodes
-        first (the greedy pick of the prefill logits).
+        first (the greedy pick of the prefill logits).  With
+        ``device_tables`` the page table is uploaded once and then grown on
+        the device inside the step (pl_page_table_advance); the host only
+        refills the page reserve about once per page of steps.
         """
+        if device_tables:
+            return self._generate_device_tables(requests, first_tokens, steps, adapters)
         B = len(requests)
         dev = self.pool.cache.device
         adapters = adapters or [0] * B
@@ -168,6 +224,50 @@ class BatchGenerator:
         return GenerateResult(tokens=history.t().cpu(), decode_seconds=dt, prefill_seconds=0.0, steps=steps,
                               batch=B, used_graph=entry is not None, graph_captures=self.graphs.capture_count,
                               graph_replays=self.graphs.replay_count, extra={"capture_seconds": capture_s})
+
+
+    def _generate_device_tables(self, requests, first_tokens, steps, adapters) -> GenerateResult:
+        B = len(requests)
+        dev = self.pool.cache.device
+        adapters = adapters or [0] * B
+        history = torch.empty((steps, B), dtype=torch.int64, device=dev)
+        reserve = self._reserves.get(B)
+        if reserve is None:
+            reserve = self._reserves[B] = PageReserve(B, self.reserve_slots, dev)
+        reserve.reset()
+        feeder = _ReserveFeeder(self.pool, requests, reserve, steps)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        capture_s = 0.0
+        self._plan(requests)  # the table of the prompts; the device grows it from here
+        entry = None
+        if self.use_graph:
+            tc = time.perf_counter()
+            n_before = self.graphs.capture_count
+            entry = self.graphs.entry(B, reserve)
+            if self.graphs.capture_count != n_before:
+                torch.cuda.synchronize(dev)
+                capture_s = time.perf_counter() - tc
+        ctx = entry.ctx if entry is not None else DecodeContext(B, dev)
+        ctx.adapter_ids.copy_(torch.tensor(adapters, dtype=torch.int32))
+        ctx.tokens.copy_(first_tokens)
+        for step in range(steps):
+            feeder.before_step(step)
+            if step:
+                ctx.tokens.copy_(ctx.next_tokens)
+            if entry is not None:
+                self.graphs.replay(entry)
+            else:
+                self.backend.advance_decode(reserve, ctx.positions, ctx.page_id, ctx.page_offset)
+                decode_step_static(self.weights, self.pool, self.backend, ctx)
+            history[step].copy_(ctx.next_tokens)
+        torch.cuda.synchronize(dev)
+        dt = time.perf_counter() - t0 - capture_s
+        reserve.check()
+        return GenerateResult(tokens=history.t().cpu(), decode_seconds=dt, prefill_seconds=0.0, steps=steps,
+                              batch=B, used_graph=entry is not None, graph_captures=self.graphs.capture_count,
+                              graph_replays=self.graphs.replay_count,
+                              extra={"capture_seconds": capture_s, "reserve_uploads": feeder.uploads})
 
 
 def prefill_requests(weights: DecoderWeights, pool: PagedKVPool, prompts: list[torch.Tensor],

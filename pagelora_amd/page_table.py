@@ -223,3 +223,124 @@ class PageTableBuffer(BatchPageTableBuffer):
 
     def __init__(self, *, page_size: int, device: torch.device | str, initial_capacity: int = 16) -> None:
         super().__init__(page_size=page_size, device=device, initial_rows=1, initial_pages=initial_capacity)
+
+
+# ------------------------------------------------ device-side advance ---
+# Status bits written by pl_page_table_advance.
+ADVANCE_MISSING_PAGE = 1  # a row needed a page and its reserve slot held -1
+ADVANCE_NO_ROOM = 2       # the table would outgrow its indices buffer
+ADVANCE_BAD_TABLE = 4     # indptr decreasing / out of range, or a bad last_page_len
+
+MAX_ADVANCE_ROWS = 4096
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, shape=None, min_numel: int = 0) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be on a ROCm device")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    if t.numel() < min_numel:
+        raise ValueError(f"{name} needs at least {min_numel} elements")
+
+
+def page_table_advance(
+    paged_kv_indptr: torch.Tensor,
+    paged_kv_indices: torch.Tensor,
+    paged_kv_last_page_len: torch.Tensor,
+    page_size: int,
+    reserve: torch.Tensor,
+    reserve_head: torch.Tensor,
+    positions: torch.Tensor,
+    page_id: torch.Tensor,
+    page_offset: torch.Tensor,
+    status: torch.Tensor,
+) -> None:
+    """Append one decode token to every row of a device page table, in place.
+
+    The device-side replacement of the reference's per-step
+    ``reserve_chunk(request, 1)`` + ``update_from_batch_spans`` (generation.py:
+    1011-1035; paged_kv_store.py:113-190; flashinfer_page_table.py:89-121):
+    a row whose last page is full (or that has none) takes its next page from
+    ``reserve[b, reserve_head[b] % slots]`` (int32, the slot is then set to
+    -1); every row's token position and KV slot go to ``positions`` /
+    ``page_id`` / ``page_offset`` (int64 [B]).  Errors found on the device
+    set bits of ``status[0]`` (ADVANCE_*) and leave the table unchanged.
+    Enqueued on the current stream; nothing is read back.
+    """
+    from . import _lib
+
+    lib = _lib.load()
+    batch = paged_kv_last_page_len.numel()
+    if batch > MAX_ADVANCE_ROWS:
+        raise NotImplementedError(f"batch {batch} exceeds {MAX_ADVANCE_ROWS} rows")
+    _need(paged_kv_indptr, "paged_kv_indptr", torch.int32, (batch + 1,))
+    _need(paged_kv_indices, "paged_kv_indices", torch.int32, min_numel=1)
+    _need(paged_kv_last_page_len, "paged_kv_last_page_len", torch.int32, (batch,))
+    if reserve.dim() != 2 or reserve.shape[0] != batch or reserve.shape[1] < 1:
+        raise ValueError(f"reserve must be [batch={batch}, slots >= 1], got {tuple(reserve.shape)}")
+    _need(reserve, "reserve", torch.int32)
+    _need(reserve_head, "reserve_head", torch.int32, (batch,))
+    for name, t in (("positions", positions), ("page_id", page_id), ("page_offset", page_offset)):
+        _need(t, name, torch.int64, (batch,))
+    _need(status, "status", torch.int32, min_numel=1)
+    st = lib.pl_page_table_advance(
+        paged_kv_indptr.data_ptr(), paged_kv_indices.data_ptr(), paged_kv_indices.numel(),
+        paged_kv_last_page_len.data_ptr(), batch, int(page_size), reserve.data_ptr(), reserve.shape[1],
+        reserve_head.data_ptr(), positions.data_ptr(), page_id.data_ptr(), page_offset.data_ptr(),
+        status.data_ptr(), _lib.stream_handle(paged_kv_indptr.device),
+    )
+    _lib.check(st, "pl_page_table_advance")
+
+
+class PageReserve:
+    """Per-row rings of pages the device takes as decode rows grow.
+
+    ``reserve[b, s]`` holds a page id or -1, ``head[b]`` counts the pages
+    row b has taken (its next page is slot ``head[b] % slots``), ``status``
+    collects the ADVANCE_* bits.  The host writes whole ring snapshots with
+    :meth:`upload` (one asynchronous copy from pinned memory); a snapshot
+    must repeat every page the device has not taken yet, in its slot.
+    """
+
+    def __init__(self, batch: int, slots: int, device) -> None:
+        if batch < 1 or slots < 1:
+            raise ValueError("batch and slots must be >= 1")
+        self.batch, self.slots = int(batch), int(slots)
+        self.device = torch.device(device)
+        self.reserve = torch.full((self.batch, self.slots), -1, dtype=torch.int32, device=self.device)
+        self.head = torch.zeros(self.batch, dtype=torch.int32, device=self.device)
+        self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._stage = [torch.empty((self.batch, self.slots), dtype=torch.int32, pin_memory=True) for _ in range(2)]
+        self._events: list = [None, None]
+        self._next = 0
+
+    def reset(self) -> None:
+        """Empty rings, zero heads and status (enqueued on the current stream)."""
+        self.reserve.fill_(-1)
+        self.head.zero_()
+        self.status.zero_()
+
+    def upload(self, ring: np.ndarray) -> None:
+        """Copy a host snapshot [batch, slots] of the rings to the device."""
+        i = self._next
+        self._next ^= 1
+        if self._events[i] is not None:
+            self._events[i].synchronize()  # the copy that last read this staging buffer has run
+        self._stage[i].numpy()[:] = ring
+        self.reserve.copy_(self._stage[i], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        self._events[i] = ev
+
+    def check(self) -> None:
+        """Raise if any advance since the last reset failed (reads back: synchronizes)."""
+        bits = int(self.status.item())
+        if bits:
+            what = [n for b, n in ((ADVANCE_MISSING_PAGE, "a row found no reserved page"),
+                                   (ADVANCE_NO_ROOM, "the page table outgrew its buffer"),
+                                   (ADVANCE_BAD_TABLE, "the page table was malformed")) if bits & b]
+            raise RuntimeError("device page-table advance failed: " + "; ".join(what))

@@ -157,6 +157,29 @@ def test_graph_replay_matches_eager(gpu_device):
     assert results[1].graph_captures == 1 and results[1].graph_replays == 12
 
 
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_device_tables_match_host_tables(gpu_device, use_graph):
+    # 40 steps carry every row (37, 49 and 33 tokens) across a page boundary;
+    # the device-grown table must give the same tokens as host packing.
+    steps = 40
+    w, pool, reqs, first, _ = _setup(gpu_device)
+    ref = BatchGenerator(w, pool, workspace_mb=8, use_graph=False).generate(reqs, first, steps, [0, 1, 1])
+    w, pool, reqs, first, _ = _setup(gpu_device)
+    gen = BatchGenerator(w, pool, workspace_mb=8, use_graph=use_graph)
+    res = gen.generate(reqs, first, steps, [0, 1, 1], device_tables=True)
+    assert res.used_graph == use_graph
+    assert torch.equal(res.tokens, ref.tokens)
+    # the table grown on the device is the host's table of the grown rows
+    indptr, indices, last = pool.tables(reqs)
+    ip_buf, ind_buf, last_buf = gen.backend._decode_graph_buffers
+    assert ip_buf.tolist() == indptr.tolist()
+    assert ind_buf[: indptr[-1]].tolist() == indices.tolist()
+    assert last_buf.tolist() == last.tolist()
+    assert res.extra["reserve_uploads"] <= steps // 16 + 2
+    if use_graph:
+        assert res.graph_captures == 1 and res.graph_replays == steps
+
+
 def _lora_seq(x, W, lora, adapter, s):
     A, Bm = lora
     return F.linear(x, W) + F.linear(F.linear(x, A[adapter]), Bm[adapter]) * s
