@@ -185,7 +185,10 @@ def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_step
     behind a shared ``prefix_len``-token prefix in shared pages plus their own
     ``suffix_len`` random-id tokens, then ``steps`` greedy steps under hipGraph
     replay.  tok/s = generated tokens / decode seconds (the graph is captured
-    in a short warm-up call first, outside the timed region)."""
+    in a short warm-up call first, outside the timed region).  Timed twice:
+    with the page table packed on the host and uploaded every step, then
+    with it grown on the device inside the captured step (``tok_per_s``,
+    the default path), each after its own warm-up."""
     import torch
 
     from pagelora_amd.decoder import QWEN3_8B, DecoderWeights
@@ -195,7 +198,7 @@ def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_step
     cfg = QWEN3_8B
     w = DecoderWeights(cfg, n_adapters=1, device=device, seed=0)
     ps = 16
-    pages = (prefix_len + rows * (suffix_len + steps + warm_steps + 16)) // ps + 8 * rows + 8
+    pages = (prefix_len + rows * (suffix_len + 2 * (steps + warm_steps) + 16)) // ps + 8 * rows + 8
     pool = PagedKVPool(num_layers=cfg.num_layers, capacity_pages=pages, page_size=ps, num_kv_heads=cfg.num_kv_heads,
                        head_dim=cfg.head_dim, dtype=torch.bfloat16, device=device)
     g = torch.Generator().manual_seed(seed)
@@ -207,15 +210,23 @@ def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_step
     prefill_s = time.perf_counter() - t
     gen = BatchGenerator(w, pool, use_graph=True)
     warm = gen.generate(reqs, first, steps=warm_steps)
-    res = gen.generate(reqs, warm.tokens[:, -1].to(device), steps=steps)
+    host = gen.generate(reqs, warm.tokens[:, -1].to(device), steps=steps)
+    context_host = reqs[0].length - steps
+    warm = gen.generate(reqs, host.tokens[:, -1].to(device), steps=warm_steps, device_tables=True)
+    context = reqs[0].length
+    res = gen.generate(reqs, warm.tokens[:, -1].to(device), steps=steps, device_tables=True)
     out = {
         "tok_per_s": round(res.decode_tokens_per_s, 1),
         "ms_per_step": round(res.decode_seconds / steps * 1e3, 3),
         "rows": rows,
-        "context_at_start": prefix_len + suffix_len + warm_steps,
+        "context_at_start": context,
         "steps": steps,
         "hip_graph": res.used_graph,
         "graph_captures": res.graph_captures,
+        "page_table": "device (reserve uploads: %d)" % res.extra["reserve_uploads"],
+        "host_tables": {"tok_per_s": round(host.decode_tokens_per_s, 1),
+                        "ms_per_step": round(host.decode_seconds / steps * 1e3, 3),
+                        "context_at_start": context_host},
         "prefill_s": round(prefill_s, 2),
     }
     del w, pool, gen

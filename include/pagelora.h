@@ -267,7 +267,20 @@ int pl_qk_norm_rope_append(const void* qkv, int64_t ld_qkv,
  * is LoRALinear.forward / _packed_lora_delta's module output
  * (multilora/linear.py:226-231, model/flashinfer/packed_ops.py:314-325)
  * without a separate expand kernel.
+ *
+ * b_layout says how B is stored.  PL_LORA_B_ROWS: row-major
+ * [num_adapters, out_features, rank], the nn.Linear weight of lora_B.
+ * PL_LORA_B_CHUNK8 (out_features % 8 == 0): the same values as
+ * [num_adapters, nblk, 8, rank / 8, 64, 8] with nblk = ceil(out_features /
+ * 512), element (a, j, i, k, l, e) = B[a][8 (64 j + l) + i][8k + e] (zero
+ * past out_features).  A wave whose 64 threads own 8 consecutive output
+ * columns each reads its block j as one contiguous region, every load
+ * instruction 1 KiB contiguous, where the row-major layout makes each
+ * thread's 16-byte piece a separate cache line.
  */
+#define PL_LORA_B_ROWS 0
+#define PL_LORA_B_CHUNK8 1
+
 typedef struct {
   const void* y;
   int64_t ldy;
@@ -276,6 +289,7 @@ typedef struct {
   int out_features;
   int rank;
   float scale;
+  int b_layout;
 } pl_lora_up;
 
 /*

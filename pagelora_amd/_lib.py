@@ -88,8 +88,12 @@ class LoraUp(ctypes.Structure):
         ("out_features", ctypes.c_int),
         ("rank", ctypes.c_int),
         ("scale", ctypes.c_float),
+        ("b_layout", ctypes.c_int),
     ]
 
+
+PL_LORA_B_ROWS = 0
+PL_LORA_B_CHUNK8 = 1
 
 PL_LINEAR_MAX_TOKENS = 64
 

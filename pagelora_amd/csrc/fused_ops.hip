@@ -72,10 +72,22 @@ struct LoraUp {
   const void* y;
   int64_t ldy;
   int y_offset;
-  const void* B;  // [n_adapters, out_features, rank]
+  const void* B;  // b_chunk8 ? [n_adapters, ceil(out/512), 8, rank/8, 64, 8] : [n_adapters, out, rank]
   int out_features, rank;
   float scale;
+  int b_chunk8;
 };
+
+// The 16-byte piece kb (ranks 8kb .. 8kb+7) of B[a][c0 + i] (c0 % 8 == 0 in
+// the chunked layout: chunk c0 / 8 is lane l of block j).  The layout flag
+// is wave-uniform: the two addresses are a select, not a branch.
+template <typename T, int R>
+__device__ __forceinline__ const uint4* lora_b_piece(const LoraUp& m, int a, int c0, int i, int kb) {
+  const int64_t rows = ((int64_t)a * m.out_features + c0 + i) * R + kb * 8;
+  const int nblk = (m.out_features + 511) / 512, ch = c0 / 8;
+  const int64_t chunk = (((((int64_t)a * nblk + (ch >> 6)) * 8 + i) * (R / 8) + kb) * 64 + (ch & 63)) * 8;
+  return reinterpret_cast<const uint4*>((const T*)m.B + (m.b_chunk8 ? chunk : rows));
+}
 
 // One token's rank-space intermediate y[t, a, :], kept packed (R/8 x 16 B).
 template <int R>
@@ -101,16 +113,31 @@ struct SplitIn {
   int64_t ld, plane;
 };
 
+// Planes are read kPlaneBatch at a time with every load of a batch issued
+// before the first add (an index past the last plane re-reads the last one
+// and is not added), so a split row costs one memory round trip, not one per
+// plane.  The sum still runs over planes 0, 1, .. in order.
+constexpr int kPlaneBatch = 4;
+
 // 8 consecutive elements (c % 8 == 0; ld, plane multiples of 8, p 16-byte aligned).
 template <typename T>
 __device__ __forceinline__ void load8_split(const SplitIn& sp, int64_t t, int c, float (&f)[8]) {
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int z = 0; z < sp.splits; ++z) {
-    const float* q = sp.p + z * sp.plane + t * sp.ld + c;
-    const float4 a = *reinterpret_cast<const float4*>(q);
-    const float4 b = *reinterpret_cast<const float4*>(q + 4);
-    acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
-    acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+  for (int z0 = 0; z0 < sp.splits; z0 += kPlaneBatch) {
+    float4 a[kPlaneBatch], b[kPlaneBatch];
+#pragma unroll
+    for (int k = 0; k < kPlaneBatch; ++k) {
+      const float* q = sp.p + min(z0 + k, sp.splits - 1) * sp.plane + t * sp.ld + c;
+      a[k] = *reinterpret_cast<const float4*>(q);
+      b[k] = *reinterpret_cast<const float4*>(q + 4);
+    }
+#pragma unroll
+    for (int k = 0; k < kPlaneBatch; ++k) {
+      if (z0 + k < sp.splits) {
+        acc[0] += a[k].x; acc[1] += a[k].y; acc[2] += a[k].z; acc[3] += a[k].w;
+        acc[4] += b[k].x; acc[5] += b[k].y; acc[6] += b[k].z; acc[7] += b[k].w;
+      }
+    }
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) f[i] = through<T>(acc[i]);
@@ -119,7 +146,14 @@ __device__ __forceinline__ void load8_split(const SplitIn& sp, int64_t t, int c,
 template <typename T>
 __device__ __forceinline__ float load1_split(const SplitIn& sp, int64_t t, int c) {
   float acc = 0.f;
-  for (int z = 0; z < sp.splits; ++z) acc += sp.p[z * sp.plane + t * sp.ld + c];
+  for (int z0 = 0; z0 < sp.splits; z0 += kPlaneBatch) {
+    float v[kPlaneBatch];
+#pragma unroll
+    for (int k = 0; k < kPlaneBatch; ++k) v[k] = sp.p[min(z0 + k, sp.splits - 1) * sp.plane + t * sp.ld + c];
+#pragma unroll
+    for (int k = 0; k < kPlaneBatch; ++k)
+      if (z0 + k < sp.splits) acc += v[k];
+  }
   return through<T>(acc);
 }
 
@@ -147,7 +181,6 @@ __device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float acc)
 template <typename T, int R>
 __device__ __forceinline__ void lora_delta8(const LoraUp& m, int a, int c0, const LoraRow<R>& y, float (&d)[8]) {
   constexpr int KB = R >= 16 ? 2 : 1;  // 16-byte pieces of a B row per pass
-  const T* b0 = (const T*)m.B + ((int64_t)a * m.out_features + c0) * R;
 #pragma unroll
   for (int i = 0; i < 8; ++i) d[i] = 0.f;
   // ranks above 16: one 16-rank pass in flight at a time (bounded registers)
@@ -158,7 +191,7 @@ __device__ __forceinline__ void lora_delta8(const LoraUp& m, int a, int c0, cons
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int k = 0; k < KB; ++k) b[i][k] = *reinterpret_cast<const uint4*>(b0 + i * R + (kb + k) * 8);
+      for (int k = 0; k < KB; ++k) b[i][k] = *lora_b_piece<T, R>(m, a, c0, i, kb + k);
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -171,10 +204,9 @@ __device__ __forceinline__ void lora_delta8(const LoraUp& m, int a, int c0, cons
 // scale * y . B[a][c]^T for one output column.
 template <typename T, int R>
 __device__ __forceinline__ float lora_delta1(const LoraUp& m, int a, int c, const LoraRow<R>& y) {
-  const T* b0 = (const T*)m.B + ((int64_t)a * m.out_features + c) * R;
   uint4 b[R / 8];
 #pragma unroll
-  for (int v = 0; v < R / 8; ++v) b[v] = *reinterpret_cast<const uint4*>(b0 + v * 8);
+  for (int v = 0; v < R / 8; ++v) b[v] = *lora_b_piece<T, R>(m, a, c & ~7, c & 7, v);
   float acc = 0.f;
 #pragma unroll
   for (int v = 0; v < R / 8; ++v) acc = dot8<T>(y.v[v], b[v], acc);
@@ -210,7 +242,9 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_kernel(
   const int row = blockIdx.x;
   const int chunks = hidden / 8;
   float v[kMaxChunks][8], xa[kMaxChunks][8], wf[kMaxChunks][8];
-  // every load that does not depend on the adapter id first
+  // The adapter id first: the y and B loads depend on it, and with it in
+  // hand they are issued together with the row's own loads.
+  const int a_raw = R > 0 ? ids[row] : -1;
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {
     const int idx = (threadIdx.x + c * THREADS) * 8;
@@ -224,22 +258,23 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_kernel(
     }
   }
   if constexpr (R > 0) {
-    const int a = ids[row];
-    if (a >= 0 && a < n_adapters) {
-      LoraRow<R> y;
-      if (xs.splits > 0)
-        load_y_split<T, R>(xs, lora, row, a, y);
-      else
-        load_y<T, R>(lora, row, a, y);
+    // No branch on the id before the loads: an id outside [0, n_adapters)
+    // reads adapter 0 (n_adapters >= 1) and its delta is not applied.
+    const bool a_ok = a_raw >= 0 && a_raw < n_adapters;
+    const int a = a_ok ? a_raw : 0;
+    LoraRow<R> y;
+    if (xs.splits > 0)
+      load_y_split<T, R>(xs, lora, row, a, y);
+    else
+      load_y<T, R>(lora, row, a, y);
 #pragma unroll
-      for (int c = 0; c < kMaxChunks; ++c) {
-        const int idx = (threadIdx.x + c * THREADS) * 8;
-        if (threadIdx.x + c * THREADS < chunks) {
-          float d[8];
-          lora_delta8<T, R>(lora, a, idx, y, d);
+    for (int c = 0; c < kMaxChunks; ++c) {
+      const int idx = (threadIdx.x + c * THREADS) * 8;
+      if (threadIdx.x + c * THREADS < chunks) {
+        float d[8];
+        lora_delta8<T, R>(lora, a, idx, y, d);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) xa[c][i] = through<T>(xa[c][i] + d[i]);
-        }
+        for (int i = 0; i < 8; ++i) xa[c][i] = a_ok ? through<T>(xa[c][i] + d[i]) : xa[c][i];
       }
     }
   }
@@ -271,6 +306,129 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_kernel(
       store_row8<T>(out + row * ldo + idx, v[c]);
     }
   }
+}
+
+// The decode-sized add + RMSNorm: one workgroup per row and exactly one
+// 8-column chunk per thread (blockDim = hidden / 8 rounded up to whole
+// waves, hidden <= 8192, 16-bit T).  Every load is issued before the first
+// wait: the row's own loads together with the adapter id, then (needing only
+// the id) the B rows and y, so the kernel costs two memory round trips.
+// P = 0: x is a T row; P = 1..4: x (and y) are exactly P split-K planes,
+// summed over planes 0, 1, .. in order.  Same arithmetic and roundings as
+// rmsnorm_kernel<T, true, R>.
+template <typename T, int P>
+__device__ __forceinline__ void load8_planes(const SplitIn& sp, int64_t t, int c, float (&f)[8]) {
+  float4 a[P], b[P];
+#pragma unroll
+  for (int k = 0; k < P; ++k) {
+    const float* q = sp.p + k * sp.plane + t * sp.ld + c;
+    a[k] = *reinterpret_cast<const float4*>(q);
+    b[k] = *reinterpret_cast<const float4*>(q + 4);
+  }
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < P; ++k) {
+    acc[0] += a[k].x; acc[1] += a[k].y; acc[2] += a[k].z; acc[3] += a[k].w;
+    acc[4] += b[k].x; acc[5] += b[k].y; acc[6] += b[k].z; acc[7] += b[k].w;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = through<T>(acc[i]);
+}
+
+constexpr int kRowNormMaxHidden = 8192;
+
+template <typename T, int R, int P>
+__global__ __launch_bounds__(1024) void add_rmsnorm_row_kernel(
+    T* __restrict__ r, int64_t ldr, const T* __restrict__ x, int64_t ldx, const T* __restrict__ w,
+    T* __restrict__ out, int64_t ldo, int hidden, float eps, LoraUp lora, const int32_t* __restrict__ ids,
+    int n_adapters, SplitIn xs) {
+  __shared__ float s_red[1024 / kWave];
+  const int row = blockIdx.x;
+  const int a_raw = R > 0 ? ids[row] : -1;
+  const bool live = (int)threadIdx.x * 8 < hidden;
+  const int idx = live ? threadIdx.x * 8 : hidden - 8;  // idle threads re-read the last chunk
+  float v[8], xa[8], wf[8];
+  if constexpr (P > 0)
+    load8_planes<T, P>(xs, row, idx, xa);
+  else
+    load_row8<T>(x + row * ldx + idx, xa);
+  load_row8<T>(r + row * ldr + idx, v);
+  load_row8<T>(w + idx, wf);
+  if constexpr (R > 0) {
+    // no branch on the id before the loads: an id outside [0, n_adapters)
+    // reads adapter 0 (n_adapters >= 1) and its delta is not applied
+    const bool a_ok = a_raw >= 0 && a_raw < n_adapters;
+    const int a = a_ok ? a_raw : 0;
+    float d[8];
+    if constexpr (R <= 16) {
+      // B rows first (they need only the id), then y, then the dots
+      uint4 b[8][R / 8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int k = 0; k < R / 8; ++k) b[i][k] = *lora_b_piece<T, R>(lora, a, idx, i, k);
+      // keep the scheduler from moving y's loads (and the wait for them)
+      // in front of the B loads: both depend only on the id
+      __builtin_amdgcn_sched_barrier(0);
+      LoraRow<R> y;
+      if constexpr (P > 0) {
+#pragma unroll
+        for (int k = 0; k < R / 8; ++k) {
+          float f[8];
+          load8_planes<T, P>(xs, row, lora.y_offset + a * R + k * 8, f);
+          y.v[k] = make_uint4(pack2<T>(f[0], f[1]), pack2<T>(f[2], f[3]), pack2<T>(f[4], f[5]),
+                              pack2<T>(f[6], f[7]));
+        }
+      } else {
+        load_y<T, R>(lora, row, a, y);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < R / 8; ++k) acc = dot8<T>(y.v[k], b[i][k], acc);
+        d[i] = acc * lora.scale;
+      }
+    } else {
+      LoraRow<R> y;
+      if constexpr (P > 0) {
+#pragma unroll
+        for (int k = 0; k < R / 8; ++k) {
+          float f[8];
+          load8_planes<T, P>(xs, row, lora.y_offset + a * R + k * 8, f);
+          y.v[k] = make_uint4(pack2<T>(f[0], f[1]), pack2<T>(f[2], f[3]), pack2<T>(f[4], f[5]),
+                              pack2<T>(f[6], f[7]));
+        }
+      } else {
+        load_y<T, R>(lora, row, a, y);
+      }
+      lora_delta8<T, R>(lora, a, idx, y, d);
+    }
+    // x + -0.f == x exactly and xa already holds a T value, so a row without
+    // an adapter keeps its bits; the delta's loads stay unconditional.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xa[i] = through<T>(xa[i] + (a_ok ? d[i] : -0.f));
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[i] = through<T>(v[i] + xa[i]);
+    ss = fmaf(v[i], v[i], ss);
+  }
+  if (live) store_row8<T>(r + row * ldr + idx, v);
+  ss = live ? ss : 0.f;
+  // block sum over the launched waves
+  ss = wave_sum(ss);
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  if (lane == 0) s_red[wave] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  const int nw = blockDim.x / kWave;
+  for (int i = 0; i < nw; ++i) tot += s_red[i];
+  const float rstd = rsqrtf(tot / (float)hidden + eps);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = v[i] * rstd * wf[i];
+  if (live) store_row8<T>(out + row * ldo + idx, v);
 }
 
 // One 8-column chunk per thread.  R > 0: lg / lu are the gate and up
@@ -438,6 +596,13 @@ using namespace pl::fused;
 // Host copy of a pl_lora_up into the device struct, with its checks.
 // With `split`, y is read from the split-K planes (h->y may be NULL) and its
 // columns y_offset + n_adapters*rank must fit the planes' row.
+static int b_layout_check(const pl_lora_up* h, const char* what) {
+  if (h->b_layout == PL_LORA_B_ROWS) return ok();
+  if (h->b_layout != PL_LORA_B_CHUNK8) return fail(PL_ERR_INVALID, "%s: unknown b_layout %d", what, h->b_layout);
+  if (h->out_features % 8) return fail(PL_ERR_INVALID, "%s: PL_LORA_B_CHUNK8 needs out_features %% 8 == 0", what);
+  return ok();
+}
+
 static int lora_up_from(const pl_lora_up* h, int need_out, LoraUp* d, const char* what,
                         const SplitIn* split = nullptr, int n_adapters = 0) {
   if (split != nullptr) {
@@ -449,7 +614,8 @@ static int lora_up_from(const pl_lora_up* h, int need_out, LoraUp* d, const char
     if (h->y_offset < 0 || h->y_offset % 8 || (int64_t)h->y_offset + (int64_t)n_adapters * h->rank > split->ld)
       return fail(PL_ERR_INVALID, "%s: y columns outside the split planes' rows", what);
     if ((uintptr_t)h->B % 16) return fail(PL_ERR_INVALID, "%s: B must be 16-byte aligned", what);
-    *d = LoraUp{nullptr, 0, h->y_offset, h->B, h->out_features, h->rank, h->scale};
+    if (const int st = b_layout_check(h, what)) return st;
+    *d = LoraUp{nullptr, 0, h->y_offset, h->B, h->out_features, h->rank, h->scale, h->b_layout};
     return ok();
   }
   if (!h->y || !h->B) return fail(PL_ERR_INVALID, "%s: null y or B", what);
@@ -460,7 +626,8 @@ static int lora_up_from(const pl_lora_up* h, int need_out, LoraUp* d, const char
   if (h->y_offset < 0 || h->ldy <= 0 || h->y_offset % 8 || h->ldy % 8 || (uintptr_t)h->y % 16)
     return fail(PL_ERR_INVALID, "%s: y must be 16-byte aligned with ldy and y_offset multiples of 8", what);
   if ((uintptr_t)h->B % 16) return fail(PL_ERR_INVALID, "%s: B must be 16-byte aligned", what);
-  *d = LoraUp{h->y, h->ldy, h->y_offset, h->B, h->out_features, h->rank, h->scale};
+  if (const int st = b_layout_check(h, what)) return st;
+  *d = LoraUp{h->y, h->ldy, h->y_offset, h->B, h->out_features, h->rank, h->scale, h->b_layout};
   return ok();
 }
 
@@ -485,10 +652,46 @@ static void launch_norm_t(void* r, int64_t ldr, const void* x, int64_t ldx, cons
                      (const T*)x, ldx, (const T*)w, (T*)out, ldo, hidden, eps, lu, ids, na, xs);
 }
 
+template <typename T, int R, int P>
+static void launch_row_norm_t(void* r, int64_t ldr, const void* x, int64_t ldx, const void* w, void* out,
+                              int64_t ldo, int rows, int hidden, float eps, const LoraUp& lu, const int32_t* ids,
+                              int na, const SplitIn& xs, hipStream_t s) {
+  const int threads = (hidden / 8 + kWave - 1) / kWave * kWave;
+  hipLaunchKernelGGL((add_rmsnorm_row_kernel<T, R, P>), dim3(rows), dim3(threads), 0, s, (T*)r, ldr, (const T*)x,
+                     ldx, (const T*)w, (T*)out, ldo, hidden, eps, lu, ids, na, xs);
+}
+
+template <typename T, int P>
+static void launch_row_norm_p(int rank, void* r, int64_t ldr, const void* x, int64_t ldx, const void* w, void* out,
+                              int64_t ldo, int rows, int hidden, float eps, const LoraUp& lu, const int32_t* ids,
+                              int na, const SplitIn& xs, hipStream_t s) {
+  switch (rank) {
+    case 0: launch_row_norm_t<T, 0, P>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+    case 8: launch_row_norm_t<T, 8, P>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+    case 16: launch_row_norm_t<T, 16, P>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+    case 32: launch_row_norm_t<T, 32, P>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+    case 64: launch_row_norm_t<T, 64, P>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+  }
+}
+
 template <typename T>
 static int launch_norm(bool add, int rank, void* r, int64_t ldr, const void* x, int64_t ldx, const void* w,
                        void* out, int64_t ldo, int rows, int hidden, float eps, const LoraUp& lu,
                        const int32_t* ids, int na, const SplitIn& xs, hipStream_t s) {
+  if constexpr (sizeof(T) == 2) {
+    // decode-sized rows: the single-chunk kernel (two memory round trips)
+    if (add && hidden <= kRowNormMaxHidden && xs.splits <= 4) {
+      switch (xs.splits) {
+        case 0: launch_row_norm_p<T, 0>(rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+        case 1: launch_row_norm_p<T, 1>(rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+        case 2: launch_row_norm_p<T, 2>(rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+        case 3: launch_row_norm_p<T, 3>(rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+        default: launch_row_norm_p<T, 4>(rank, r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s); break;
+      }
+      PL_LAUNCH_CHECK("add_rmsnorm_row_kernel");
+      return ok();
+    }
+  }
   if (rank == 0) {
     if (add)
       launch_norm_t<T, true, 0>(r, ldr, x, ldx, w, out, ldo, rows, hidden, eps, lu, ids, na, xs, s);

@@ -67,11 +67,14 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) {
 __device__ __forceinline__ float bf16_hi(uint32_t w) {
   return __uint_as_float(w & 0xffff0000u);
 }
+// Round to nearest even; a NaN stays a (quiet) NaN.  Written as a select, not
+// a branch: on wave-uniform values a branch becomes a scalar jump that splits
+// the block and keeps loads after it from being issued early.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // NaN stays NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t qnan = (u >> 16) | 0x40u;
+  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? qnan : rne);
 }
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));

@@ -26,6 +26,23 @@ def _rows2d(t: torch.Tensor, name: str) -> None:
         raise ValueError(f"{name} must be 2-D with unit column stride")
 
 
+def lora_b_chunk8(B: torch.Tensor) -> torch.Tensor:
+    """B [n, out, r] (or [out, r]) in the consumer-coalesced layout
+    PL_LORA_B_CHUNK8: [n, nblk, 8, r/8, 64, 8] with nblk = ceil(out/512) and
+    element (a, j, i, k, l, e) = B[a][8(64j + l) + i][8k + e], zero past
+    ``out``.  A wave whose threads own 8 output columns each reads its block
+    as one contiguous region, each load instruction 1 KiB contiguous."""
+    B3 = B if B.dim() == 3 else B.unsqueeze(0)
+    n, out, r = B3.shape
+    if out % 8 or r % 8:
+        raise ValueError("chunked LoRA B needs out_features and rank multiples of 8")
+    nblk = -(-out // 512)
+    padded = B3.new_zeros((n, nblk * 512, r))
+    padded[:, :out] = B3
+    # [n, j, l, i, k, e] -> [n, j, i, k, l, e]
+    return padded.reshape(n, nblk, 64, 8, r // 8, 8).permute(0, 1, 3, 4, 2, 5).contiguous()
+
+
 @dataclass
 class LoraUp:
     """The up-projection half of a no-merge LoRA module, applied by the kernel
@@ -34,8 +51,10 @@ class LoraUp:
     ``y`` is the producer GEMM's output row block ``[T, *]`` (a GEMM on the
     base weight with the adapters' A rows stacked under it); adapter a's
     rank-space intermediate sits at columns ``y_offset + a*r .. + r``.  ``B``
-    is ``[n_adapters, out, r]``.  The module output is
-    ``round(base + scale * y[a] . B[a]^T)`` (multilora/linear.py:226-231).
+    is ``[n_adapters, out, r]`` (row-major) or the same values from
+    :func:`lora_b_chunk8` (5-D, the layout the kernels read fastest).  The
+    module output is ``round(base + scale * y[a] . B[a]^T)``
+    (multilora/linear.py:226-231).
     """
 
     y: "torch.Tensor | SplitOutput"
@@ -43,27 +62,41 @@ class LoraUp:
     B: torch.Tensor
     scale: float
 
+    def _b_shape(self) -> tuple[int, int, int, int]:
+        """(n_adapters, out_features, rank, b_layout)."""
+        B = self.B
+        if B.dim() == 6:
+            # padded to whole 512-column blocks: the pad holds zeros and the
+            # kernels read only the columns they are asked for
+            n, nblk, eight, rk, lanes, e = B.shape
+            if eight != 8 or lanes != 64 or e != 8:
+                raise ValueError("a 6-D LoraUp.B must be lora_b_chunk8 output [n, ceil(out/512), 8, r/8, 64, 8]")
+            return n, nblk * 512, rk * 8, _lib.PL_LORA_B_CHUNK8
+        B3 = B if B.dim() == 3 else B.unsqueeze(0)
+        return B3.shape[0], B3.shape[1], B3.shape[2], _lib.PL_LORA_B_ROWS
+
     def struct(self) -> "_lib.LoraUp":
-        B = self.B if self.B.dim() == 3 else self.B.unsqueeze(0)
-        n, _, r = B.shape
+        n, out, r, layout = self._b_shape()
+        B = self.B
         if isinstance(self.y, SplitOutput):  # read from the split planes by the kernel
             if not B.is_contiguous() or B.dtype != self.y.dtype:
-                raise ValueError("LoraUp.B must be contiguous [n, out, r] of the model dtype")
+                raise ValueError("LoraUp.B must be contiguous and of the model dtype")
             if self.y_offset < 0 or self.y_offset + n * r > self.y.ld:
                 raise ValueError("LoraUp: y columns out of range")
-            return _lib.LoraUp(None, 0, int(self.y_offset), B.data_ptr(), int(B.shape[1]), int(r), float(self.scale))
+            return _lib.LoraUp(None, 0, int(self.y_offset), B.data_ptr(), int(out), int(r), float(self.scale),
+                               int(layout))
         if self.y.dim() != 2 or self.y.stride(1) != 1:
             raise ValueError("LoraUp.y must be 2-D with unit column stride")
         if not B.is_contiguous() or B.dtype != self.y.dtype:
-            raise ValueError("LoraUp.B must be contiguous [n, out, r] of y's dtype")
+            raise ValueError("LoraUp.B must be contiguous and of y's dtype")
         if self.y_offset < 0 or self.y_offset + n * r > self.y.shape[1]:
             raise ValueError("LoraUp: y columns out of range")
-        return _lib.LoraUp(self.y.data_ptr(), self.y.stride(0), int(self.y_offset), B.data_ptr(), int(B.shape[1]),
-                           int(r), float(self.scale))
+        return _lib.LoraUp(self.y.data_ptr(), self.y.stride(0), int(self.y_offset), B.data_ptr(), int(out), int(r),
+                           float(self.scale), int(layout))
 
     @property
     def n_adapters(self) -> int:
-        return self.B.shape[0] if self.B.dim() == 3 else 1
+        return self._b_shape()[0]
 
 
 def _lora_args(lora: Sequence[LoraUp], adapter_ids: torch.Tensor | None, rows: int):

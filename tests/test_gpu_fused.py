@@ -155,6 +155,34 @@ def test_add_rmsnorm_lora(gpu_device, dtype, hidden):
     _check2(out, want, dtype)
 
 
+@pytest.mark.parametrize("rank", [8, 32, 64])
+@pytest.mark.parametrize("hidden", [4096, 12288])
+def test_add_rmsnorm_lora_ranks(gpu_device, rank, hidden):
+    # every built rank, through the single-chunk kernel (4096) and the general one (12288)
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(rank + hidden)
+    rows = len(IDS)
+    full = torch.randn((rows, hidden + N_ADAPTERS * rank), generator=g).to(dtype)
+    B = (torch.randn((N_ADAPTERS, hidden, rank), generator=g) * 0.05).to(dtype)
+    r = torch.randn((rows, hidden), generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(dtype)
+    fd, rd = full.to(gpu_device), r.to(gpu_device)
+    ids = torch.tensor(IDS, dtype=torch.int32, device=gpu_device)
+    up = fused_ops.LoraUp(fd, hidden, B.to(gpu_device), SCALE)
+    out = fused_ops.add_rmsnorm(rd, fd[:, :hidden], w.to(gpu_device), 1e-6, lora=up, adapter_ids=ids)
+    torch.cuda.synchronize()
+    f = full.double().numpy()
+    x_eff = f[:, :hidden].copy()
+    for t, a in enumerate(IDS):
+        if 0 <= a < N_ADAPTERS:
+            y = f[t:t + 1, hidden + a * rank: hidden + (a + 1) * rank]
+            x_eff[t] += ol.lora_delta(y, np.eye(rank), B[a].double().numpy(), SCALE)[0]
+    x_eff = _round(dtype)(x_eff)
+    new_r, want = of.add_rmsnorm(r.double().numpy(), x_eff, w.double().numpy(), 1e-6, round_sum=_round(dtype))
+    _check2(rd, new_r, dtype)
+    _check2(out, want, dtype)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_silu_mul_lora(gpu_device, dtype):
     inter = 1024
@@ -238,9 +266,11 @@ def _random_split(g, splits, rows, cols, dtype, device):
     return SplitOutput(parts, cols, dtype)
 
 
-@pytest.mark.parametrize("splits", [1, 3, 4])
-def test_add_rmsnorm_lora_split_input_matches_summed_input(gpu_device, splits):
-    hidden, rows = 4096, len(IDS)
+# Splits 1-4 at hidden <= 8192 take the single-chunk decode kernel; 6 splits
+# and hidden 12288 take the general one.
+@pytest.mark.parametrize("splits,hidden", [(1, 4096), (2, 4096), (3, 4096), (4, 4096), (6, 4096), (3, 12288)])
+def test_add_rmsnorm_lora_split_input_matches_summed_input(gpu_device, splits, hidden):
+    rows = len(IDS)
     g = torch.Generator().manual_seed(splits)
     so = _random_split(g, splits, rows, hidden + N_ADAPTERS * RANK, torch.bfloat16, gpu_device)
     B = (torch.randn((N_ADAPTERS, hidden, RANK), generator=g) * 0.05).to(torch.bfloat16).to(gpu_device)
@@ -284,3 +314,61 @@ def test_qk_norm_rope_append_lora_split_input_matches_summed_input(gpu_device, s
         outs.append((q, cache))
     torch.cuda.synchronize()
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+# The chunked B layout (PL_LORA_B_CHUNK8) holds the same values in another
+# order: every consumer must give bit-identical results with it.
+@pytest.mark.parametrize("hidden,splits", [(4096, 0), (4096, 3), (12288, 0), (256, 2)])
+def test_lora_b_chunk8_add_rmsnorm_bitwise(gpu_device, hidden, splits):
+    rows, dev = len(IDS), gpu_device
+    g = torch.Generator().manual_seed(hidden + splits)
+    cols = hidden + N_ADAPTERS * RANK
+    if splits:
+        y = _random_split(g, splits, rows, cols, torch.bfloat16, dev)
+        x = y
+    else:
+        y = torch.randn((rows, cols), generator=g).to(torch.bfloat16).to(dev)
+        x = y[:, :hidden]
+    B = (torch.randn((N_ADAPTERS, hidden, RANK), generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    r0 = torch.randn((rows, hidden), generator=g).to(torch.bfloat16).to(dev)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(dev)
+    ids = torch.tensor(IDS, dtype=torch.int32, device=dev)
+    outs = []
+    for Bx in (B, fused_ops.lora_b_chunk8(B)):
+        r = r0.clone()
+        o = fused_ops.add_rmsnorm(r, x, w, 1e-6, lora=fused_ops.LoraUp(y, hidden, Bx, SCALE), adapter_ids=ids)
+        outs.append((r, o))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+def test_lora_b_chunk8_silu_and_qk_bitwise(gpu_device):
+    rows, dev, dtype = len(IDS), gpu_device, torch.bfloat16
+    g = torch.Generator().manual_seed(77)
+    inter = 1024
+    full, Bs, offs = _lora_inputs(g, rows, 2 * inter, [("gate", inter), ("up", inter)], dtype)
+    fd = full.to(dev)
+    ids = torch.tensor(IDS, dtype=torch.int32, device=dev)
+    res = []
+    for conv in (lambda b: b, fused_ops.lora_b_chunk8):
+        ups = tuple(fused_ops.LoraUp(fd, offs[m], conv(Bs[m].to(dev)), SCALE) for m in ("gate", "up"))
+        res.append(fused_ops.silu_mul(fd[:, : 2 * inter], lora=ups, adapter_ids=ids))
+    assert torch.equal(res[0], res[1])
+
+    hq, hkv, d, ps, pool = 8, 2, 128, 16, 10
+    qd, kd = hq * d, hkv * d
+    full, Bs, offs = _lora_inputs(g, rows, qd + 2 * kd, [("q", qd), ("k", kd), ("v", kd)], dtype)
+    fd = full.to(dev)
+    qw = torch.ones(d, dtype=dtype, device=dev)
+    pos = torch.tensor([0, 17, 4095, 40000, 5], device=dev)
+    pid = torch.tensor([3, 9, 0, 5, 7], device=dev)
+    off = torch.tensor([0, 15, 7, 1, 2], device=dev)
+    got = []
+    for conv in (lambda b: b, fused_ops.lora_b_chunk8):
+        cd = torch.zeros((pool, 2, ps, hkv, d), dtype=dtype, device=dev)
+        ups = tuple(fused_ops.LoraUp(fd, offs[m], conv(Bs[m].to(dev)), SCALE) for m in ("q", "k", "v"))
+        q = fused_ops.qk_norm_rope_append(fd[:, : qd + 2 * kd], qw, qw, pos, pid, off, cd, num_qo_heads=hq,
+                                          num_kv_heads=hkv, head_dim=d, page_size=ps, rope_theta=1e6, eps=1e-6,
+                                          lora=ups, adapter_ids=ids)
+        got.append((q, cd))
+    assert torch.equal(got[0][0], got[1][0]) and torch.equal(got[0][1], got[1][1])

@@ -111,3 +111,4 @@ def test_batch_buffer_reuses_tensors_until_growth():
     # Growth past capacity replaces the buffers (new data pointers).
     buf.update_from_batch_spans([[KVBlockSpan(i, 0, 4)] for i in range(5)])
     assert buf.signature() != sig
+
