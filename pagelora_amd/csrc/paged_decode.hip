@@ -40,6 +40,7 @@ struct Item {   // one split-KV work item; lives in the workspace
   int flags;    // bit0: row has a single item (write o directly)
                 // bit1: item holds the row's last (possibly partial) page
 };
+static_assert(sizeof(Item) == 16, "the decode kernel reads an item as one 16-byte load");
 
 struct Layout {
   size_t header, items, row_info, lse, partial_o, total;
@@ -311,6 +312,62 @@ struct DecodeWave {
   }
 };
 
+// Stream blocks [blk0, blk1) of an item (16 tokens each, the item's first
+// `ntok` tokens are real) through one wave's online-softmax state: each
+// block's K and V rows are loaded one block ahead of their use (two blocks
+// in flight per wave).
+template <typename T, int D, int G>
+__device__ __forceinline__ void stream_blocks(DecodeWave<T, D, G>& st, const T* __restrict__ kc,
+                                              const T* __restrict__ vc, int64_t page_stride,
+                                              int64_t token_stride, int64_t lane_off,
+                                              const int32_t* __restrict__ indices, int pbeg, int page_size,
+                                              int64_t num_pages, int ntok, int blk0, int blk1, float scale_log2,
+                                              int row, int first_page = -1) {
+  using WaveT = DecodeWave<T, D, G>;
+  constexpr int TPI = WaveT::TPI, NS = WaveT::NS, W = WaveT::W;
+  using L8 = Lane8<T>;
+  // first_page >= 0: the caller already holds the page id of blk0's page
+  // (read in an earlier round trip); it serves the first block only, so the
+  // loop itself carries no extra test
+  auto load_at = [&](int blk, int64_t page, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
+    const int t0 = blk * kBlockTokens;
+    const int tip = t0 - (t0 / page_size) * page_size;
+    page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);  // stay inside the pool
+    const int64_t base = page * page_stride + (int64_t)tip * token_stride + lane_off;
+    const T* kp = kc + base;
+    const T* vp = vc + base;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) L8::load(kw[s], kp + (int64_t)s * TPI * token_stride);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) L8::load(vw[s], vp + (int64_t)s * TPI * token_stride);
+  };
+  auto load_block = [&](int blk, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
+    load_at(blk, uniform(indices[pbeg + blk * kBlockTokens / page_size]), kw, vw);
+  };
+  if (blk1 <= blk0) return;
+  uint32_t ka[NS][W], va[NS][W], kb[NS][W], vb[NS][W];
+  if (first_page >= 0)
+    load_at(blk0, first_page, ka, va);
+  else
+    load_block(blk0, ka, va);
+  for (int i = blk0; i < blk1; i += 2) {
+    // Prefetch the next block before consuming this one.  The index is
+    // clamped instead of branched on so the load count is the same on
+    // every path (a re-load of the last block hits in cache).
+    load_block(min(i + 1, blk1 - 1), kb, vb);
+    if ((i + 1) * kBlockTokens <= ntok)
+      st.template consume<false>(ka, va, scale_log2, row, kBlockTokens);
+    else
+      st.template consume<true>(ka, va, scale_log2, row, ntok - i * kBlockTokens);
+    if (i + 1 >= blk1) break;
+    load_block(min(i + 2, blk1 - 1), ka, va);
+    if ((i + 2) * kBlockTokens <= ntok)
+      st.template consume<false>(kb, vb, scale_log2, row, kBlockTokens);
+    else
+      st.template consume<true>(kb, vb, scale_log2, row, ntok - (i + 1) * kBlockTokens);
+  }
+}
+
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
     const T* __restrict__ q, int64_t q_sb, int64_t q_sh, const T* __restrict__ kc,
@@ -321,7 +378,7 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
     const int* __restrict__ header, const Item* __restrict__ items, int batch, int max_items,
     float* __restrict__ part_lse, float* __restrict__ part_o) {
   using WaveT = DecodeWave<T, D, G>;
-  constexpr int LPT = WaveT::LPT, TPI = WaveT::TPI, NS = WaveT::NS, W = WaveT::W;
+  constexpr int LPT = WaveT::LPT;
   using L8 = Lane8<T>;
 
   const int lane = threadIdx.x % kWave;
@@ -329,11 +386,22 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
   const int item_idx = wave / num_kv_heads;
   const int h = wave - item_idx * num_kv_heads;
   if (item_idx >= max_items) return;
-  if (uniform(header[2]) != batch || uniform(header[3]) != plan_stamp(batch, max_items)) return;
-  const Item it = items[item_idx];
-  const int b = uniform(it.row);
-  if (b < 0 || b >= batch) return;
-  const int pbeg = uniform(it.page_begin), pend = uniform(it.page_end), flags = uniform(it.flags);
+  // The item is read together with the plan stamp (item_idx < max_items
+  // keeps the read inside the item table) and used only if the stamp
+  // matches: one combined check needs both, so both loads issue together.
+  const int stamp_batch = uniform(header[2]), stamp = uniform(header[3]);
+  const int4 iv = *reinterpret_cast<const int4*>(items + item_idx);  // the whole item in one load
+  const int b = uniform(iv.x), pbeg = uniform(iv.y), pend = uniform(iv.z), flags = uniform(iv.w);
+  // (every field takes part in the check, so no part of the item load is
+  // deferred past it)
+  if (!((stamp_batch == batch) & (stamp == plan_stamp(batch, max_items)) & (b >= 0) & (b < batch) & (pbeg >= 0) &
+        (pend >= pbeg) & ((flags & ~3) == 0)))
+    return;
+  // Second round trip, all at once: the row's last-page fill, the item's
+  // first page id and q (below).  The item's pages lie inside the indices
+  // buffer (the plan clamps them), so indices[pbeg] exists when pend > pbeg.
+  const int last_raw = last_page_len[b];
+  const int first_page = pend > pbeg ? indices[pbeg] : -1;
 
   const int row = lane / LPT;   // token row inside a load instruction
   const int col = lane % LPT;   // 8-element slice of the head dim
@@ -348,52 +416,15 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
 
   int ntok = 0;
   if (pend > pbeg) {
-    ntok = (pend - pbeg) * page_size;
-    if (flags & 2) {
-      int last = last_page_len[b];
-      last = last < 1 ? 1 : (last > page_size ? page_size : last);
-      ntok -= page_size - last;
-    }
+    const int last = last_raw < 1 ? 1 : (last_raw > page_size ? page_size : last_raw);
+    ntok = (pend - pbeg) * page_size - ((flags & 2) ? page_size - last : 0);
   }
   ntok = uniform(ntok);
   const int nblk = (ntok + kBlockTokens - 1) / kBlockTokens;
 
   const int64_t lane_off = (int64_t)row * token_stride + (int64_t)h * head_stride + col * 8;
-  auto load_block = [&](int blk, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
-    const int t0 = blk * kBlockTokens;
-    const int pg = t0 / page_size;
-    const int tip = t0 - pg * page_size;
-    int64_t page = uniform(indices[pbeg + pg]);
-    page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);  // stay inside the pool
-    const int64_t base = page * page_stride + (int64_t)tip * token_stride + lane_off;
-    const T* kp = kc + base;
-    const T* vp = vc + base;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) L8::load(kw[s], kp + (int64_t)s * TPI * token_stride);
-#pragma unroll
-    for (int s = 0; s < NS; ++s) L8::load(vw[s], vp + (int64_t)s * TPI * token_stride);
-  };
-
-  if (nblk > 0) {
-    uint32_t ka[NS][W], va[NS][W], kb[NS][W], vb[NS][W];
-    load_block(0, ka, va);
-    for (int i = 0; i < nblk; i += 2) {
-      // Prefetch the next block before consuming this one.  The index is
-      // clamped instead of branched on so the load count is the same on
-      // every path (a re-load of the last block hits in cache).
-      load_block(min(i + 1, nblk - 1), kb, vb);
-      if ((i + 1) * kBlockTokens <= ntok)
-        st.template consume<false>(ka, va, scale_log2, row, kBlockTokens);
-      else
-        st.template consume<true>(ka, va, scale_log2, row, ntok - i * kBlockTokens);
-      if (i + 1 >= nblk) break;
-      load_block(min(i + 2, nblk - 1), ka, va);
-      if ((i + 2) * kBlockTokens <= ntok)
-        st.template consume<false>(kb, vb, scale_log2, row, kBlockTokens);
-      else
-        st.template consume<true>(kb, vb, scale_log2, row, ntok - (i + 1) * kBlockTokens);
-    }
-  }
+  stream_blocks<T, D, G>(st, kc, vc, page_stride, token_stride, lane_off, indices, pbeg, page_size, num_pages, ntok,
+                         0, nblk, scale_log2, row, uniform(first_page));
 
   st.merge_rows();
 
@@ -433,61 +464,106 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
 }
 
 // ----------------------------------------------------------------- merge ---
-// One wavefront per (row, q head) of a split row.  LPT lanes cover one
-// partial row of D floats (32 bytes each), so a wave folds 64/LPT partials
-// per iteration; the lane rows are summed with xor shuffles at the end.
+// One workgroup of kMergeThreads per (row, q head) of a split row.  LPT
+// lanes cover one partial row of D floats; the workgroup takes RPI partial
+// rows per pass and issues up to kMergeBatch passes of loads (each partial's
+// lse and output together) before folding any of them, so a row of up to
+// RPI * kMergeBatch items costs one memory round trip.  Each thread folds its
+// partials online (running max, weight sum, weighted output); the threads'
+// states are combined with xor shuffles inside a wave and through LDS across
+// waves.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeBatch = 8;
+
+struct MergeState {
+  float m, w, a[8];  // log2 max, sum of weights, weighted output (8 dims)
+  __device__ __forceinline__ void add(float m_o, float w_o, const float (&a_o)[8]) {
+    const float m_new = fmaxf(m, m_o);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float s = fast_exp2(m - m_use), so = fast_exp2(m_o - m_use);
+    w = w * s + w_o * so;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = a[i] * s + a_o[i] * so;
+    m = m_new;
+  }
+};
+
 template <typename T, int D>
-__global__ __launch_bounds__(kWave * kWavesPerWG) void merge_kernel(
+__global__ __launch_bounds__(kMergeThreads) void merge_kernel(
     const int2* __restrict__ row_info, const float* __restrict__ part_lse,
     const float* __restrict__ part_o, T* __restrict__ o, int64_t o_sb, int64_t o_sh,
     float* __restrict__ lse, const int* __restrict__ header, int batch, int num_qo_heads,
     int max_items) {
-  constexpr int LPT = D / 8, CPI = kWave / LPT;
-  const int lane = threadIdx.x % kWave;
-  const int wave = uniform(blockIdx.x * kWavesPerWG + threadIdx.x / kWave);
-  if (wave >= batch * num_qo_heads) return;
-  if (uniform(header[2]) != batch || uniform(header[3]) != plan_stamp(batch, max_items)) return;
-  const int b = wave / num_qo_heads;
-  const int hq = wave - b * num_qo_heads;
+  constexpr int LPT = D / 8, RPI = kMergeThreads / LPT, NWV = kMergeThreads / kWave;
+  __shared__ float s_m[NWV][LPT], s_w[NWV][LPT], s_a[NWV][LPT][8];
+  const int pair = blockIdx.x;
+  if (pair >= batch * num_qo_heads) return;
+  const int b = pair / num_qo_heads;
+  const int hq = pair - b * num_qo_heads;
+  // One combined check that needs all three loads, so they are issued
+  // together (separate early exits would sink each load below the last).
+  const int stamp_batch = uniform(header[2]), stamp = uniform(header[3]);
   const int2 info = row_info[b];
   const int first = uniform(info.x), n = uniform(info.y);
-  if (n <= 1 || first < 0 || first + n > max_items) return;
+  const bool planned = (stamp_batch == batch) & (stamp == plan_stamp(batch, max_items));
+  if (!(planned & (n > 1) & (first >= 0) & (first + n <= max_items))) return;
 
-  float mx = -INFINITY;
-  for (int c = lane; c < n; c += kWave)
-    mx = fmaxf(mx, part_lse[(int64_t)(first + c) * num_qo_heads + hq]);
-  mx = wave_max(mx);
-  const float m_use = mx == -INFINITY ? 0.f : mx;
-
-  const int row = lane / LPT, col = lane % LPT;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float wsum = 0.f;
-#pragma unroll 2
-  for (int c = row; c < n; c += CPI) {
-    const int64_t slot = (int64_t)(first + c) * num_qo_heads + hq;
-    const float w = fast_exp2(part_lse[slot] - m_use);
-    const float4 a = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8);
-    const float4 bq = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8 + 4);
-    wsum += w;
-    acc[0] = fmaf(w, a.x, acc[0]); acc[1] = fmaf(w, a.y, acc[1]);
-    acc[2] = fmaf(w, a.z, acc[2]); acc[3] = fmaf(w, a.w, acc[3]);
-    acc[4] = fmaf(w, bq.x, acc[4]); acc[5] = fmaf(w, bq.y, acc[5]);
-    acc[6] = fmaf(w, bq.z, acc[6]); acc[7] = fmaf(w, bq.w, acc[7]);
+  const int r = threadIdx.x / LPT, col = threadIdx.x % LPT;
+  MergeState st{-INFINITY, 0.f, {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}};
+  for (int c0 = 0; c0 < n; c0 += RPI * kMergeBatch) {
+    float lv[kMergeBatch];
+    float4 oa[kMergeBatch], ob[kMergeBatch];
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      // past the last item: re-read the last one (in bounds); its weight is dropped below
+      const int c = min(c0 + r + k * RPI, n - 1);
+      const int64_t slot = (int64_t)(first + c) * num_qo_heads + hq;
+      lv[k] = part_lse[slot];
+      oa[k] = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8);
+      ob[k] = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8 + 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the whole batch in flight before the first fold
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const bool on = c0 + r + k * RPI < n;
+      const float v[8] = {oa[k].x, oa[k].y, oa[k].z, oa[k].w, ob[k].x, ob[k].y, ob[k].z, ob[k].w};
+      st.add(on ? lv[k] : -INFINITY, on ? 1.f : 0.f, v);
+    }
   }
+  // fold the RPI rows: within a wave (xor over the row bits of the lane id) ...
 #pragma unroll
   for (int off = LPT; off < kWave; off <<= 1) {
-    wsum += __shfl_xor(wsum, off);
+    float a_o[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] += __shfl_xor(acc[i], off);
+    for (int i = 0; i < 8; ++i) a_o[i] = __shfl_xor(st.a[i], off);
+    const float m_o = __shfl_xor(st.m, off), w_o = __shfl_xor(st.w, off);
+    st.add(m_o, w_o, a_o);
   }
-  if (row != 0) return;
-  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  // ... then across the waves through LDS
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (lane < LPT) {
+    s_m[wave][col] = st.m;
+    s_w[wave][col] = st.w;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s_a[wave][col][i] = st.a[i];
+  }
+  __syncthreads();
+  if (threadIdx.x >= LPT) return;
+#pragma unroll
+  for (int w = 1; w < NWV; ++w) {
+    float a_o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a_o[i] = s_a[w][col][i];
+    st.add(s_m[w][col], s_w[w][col], a_o);
+  }
+  const float inv = st.w > 0.f ? 1.f / st.w : 0.f;
   T* op = o + (int64_t)b * o_sb + (int64_t)hq * o_sh + col * 8;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) op[i] = from_float<T>(acc[i] * inv);
+  for (int i = 0; i < 8; ++i) op[i] = from_float<T>(st.a[i] * inv);
   if (lse != nullptr && col == 0) {
     constexpr float kLn2 = 0.69314718055994530942f;
-    lse[(int64_t)b * num_qo_heads + hq] = wsum > 0.f ? (m_use + __log2f(wsum)) * kLn2 : -INFINITY;
+    const float m_use = st.m == -INFINITY ? 0.f : st.m;
+    lse[(int64_t)b * num_qo_heads + hq] = st.w > 0.f ? (m_use + __log2f(st.w)) * kLn2 : -INFINITY;
   }
 }
 
@@ -516,8 +592,7 @@ int launch(const RunArgs& a) {
     PL_LAUNCH_CHECK("decode_kernel");
   }
   if (!(a.flags & PL_DECODE_SKIP_MERGE)) {
-    const int mgrid = (a.batch * a.hq + kWavesPerWG - 1) / kWavesPerWG;
-    hipLaunchKernelGGL((merge_kernel<T, D>), dim3(mgrid), dim3(kWave * kWavesPerWG), 0, a.stream,
+    hipLaunchKernelGGL((merge_kernel<T, D>), dim3(a.batch * a.hq), dim3(kMergeThreads), 0, a.stream,
                        a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
                        a.batch, a.hq, a.max_items);
     PL_LAUNCH_CHECK("merge_kernel");

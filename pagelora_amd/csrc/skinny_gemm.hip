@@ -17,6 +17,8 @@
 //                       streams its contiguous run of blocks four at a time
 //                       (non-temporal loads) against x rows read from L2,
 //                       and the 16 partial tiles are summed through LDS.
+//                       Eight at a time measured slower at every decode
+//                       shape (74 VGPRs: one workgroup per CU instead of two).
 //
 // Reference: the base F.linear of project_qkv_packed / project_gate_up_packed
 // / project_linear (model/flashinfer/packed_ops.py:143, 179, 251-265) and
@@ -48,8 +50,6 @@ template <> __device__ __forceinline__ f32x4 mfma32<f16_t>(u32x4 a, u32x4 b, f32
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
                                                 0);
 }
-
-__device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
 
 // One thread per 16-byte piece of the shuffled buffer (N_pad x K elements).
 __global__ void shuffle_kernel(const uint16_t* __restrict__ W, int64_t ldw, int N, int K, uint16_t* __restrict__ Ws,
@@ -90,6 +90,10 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_kernel(const T* __rest
   const u32x4* wb = reinterpret_cast<const u32x4*>(Ws + (int64_t)nb * ksteps * kBlockElems) + lane;
   const T* xr = x + (int64_t)(t_ok ? t : 0) * ldx + kq;
 
+  // A rows of tokens >= `tokens` read token 0's row (xr is clamped): row i of
+  // the MFMA result depends only on row i of A, and those rows are never
+  // written, so the loads need no condition (a condition here becomes a
+  // branch around each load, and a wait before the next batch).
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   int s = sb;
   for (; s + kUnroll <= se; s += kUnroll) {
@@ -97,13 +101,16 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_kernel(const T* __rest
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) b[u] = __builtin_nontemporal_load(wb + (s + u) * kWave);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) a[u] = t_ok ? *reinterpret_cast<const u32x4*>(xr + (s + u) * 32) : zero4();
+    for (int u = 0; u < kUnroll; ++u) a[u] = *reinterpret_cast<const u32x4*>(xr + (s + u) * 32);
+    // all of a batch's loads before its first MFMA (measured: lm_head at 4
+    // tokens 180.9 -> 175.6 us, down_proj split 3 20.0 -> 19.7 us)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[u], b[u], acc);
   }
   for (; s < se; ++s) {
     const u32x4 b = __builtin_nontemporal_load(wb + s * kWave);
-    const u32x4 a = t_ok ? *reinterpret_cast<const u32x4*>(xr + s * 32) : zero4();
+    const u32x4 a = *reinterpret_cast<const u32x4*>(xr + s * 32);
     acc = mfma32<T>(a, b, acc);
   }
   // D: rows = tokens 4*(lane/16)+i of the tile, column = lr
