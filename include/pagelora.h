@@ -553,6 +553,20 @@ int pl_page_table_advance(int32_t* indptr, int32_t* indices,
                           int64_t* positions, int64_t* page_id,
                           int64_t* page_offset, int32_t* status, void* stream);
 
+/*
+ * Greedy next token: next_tokens[r] = the index of the largest of
+ * logits[r, 0 .. vocab) (row stride ld elements, rows 16-byte aligned),
+ * int64.  Ties go to the first index and a NaN counts as the largest value
+ * (the first NaN wins), as torch.argmax does.  tokens_out (nullable)
+ * receives the same indices: the decode step's input-token buffer, so the
+ * next step needs no copy.  One workgroup per row.
+ *
+ * Replaces greedy_argmax_token (model/flashinfer/sampling.py:8-15).
+ */
+int pl_greedy_argmax(const void* logits, int64_t ld, int rows, int vocab,
+                     int dtype, int64_t* next_tokens, int64_t* tokens_out,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -142,6 +142,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _vp, _vp, _vp, _vp,      # positions, page_id, page_offset, status, stream
         ],
     ),
+    "pl_greedy_argmax": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp]),
     "pl_prefill_plan": (
         _i32,
         [

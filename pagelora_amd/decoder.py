@@ -280,7 +280,8 @@ def decode_layer_static(
 
 def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: PagedDecodeAttention,
                        ctx: DecodeContext) -> torch.Tensor:
-    """embed -> layers -> final norm -> lm_head -> greedy argmax into ctx.next_tokens.
+    """embed -> layers -> final norm -> lm_head -> greedy argmax into ctx.next_tokens
+    and ctx.tokens (the next step's input).
 
     Returns the logits [B, vocab] (graph-owned under capture).
     """
@@ -295,7 +296,8 @@ def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: Page
         logits = linear_shuffled(x, weights.lm_head_shuffled)
     else:
         logits = F.linear(x, weights.lm_head)
-    ctx.next_tokens.copy_(torch.argmax(logits, dim=-1))  # greedy, sampling.py:8-15
+    # greedy (sampling.py:8-15); the pick also becomes the next step's input token
+    fused_ops.greedy_argmax(logits, out=ctx.next_tokens, tokens_out=ctx.tokens)
     return logits
 
 

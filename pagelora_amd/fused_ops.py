@@ -275,3 +275,23 @@ def qk_norm_rope_append(
         inv_freq.data_ptr(), float(eps), _lib.dtype_code(qkv.dtype),
         _lib.stream_handle(qkv.device)), "pl_qk_norm_rope_append")
     return q_out
+
+
+def greedy_argmax(logits: torch.Tensor, out: torch.Tensor | None = None,
+                  tokens_out: torch.Tensor | None = None) -> torch.Tensor:
+    """``torch.argmax(logits, dim=-1)`` for 2-D logits on the device (``pl_greedy_argmax``):
+    the first maximal index per row, a NaN counting as the largest value
+    (sampling.py:8-15).  ``tokens_out`` (int64 [rows], optional) receives the
+    same indices: the next decode step's input-token buffer."""
+    _rows2d(logits, "logits")
+    rows, vocab = logits.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    for name, t in (("out", out), ("tokens_out", tokens_out)):
+        if t is not None and (t.dtype != torch.int64 or t.numel() != rows or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous int64 tensor of {rows} elements")
+    st = _lib.load().pl_greedy_argmax(logits.data_ptr(), logits.stride(0), rows, vocab, _lib.dtype_code(logits.dtype),
+                                      out.data_ptr(), tokens_out.data_ptr() if tokens_out is not None else None,
+                                      _lib.stream_handle(logits.device))
+    _lib.check(st, "pl_greedy_argmax")
+    return out

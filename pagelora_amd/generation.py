@@ -212,8 +212,7 @@ class BatchGenerator:
                 ctx.tokens.copy_(first_tokens)
             else:
                 self._stage_inputs(ctx, requests, adapters)
-                self._plan(requests)
-                ctx.tokens.copy_(ctx.next_tokens)
+                self._plan(requests)  # ctx.tokens holds the last pick (the step wrote it)
             if entry is not None:
                 self.graphs.replay(entry)
             else:
@@ -252,9 +251,7 @@ class BatchGenerator:
         ctx.adapter_ids.copy_(torch.tensor(adapters, dtype=torch.int32))
         ctx.tokens.copy_(first_tokens)
         for step in range(steps):
-            feeder.before_step(step)
-            if step:
-                ctx.tokens.copy_(ctx.next_tokens)
+            feeder.before_step(step)  # ctx.tokens holds the last pick (the step wrote it)
             if entry is not None:
                 self.graphs.replay(entry)
             else:
