@@ -280,7 +280,14 @@ int pl_qk_norm_rope_append(const void* qkv, int64_t ld_qkv,
  */
 #define PL_LORA_B_ROWS 0
 #define PL_LORA_B_CHUNK8 1
-
+/*
+ * adapter: -1 selects each token's adapter from adapter_ids (as above).
+ * 0 <= adapter < num_adapters binds that one adapter to every token, the
+ * reference's model (one active adapter per batch, multilora/runtime.py:
+ * 138-174); adapter_ids may then be null.  Kernels then skip the
+ * adapter-id load, and its dependent round trip, in front of the y and B
+ * reads.  All modules of one call must agree on it.
+ */
 typedef struct {
   const void* y;
   int64_t ldy;
@@ -290,6 +297,7 @@ typedef struct {
   int rank;
   float scale;
   int b_layout;
+  int adapter;
 } pl_lora_up;
 
 /*
@@ -559,13 +567,17 @@ int pl_page_table_advance(int32_t* indptr, int32_t* indices,
  * int64.  Ties go to the first index and a NaN counts as the largest value
  * (the first NaN wins), as torch.argmax does.  tokens_out (nullable)
  * receives the same indices: the decode step's input-token buffer, so the
- * next step needs no copy.  One workgroup per row.
+ * next step needs no copy.  Each row is split over many workgroups whose
+ * partial maxima go to the caller's workspace
+ * (pl_greedy_argmax_workspace_size bytes, 8-byte aligned); a second kernel
+ * folds them.
  *
  * Replaces greedy_argmax_token (model/flashinfer/sampling.py:8-15).
  */
+size_t pl_greedy_argmax_workspace_size(int rows, int vocab, int dtype);
 int pl_greedy_argmax(const void* logits, int64_t ld, int rows, int vocab,
                      int dtype, int64_t* next_tokens, int64_t* tokens_out,
-                     void* stream);
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -89,6 +89,7 @@ class LoraUp(ctypes.Structure):
         ("rank", ctypes.c_int),
         ("scale", ctypes.c_float),
         ("b_layout", ctypes.c_int),
+        ("adapter", ctypes.c_int),
     ]
 
 
@@ -142,7 +143,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _vp, _vp, _vp, _vp,      # positions, page_id, page_offset, status, stream
         ],
     ),
-    "pl_greedy_argmax": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "pl_greedy_argmax_workspace_size": (_sz, [_i32, _i32, _i32]),
+    "pl_greedy_argmax": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "pl_prefill_plan": (
         _i32,
         [

@@ -76,6 +76,7 @@ struct LoraUp {
   int out_features, rank;
   float scale;
   int b_chunk8;
+  int adapter;  // >= 0: every token's adapter (no adapter-id load); -1: per-token ids
 };
 
 // The 16-byte piece kb (ranks 8kb .. 8kb+7) of B[a][c0 + i] (c0 % 8 == 0 in
@@ -244,7 +245,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_kernel(
   float v[kMaxChunks][8], xa[kMaxChunks][8], wf[kMaxChunks][8];
   // The adapter id first: the y and B loads depend on it, and with it in
   // hand they are issued together with the row's own loads.
-  const int a_raw = R > 0 ? ids[row] : -1;
+  const int a_raw = R > 0 ? (lora.adapter >= 0 ? lora.adapter : ids[row]) : -1;
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {
     const int idx = (threadIdx.x + c * THREADS) * 8;
@@ -344,7 +345,7 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_row_kernel(
     int n_adapters, SplitIn xs) {
   __shared__ float s_red[1024 / kWave];
   const int row = blockIdx.x;
-  const int a_raw = R > 0 ? ids[row] : -1;
+  const int a_raw = R > 0 ? (lora.adapter >= 0 ? lora.adapter : ids[row]) : -1;
   const bool live = (int)threadIdx.x * 8 < hidden;
   const int idx = live ? threadIdx.x * 8 : hidden - 8;  // idle threads re-read the last chunk
   float v[8], xa[8], wf[8];
@@ -443,7 +444,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const T* __restrict_
   load_row8<T>(gu + row * ldg + chunk * 8, g);
   load_row8<T>(gu + row * ldg + inter + chunk * 8, u);
   if constexpr (R > 0) {
-    const int a = ids[row];
+    const int a = lg.adapter >= 0 ? lg.adapter : ids[row];
     if (a >= 0 && a < n_adapters) {
       LoraRow<R> yg, yu;
       load_y<T, R>(lg, row, a, yg);
@@ -488,7 +489,7 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(
   int a = -1;
   LoraRow<RR> y[3];
   if constexpr (R > 0) {
-    a = ids[b];
+    a = lora.m[0].adapter >= 0 ? lora.m[0].adapter : ids[b];
     if (a < 0 || a >= n_adapters) a = -1;
     if (a >= 0) {
 #pragma unroll
@@ -596,6 +597,19 @@ using namespace pl::fused;
 // Host copy of a pl_lora_up into the device struct, with its checks.
 // With `split`, y is read from the split-K planes (h->y may be NULL) and its
 // columns y_offset + n_adapters*rank must fit the planes' row.
+// adapter ids: per token (ids required) or one bound adapter for all tokens
+static int adapter_check(const pl_lora_up* mods, int n, const int32_t* ids, int n_adapters, const char* what) {
+  if (n_adapters < 1) return fail(PL_ERR_INVALID, "%s: n_adapters must be >= 1", what);
+  for (int m = 0; m < n; ++m) {
+    if (mods[m].adapter != mods[0].adapter)
+      return fail(PL_ERR_INVALID, "%s: every module of a call must bind the same adapter", what);
+  }
+  const int a = mods[0].adapter;
+  if (a < -1 || a >= n_adapters) return fail(PL_ERR_INVALID, "%s: adapter %d outside [-1, %d)", what, a, n_adapters);
+  if (a < 0 && !ids) return fail(PL_ERR_INVALID, "%s: per-token adapters need adapter_ids", what);
+  return ok();
+}
+
 static int b_layout_check(const pl_lora_up* h, const char* what) {
   if (h->b_layout == PL_LORA_B_ROWS) return ok();
   if (h->b_layout != PL_LORA_B_CHUNK8) return fail(PL_ERR_INVALID, "%s: unknown b_layout %d", what, h->b_layout);
@@ -615,7 +629,7 @@ static int lora_up_from(const pl_lora_up* h, int need_out, LoraUp* d, const char
       return fail(PL_ERR_INVALID, "%s: y columns outside the split planes' rows", what);
     if ((uintptr_t)h->B % 16) return fail(PL_ERR_INVALID, "%s: B must be 16-byte aligned", what);
     if (const int st = b_layout_check(h, what)) return st;
-    *d = LoraUp{nullptr, 0, h->y_offset, h->B, h->out_features, h->rank, h->scale, h->b_layout};
+    *d = LoraUp{nullptr, 0, h->y_offset, h->B, h->out_features, h->rank, h->scale, h->b_layout, h->adapter};
     return ok();
   }
   if (!h->y || !h->B) return fail(PL_ERR_INVALID, "%s: null y or B", what);
@@ -627,7 +641,7 @@ static int lora_up_from(const pl_lora_up* h, int need_out, LoraUp* d, const char
     return fail(PL_ERR_INVALID, "%s: y must be 16-byte aligned with ldy and y_offset multiples of 8", what);
   if ((uintptr_t)h->B % 16) return fail(PL_ERR_INVALID, "%s: B must be 16-byte aligned", what);
   if (const int st = b_layout_check(h, what)) return st;
-  *d = LoraUp{h->y, h->ldy, h->y_offset, h->B, h->out_features, h->rank, h->scale, h->b_layout};
+  *d = LoraUp{h->y, h->ldy, h->y_offset, h->B, h->out_features, h->rank, h->scale, h->b_layout, h->adapter};
   return ok();
 }
 
@@ -732,7 +746,7 @@ static int norm_common(bool add, void* r, int64_t ldr, const void* x, int64_t ld
   LoraUp lu{};
   int rank = 0;
   if (lora) {
-    if (!ids || n_adapters < 1) return fail(PL_ERR_INVALID, "LoRA needs adapter ids and n_adapters >= 1");
+    if (const int st = adapter_check(lora, 1, ids, n_adapters, "add_rmsnorm LoRA")) return st;
     if (const int st = lora_up_from(lora, hidden, &lu, "add_rmsnorm LoRA", x_split ? &xs : nullptr, n_adapters))
       return st;
     rank = lu.rank;
@@ -806,7 +820,7 @@ static int silu_common(const void* gate_up, int64_t ldg, void* out, int64_t ldo,
   LoraUp lg{}, lu{};
   int rank = 0;
   if (lora) {
-    if (!ids || n_adapters < 1) return fail(PL_ERR_INVALID, "LoRA needs adapter ids and n_adapters >= 1");
+    if (const int st = adapter_check(lora, 2, ids, n_adapters, "silu_mul LoRA")) return st;
     if (const int st = lora_up_from(&lora[0], inter, &lg, "silu_mul gate LoRA")) return st;
     if (const int st = lora_up_from(&lora[1], inter, &lu, "silu_mul up LoRA")) return st;
     if (lg.rank != lu.rank) return fail(PL_ERR_UNSUPPORTED, "gate and up LoRA ranks differ (%d, %d)", lg.rank, lu.rank);
@@ -917,7 +931,7 @@ static int qkr_common(const void* qkv, int64_t ld_qkv, const void* q_norm_weight
             page_stride, token_stride, head_stride, num_pages, page_size, batch, num_qo_heads, num_kv_heads,
             inv_freq, eps, QkvLora{}, ids, n_adapters, xs};
   if (lora) {
-    if (!ids || n_adapters < 1) return fail(PL_ERR_INVALID, "LoRA needs adapter ids and n_adapters >= 1");
+    if (const int st = adapter_check(lora, 3, ids, n_adapters, "qk_norm_rope_append LoRA")) return st;
     const int need[3] = {num_qo_heads * head_dim, num_kv_heads * head_dim, num_kv_heads * head_dim};
     const char* names[3] = {"q LoRA", "k LoRA", "v LoRA"};
     for (int m = 0; m < 3; ++m)

@@ -36,6 +36,7 @@ class DecodeGraphKey:
     batch: int
     adapter_version: int
     reserve_ptrs: tuple = ()  # device page-table advance captured in (its ring buffers)
+    uniform_adapter: int = -1  # >= 0: one adapter bound to every row, baked into the kernels
 
 
 @dataclass
@@ -60,7 +61,7 @@ class BatchDecodeGraphRunner:
         self.replay_count = 0
         self._graphs: OrderedDict[DecodeGraphKey, DecodeGraphEntry] = OrderedDict()
 
-    def key(self, batch: int, reserve=None) -> DecodeGraphKey:
+    def key(self, batch: int, reserve=None, uniform_adapter: int = -1) -> DecodeGraphKey:
         cache = self.pool.cache
         ptrs = () if reserve is None else (reserve.reserve.data_ptr(), reserve.head.data_ptr(),
                                            reserve.status.data_ptr())
@@ -73,9 +74,10 @@ class BatchDecodeGraphRunner:
             batch=batch,
             adapter_version=self.adapter_version,
             reserve_ptrs=ptrs,
+            uniform_adapter=uniform_adapter,
         )
 
-    def entry(self, batch: int, reserve=None) -> DecodeGraphEntry | None:
+    def entry(self, batch: int, reserve=None, uniform_adapter: int = -1) -> DecodeGraphEntry | None:
         """The graph for ``batch``: captured on first use (needs a current plan).
 
         With a :class:`PageReserve` the graph starts with the device-side
@@ -83,13 +85,13 @@ class BatchDecodeGraphRunner:
         """
         if self.disabled_reason is not None:
             return None
-        k = self.key(batch, reserve)
+        k = self.key(batch, reserve, uniform_adapter)
         e = self._graphs.get(k)
         if e is not None:
             self._graphs.move_to_end(k)
             return e
         try:
-            e = self._capture(batch, reserve)
+            e = self._capture(batch, reserve, uniform_adapter)
         except Exception as exc:  # capture failure: fall back to eager for good
             self.disabled_reason = f"{type(exc).__name__}: {exc}"
             self._graphs.clear()
@@ -100,9 +102,10 @@ class BatchDecodeGraphRunner:
         self.capture_count += 1
         return e
 
-    def _capture(self, batch: int, reserve=None) -> DecodeGraphEntry:
+    def _capture(self, batch: int, reserve=None, uniform_adapter: int = -1) -> DecodeGraphEntry:
         dev = self.pool.cache.device
         ctx = DecodeContext(batch, dev)
+        ctx.uniform_adapter = uniform_adapter
         # Warm up once on a side stream (allocator pools, library workspaces),
         # writing to a slot nobody reads: page 0 of the pool is never handed out.
         cur = torch.cuda.current_stream(dev)

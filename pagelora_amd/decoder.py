@@ -133,10 +133,11 @@ class LayerWeights:
             if name in self.lora:
                 self.lora_b8[name] = fused_ops.lora_b_chunk8(self.lora[name][1])
 
-    def up(self, name: str, y: torch.Tensor, scale: float) -> fused_ops.LoraUp:
-        """The up-projection of module ``name`` reading its intermediate from ``y``."""
+    def up(self, name: str, y: torch.Tensor, scale: float, adapter: int = -1) -> fused_ops.LoraUp:
+        """The up-projection of module ``name`` reading its intermediate from ``y``
+        (``adapter`` >= 0: that one adapter for every token)."""
         B = self.lora_b8.get(name)
-        return fused_ops.LoraUp(y, self.y_offset[name], self.lora[name][1] if B is None else B, scale)
+        return fused_ops.LoraUp(y, self.y_offset[name], self.lora[name][1] if B is None else B, scale, adapter)
 
 
 class DecoderWeights:
@@ -173,6 +174,11 @@ class DecodeContext:
         self.page_offset = torch.zeros(batch, dtype=torch.int64, device=device)
         self.adapter_ids = torch.zeros(batch, dtype=torch.int32, device=device)
         self.next_tokens = torch.zeros(batch, dtype=torch.int64, device=device)
+        # >= 0: every row uses this adapter (the reference binds one adapter
+        # per batch); the LoRA kernels then skip the per-row adapter-id load.
+        # A captured step bakes it in (part of the graph key).
+        self.uniform_adapter = -1
+        self.argmax_ws: torch.Tensor | None = None  # greedy-argmax partial maxima
 
 
 # Decode-sized inputs (up to 16 tokens) take the GEMM on shuffled weights
@@ -211,7 +217,7 @@ def _cols(out, n: int):
 
 def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Tensor, pending, ids: torch.Tensor,
            positions: torch.Tensor, page_id: torch.Tensor, page_offset: torch.Tensor, layer_cache: torch.Tensor,
-           page_size: int, attend):
+           page_size: int, attend, adapter: int = -1):
     """One decoder layer over T tokens (decode or prefill), no-merge LoRA on
     all seven modules.  ``hidden`` is the residual stream, updated in place;
     ``pending`` = (previous layer's down_proj output, its LoRA up-projection)
@@ -222,9 +228,11 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
     Per projection, one GEMM on [W; A] yields base output + LoRA intermediate
     and the consumer kernel applies the up-projection: the q/k/v deltas in
     the head-norm/RoPE/append kernel, o's and down's in the next
-    add+RMSNorm, gate's and up's in SiLU*up.
+    add+RMSNorm, gate's and up's in SiLU*up.  ``adapter`` >= 0 binds that
+    adapter to every token (``ids`` is then not read).
     """
     h, qd, kd, I = cfg.hidden, cfg.q_dim, cfg.kv_dim, cfg.intermediate
+    a = adapter
     if pending is None:
         x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
     else:
@@ -237,16 +245,16 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
         positions, page_id, page_offset, layer_cache, num_qo_heads=cfg.num_qo_heads,
         num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=page_size,
         rope_theta=cfg.rope_theta, eps=cfg.rms_eps,
-        lora=(lw.up("q", qkv, scale), lw.up("k", qkv, scale), lw.up("v", qkv, scale)), adapter_ids=ids)
+        lora=(lw.up("q", qkv, scale, a), lw.up("k", qkv, scale, a), lw.up("v", qkv, scale, a)), adapter_ids=ids)
     attn = attend(q).view(q.shape[0], qd)
     o = _project(attn, lw, "o")
-    x2 = fused_ops.add_rmsnorm(hidden, _cols(o, h), lw.post_norm, cfg.rms_eps, lora=lw.up("o", o, scale),
+    x2 = fused_ops.add_rmsnorm(hidden, _cols(o, h), lw.post_norm, cfg.rms_eps, lora=lw.up("o", o, scale, a),
                                adapter_ids=ids)
     gu = _project(x2, lw, "gate_up")
-    act = fused_ops.silu_mul(gu[:, : 2 * I], lora=(lw.up("gate", gu, scale), lw.up("up", gu, scale)),
+    act = fused_ops.silu_mul(gu[:, : 2 * I], lora=(lw.up("gate", gu, scale, a), lw.up("up", gu, scale, a)),
                              adapter_ids=ids)
     d = _project(act, lw, "down")
-    return d, lw.up("down", d, scale)
+    return d, lw.up("down", d, scale, a)
 
 
 def _final_norm(weights: "DecoderWeights", hidden: torch.Tensor, pending, ids: torch.Tensor) -> torch.Tensor:
@@ -275,7 +283,7 @@ def decode_layer_static(
         return out
 
     return _layer(cfg, lw, lora_scale, hidden, pending, ctx.adapter_ids, ctx.positions, ctx.page_id,
-                  ctx.page_offset, layer_cache, backend.page_size, attend)
+                  ctx.page_offset, layer_cache, backend.page_size, attend, ctx.uniform_adapter)
 
 
 def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: PagedDecodeAttention,
@@ -297,7 +305,10 @@ def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: Page
     else:
         logits = F.linear(x, weights.lm_head)
     # greedy (sampling.py:8-15); the pick also becomes the next step's input token
-    fused_ops.greedy_argmax(logits, out=ctx.next_tokens, tokens_out=ctx.tokens)
+    if ctx.argmax_ws is None:  # the first (eager) call allocates it, before any capture
+        ctx.argmax_ws = fused_ops.greedy_argmax_workspace(logits.shape[0], logits.shape[1], logits.dtype,
+                                                          logits.device)
+    fused_ops.greedy_argmax(logits, out=ctx.next_tokens, tokens_out=ctx.tokens, workspace=ctx.argmax_ws)
     return logits
 
 
@@ -355,7 +366,8 @@ def prefill(weights: DecoderWeights, pool: PagedKVPool, request: Request, tokens
             def attend(q, cache=cache):
                 return backend.run_prefill_into(q, cache, attn)
 
-            pending = _layer(cfg, lw, s, hidden, pending, ids, pos, page_of, off_of, cache, ps, attend)
+            pending = _layer(cfg, lw, s, hidden, pending, ids, pos, page_of, off_of, cache, ps, attend,
+                             adapter if 0 <= adapter < weights.n_adapters else -1)
         x = _final_norm(weights, hidden, pending, ids)
         last_logits = F.linear(x[-1:], weights.lm_head)
     return last_logits

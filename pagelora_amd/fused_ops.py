@@ -61,6 +61,9 @@ class LoraUp:
     y_offset: int
     B: torch.Tensor
     scale: float
+    # >= 0: every token uses this adapter (the reference's one bound adapter
+    # per batch) and adapter_ids may be omitted; -1: per-token adapter_ids
+    adapter: int = -1
 
     def _b_shape(self) -> tuple[int, int, int, int]:
         """(n_adapters, out_features, rank, b_layout)."""
@@ -84,7 +87,7 @@ class LoraUp:
             if self.y_offset < 0 or self.y_offset + n * r > self.y.ld:
                 raise ValueError("LoraUp: y columns out of range")
             return _lib.LoraUp(None, 0, int(self.y_offset), B.data_ptr(), int(out), int(r), float(self.scale),
-                               int(layout))
+                               int(layout), int(self.adapter))
         if self.y.dim() != 2 or self.y.stride(1) != 1:
             raise ValueError("LoraUp.y must be 2-D with unit column stride")
         if not B.is_contiguous() or B.dtype != self.y.dtype:
@@ -92,7 +95,7 @@ class LoraUp:
         if self.y_offset < 0 or self.y_offset + n * r > self.y.shape[1]:
             raise ValueError("LoraUp: y columns out of range")
         return _lib.LoraUp(self.y.data_ptr(), self.y.stride(0), int(self.y_offset), B.data_ptr(), int(out), int(r),
-                           float(self.scale), int(layout))
+                           float(self.scale), int(layout), int(self.adapter))
 
     @property
     def n_adapters(self) -> int:
@@ -103,14 +106,21 @@ def _lora_args(lora: Sequence[LoraUp], adapter_ids: torch.Tensor | None, rows: i
     n = lora[0].n_adapters
     if any(m.n_adapters != n for m in lora):
         raise ValueError("every LoRA module of a call must stack the same adapters")
-    if adapter_ids is None or adapter_ids.dtype != torch.int32 or adapter_ids.numel() != rows:
+    bound = lora[0].adapter
+    if any(m.adapter != bound for m in lora):
+        raise ValueError("every LoRA module of a call must bind the same adapter")
+    if bound >= n or bound < -1:
+        raise ValueError(f"adapter {bound} outside [-1, {n})")
+    if bound < 0 and adapter_ids is None:
+        raise ValueError("adapter_ids is required unless the modules bind one adapter")
+    if adapter_ids is not None and (adapter_ids.dtype != torch.int32 or adapter_ids.numel() != rows):
         raise ValueError("adapter_ids must be int32 [rows]")
     for m in lora:
         y_rows = m.y.rows if isinstance(m.y, SplitOutput) else m.y.shape[0]
         if y_rows != rows:
             raise ValueError("LoraUp.y must have one row per token")
     arr = (_lib.LoraUp * len(lora))(*[m.struct() for m in lora])
-    return arr, adapter_ids.data_ptr(), n
+    return arr, (adapter_ids.data_ptr() if adapter_ids is not None else None), n
 
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -278,20 +288,31 @@ def qk_norm_rope_append(
 
 
 def greedy_argmax(logits: torch.Tensor, out: torch.Tensor | None = None,
-                  tokens_out: torch.Tensor | None = None) -> torch.Tensor:
+                  tokens_out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """``torch.argmax(logits, dim=-1)`` for 2-D logits on the device (``pl_greedy_argmax``):
     the first maximal index per row, a NaN counting as the largest value
     (sampling.py:8-15).  ``tokens_out`` (int64 [rows], optional) receives the
-    same indices: the next decode step's input-token buffer."""
+    same indices: the next decode step's input-token buffer.  ``workspace``
+    (uint8, optional; see :func:`greedy_argmax_workspace`) holds the
+    per-slice maxima."""
     _rows2d(logits, "logits")
     rows, vocab = logits.shape
+    lib = _lib.load()
     if out is None:
         out = torch.empty(rows, dtype=torch.int64, device=logits.device)
     for name, t in (("out", out), ("tokens_out", tokens_out)):
         if t is not None and (t.dtype != torch.int64 or t.numel() != rows or not t.is_contiguous()):
             raise ValueError(f"{name} must be a contiguous int64 tensor of {rows} elements")
-    st = _lib.load().pl_greedy_argmax(logits.data_ptr(), logits.stride(0), rows, vocab, _lib.dtype_code(logits.dtype),
-                                      out.data_ptr(), tokens_out.data_ptr() if tokens_out is not None else None,
-                                      _lib.stream_handle(logits.device))
+    if workspace is None:
+        workspace = greedy_argmax_workspace(rows, vocab, logits.dtype, logits.device)
+    st = lib.pl_greedy_argmax(logits.data_ptr(), logits.stride(0), rows, vocab, _lib.dtype_code(logits.dtype),
+                              out.data_ptr(), tokens_out.data_ptr() if tokens_out is not None else None,
+                              workspace.data_ptr(), workspace.numel(), _lib.stream_handle(logits.device))
     _lib.check(st, "pl_greedy_argmax")
     return out
+
+
+def greedy_argmax_workspace(rows: int, vocab: int, dtype: torch.dtype, device) -> torch.Tensor:
+    """A workspace for :func:`greedy_argmax` on [rows, vocab] logits of ``dtype``."""
+    n = _lib.load().pl_greedy_argmax_workspace_size(rows, vocab, _lib.dtype_code(dtype))
+    return torch.empty(max(int(n), 8), dtype=torch.uint8, device=device)

@@ -187,9 +187,11 @@ class BatchGenerator:
         B = len(requests)
         dev = self.pool.cache.device
         adapters = adapters or [0] * B
+        uniform = self._uniform_adapter(adapters)
         history = torch.empty((steps, B), dtype=torch.int64, device=dev)
         entry = None
         ctx = DecodeContext(B, dev)
+        ctx.uniform_adapter = uniform
         torch.cuda.synchronize(dev)
         t0 = time.perf_counter()
         capture_s = 0.0
@@ -201,7 +203,7 @@ class BatchGenerator:
                 if self.use_graph:
                     tc = time.perf_counter()
                     n_before = self.graphs.capture_count
-                    entry = self.graphs.entry(B)
+                    entry = self.graphs.entry(B, uniform_adapter=uniform)
                     if self.graphs.capture_count != n_before:
                         torch.cuda.synchronize(dev)
                         capture_s = time.perf_counter() - tc
@@ -225,10 +227,16 @@ class BatchGenerator:
                               graph_replays=self.graphs.replay_count, extra={"capture_seconds": capture_s})
 
 
+    def _uniform_adapter(self, adapters) -> int:
+        """The one adapter every row uses, else -1 (per-row ids)."""
+        a = adapters[0] if adapters and all(x == adapters[0] for x in adapters) else -1
+        return a if 0 <= a < self.weights.n_adapters else -1
+
     def _generate_device_tables(self, requests, first_tokens, steps, adapters) -> GenerateResult:
         B = len(requests)
         dev = self.pool.cache.device
         adapters = adapters or [0] * B
+        uniform = self._uniform_adapter(adapters)
         history = torch.empty((steps, B), dtype=torch.int64, device=dev)
         reserve = self._reserves.get(B)
         if reserve is None:
@@ -243,11 +251,15 @@ class BatchGenerator:
         if self.use_graph:
             tc = time.perf_counter()
             n_before = self.graphs.capture_count
-            entry = self.graphs.entry(B, reserve)
+            entry = self.graphs.entry(B, reserve, uniform)
             if self.graphs.capture_count != n_before:
                 torch.cuda.synchronize(dev)
                 capture_s = time.perf_counter() - tc
-        ctx = entry.ctx if entry is not None else DecodeContext(B, dev)
+        if entry is not None:
+            ctx = entry.ctx
+        else:
+            ctx = DecodeContext(B, dev)
+            ctx.uniform_adapter = uniform
         ctx.adapter_ids.copy_(torch.tensor(adapters, dtype=torch.int32))
         ctx.tokens.copy_(first_tokens)
         for step in range(steps):

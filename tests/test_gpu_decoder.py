@@ -238,3 +238,19 @@ def test_prefill_matches_torch_reference(gpu_device, chunk):
     torch.cuda.synchronize()
     assert torch.allclose(got, ref, atol=0.1, rtol=0.01), f"max diff {(got - ref).abs().max().item():.4f}"
     _assert_same_greedy(got.argmax(-1), ref, got)
+
+
+@pytest.mark.parametrize("device_tables", [False, True])
+def test_uniform_adapter_matches_per_row_ids(gpu_device, device_tables, monkeypatch):
+    # every row on adapter 1: the kernels take the bound adapter (no id loads);
+    # forcing per-row ids instead must give the same tokens bit for bit
+    results = []
+    for force_per_row in (False, True):
+        w, pool, reqs, first, _ = _setup(gpu_device)
+        gen = BatchGenerator(w, pool, workspace_mb=8, use_graph=True)
+        if force_per_row:
+            monkeypatch.setattr(gen, "_uniform_adapter", lambda adapters: -1)
+        res = gen.generate(reqs, first, steps=20, adapters=[1, 1, 1], device_tables=device_tables)
+        assert res.used_graph
+        results.append(res.tokens)
+    assert torch.equal(results[0], results[1])

@@ -372,3 +372,74 @@ def test_lora_b_chunk8_silu_and_qk_bitwise(gpu_device):
                                           lora=ups, adapter_ids=ids)
         got.append((q, cd))
     assert torch.equal(got[0][0], got[1][0]) and torch.equal(got[0][1], got[1][1])
+
+
+# One adapter bound to every token (pl_lora_up.adapter >= 0, the reference's
+# single active adapter) must equal per-token ids that all name it.
+@pytest.mark.parametrize("hidden,splits", [(4096, 0), (4096, 3), (12288, 0)])
+def test_uniform_adapter_add_rmsnorm_bitwise(gpu_device, hidden, splits):
+    rows, dev = 5, gpu_device
+    g = torch.Generator().manual_seed(hidden + splits + 1)
+    cols = hidden + N_ADAPTERS * RANK
+    if splits:
+        y = _random_split(g, splits, rows, cols, torch.bfloat16, dev)
+        x = y
+    else:
+        y = torch.randn((rows, cols), generator=g).to(torch.bfloat16).to(dev)
+        x = y[:, :hidden]
+    B = (torch.randn((N_ADAPTERS, hidden, RANK), generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    r0 = torch.randn((rows, hidden), generator=g).to(torch.bfloat16).to(dev)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(dev)
+    ids = torch.full((rows,), 2, dtype=torch.int32, device=dev)
+    r1, r2 = r0.clone(), r0.clone()
+    o1 = fused_ops.add_rmsnorm(r1, x, w, 1e-6, lora=fused_ops.LoraUp(y, hidden, B, SCALE), adapter_ids=ids)
+    o2 = fused_ops.add_rmsnorm(r2, x, w, 1e-6, lora=fused_ops.LoraUp(y, hidden, B, SCALE, adapter=2))
+    torch.cuda.synchronize()
+    assert torch.equal(r1, r2) and torch.equal(o1, o2)
+
+
+def test_uniform_adapter_silu_and_qk_bitwise(gpu_device):
+    rows, dev, dtype = 5, gpu_device, torch.bfloat16
+    g = torch.Generator().manual_seed(91)
+    ids = torch.full((rows,), 1, dtype=torch.int32, device=dev)
+    inter = 1024
+    full, Bs, offs = _lora_inputs(g, rows, 2 * inter, [("gate", inter), ("up", inter)], dtype)
+    fd = full.to(dev)
+    res = []
+    for a, i in ((-1, ids), (1, None)):
+        ups = tuple(fused_ops.LoraUp(fd, offs[m], Bs[m].to(dev), SCALE, a) for m in ("gate", "up"))
+        res.append(fused_ops.silu_mul(fd[:, : 2 * inter], lora=ups, adapter_ids=i))
+    assert torch.equal(res[0], res[1])
+
+    hq, hkv, d, ps, pool = 8, 2, 128, 16, 10
+    qd, kd = hq * d, hkv * d
+    full, Bs, offs = _lora_inputs(g, rows, qd + 2 * kd, [("q", qd), ("k", kd), ("v", kd)], dtype)
+    fd = full.to(dev)
+    qw = torch.ones(d, dtype=dtype, device=dev)
+    pos = torch.tensor([0, 17, 4095, 40000, 5], device=dev)
+    pid = torch.tensor([3, 9, 0, 5, 7], device=dev)
+    off = torch.tensor([0, 15, 7, 1, 2], device=dev)
+    got = []
+    for a, i in ((-1, ids), (1, None)):
+        cd = torch.zeros((pool, 2, ps, hkv, d), dtype=dtype, device=dev)
+        ups = tuple(fused_ops.LoraUp(fd, offs[m], Bs[m].to(dev), SCALE, a) for m in ("q", "k", "v"))
+        q = fused_ops.qk_norm_rope_append(fd[:, : qd + 2 * kd], qw, qw, pos, pid, off, cd, num_qo_heads=hq,
+                                          num_kv_heads=hkv, head_dim=d, page_size=ps, rope_theta=1e6, eps=1e-6,
+                                          lora=ups, adapter_ids=i)
+        got.append((q, cd))
+    assert torch.equal(got[0][0], got[1][0]) and torch.equal(got[0][1], got[1][1])
+
+
+def test_uniform_adapter_validation(gpu_device):
+    dev = gpu_device
+    x = torch.zeros((2, 64 + 3 * 16), dtype=torch.bfloat16, device=dev)
+    B = torch.zeros((3, 64, 16), dtype=torch.bfloat16, device=dev)
+    r = torch.zeros((2, 64), dtype=torch.bfloat16, device=dev)
+    w = torch.ones(64, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):   # per-token mode without ids
+        fused_ops.add_rmsnorm(r, x[:, :64], w, 1e-6, lora=fused_ops.LoraUp(x, 64, B, 1.0))
+    with pytest.raises(ValueError):   # bound adapter outside the stack
+        fused_ops.add_rmsnorm(r, x[:, :64], w, 1e-6, lora=fused_ops.LoraUp(x, 64, B, 1.0, adapter=3))
+    gu = torch.zeros((2, 2 * 64 + 2 * 3 * 16), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):   # modules of one call bind different adapters
+        fused_ops.silu_mul(gu[:, :128], lora=(fused_ops.LoraUp(gu, 128, B, 1.0, 0), fused_ops.LoraUp(gu, 176, B, 1.0, 1)))

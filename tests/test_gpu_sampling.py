@@ -7,7 +7,7 @@ the Qwen3 vocab."""
 import pytest
 import torch
 
-from pagelora_amd import fused_ops
+from pagelora_amd import _lib, fused_ops
 
 pytestmark = pytest.mark.gpu
 
@@ -60,3 +60,16 @@ def test_rejects_misaligned_rows(gpu_device):
     x = torch.zeros((2, 1003), dtype=torch.bfloat16, device=gpu_device)
     with pytest.raises(ValueError):
         fused_ops.greedy_argmax(x)             # row stride 1003 elements: rows not 16-byte aligned
+
+
+def test_workspace_size_and_reuse(gpu_device):
+    # slices of 2048 16-byte chunks: 151,936 bf16 logits -> 10 slices per row
+    ws = fused_ops.greedy_argmax_workspace(4, 151936, torch.bfloat16, gpu_device)
+    assert ws.numel() == 4 * 10 * 8
+    g = torch.Generator().manual_seed(3)
+    for _ in range(3):  # the same workspace serves consecutive calls
+        x = torch.randn((4, 151936), generator=g).to(torch.bfloat16)
+        got = fused_ops.greedy_argmax(x.to(gpu_device), workspace=ws)
+        assert torch.equal(got.cpu(), torch.argmax(x.float(), dim=-1))
+    with pytest.raises(_lib.WorkspaceTooSmallError):
+        fused_ops.greedy_argmax(x.to(gpu_device), workspace=ws[:16])
