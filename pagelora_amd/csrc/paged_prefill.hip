@@ -16,16 +16,18 @@
 // long prompt see the most tiles).  Grid = (items, kv heads), 4 waves of
 // 16 rows each.
 //
-// Per 32-token kv tile: K and V (both row-major) are staged in LDS
-// straight from the pages while the next tile's loads are already in
-// flight in registers; each wave computes S = Q K^T (MFMA 16x16x32, Q held
-// in registers), masks, runs an fp32 online softmax in the log2 domain,
-// moves P from the accumulator layout to the operand layout through LDS
-// and accumulates O += P V (MFMA).  For bf16, P (in [0, 1]) is split into
+// Per kv tile (64 tokens; 32 at head_dim 256): K and V (both row-major)
+// are staged in LDS straight from the pages while the next tile's loads are
+// already in flight in registers.  Each wave computes S^T = K Q^T (MFMA
+// 16x16x32, Q held in registers as the B operand), so a lane holds one
+// query and 16 of the tile's tokens: masking and the fp32 online softmax
+// (log2 domain) reduce within the lane and across the column's four lanes.
+// The probabilities are then already in the B-operand layout of
+// O^T += V^T P^T (no LDS round trip).  For bf16, P (in [0, 1]) is split into
 // bf16 hi + lo parts and P V runs as two MFMAs, so P carries ~16 mantissa
-// bits instead of 8 (fp16's 11 bits are used as is).  The V operand pairs two adjacent
-// head-dim columns per lane: column tile 2a holds d = 32a + 2c and tile
-// 2a+1 holds d = 32a + 2c + 1, so a lane builds both B operands from eight
+// bits instead of 8 (fp16's 11 bits are used as is).  The V operand pairs
+// two adjacent head-dim rows per lane: tile 2a holds d = 32a + 2c and tile
+// 2a+1 holds d = 32a + 2c + 1, so a lane builds both A operands from eight
 // 32-bit LDS reads and byte permutes, and writes both outputs as one
 // 32-bit store.
 //
@@ -45,7 +47,7 @@ constexpr int kWave = 64;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWave * kWaves;
 constexpr int kRows = 16 * kWaves;  // rows per work item
-constexpr int kTile = 32;           // kv tokens per tile
+constexpr int kPlanTile = 64;       // kv tokens per unit of the plan's work estimate
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -63,26 +65,21 @@ template <> __device__ __forceinline__ f32x4 mfma32<f16_t>(u32x4 a, u32x4 b, f32
                                                 0);
 }
 
-__device__ __forceinline__ float row16_max(float x) {
-  x = fmaxf(x, dpp_mov<0x128>(x));
-  x = fmaxf(x, dpp_mov<0x124>(x));
-  x = fmaxf(x, dpp_mov<0x122>(x));
-  x = fmaxf(x, dpp_mov<0x121>(x));
-  return x;
-}
-
-// Orders this wave's LDS stores before its later LDS loads (the compiler
-// may not move them across; the hardware drains lgkmcnt).
-__device__ __forceinline__ void wave_lds_fence() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
-
+// Tile geometry per head dim.  KT kv tokens per tile (64, or 32 at
+// D = 256 to bound registers and LDS), NB 16-token blocks of S^T, NKC
+// 32-token k-chunks of P V.
 template <int D>
-struct Stage {
-  static constexpr int kChunks = D / 8;  // 16-byte chunks per token row
-  static constexpr int kPerThread = kTile * kChunks / kThreads;
-  static_assert(kTile * kChunks % kThreads == 0, "tile must split evenly");
+struct Cfg {
+  static constexpr int KT = D <= 128 ? 64 : 32;
+  static constexpr int NB = KT / 16;
+  static constexpr int NKC = KT / 32;
+  static constexpr int CH = D / 8;                // 16-byte chunks per token row
+  static constexpr int PER = KT * CH / kThreads;  // chunks per thread per tile (K and V each)
+  static constexpr int KSTEPS = D / 32;           // MFMA k-steps of S over the head dim
+  static constexpr int NPAIR = D / 32;            // pairs of 16-dim O tiles
+  static constexpr int KP = D + 8;                // K row pitch (elements): conflict-free 16-byte reads
+  static constexpr int VPW = D / 2 + 4;           // V row pitch (words): rows 4 apart land 16 banks apart
+  static_assert(KT * CH % kThreads == 0, "tile must split evenly");
 };
 
 // Loads this thread's K and V chunks of kv tile `tile` into registers.
@@ -90,14 +87,13 @@ template <typename T, int D>
 __device__ __forceinline__ void load_tile(const T* __restrict__ kc, const T* __restrict__ vc,
                                           const int32_t* __restrict__ ind, int tile, int kv_len, int page_size,
                                           int64_t num_pages, int64_t page_stride, int64_t token_stride,
-                                          int64_t head_off, u32x4 (&kr)[Stage<D>::kPerThread],
-                                          u32x4 (&vr)[Stage<D>::kPerThread]) {
-  constexpr int CH = Stage<D>::kChunks;
+                                          int64_t head_off, u32x4 (&kr)[Cfg<D>::PER], u32x4 (&vr)[Cfg<D>::PER]) {
+  constexpr int CH = Cfg<D>::CH;
 #pragma unroll
-  for (int j = 0; j < Stage<D>::kPerThread; ++j) {
+  for (int j = 0; j < Cfg<D>::PER; ++j) {
     const int c = threadIdx.x + j * kThreads;
     const int tok = c / CH, ch = c % CH;
-    const int pos = tile * kTile + tok;
+    const int pos = tile * Cfg<D>::KT + tok;
     kr[j] = u32x4{0u, 0u, 0u, 0u};
     vr[j] = u32x4{0u, 0u, 0u, 0u};
     if (pos < kv_len) {
@@ -110,6 +106,14 @@ __device__ __forceinline__ void load_tile(const T* __restrict__ kc, const T* __r
   }
 }
 
+// S^T = K Q^T: kv tokens are the MFMA rows and the wave's 16 query rows the
+// columns, so a lane holds one query (column lr) and tokens 4*grp + i of
+// each 16-token block.  The softmax then reduces within the lane and across
+// the four lanes of the column, and the scores are already in the B-operand
+// layout of O^T += V^T P^T: MFMA only needs A and B to agree on which token
+// each k index is, so k index 8*grp + e of a 32-token chunk stands for token
+// 4*grp + e (e < 4) or 16 + 4*grp + (e - 4) (e >= 4) in both operands.  No
+// LDS round trip for P.
 template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(
     const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kc, const T* __restrict__ vc,
@@ -118,17 +122,12 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
     const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ kv_last, const int2* __restrict__ items,
     int n_items, T* __restrict__ o, int64_t o_st, int64_t o_sh, int batch, int hq, int hkv, int page_size,
     int causal, float scale_log2) {
-  constexpr int KSTEPS = D / 32;  // MFMA k-steps over the head dim for S
-  constexpr int NP = D / 32;      // column-tile pairs of O
-  constexpr int CH = Stage<D>::kChunks;
-  constexpr int PER = Stage<D>::kPerThread;
-  constexpr int KP = D + 8;       // K row pitch (elements): 16-byte aligned rows, conflict-free 16-byte reads
-  constexpr int VPW = D / 2 + 2;  // V row pitch in 32-bit words: rows 8 apart land 16 banks apart
-  constexpr int PP = kTile + 8;   // P row pitch (elements)
+  using C = Cfg<D>;
+  constexpr int KT = C::KT, NB = C::NB, NKC = C::NKC, CH = C::CH, PER = C::PER;
+  constexpr int KSTEPS = C::KSTEPS, NPAIR = C::NPAIR, KP = C::KP, VPW = C::VPW;
   constexpr int NPP = std::is_same<T, bf16_t>::value ? 2 : 1;  // P planes: hi (+ lo)
-  __shared__ __align__(16) uint16_t s_k[kTile * KP];
-  __shared__ __align__(16) uint32_t s_v[kTile * VPW];
-  __shared__ __align__(16) uint16_t s_p[kWaves][NPP][16 * PP];
+  __shared__ __align__(16) uint16_t s_k[KT * KP];
+  __shared__ __align__(16) uint32_t s_v[KT * VPW];
 
   const int item = blockIdx.x;
   const int h = blockIdx.y;  // kv head
@@ -150,43 +149,31 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int lr = lane % 16, grp = lane / 16;
 
-  // rows this lane accumulates (accumulator layout: row 4*grp+i of the wave's 16)
-  int c_limit[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int crow = row0 + wave * 16 + grp * 4 + i;
-    const int pos = crow / g;
-    // last visible kv position; rows past the request stay fully masked
-    const int lim = crow >= n_rows ? -1 : (causal ? kv_len - qo_len + pos : kv_len - 1);
-    c_limit[i] = min(lim, kv_len - 1);
-  }
+  // this lane's query row (column lr of the wave's tile) and its last visible kv position
+  const int qrow = row0 + wave * 16 + lr;
+  const int q_pos = qrow / g, q_hg = qrow - q_pos * g;
+  const bool q_ok = qrow < n_rows;
+  const int lim = min(!q_ok ? -1 : (causal ? kv_len - qo_len + q_pos : kv_len - 1), kv_len - 1);
 
-  // Q as the A operand: row lr of the wave, head-dim 32*ks + 8*grp .. +8
-  u32x4 qa[KSTEPS];
+  // Q as the B operand: column lr, head-dim 32*ks + 8*grp .. +8
+  u32x4 qb[KSTEPS];
   {
-    const int arow = row0 + wave * 16 + lr;
-    const int a_pos = arow / g, a_hg = arow - a_pos * g;
-    const bool ok_row = arow < n_rows;
-    const T* qp = q + (int64_t)(qo_begin + a_pos) * q_st + (int64_t)(h * g + a_hg) * q_sh + grp * 8;
+    const T* qp = q + (int64_t)(qo_begin + q_pos) * q_st + (int64_t)(h * g + q_hg) * q_sh + grp * 8;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks)
-      qa[ks] = ok_row ? *reinterpret_cast<const u32x4*>(qp + ks * 32) : u32x4{0u, 0u, 0u, 0u};
+      qb[ks] = q_ok ? *reinterpret_cast<const u32x4*>(qp + ks * 32) : u32x4{0u, 0u, 0u, 0u};
   }
 
-  f32x4 acc[2 * NP];
+  // O^T tiles: tile 2a holds dims 32a + 2*(4*grp + i), tile 2a+1 the next dim; column lr
+  f32x4 acc[2 * NPAIR];
 #pragma unroll
-  for (int nt = 0; nt < 2 * NP; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m[4], l[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m[i] = -INFINITY;
-    l[i] = 0.f;
-  }
+  for (int nt = 0; nt < 2 * NPAIR; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;  // this query's online-softmax state (log2 domain)
 
   // kv tiles this item needs: up to the largest causal limit among its rows
   const int last_row = min(row0 + kRows, n_rows) - 1;
   const int max_pos = min(causal ? kv_len - qo_len + last_row / g : kv_len - 1, kv_len - 1);
-  const int n_tiles = uniform(max_pos < 0 ? 0 : max_pos / kTile + 1);
+  const int n_tiles = uniform(max_pos < 0 ? 0 : max_pos / KT + 1);
 
   u32x4 kr[PER], vr[PER];
   if (n_tiles > 0)
@@ -199,97 +186,114 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
       const int c = threadIdx.x + j * kThreads;
       const int tok = c / CH, ch = c % CH;
       *reinterpret_cast<u32x4*>(&s_k[tok * KP + ch * 8]) = kr[j];
-      u32x2* vd = reinterpret_cast<u32x2*>(&s_v[tok * VPW + ch * 4]);
-      vd[0] = u32x2{vr[j].x, vr[j].y};
-      vd[1] = u32x2{vr[j].z, vr[j].w};
+      *reinterpret_cast<u32x4*>(&s_v[tok * VPW + ch * 4]) = vr[j];
     }
     __syncthreads();
     if (tile + 1 < n_tiles)
       load_tile<T, D>(kc, vc, ind, tile + 1, kv_len, page_size, num_pages, page_stride, token_stride, head_off, kr,
                       vr);
 
-    // ---- S = Q K^T for two 16-token blocks: lane holds rows 4*grp+i, token blk*16+lr
-    f32x4 s[2];
+    // ---- S^T for NB 16-token blocks: lane holds tokens blk*16 + 4*grp + i of query lr
+    f32x4 s[NB];
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
+    for (int blk = 0; blk < NB; ++blk) {
       s[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks) {
-        const u32x4 kb = *reinterpret_cast<const u32x4*>(&s_k[(blk * 16 + lr) * KP + ks * 32 + grp * 8]);
-        s[blk] = mfma32<T>(qa[ks], kb, s[blk]);
+        const u32x4 ka = *reinterpret_cast<const u32x4*>(&s_k[(blk * 16 + lr) * KP + ks * 32 + grp * 8]);
+        s[blk] = mfma32<T>(ka, qb[ks], s[blk]);
       }
     }
-    // ---- mask and online softmax; a row's 16 tokens of a block sit in one 16-lane DPP row
-    float alpha[4];
-    const int p0 = tile * kTile + lr, p1 = p0 + 16;
+    // ---- mask, online softmax: reduce over the lane's tokens, then the column's 4 lanes
+    float mx = -INFINITY;
+    const int t0 = tile * KT + 4 * grp;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v0 = p0 <= c_limit[i] ? s[0][i] * scale_log2 : -INFINITY;
-      const float v1 = p1 <= c_limit[i] ? s[1][i] * scale_log2 : -INFINITY;
-      const float m_new = fmaxf(m[i], row16_max(fmaxf(v0, v1)));
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      alpha[i] = fast_exp2(m[i] - m_use);
-      const float e0 = fast_exp2(v0 - m_use), e1 = fast_exp2(v1 - m_use);
-      l[i] = l[i] * alpha[i] + row16_sum(e0 + e1);
-      m[i] = m_new;
-      s[0][i] = e0;
-      s[1][i] = e1;
-    }
-    // ---- P: accumulator layout -> LDS -> operand layout (row lr, tokens 8*grp .. +8)
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
+    for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const T hi = from_float<T>(s[blk][i]);
-        s_p[wave][0][(grp * 4 + i) * PP + blk * 16 + lr] = __builtin_bit_cast(uint16_t, hi);
-        if constexpr (NPP == 2)
-          s_p[wave][NPP - 1][(grp * 4 + i) * PP + blk * 16 + lr] =
-              __builtin_bit_cast(uint16_t, from_float<T>(s[blk][i] - to_float<T>(hi)));
+        const float v = t0 + blk * 16 + i <= lim ? s[blk][i] * scale_log2 : -INFINITY;
+        s[blk][i] = v;
+        mx = fmaxf(mx, v);
       }
-    wave_lds_fence();
-    u32x4 pa[NPP];
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = fast_exp2(m - m_use);
+    float ps = 0.f;
 #pragma unroll
-    for (int pl = 0; pl < NPP; ++pl) pa[pl] = *reinterpret_cast<const u32x4*>(&s_p[wave][pl][lr * PP + grp * 8]);
+    for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = fast_exp2(s[blk][i] - m_use);
+        s[blk][i] = e;
+        ps += e;
+      }
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    l = l * alpha + ps;
+    m = m_new;
+#pragma unroll
+    for (int nt = 0; nt < 2 * NPAIR; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[nt][i] *= alpha;
 
-    // ---- O = O * alpha + P V; lane column lr of tile pair a covers d = 32a + 2lr (+1)
+    // ---- O^T += V^T P^T per 32-token chunk
 #pragma unroll
-    for (int nt = 0; nt < 2 * NP; ++nt)
+    for (int kc = 0; kc < NKC; ++kc) {
+      // P^T as the B operand: k = 8*grp + e <-> tokens of blocks 2kc (e < 4) and 2kc+1 (e >= 4)
+      u32x4 pbv[NPP];
+      {
+        const f32x4 a0 = s[2 * kc], a1 = s[2 * kc + 1];
+        const float pv[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        uint32_t hw[4], lw[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[nt][i] *= alpha[i];
+        for (int e = 0; e < 4; ++e) {
+          const T h0 = from_float<T>(pv[2 * e]), h1 = from_float<T>(pv[2 * e + 1]);
+          hw[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+          if constexpr (NPP == 2)
+            lw[e] = pack2<T>(pv[2 * e] - to_float<T>(h0), pv[2 * e + 1] - to_float<T>(h1));
+        }
+        pbv[0] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+        if constexpr (NPP == 2) pbv[NPP - 1] = u32x4{lw[0], lw[1], lw[2], lw[3]};
+      }
+      // V^T as the A operand: row lr = dims 32a + 2lr (lo) / +1 (hi), the same 8 tokens
+      int trow[8];
 #pragma unroll
-    for (int a = 0; a < NP; ++a) {
-      uint32_t w[8];
+      for (int e = 0; e < 8; ++e) trow[e] = (kc * 32 + (e < 4 ? 4 * grp + e : 16 + 4 * grp + e - 4)) * VPW;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) w[j] = s_v[(grp * 8 + j) * VPW + 16 * a + lr];
-      u32x4 b_lo, b_hi;
-      b_lo.x = __builtin_amdgcn_perm(w[1], w[0], 0x05040100u);
-      b_hi.x = __builtin_amdgcn_perm(w[1], w[0], 0x07060302u);
-      b_lo.y = __builtin_amdgcn_perm(w[3], w[2], 0x05040100u);
-      b_hi.y = __builtin_amdgcn_perm(w[3], w[2], 0x07060302u);
-      b_lo.z = __builtin_amdgcn_perm(w[5], w[4], 0x05040100u);
-      b_hi.z = __builtin_amdgcn_perm(w[5], w[4], 0x07060302u);
-      b_lo.w = __builtin_amdgcn_perm(w[7], w[6], 0x05040100u);
-      b_hi.w = __builtin_amdgcn_perm(w[7], w[6], 0x07060302u);
+      for (int a = 0; a < NPAIR; ++a) {
+        uint32_t w[8];
 #pragma unroll
-      for (int pl = 0; pl < NPP; ++pl) {
-        acc[2 * a] = mfma32<T>(pa[pl], b_lo, acc[2 * a]);
-        acc[2 * a + 1] = mfma32<T>(pa[pl], b_hi, acc[2 * a + 1]);
+        for (int e = 0; e < 8; ++e) w[e] = s_v[trow[e] + 16 * a + lr];
+        u32x4 a_lo, a_hi;
+        a_lo.x = __builtin_amdgcn_perm(w[1], w[0], 0x05040100u);
+        a_hi.x = __builtin_amdgcn_perm(w[1], w[0], 0x07060302u);
+        a_lo.y = __builtin_amdgcn_perm(w[3], w[2], 0x05040100u);
+        a_hi.y = __builtin_amdgcn_perm(w[3], w[2], 0x07060302u);
+        a_lo.z = __builtin_amdgcn_perm(w[5], w[4], 0x05040100u);
+        a_hi.z = __builtin_amdgcn_perm(w[5], w[4], 0x07060302u);
+        a_lo.w = __builtin_amdgcn_perm(w[7], w[6], 0x05040100u);
+        a_hi.w = __builtin_amdgcn_perm(w[7], w[6], 0x07060302u);
+#pragma unroll
+        for (int pl = 0; pl < NPP; ++pl) {
+          acc[2 * a] = mfma32<T>(a_lo, pbv[pl], acc[2 * a]);
+          acc[2 * a + 1] = mfma32<T>(a_hi, pbv[pl], acc[2 * a + 1]);
+        }
       }
     }
     __syncthreads();  // the next tile overwrites s_k / s_v
   }
 
-  // ---- write: row 4*grp+i, d = 32a + 2lr and +1 as one 32-bit store
+  // ---- write: query lr, dims 32a + 8*grp + 2i and +1 as one 32-bit store
+  if (q_ok) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    T* op = o + (int64_t)(qo_begin + q_pos) * o_st + (int64_t)(h * g + q_hg) * o_sh + 8 * grp;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int crow = row0 + wave * 16 + grp * 4 + i;
-    if (crow >= n_rows) continue;
-    const int pos = crow / g, hg = crow - pos * g;
-    const float inv = l[i] > 0.f ? 1.f / l[i] : 0.f;
-    T* op = o + (int64_t)(qo_begin + pos) * o_st + (int64_t)(h * g + hg) * o_sh;
+    for (int a = 0; a < NPAIR; ++a)
 #pragma unroll
-    for (int a = 0; a < NP; ++a)
-      *reinterpret_cast<uint32_t*>(op + 32 * a + 2 * lr) = pack2<T>(acc[2 * a][i] * inv, acc[2 * a + 1][i] * inv);
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<uint32_t*>(op + 32 * a + 2 * i) = pack2<T>(acc[2 * a][i] * inv, acc[2 * a + 1][i] * inv);
   }
 }
 
@@ -350,7 +354,7 @@ extern "C" int pl_prefill_plan(const int32_t* qo_indptr_h, const int32_t* kv_ind
     for (int64_t r0 = 0; r0 < rows; r0 += kRows) {
       const int64_t last_row = std::min<int64_t>(r0 + kRows, rows) - 1;
       const int64_t max_pos = causal ? kv_len - qo_len + last_row / g : kv_len - 1;
-      list.push_back(Entry{max_pos / kTile + 1, r, (int32_t)r0});
+      list.push_back(Entry{max_pos / kPlanTile + 1, r, (int32_t)r0});
     }
   }
   if (list.size() > (size_t)INT32_MAX / 2) return fail(PL_ERR_INVALID, "too many prefill work items");
