@@ -13,7 +13,7 @@ import pytest
 from pagelora_amd import _lib
 
 ROWS_PER_ITEM = 64
-TILE = 32
+TILE = 64  # kv tokens per unit of the plan's work estimate (kPlanTile)
 
 
 def _plan(qo_indptr, kv_indptr, last, hq, hkv, page_size, causal=True, max_items=None):
