@@ -7,7 +7,8 @@
 //   plan_kernel    one workgroup; reads indptr[B+1] and cuts every row into
 //                  chunks of `chunk_pages` pages (chunk_pages chosen on the
 //                  device from the total page count) -> a work list of
-//                  (row, page range) items.
+//                  (row, page range) items, full-size chunks first and the
+//                  rows' shorter last chunks after them, longest first.
 //   decode_kernel  one wavefront per (item, kv head).  Streams the item's
 //                  pages 16 tokens at a time straight from HBM into VGPRs
 //                  (16 lanes x 16 B cover one 128-dim token row, so one
@@ -39,6 +40,7 @@ struct Item {   // one split-KV work item; lives in the workspace
   int page_end;
   int flags;    // bit0: row has a single item (write o directly)
                 // bit1: item holds the row's last (possibly partial) page
+                // bits 2..: the item's slot (index of its partial output)
 };
 static_assert(sizeof(Item) == 16, "the decode kernel reads an item as one 16-byte load");
 
@@ -59,6 +61,8 @@ inline Layout layout(int batch, int max_items, int hq, int d) {
 
 // ------------------------------------------------------------------ plan ---
 constexpr int kPlanThreads = 1024;
+constexpr int kPlanBuckets = 1024;  // size classes of the rows' last (short) chunks
+static_assert(kPlanBuckets == kPlanThreads, "the class scan takes one class per thread");
 
 // Stamp written into header[2..3] by the plan and checked by the decode and
 // merge kernels, so a run on an unplanned or differently planned workspace
@@ -67,11 +71,47 @@ __host__ __device__ inline int plan_stamp(int batch, int max_items) {
   return (int)(0x51A70000u ^ ((unsigned)batch * 2654435761u) ^ (unsigned)max_items);
 }
 
+// Exclusive prefix sum of one int per thread over the 1024-thread block
+// (shuffles inside each wave, then the 16 wave totals); returns the prefix,
+// writes the block total to *total.  Every thread of the block must call it.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s_wave, int* total) {
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    x += lane >= off ? y : 0;
+  }
+  if (lane == 63) s_wave[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kPlanThreads / 64; ++w) {
+    const int t = s_wave[w];
+    before += w < wave ? t : 0;
+    all += t;
+  }
+  __syncthreads();  // s_wave may be reused by the next scan
+  *total = all;
+  return before + x - v;
+}
+
+// Cuts every row into chunks of `chunk` pages and writes the work list.
+//
+// Two orders are involved.  A row's items get consecutive *slots* (its
+// partial outputs and row_info use them, so the merge reads a row's partials
+// as one range).  The *list* order, which is the order the hardware
+// dispatches the items' waves in, is: every full-size chunk first (row by
+// row), then the rows' last, shorter chunks from the longest to the shortest,
+// so the waves that start last are the ones that finish soonest.  Measured on
+// the ragged batch-64 workload: 743.5 us in row order, 721.2 us in this order.
+// An item's slot travels in its flags (bits 2 and up).
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ indptr, int batch, int indices_capacity, int target_items,
     int min_chunk_pages, int max_items, Item* __restrict__ items,
     int2* __restrict__ row_info, int* __restrict__ header) {
-  __shared__ int s_scan[kPlanThreads];
+  __shared__ int s_wave[kPlanThreads / 64];
+  __shared__ int s_hist[kPlanBuckets];
   __shared__ int s_chunk;
   const int tid = threadIdx.x;
   // Page ranges are clamped to [0, indices_capacity] so a malformed indptr
@@ -83,45 +123,76 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     c = c > min_chunk_pages ? c : min_chunk_pages;
     s_chunk = c > 1 ? c : 1;
   }
+  for (int i = tid; i < kPlanBuckets; i += kPlanThreads) s_hist[i] = 0;
   __syncthreads();
   const int chunk = s_chunk;
+  // size class of a short chunk of `pages` pages (< chunk): longest first
+  auto bucket = [&](int pages) {
+    const int64_t k = chunk - 1 - pages;  // 0 for the longest possible
+    return chunk <= kPlanBuckets ? (int)k : (int)(k * kPlanBuckets / chunk);
+  };
+  auto row_pages = [&](int r, int& pb, int& pe) {
+    pb = clampi(indptr[r]);
+    pe = clampi(indptr[r + 1]);
+    pe = pe > pb ? pe : pb;
+  };
   const int per = (batch + kPlanThreads - 1) / kPlanThreads;
   const int r0 = tid * per;
   const int r1 = min(batch, r0 + per);
-  int local = 0;
+  // pass 1: per-thread counts of slots and full chunks; size classes of the
+  // short chunks (their rank inside the class parked in row_info until pass 2)
+  int n_slots = 0, n_full = 0;
   for (int r = r0; r < r1; ++r) {
-    const int n = clampi(indptr[r + 1]) - clampi(indptr[r]);
+    int pb, pe;
+    row_pages(r, pb, pe);
+    const int n = pe - pb;
     const int nch = n > 0 ? (n + chunk - 1) / chunk : 1;
-    local += nch > 1 ? nch : 1;
+    const int full = n / chunk;
+    n_slots += nch;
+    n_full += full;
+    if (nch > full) {
+      const int k = bucket(n - full * chunk);
+      row_info[r] = make_int2(k, atomicAdd(&s_hist[k], 1));
+    }
   }
-  s_scan[tid] = local;
+  int total_items, total_full;
+  int slot = block_exclusive_scan(n_slots, s_wave, &total_items);
+  int fpos = block_exclusive_scan(n_full, s_wave, &total_full);
+  // exclusive scan of the size classes (one per thread), offset past the full chunks
+  int hist_total;
+  const int hcount = s_hist[tid];
+  const int hstart = block_exclusive_scan(hcount, s_wave, &hist_total);
+  s_hist[tid] = total_full + hstart;
   __syncthreads();
-  for (int off = 1; off < kPlanThreads; off <<= 1) {
-    const int v = tid >= off ? s_scan[tid - off] : 0;
-    __syncthreads();
-    s_scan[tid] += v;
-    __syncthreads();
-  }
-  int it = s_scan[tid] - local;
-  const int total_items = s_scan[kPlanThreads - 1];
+  // pass 2: write the items at their list positions
   for (int r = r0; r < r1; ++r) {
-    const int pb = clampi(indptr[r]);
-    const int pe = pb > clampi(indptr[r + 1]) ? pb : clampi(indptr[r + 1]);
-    int nch = (pe - pb + chunk - 1) / chunk;
-    nch = nch > 1 ? nch : 1;
-    const int room = max_items - it;
-    row_info[r] = make_int2(it < max_items ? it : max_items, nch < room ? nch : (room > 0 ? room : 0));
-    for (int j = 0; j < nch; ++j, ++it) {
-      if (it >= max_items) break;  // unreachable by construction; keeps writes in bounds
+    int pb, pe;
+    row_pages(r, pb, pe);
+    const int n = pe - pb;
+    const int nch = n > 0 ? (n + chunk - 1) / chunk : 1;
+    const int full = n / chunk;
+    int short_pos = -1;
+    if (nch > full) {
+      const int2 kr = row_info[r];  // this thread's own pass-1 write
+      short_pos = s_hist[kr.x] + kr.y;
+    }
+    const int room = max_items - slot;
+    row_info[r] = make_int2(slot < max_items ? slot : max_items, nch < room ? nch : (room > 0 ? room : 0));
+    for (int j = 0; j < nch; ++j) {
+      const int pos = j < full ? fpos + j : short_pos;
+      const int sl = slot + j;
+      if (pos < 0 || pos >= max_items || sl >= max_items) continue;  // unreachable by construction; keeps writes in bounds
       const int a = pb + j * chunk;
       const int e = min(pe, a + chunk);
       Item item;
       item.row = r;
       item.page_begin = a;
       item.page_end = e;
-      item.flags = (nch == 1 ? 1 : 0) | (e == pe ? 2 : 0);
-      items[it] = item;
+      item.flags = (sl << 2) | (nch == 1 ? 1 : 0) | (e == pe ? 2 : 0);
+      items[pos] = item;
     }
+    slot += nch;
+    fpos += full;
   }
   for (int i = total_items + tid; i < max_items; i += kPlanThreads) {
     Item item;
@@ -405,7 +476,7 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
   // (every field takes part in the check, so no part of the item load is
   // deferred past it)
   if (!((stamp_batch == batch) & (stamp == plan_stamp(batch, max_items)) & (b >= 0) & (b < batch) & (pbeg >= 0) &
-        (pend >= pbeg) & ((flags & ~3) == 0)))
+        (pend >= pbeg) & (flags >= 0) & ((flags >> 2) < max_items)))
     return;
   // Second round trip, all at once: the row's last-page fill, the item's
   // first page id and q (below).  The item's pages lie inside the indices
@@ -456,9 +527,10 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
     return;
   }
 
-  // Split row: publish this item's normalised partial and its log2-sum-exp;
-  // merge_kernel combines them after this kernel has finished.
+  // Split row: publish this item's normalised partial and its log2-sum-exp at
+  // the item's slot; merge_kernel combines them after this kernel has finished.
   if (row != 0) return;
+  const int slot = flags >> 2;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int hq = h * G + g;
@@ -466,9 +538,9 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
     float out[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) out[i] = st.acc[g][i] * inv;
-    Lane8<float>::store(part_o + ((int64_t)item_idx * num_qo_heads + hq) * D + col * 8, out);
+    Lane8<float>::store(part_o + ((int64_t)slot * num_qo_heads + hq) * D + col * 8, out);
     if (col == 0)
-      part_lse[(int64_t)item_idx * num_qo_heads + hq] =
+      part_lse[(int64_t)slot * num_qo_heads + hq] =
           st.l[g] > 0.f ? st.m[g] + __log2f(st.l[g]) : -INFINITY;
   }
 }
