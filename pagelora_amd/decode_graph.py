@@ -16,6 +16,8 @@ on every new page.  torch's CUDAGraph is hipGraph on ROCm.
 
 from __future__ import annotations
 
+import gc
+
 from collections import OrderedDict
 from dataclasses import dataclass
 
@@ -115,10 +117,22 @@ class BatchDecodeGraphRunner:
             decode_step_static(self.weights, self.pool, self.backend, ctx)
         cur.wait_stream(side)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            if reserve is not None:  # not in the warm-up: it would grow the rows
-                self.backend.advance_decode(reserve, ctx.positions, ctx.page_id, ctx.page_offset)
-            logits = decode_step_static(self.weights, self.pool, self.backend, ctx)
+        # No Python garbage collection while the stream captures (torch's
+        # graph context no longer collects first): a collected object that
+        # owns pinned host memory or an event, such as an earlier generation's
+        # staging buffers, would make HIP calls from its destructor that are
+        # illegal during capture, and the error raised there aborts the process.
+        gc.collect()
+        gc_was_enabled = gc.isenabled()
+        gc.disable()
+        try:
+            with torch.cuda.graph(graph):
+                if reserve is not None:  # not in the warm-up: it would grow the rows
+                    self.backend.advance_decode(reserve, ctx.positions, ctx.page_id, ctx.page_offset)
+                logits = decode_step_static(self.weights, self.pool, self.backend, ctx)
+        finally:
+            if gc_was_enabled:
+                gc.enable()
         return DecodeGraphEntry(graph=graph, ctx=ctx, logits=logits)
 
     def replay(self, entry: DecodeGraphEntry) -> torch.Tensor:
