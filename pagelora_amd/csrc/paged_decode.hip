@@ -546,16 +546,17 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
 }
 
 // ----------------------------------------------------------------- merge ---
-// One workgroup of kMergeThreads per (row, q head) of a split row.  LPT
-// lanes cover one partial row of D floats; the workgroup takes RPI partial
-// rows per pass and issues up to kMergeBatch passes of loads (each partial's
-// lse and output together) before folding any of them, so a row of up to
+// One workgroup of MT threads per (row, q head) of a split row.  LPT lanes
+// cover one partial row of D floats; the workgroup takes RPI partial rows per
+// pass and issues up to kMergeBatch passes of loads (each partial's lse and
+// output together) before folding any of them, so a row of up to
 // RPI * kMergeBatch items costs one memory round trip.  Each thread folds its
 // partials online (running max, weight sum, weighted output); the threads'
 // states are combined with xor shuffles inside a wave and through LDS across
-// waves.
-constexpr int kMergeThreads = 256;
+// waves.  MT is one wave when the plan averages a few items per row (the
+// ragged batch-64 case: ~5), four waves when rows hold tens of items.
 constexpr int kMergeBatch = 8;
+constexpr int kMergeFewItems = 8;  // average items per row up to which one wave merges
 
 struct MergeState {
   float m, w, a[8];  // log2 max, sum of weights, weighted output (8 dims)
@@ -570,13 +571,13 @@ struct MergeState {
   }
 };
 
-template <typename T, int D>
-__global__ __launch_bounds__(kMergeThreads) void merge_kernel(
+template <typename T, int D, int MT>
+__global__ __launch_bounds__(MT) void merge_kernel(
     const int2* __restrict__ row_info, const float* __restrict__ part_lse,
     const float* __restrict__ part_o, T* __restrict__ o, int64_t o_sb, int64_t o_sh,
     float* __restrict__ lse, const int* __restrict__ header, int batch, int num_qo_heads,
     int max_items) {
-  constexpr int LPT = D / 8, RPI = kMergeThreads / LPT, NWV = kMergeThreads / kWave;
+  constexpr int LPT = D / 8, RPI = MT / LPT, NWV = MT / kWave;
   __shared__ float s_m[NWV][LPT], s_w[NWV][LPT], s_a[NWV][LPT][8];
   const int pair = blockIdx.x;
   if (pair >= batch * num_qo_heads) return;
@@ -595,21 +596,28 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(
   for (int c0 = 0; c0 < n; c0 += RPI * kMergeBatch) {
     float lv[kMergeBatch];
     float4 oa[kMergeBatch], ob[kMergeBatch];
+    // passes of this batch that hold any item (uniform): a row of a few items
+    // issues one pass of loads, not kMergeBatch passes of re-reads
+    const int passes = min(kMergeBatch, (n - c0 + RPI - 1) / RPI);
 #pragma unroll
     for (int k = 0; k < kMergeBatch; ++k) {
-      // past the last item: re-read the last one (in bounds); its weight is dropped below
-      const int c = min(c0 + r + k * RPI, n - 1);
-      const int64_t slot = (int64_t)(first + c) * num_qo_heads + hq;
-      lv[k] = part_lse[slot];
-      oa[k] = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8);
-      ob[k] = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8 + 4);
+      if (k < passes) {
+        // past the last item: re-read the last one (in bounds); its weight is dropped below
+        const int c = min(c0 + r + k * RPI, n - 1);
+        const int64_t slot = (int64_t)(first + c) * num_qo_heads + hq;
+        lv[k] = part_lse[slot];
+        oa[k] = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8);
+        ob[k] = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8 + 4);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);  // the whole batch in flight before the first fold
 #pragma unroll
     for (int k = 0; k < kMergeBatch; ++k) {
-      const bool on = c0 + r + k * RPI < n;
-      const float v[8] = {oa[k].x, oa[k].y, oa[k].z, oa[k].w, ob[k].x, ob[k].y, ob[k].z, ob[k].w};
-      st.add(on ? lv[k] : -INFINITY, on ? 1.f : 0.f, v);
+      if (k < passes) {
+        const bool on = c0 + r + k * RPI < n;
+        const float v[8] = {oa[k].x, oa[k].y, oa[k].z, oa[k].w, ob[k].x, ob[k].y, ob[k].z, ob[k].w};
+        st.add(on ? lv[k] : -INFINITY, on ? 1.f : 0.f, v);
+      }
     }
   }
   // fold the RPI rows: within a wave (xor over the row bits of the lane id) ...
@@ -622,14 +630,16 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(
     st.add(m_o, w_o, a_o);
   }
   // ... then across the waves through LDS
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  if (lane < LPT) {
-    s_m[wave][col] = st.m;
-    s_w[wave][col] = st.w;
+  if constexpr (NWV > 1) {
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    if (lane < LPT) {
+      s_m[wave][col] = st.m;
+      s_w[wave][col] = st.w;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s_a[wave][col][i] = st.a[i];
+      for (int i = 0; i < 8; ++i) s_a[wave][col][i] = st.a[i];
+    }
+    __syncthreads();
   }
-  __syncthreads();
   if (threadIdx.x >= LPT) return;
 #pragma unroll
   for (int w = 1; w < NWV; ++w) {
@@ -674,9 +684,14 @@ int launch(const RunArgs& a) {
     PL_LAUNCH_CHECK("decode_kernel");
   }
   if (!(a.flags & PL_DECODE_SKIP_MERGE)) {
-    hipLaunchKernelGGL((merge_kernel<T, D>), dim3(a.batch * a.hq), dim3(kMergeThreads), 0, a.stream,
-                       a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
-                       a.batch, a.hq, a.max_items);
+    if (a.max_items <= kMergeFewItems * a.batch)
+      hipLaunchKernelGGL((merge_kernel<T, D, kWave>), dim3(a.batch * a.hq), dim3(kWave), 0, a.stream,
+                         a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
+                         a.batch, a.hq, a.max_items);
+    else
+      hipLaunchKernelGGL((merge_kernel<T, D, 4 * kWave>), dim3(a.batch * a.hq), dim3(4 * kWave), 0, a.stream,
+                         a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
+                         a.batch, a.hq, a.max_items);
     PL_LAUNCH_CHECK("merge_kernel");
   }
   return ok();
