@@ -141,6 +141,53 @@ def time_decode(w, steps, warmup):
     return t0.elapsed_time(t1) / steps, decode, merge
 
 
+def time_decode_spaced(w, steps, warmup, evict_bytes=0):
+    """Per-step times of a small decode workload, each step measured on its own.
+
+    A small step (tens of microseconds) is shorter than the host's time to
+    issue its three launches, so back-to-back timing would measure the host.
+    Each step is therefore preceded by GPU work that keeps the device busy
+    while the host queues the step: a spin (warm caches) or, with
+    ``evict_bytes``, a fill of that many bytes, which also evicts the step's
+    K/V from the L2 and the Infinity Cache (cold caches).  Events bracket the
+    plan, decode and merge kernels; returns per-step lists in ms
+    (step = plan + decode + merge, decode, merge).
+    """
+    import torch
+
+    from pagelora_amd import _lib
+    from pagelora_amd.attention_backend import PagedDecodeAttention
+
+    dev = w["q"].device
+    be = PagedDecodeAttention(device=dev, workspace_mb=256, num_qo_heads=w["hq"], num_kv_heads=w["hkv"],
+                              head_dim=w["d"], page_size=w["ps"])
+    be.plan_decode(paged_kv_indptr=w["indptr"], paged_kv_indices=w["indices"], paged_kv_last_page_len=w["last"])
+    out = torch.empty_like(w["q"])
+    junk = torch.empty(evict_bytes, dtype=torch.uint8, device=dev) if evict_bytes else None
+    stream = torch.cuda.current_stream(dev)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    for i in range(warmup + steps):
+        if junk is not None:
+            junk.fill_(i & 0xFF)
+        else:
+            torch.cuda._sleep(200_000)  # ~0.1 ms of spinning while the host queues the step
+        e = ev[i - warmup] if i >= warmup else None
+        if e: e[0].record(stream)
+        be.replan_decode()
+        if e: e[1].record(stream)
+        be.run_decode_into(w["q"], w["cache"], out, flags=_lib.PL_DECODE_SKIP_MERGE)
+        if e: e[2].record(stream)
+        be.run_decode_into(w["q"], w["cache"], out, flags=_lib.PL_DECODE_MERGE_ONLY)
+        if e: e[3].record(stream)
+        if i % 16 == 15:
+            torch.cuda.synchronize(dev)  # bounded queue
+    torch.cuda.synchronize(dev)
+    step = [e[0].elapsed_time(e[3]) for e in ev]
+    decode = [e[1].elapsed_time(e[2]) for e in ev]
+    merge = [e[2].elapsed_time(e[3]) for e in ev]
+    return step, decode, merge
+
+
 def time_lora(device, steps=20):
     """Per-layer no-merge LoRA delta: 64 tokens over 4 adapters, r=16, the 7
     Qwen3-8B modules in their 4 groups (q/k/v, o, gate/up, down)."""
@@ -267,6 +314,58 @@ def cpu_baseline(w, budget_s):
     }
 
 
+def cpu_small_configs():
+    """The float64 numpy oracle on the three small workloads (cfg1: batch 4 x
+    512 tokens fp32, GQA 4; cfg2: batch 1 x 2048 bf16, GQA 4; cfg4: the LoRA
+    delta of 64 tokens over 4 adapters and 7 modules): algorithmic GB/s, the
+    median of 10 runs after 2 warm-ups, one thread."""
+    import torch
+
+    from oracle import lora as olora
+    from oracle import paged_decode as opd
+
+    def median_s(fn):
+        for _ in range(2):
+            fn()
+        ts = []
+        for _ in range(10):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return float(np.median(ts))
+
+    res = {}
+    for name, B, L, dtype, kvb, seed in (("cfg1_b4_512_fp32_gqa4", 4, 512, torch.float32, 4, 1234),
+                                         ("cfg2_b1_2048_bf16_gqa4", 1, 2048, torch.bfloat16, 2, 1235)):
+        ps, hq, hkv, d = 16, 32, 8, 128
+        npg = L // ps
+        gen = torch.Generator().manual_seed(seed)
+        # only the rows' own pages: the pool's other pages cost the oracle nothing
+        cache = torch.randn((B * npg, 2, ps, hkv, d), generator=gen).to(dtype).float().numpy()
+        q = torch.randn((B, hq, d), generator=gen).to(dtype).float().numpy()
+        indptr = np.arange(0, B * npg + 1, npg)
+        indices = np.arange(B * npg)
+        last = [ps] * B
+        sec = median_s(lambda: opd.paged_decode(q, cache, indptr, indices, last))
+        nb = opd.algorithmic_bytes(indptr, last, ps, hq, hkv, d, kvb, kvb)
+        res[name] = {"GBps": round(float(nb) / sec / 1e9, 4), "ms": round(sec * 1e3, 2), "algorithmic_bytes": int(nb)}
+    gen = torch.Generator().manual_seed(1237)
+    T, H, I, r, n = 64, 4096, 12288, 16, 4
+    ids = torch.randint(0, n, (T,), generator=gen).tolist()
+    mods, nb = [], 0
+    for fin, fout in ((H, 4096), (H, 1024), (H, 1024), (H, 4096), (H, I), (H, I), (I, H)):
+        x = torch.randn((T, fin), generator=gen).to(torch.bfloat16).float().numpy()
+        A = (torch.randn((n, r, fin), generator=gen) / fin**0.5).to(torch.bfloat16).float().numpy()
+        Bm = (torch.randn((n, fout, r), generator=gen) * 0.01).to(torch.bfloat16).float().numpy()
+        mods.append((x, A, Bm))
+        nb += (A.size + Bm.size) * 2 + T * fout * 4 + x.size * 2
+    sec = median_s(lambda: [olora.multi_adapter_delta(x, ids, A, Bm, 2.0, intermediate="bf16") for x, A, Bm in mods])
+    res["cfg4_lora_64tok_4adapters_7modules"] = {"GBps": round(float(nb) / sec / 1e9, 4), "ms": round(sec * 1e3, 2),
+                                                 "algorithmic_bytes": int(nb)}
+    res["note"] = "float64 numpy oracle, 1 thread; same algorithmic-byte definitions as the GPU legs"
+    return res
+
+
 def copy_calibration(device):
     import torch
 
@@ -313,17 +412,25 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(w, args.cpu_seconds)
+        if not args.no_extra:
+            extra["cpu_oracle_small_configs"] = cpu_small_configs()
     del w
     torch.cuda.empty_cache()
     if not args.no_extra:
         w2 = qwen3_layer_workload(dev)
-        ms2, per2, merge2 = time_decode(w2, max(args.steps, 100), args.warmup)
-        extra["qwen3_layer_b1_2048_bf16"] = {
-            "decode_kernel_us": round(float(np.mean(per2)) * 1e3, 2),
-            "merge_kernel_us": round(float(np.mean(merge2)) * 1e3, 2),
-            "step_us_incl_plan": round(ms2 * 1e3, 2),
-            "algorithmic_GBps": round(algorithmic_bytes(w2) / (float(np.mean(per2)) * 1e-3) / 1e9, 1),
-        }
+        nb2 = algorithmic_bytes(w2)
+        leg = {"algorithmic_bytes": nb2, "timing": "events around each kernel, the step queued behind GPU work"}
+        for tag, evict in (("warm", 0), ("cold", 512 << 20)):
+            st2, per2, merge2 = time_decode_spaced(w2, max(args.steps, 100), args.warmup, evict_bytes=evict)
+            dk = float(np.median(per2))
+            leg[tag] = {
+                "decode_kernel_us": round(dk * 1e3, 2),
+                "merge_kernel_us": round(float(np.median(merge2)) * 1e3, 2),
+                "step_us_incl_plan": round(float(np.median(st2)) * 1e3, 2),
+                "algorithmic_GBps": round(nb2 / (dk * 1e-3) / 1e9, 1),
+            }
+        leg["cold"]["note"] = "a 512 MiB fill before each step evicts the K/V from the L2 and the 256 MB Infinity Cache"
+        extra["qwen3_layer_b1_2048_bf16"] = leg
         del w2
         torch.cuda.empty_cache()
         lora_ms, lora_bytes = time_lora(dev)

@@ -36,16 +36,26 @@ from . import _lib
 # Split-KV sizing.  The decode grid is (target_items + batch) x kv heads
 # waves whatever the lengths (so one captured graph replays as rows grow), and
 # the device plan cuts rows into chunks of max(min_chunk, total/target_items)
-# pages.  Unset, target waves scale with the batch: 256 per row, at least
-# 1024 and at most 8192 (about 32 waves per CU on MI355X's 256 CUs).
+# pages.  The default item count was measured on MI355X (1,024 SIMDs), step
+# time of plan + decode + merge:
+#   - batch <= 32: 128 items (4 x 2114 and 1 x 32K tokens, GQA 4: 1,024 waves,
+#     one per SIMD; 256 or 64 items were 5-10% slower);
+#   - larger batches with 8 kv heads: 256 items (64 x 2048 GQA 4: 99 us
+#     against 118 us at 1,024 items; ragged 64 x U[128, 8192]: 204 vs 217 us);
+#   - larger batches with >= 16 kv heads: 192 items, i.e. 6 waves per SIMD
+#     (ragged batch-64 MHA: 713.5 us against 729 us at 256 items).
+# An item count that leaves an uneven number of waves per SIMD is slower
+# (64 x 2048 GQA 4 at 192 items: 108 us).
 _ENV_TARGET_WAVES = os.environ.get("PAGELORA_DECODE_TARGET_WAVES")
 _DEFAULT_MIN_CHUNK_PAGES = int(os.environ.get("PAGELORA_DECODE_MIN_CHUNK_PAGES", "4"))
 
 
-def default_target_waves(batch: int) -> int:
+def default_target_items(batch: int, num_kv_heads: int) -> int:
     if _ENV_TARGET_WAVES:
-        return int(_ENV_TARGET_WAVES)
-    return max(1024, min(8192, 256 * batch))
+        return max(1, int(_ENV_TARGET_WAVES) // num_kv_heads)
+    if batch <= 32:
+        return 128
+    return 192 if num_kv_heads >= 16 else 256
 
 
 def _validate_host_table(indptr: torch.Tensor, indices: torch.Tensor, last: torch.Tensor, page_size: int) -> int:
@@ -119,7 +129,7 @@ class PagedDecodeAttention:
         # FlashInfer's tensor-core kernel for ratios outside {1,2,4,8}).
         self.decode_use_tensor_cores = False
         self.use_flashinfer_qk_norm = False
-        self.target_waves = int(target_waves) if target_waves else None  # None: default_target_waves(batch)
+        self.target_waves = int(target_waves) if target_waves else None  # None: default_target_items(...)
         self.min_chunk_pages = int(min_chunk_pages or _DEFAULT_MIN_CHUNK_PAGES)
         if self.device.type == "cuda":
             self._lib = _lib.load()  # fails loudly when the extension is not built
@@ -250,10 +260,13 @@ class PagedDecodeAttention:
         _lib.check(status, "pl_decode_plan")
 
     def _target_items(self, batch: int) -> int:
-        """Work items per step: about target_waves wavefronts, within the workspace."""
+        """Work items per step (target_waves / kv heads if set, else the
+        measured default), within the workspace."""
 
-        waves = self.target_waves if self.target_waves else default_target_waves(batch)
-        t = max(1, waves // self.num_kv_heads)
+        if self.target_waves:
+            t = max(1, self.target_waves // self.num_kv_heads)
+        else:
+            t = default_target_items(batch, self.num_kv_heads)
         cap = self.workspace_buffer.numel()
         while t > 1 and self._lib.pl_decode_workspace_size(batch, t, self.num_qo_heads, self.head_dim) > cap:
             t //= 2
