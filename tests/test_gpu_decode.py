@@ -92,6 +92,33 @@ def test_random_shapes(gpu_device, dtype, heads, head_dim):
         np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=2e-3 if dtype != torch.float32 else 1e-4)
 
 
+def test_large_batch_plan(gpu_device):
+    """2,500 rows: the plan kernel's threads each own several rows (its
+    per-thread row loop and the size-class stash), and the rows' short last
+    chunks fill many size classes; split and unsplit plans."""
+    lens = [0, 1, 16, 17] + uniform_lens(2496, 0, 200, 77)
+    case = ragged_case(lens=lens, hq=8, hkv=2, head_dim=64, page_size=16, dtype=torch.float16,
+                       device=gpu_device, seed=78, pool_extra=9)
+    ref, ref_lse = _oracle(case)
+    for tw in (2 * 600, 2 * 20000):
+        out, lse, _ = _run(case, 8, 2, 64, 16, torch.float16, gpu_device, lse=True, target_waves=tw,
+                           min_chunk_pages=1, workspace_mb=128)
+        _check(out, ref, torch.float16)
+        np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=2e-3)
+
+
+def test_plan_coarse_size_classes(gpu_device):
+    """Chunks longer than the plan's 1,024 size classes (one or two items for
+    the whole batch): the short chunks are ordered by coarse classes."""
+    lens = [16 * 2900, 16 * 100 + 5, 16 * 1500, 0, 16 * 2999 + 1, 7]
+    case = ragged_case(lens=lens, hq=4, hkv=1, head_dim=64, page_size=16, dtype=torch.float16,
+                       device=gpu_device, seed=79, pool_extra=5)
+    ref, _ = _oracle(case)
+    for tw in (1, 2, 3):
+        out, _, _ = _run(case, 4, 1, 64, 16, torch.float16, gpu_device, target_waves=tw, min_chunk_pages=1)
+        _check(out, ref, torch.float16)
+
+
 @pytest.mark.parametrize("page_size", [16, 32, 64])
 def test_page_sizes(gpu_device, page_size):
     lens = [1, page_size - 1, page_size, page_size + 1, 5 * page_size + 3, 700]
