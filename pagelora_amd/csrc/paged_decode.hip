@@ -164,35 +164,50 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   const int hstart = block_exclusive_scan(hcount, s_wave, &hist_total);
   s_hist[tid] = total_full + hstart;
   __syncthreads();
-  // pass 2: write the items at their list positions
-  for (int r = r0; r < r1; ++r) {
-    int pb, pe;
-    row_pages(r, pb, pe);
-    const int n = pe - pb;
-    const int nch = n > 0 ? (n + chunk - 1) / chunk : 1;
-    const int full = n / chunk;
-    int short_pos = -1;
-    if (nch > full) {
-      const int2 kr = row_info[r];  // this thread's own pass-1 write
-      short_pos = s_hist[kr.x] + kr.y;
+  // pass 2: row_info, then the items.  The lanes of a wave take turns
+  // broadcasting their row and the whole wave writes that row's chunks, so a
+  // row of hundreds of chunks is not written by one thread alone (a single
+  // 32K-token row cut into 128 items took 16 us that way).
+  const int lane = tid % 64;
+  for (int k = 0; k < per; ++k) {  // the same trip count in every thread
+    const int r = r0 + k;
+    int pb = 0, pe = 0, nch = 0, full = 0, short_pos = -1;
+    const int my_slot = slot, my_fpos = fpos;
+    if (r < r1) {
+      row_pages(r, pb, pe);
+      const int n = pe - pb;
+      nch = n > 0 ? (n + chunk - 1) / chunk : 1;
+      full = n / chunk;
+      if (nch > full) {
+        const int2 kr = row_info[r];  // this thread's own pass-1 write
+        short_pos = s_hist[kr.x] + kr.y;
+      }
+      const int room = max_items - slot;
+      row_info[r] = make_int2(slot < max_items ? slot : max_items, nch < room ? nch : (room > 0 ? room : 0));
+      slot += nch;
+      fpos += full;
     }
-    const int room = max_items - slot;
-    row_info[r] = make_int2(slot < max_items ? slot : max_items, nch < room ? nch : (room > 0 ? room : 0));
-    for (int j = 0; j < nch; ++j) {
-      const int pos = j < full ? fpos + j : short_pos;
-      const int sl = slot + j;
-      if (pos < 0 || pos >= max_items || sl >= max_items) continue;  // unreachable by construction; keeps writes in bounds
-      const int a = pb + j * chunk;
-      const int e = min(pe, a + chunk);
-      Item item;
-      item.row = r;
-      item.page_begin = a;
-      item.page_end = e;
-      item.flags = (sl << 2) | (nch == 1 ? 1 : 0) | (e == pe ? 2 : 0);
-      items[pos] = item;
+    for (int src = 0; src < 64; ++src) {
+      const int nL = __builtin_amdgcn_readlane(nch, src);
+      if (nL == 0) continue;  // no row in that lane
+      const int rL = __builtin_amdgcn_readlane(r, src), pbL = __builtin_amdgcn_readlane(pb, src);
+      const int peL = __builtin_amdgcn_readlane(pe, src), fullL = __builtin_amdgcn_readlane(full, src);
+      const int slotL = __builtin_amdgcn_readlane(my_slot, src), fposL = __builtin_amdgcn_readlane(my_fpos, src);
+      const int shortL = __builtin_amdgcn_readlane(short_pos, src);
+      for (int j = lane; j < nL; j += 64) {
+        const int pos = j < fullL ? fposL + j : shortL;
+        const int sl = slotL + j;
+        if (pos < 0 || pos >= max_items || sl >= max_items) continue;  // unreachable by construction; keeps writes in bounds
+        const int a = pbL + j * chunk;
+        const int e = min(peL, a + chunk);
+        Item item;
+        item.row = rL;
+        item.page_begin = a;
+        item.page_end = e;
+        item.flags = (sl << 2) | (nL == 1 ? 1 : 0) | (e == peL ? 2 : 0);
+        items[pos] = item;
+      }
     }
-    slot += nch;
-    fpos += full;
   }
   for (int i = total_items + tid; i < max_items; i += kPlanThreads) {
     Item item;
