@@ -68,6 +68,19 @@ template <> __device__ __forceinline__ f32x4 mfma32<f16_t>(u32x4 a, u32x4 b, f32
 // Tile geometry per head dim.  KT kv tokens per tile (64, or 32 at
 // D = 256 to bound registers and LDS), NB 16-token blocks of S^T, NKC
 // 32-token k-chunks of P V.
+// Two probabilities (finite, in [0, 1]) packed as the PV operand type with
+// the hardware round-to-nearest-even conversion: v_cvt_pk_bf16_f32 for bf16,
+// one instruction per pair instead of the bit-level rounding the outputs use
+// (which also handles NaN).
+typedef float f32x2_pp __attribute__((ext_vector_type(2)));
+template <typename T> __device__ __forceinline__ uint32_t pack_p(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack_p<bf16_t>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_pp{a, b}, bf16x2_t));
+}
+template <> __device__ __forceinline__ uint32_t pack_p<f16_t>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_pp{a, b}, half2_t));
+}
+
 template <int D>
 struct Cfg {
   static constexpr int KT = D <= 128 ? 64 : 32;
@@ -232,11 +245,18 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
     ps += __shfl_xor(ps, 16);
     ps += __shfl_xor(ps, 32);
     l = l * alpha + ps;
+    // Rescale the accumulators only when some query's running max rose in
+    // this tile (alpha is exactly 1 everywhere else); after the first tiles
+    // that is the exception, and the rescale is 32 multiplies plus the moves
+    // of the accumulators between register files.
+    const bool rose = m_new > m;
     m = m_new;
+    if (__builtin_amdgcn_ballot_w64(rose) != 0) {
 #pragma unroll
-    for (int nt = 0; nt < 2 * NPAIR; ++nt)
+      for (int nt = 0; nt < 2 * NPAIR; ++nt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[nt][i] *= alpha;
+        for (int i = 0; i < 4; ++i) acc[nt][i] *= alpha;
+    }
 
     // ---- O^T += V^T P^T per 32-token chunk
 #pragma unroll
@@ -249,10 +269,12 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
         uint32_t hw[4], lw[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const T h0 = from_float<T>(pv[2 * e]), h1 = from_float<T>(pv[2 * e + 1]);
-          hw[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-          if constexpr (NPP == 2)
-            lw[e] = pack2<T>(pv[2 * e] - to_float<T>(h0), pv[2 * e + 1] - to_float<T>(h1));
+          hw[e] = pack_p<T>(pv[2 * e], pv[2 * e + 1]);
+          if constexpr (NPP == 2) {
+            float h0, h1;
+            unpack2<T>(hw[e], h0, h1);
+            lw[e] = pack_p<T>(pv[2 * e] - h0, pv[2 * e + 1] - h1);
+          }
         }
         pbv[0] = u32x4{hw[0], hw[1], hw[2], hw[3]};
         if constexpr (NPP == 2) pbv[NPP - 1] = u32x4{lw[0], lw[1], lw[2], lw[3]};
