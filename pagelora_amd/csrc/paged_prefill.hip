@@ -96,25 +96,51 @@ struct Cfg {
 };
 
 // Loads this thread's K and V chunks of kv tile `tile` into registers.
-template <typename T, int D>
+// Chunk j of a thread holds token RPP*j + threadIdx.x / CH of the tile
+// (RPP = kThreads / CH token rows per pass).  ALIGNED (page_size a multiple
+// of RPP): the RPP tokens of a pass lie in one page, so the page id and the
+// pass's base offset are the same for the whole workgroup and come from
+// scalar loads and scalar arithmetic; each lane only adds its fixed offset.
+template <typename T, int D, bool ALIGNED>
 __device__ __forceinline__ void load_tile(const T* __restrict__ kc, const T* __restrict__ vc,
                                           const int32_t* __restrict__ ind, int tile, int kv_len, int page_size,
                                           int64_t num_pages, int64_t page_stride, int64_t token_stride,
                                           int64_t head_off, u32x4 (&kr)[Cfg<D>::PER], u32x4 (&vr)[Cfg<D>::PER]) {
   constexpr int CH = Cfg<D>::CH;
+  constexpr int RPP = kThreads / CH;
+  if constexpr (ALIGNED) {
+    const int tok0 = threadIdx.x / CH;
+    const int64_t lane_off = (int64_t)tok0 * token_stride + head_off + (threadIdx.x % CH) * 8;
 #pragma unroll
-  for (int j = 0; j < Cfg<D>::PER; ++j) {
-    const int c = threadIdx.x + j * kThreads;
-    const int tok = c / CH, ch = c % CH;
-    const int pos = tile * Cfg<D>::KT + tok;
-    kr[j] = u32x4{0u, 0u, 0u, 0u};
-    vr[j] = u32x4{0u, 0u, 0u, 0u};
-    if (pos < kv_len) {
-      int64_t page = ind[pos / page_size];
-      page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);
-      const int64_t off = page * page_stride + (int64_t)(pos % page_size) * token_stride + head_off + ch * 8;
-      kr[j] = *reinterpret_cast<const u32x4*>(kc + off);
-      vr[j] = *reinterpret_cast<const u32x4*>(vc + off);
+    for (int j = 0; j < Cfg<D>::PER; ++j) {
+      const int g0 = uniform(tile * Cfg<D>::KT + RPP * j);  // first token of the pass
+      kr[j] = u32x4{0u, 0u, 0u, 0u};
+      vr[j] = u32x4{0u, 0u, 0u, 0u};
+      if (g0 < kv_len) {
+        int64_t page = uniform(ind[g0 / page_size]);
+        page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);
+        const int64_t base = page * page_stride + (int64_t)(g0 % page_size) * token_stride;
+        if (g0 + tok0 < kv_len) {
+          kr[j] = *reinterpret_cast<const u32x4*>(kc + base + lane_off);
+          vr[j] = *reinterpret_cast<const u32x4*>(vc + base + lane_off);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < Cfg<D>::PER; ++j) {
+      const int c = threadIdx.x + j * kThreads;
+      const int tok = c / CH, ch = c % CH;
+      const int pos = tile * Cfg<D>::KT + tok;
+      kr[j] = u32x4{0u, 0u, 0u, 0u};
+      vr[j] = u32x4{0u, 0u, 0u, 0u};
+      if (pos < kv_len) {
+        int64_t page = ind[pos / page_size];
+        page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);
+        const int64_t off = page * page_stride + (int64_t)(pos % page_size) * token_stride + head_off + ch * 8;
+        kr[j] = *reinterpret_cast<const u32x4*>(kc + off);
+        vr[j] = *reinterpret_cast<const u32x4*>(vc + off);
+      }
     }
   }
 }
@@ -127,7 +153,7 @@ __device__ __forceinline__ void load_tile(const T* __restrict__ kc, const T* __r
 // each k index is, so k index 8*grp + e of a 32-token chunk stands for token
 // 4*grp + e (e < 4) or 16 + 4*grp + (e - 4) (e >= 4) in both operands.  No
 // LDS round trip for P.
-template <typename T, int D>
+template <typename T, int D, bool ALIGNED>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(
     const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kc, const T* __restrict__ vc,
     int64_t page_stride, int64_t token_stride, int64_t head_stride, int64_t num_pages,
@@ -190,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
 
   u32x4 kr[PER], vr[PER];
   if (n_tiles > 0)
-    load_tile<T, D>(kc, vc, ind, 0, kv_len, page_size, num_pages, page_stride, token_stride, head_off, kr, vr);
+    load_tile<T, D, ALIGNED>(kc, vc, ind, 0, kv_len, page_size, num_pages, page_stride, token_stride, head_off, kr, vr);
 
   for (int tile = 0; tile < n_tiles; ++tile) {
     // ---- registers -> LDS, then start the next tile's loads
@@ -203,7 +229,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
     }
     __syncthreads();
     if (tile + 1 < n_tiles)
-      load_tile<T, D>(kc, vc, ind, tile + 1, kv_len, page_size, num_pages, page_stride, token_stride, head_off, kr,
+      load_tile<T, D, ALIGNED>(kc, vc, ind, tile + 1, kv_len, page_size, num_pages, page_stride, token_stride, head_off, kr,
                       vr);
 
     // ---- S^T for NB 16-token blocks: lane holds tokens blk*16 + 4*grp + i of query lr
@@ -324,7 +350,10 @@ int launch(dim3 grid, hipStream_t s, const void* q, int64_t q_st, int64_t q_sh, 
            int64_t ps_, int64_t ts, int64_t hs, int64_t np, const int32_t* qo, const int32_t* kvi,
            const int32_t* ind, const int32_t* last, const int2* items, int n_items, void* o, int64_t o_st,
            int64_t o_sh, int batch, int hq, int hkv, int page_size, int causal, float sl2) {
-  hipLaunchKernelGGL((prefill_kernel<T, D>), grid, dim3(kThreads), 0, s, (const T*)q, q_st, q_sh, (const T*)kc,
+  // pages a whole number of token rows per load pass: scalar page addressing
+  const bool aligned = page_size % (kThreads / Cfg<D>::CH) == 0;
+  auto kern = aligned ? prefill_kernel<T, D, true> : prefill_kernel<T, D, false>;
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, s, (const T*)q, q_st, q_sh, (const T*)kc,
                      (const T*)vc, ps_, ts, hs, np, qo, kvi, ind, last, items, n_items, (T*)o, o_st, o_sh, batch,
                      hq, hkv, page_size, causal, sl2);
   PL_LAUNCH_CHECK("prefill_kernel");
