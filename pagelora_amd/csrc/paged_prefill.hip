@@ -111,18 +111,33 @@ __device__ __forceinline__ void load_tile(const T* __restrict__ kc, const T* __r
   if constexpr (ALIGNED) {
     const int tok0 = threadIdx.x / CH;
     const int64_t lane_off = (int64_t)tok0 * token_stride + head_off + (threadIdx.x % CH) * 8;
+    auto pass_base = [&](int g0) -> int64_t {  // g0: first token of the pass (< kv_len)
+      int64_t page = uniform(ind[g0 / page_size]);
+      page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);
+      return page * page_stride + (int64_t)(g0 % page_size) * token_stride;
+    };
+    if (uniform((tile + 1) * Cfg<D>::KT <= kv_len ? 1 : 0)) {
+      // a whole tile: every token exists, no zero fill
 #pragma unroll
-    for (int j = 0; j < Cfg<D>::PER; ++j) {
-      const int g0 = uniform(tile * Cfg<D>::KT + RPP * j);  // first token of the pass
-      kr[j] = u32x4{0u, 0u, 0u, 0u};
-      vr[j] = u32x4{0u, 0u, 0u, 0u};
-      if (g0 < kv_len) {
-        int64_t page = uniform(ind[g0 / page_size]);
-        page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);
-        const int64_t base = page * page_stride + (int64_t)(g0 % page_size) * token_stride;
-        if (g0 + tok0 < kv_len) {
-          kr[j] = *reinterpret_cast<const u32x4*>(kc + base + lane_off);
-          vr[j] = *reinterpret_cast<const u32x4*>(vc + base + lane_off);
+      for (int j = 0; j < Cfg<D>::PER; ++j) {
+        const int64_t base = pass_base(uniform(tile * Cfg<D>::KT + RPP * j));
+        kr[j] = *reinterpret_cast<const u32x4*>(kc + base + lane_off);
+        vr[j] = *reinterpret_cast<const u32x4*>(vc + base + lane_off);
+      }
+    } else {
+      // the row's last tile: tokens past kv_len read as zeros (their scores
+      // are masked, and a zero V keeps an unused slot's contents out of P V)
+#pragma unroll
+      for (int j = 0; j < Cfg<D>::PER; ++j) {
+        const int g0 = uniform(tile * Cfg<D>::KT + RPP * j);
+        kr[j] = u32x4{0u, 0u, 0u, 0u};
+        vr[j] = u32x4{0u, 0u, 0u, 0u};
+        if (g0 < kv_len) {
+          const int64_t base = pass_base(g0);
+          if (g0 + tok0 < kv_len) {
+            kr[j] = *reinterpret_cast<const u32x4*>(kc + base + lane_off);
+            vr[j] = *reinterpret_cast<const u32x4*>(vc + base + lane_off);
+          }
         }
       }
     }
