@@ -33,12 +33,15 @@ HIPCC_FLAGS = [
 ]
 
 
-# Per-source additions.  paged_prefill: MFMA accumulators in ordinary VGPRs
-# rather than AGPRs, so the softmax rescale works on them in place (no copies
-# between the register files each tile) and the kernel needs 164 registers
-# instead of 192 (three waves per SIMD instead of two).
+# Per-source additions: MFMA accumulators in ordinary VGPRs rather than
+# AGPRs.  paged_prefill: the softmax rescale then works on them in place (no
+# copies between the register files each tile) and the kernel needs 158
+# registers instead of 192 (three waves per SIMD instead of two).  lora: the
+# shrink kernel 72 -> 56 registers, the expand 72 -> 66.
+_MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 FILE_FLAGS = {
-    "paged_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "paged_prefill.hip": _MFMA_VGPR,
+    "lora.hip": _MFMA_VGPR,
 }
 
 

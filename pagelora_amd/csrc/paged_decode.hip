@@ -62,6 +62,7 @@ inline Layout layout(int batch, int max_items, int hq, int d) {
 // ------------------------------------------------------------------ plan ---
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanBuckets = 1024;  // size classes of the rows' last (short) chunks
+constexpr int kPlanOwnChunks = 8;   // rows of up to this many chunks are written by their own thread
 static_assert(kPlanBuckets == kPlanThreads, "the class scan takes one class per thread");
 
 // Stamp written into header[2..3] by the plan and checked by the decode and
@@ -164,10 +165,11 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   const int hstart = block_exclusive_scan(hcount, s_wave, &hist_total);
   s_hist[tid] = total_full + hstart;
   __syncthreads();
-  // pass 2: row_info, then the items.  The lanes of a wave take turns
-  // broadcasting their row and the whole wave writes that row's chunks, so a
-  // row of hundreds of chunks is not written by one thread alone (a single
-  // 32K-token row cut into 128 items took 16 us that way).
+  // pass 2: row_info, then the items.  A row of a few chunks is written by
+  // its own thread; a longer row is broadcast to its wave, whose 64 lanes
+  // write its chunks together (a single 32K-token row cut into 128 items took
+  // 16 us in one thread; walking every lane's row through the whole wave cost
+  // the batch-64 plan ~12 us instead).
   const int lane = tid % 64;
   for (int k = 0; k < per; ++k) {  // the same trip count in every thread
     const int r = r0 + k;
@@ -187,26 +189,32 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       slot += nch;
       fpos += full;
     }
-    for (int src = 0; src < 64; ++src) {
+    // item j of a row: list position, slot, page range, flags
+    auto put = [&](int rr, int pb_, int pe_, int n_, int full_, int slot_, int fpos_, int short_, int j) {
+      const int pos = j < full_ ? fpos_ + j : short_;
+      const int sl = slot_ + j;
+      if (pos < 0 || pos >= max_items || sl >= max_items) return;  // unreachable by construction; keeps writes in bounds
+      const int a = pb_ + j * chunk;
+      const int e = min(pe_, a + chunk);
+      Item item;
+      item.row = rr;
+      item.page_begin = a;
+      item.page_end = e;
+      item.flags = (sl << 2) | (n_ == 1 ? 1 : 0) | (e == pe_ ? 2 : 0);
+      items[pos] = item;
+    };
+    if (nch <= kPlanOwnChunks)
+      for (int j = 0; j < nch; ++j) put(r, pb, pe, nch, full, my_slot, my_fpos, short_pos, j);
+    uint64_t long_rows = __builtin_amdgcn_ballot_w64(nch > kPlanOwnChunks);
+    while (long_rows) {  // the same mask in every lane: a uniform loop
+      const int src = __builtin_ctzll(long_rows);
+      long_rows &= long_rows - 1;
       const int nL = __builtin_amdgcn_readlane(nch, src);
-      if (nL == 0) continue;  // no row in that lane
       const int rL = __builtin_amdgcn_readlane(r, src), pbL = __builtin_amdgcn_readlane(pb, src);
       const int peL = __builtin_amdgcn_readlane(pe, src), fullL = __builtin_amdgcn_readlane(full, src);
       const int slotL = __builtin_amdgcn_readlane(my_slot, src), fposL = __builtin_amdgcn_readlane(my_fpos, src);
       const int shortL = __builtin_amdgcn_readlane(short_pos, src);
-      for (int j = lane; j < nL; j += 64) {
-        const int pos = j < fullL ? fposL + j : shortL;
-        const int sl = slotL + j;
-        if (pos < 0 || pos >= max_items || sl >= max_items) continue;  // unreachable by construction; keeps writes in bounds
-        const int a = pbL + j * chunk;
-        const int e = min(peL, a + chunk);
-        Item item;
-        item.row = rL;
-        item.page_begin = a;
-        item.page_end = e;
-        item.flags = (sl << 2) | (nL == 1 ? 1 : 0) | (e == peL ? 2 : 0);
-        items[pos] = item;
-      }
+      for (int j = lane; j < nL; j += 64) put(rL, pbL, peL, nL, fullL, slotL, fposL, shortL, j);
     }
   }
   for (int i = total_items + tid; i < max_items; i += kPlanThreads) {
