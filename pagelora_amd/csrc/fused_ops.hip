@@ -472,7 +472,7 @@ struct QkvLora {
 
 // Grid (token, group of 4 heads); a wave takes one head; lane l holds dims l
 // and l + D/2 (the rotate-half pair), i.e. D/128 pairs per lane.
-template <typename T, int D, int R>
+template <typename T, int D, int R, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(
     const T* __restrict__ qkv, int64_t ld_qkv, const T* __restrict__ q_norm_w,
     const T* __restrict__ k_norm_w, const int64_t* __restrict__ positions,
@@ -485,105 +485,114 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(
   constexpr int kPPL = (kPairs + kWave - 1) / kWave;  // pairs per lane
   constexpr int RR = R > 0 ? R : 8;
   const int b = blockIdx.x;
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  int a = -1;
-  LoraRow<RR> y[3];
-  if constexpr (R > 0) {
-    a = lora.m[0].adapter >= 0 ? lora.m[0].adapter : ids[b];
-    if (a < 0 || a >= n_adapters) a = -1;
-    if (a >= 0) {
-#pragma unroll
-      for (int m = 0; m < 3; ++m) {
-        if (xs.splits > 0)
-          load_y_split<T, R>(xs, lora.m[m], b, a, y[m]);
-        else
-          load_y<T, R>(lora.m[m], b, a, y[m]);
-      }
-    }
-  }
-  const float pos = (float)positions[b];
-  // rotation of pair i: angle = pos * inv_freq[i], the fp32 product the
-  // reference forms (inv_freq is the caller's table, scaling folded in)
-  float cs[kPPL], sn[kPPL];
+  // the wave's head: the grid has ceil(heads / 4) groups of 4 waves, so each
+  // wave has at most one; it is wave-uniform, and so is its LoRA module,
+  // whose descriptor then comes from scalar loads
+  const int lane = threadIdx.x % kWave, wave = uniform(threadIdx.x / kWave);
+  const int heads = hq + 2 * hkv;
+  const int h = blockIdx.y * (kThreads / kWave) + wave;
+  if (h >= heads) return;
+  const bool is_q = h < hq, is_k = !is_q && h < hq + hkv;
+  const T* src = qkv + b * ld_qkv + (int64_t)h * D;
+
+  // ---- every load first: the row's values, the norm weights, the LoRA
+  // rows, the position and the append slot, all in one round trip
+  float lo[kPPL], hi[kPPL];
 #pragma unroll
   for (int j = 0; j < kPPL; ++j) {
     const int i = lane + j * kWave;
-    sincosf(pos * (i < kPairs ? inv_freq[i] : 0.f), &sn[j], &cs[j]);
-  }
-  const int64_t p = page_id[b], off = offset[b];
-  const bool slot_ok = p >= 0 && p < num_pages && off >= 0 && off < page_size;
-  const T* row = qkv + b * ld_qkv;
-  const int heads = hq + 2 * hkv;
-  // grid.y spreads the heads: this wave's heads are h = blockIdx.y * 4 + wave (+ stride)
-  for (int h = blockIdx.y * (kThreads / kWave) + wave; h < heads; h += gridDim.y * (kThreads / kWave)) {
-    const bool is_q = h < hq, is_k = !is_q && h < hq + hkv;
-    const T* src = row + (int64_t)h * D;
-    float lo[kPPL], hi[kPPL];
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < kPPL; ++j) {
-      const int i = lane + j * kWave;
-      if (xs.splits > 0) {
-        lo[j] = i < kPairs ? load1_split<T>(xs, b, h * D + i) : 0.f;
-        hi[j] = i < kPairs ? load1_split<T>(xs, b, h * D + i + kPairs) : 0.f;
-      } else {
-        lo[j] = i < kPairs ? to_float<T>(src[i]) : 0.f;
-        hi[j] = i < kPairs ? to_float<T>(src[i + kPairs]) : 0.f;
-      }
-    }
-    if constexpr (R > 0) {
-      if (a >= 0) {
-        const int mod = is_q ? 0 : (is_k ? 1 : 2);
-        const int mcol = (h - (is_q ? 0 : (is_k ? hq : hq + hkv))) * D;  // first column in its module
-        const LoraRow<RR>& ym = mod == 0 ? y[0] : (mod == 1 ? y[1] : y[2]);
-#pragma unroll
-        for (int j = 0; j < kPPL; ++j) {
-          const int i = lane + j * kWave;
-          if (i < kPairs) {
-            lo[j] = through<T>(lo[j] + lora_delta1<T, R>(lora.m[mod], a, mcol + i, ym));
-            hi[j] = through<T>(hi[j] + lora_delta1<T, R>(lora.m[mod], a, mcol + i + kPairs, ym));
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < kPPL; ++j) ss += lo[j] * lo[j] + hi[j] * hi[j];
-    T* dst;
-    if (is_q) {
-      dst = q_out + ((int64_t)b * hq + h) * D;
+    if constexpr (SPLIT) {
+      lo[j] = i < kPairs ? load1_split<T>(xs, b, h * D + i) : 0.f;
+      hi[j] = i < kPairs ? load1_split<T>(xs, b, h * D + i + kPairs) : 0.f;
     } else {
-      if (!slot_ok) continue;  // a slot outside the pool is skipped, never written
-      const int kvh = is_k ? h - hq : h - hq - hkv;
-      dst = (is_k ? k_cache : v_cache) + p * page_stride + off * token_stride + (int64_t)kvh * head_stride;
+      lo[j] = i < kPairs ? to_float<T>(src[i]) : 0.f;
+      hi[j] = i < kPairs ? to_float<T>(src[i + kPairs]) : 0.f;
     }
-    if (is_q || is_k) {
-      const T* nw = is_q ? q_norm_w : k_norm_w;
-      if (nw != nullptr) {
-        ss = wave_sum(ss);
-        const float rstd = rsqrtf(ss / (float)D + eps);
+  }
+  // norm weights: loaded unconditionally (from the row itself when the head
+  // has none) and blended in with bit operations, so the loads are not moved
+  // under a branch behind the sum of squares
+  const T* nw = is_q ? q_norm_w : (is_k ? k_norm_w : nullptr);
+  const bool do_norm = nw != nullptr;
+  const T* nwp = do_norm ? nw : src;
+  const uint32_t keep = do_norm ? 0xffffffffu : 0u;
+  float wlo[kPPL], whi[kPPL];
 #pragma unroll
-        for (int j = 0; j < kPPL; ++j) {
-          const int i = lane + j * kWave;
-          if (i < kPairs) {
-            lo[j] *= rstd * to_float<T>(nw[i]);
-            hi[j] *= rstd * to_float<T>(nw[i + kPairs]);
-          }
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < kPPL; ++j) {
-        const float a0 = lo[j], c = hi[j];
-        lo[j] = a0 * cs[j] - c * sn[j];
-        hi[j] = c * cs[j] + a0 * sn[j];
-      }
-    }
+  for (int j = 0; j < kPPL; ++j) {
+    const int i = lane + j * kWave;
+    const float a0 = i < kPairs ? to_float<T>(nwp[i]) : 0.f;
+    const float a1 = i < kPairs ? to_float<T>(nwp[i + kPairs]) : 0.f;
+    wlo[j] = __uint_as_float((__float_as_uint(a0) & keep) | (0x3f800000u & ~keep));
+    whi[j] = __uint_as_float((__float_as_uint(a1) & keep) | (0x3f800000u & ~keep));
+  }
+  // LoRA: the rows are read whether or not the token has an adapter (adapter
+  // 0's when it has none, and a -0 added instead of the delta)
+  if constexpr (R > 0) {
+    const int a = lora.m[0].adapter >= 0 ? lora.m[0].adapter : ids[b];
+    const bool a_ok = a >= 0 && a < n_adapters;
+    const int a_ld = a_ok ? a : 0;
+    const int mod = is_q ? 0 : (is_k ? 1 : 2);
+    const int mcol = (h - (is_q ? 0 : (is_k ? hq : hq + hkv))) * D;  // first column in its module
+    LoraRow<RR> ym;
+    if constexpr (SPLIT)
+      load_y_split<T, R>(xs, lora.m[mod], b, a_ld, ym);
+    else
+      load_y<T, R>(lora.m[mod], b, a_ld, ym);
 #pragma unroll
     for (int j = 0; j < kPPL; ++j) {
       const int i = lane + j * kWave;
       if (i < kPairs) {
-        dst[i] = from_float<T>(lo[j]);
-        dst[i + kPairs] = from_float<T>(hi[j]);
+        const float dl = lora_delta1<T, R>(lora.m[mod], a_ld, mcol + i, ym);
+        const float dh = lora_delta1<T, R>(lora.m[mod], a_ld, mcol + i + kPairs, ym);
+        // no adapter: + (-0) and a rounding that leaves the T value as it is
+        lo[j] = through<T>(lo[j] + (a_ok ? dl : -0.f));
+        hi[j] = through<T>(hi[j] + (a_ok ? dh : -0.f));
       }
+    }
+  }
+  const float pos = (float)positions[b];
+  const int64_t p = page_id[b], off = offset[b];
+
+  // ---- q/k: per-head RMSNorm, then the rotation.  Computed for every head
+  // and kept for q/k only by a bit blend: under a q/k branch the compiler
+  // moves the weight and position loads into it, behind the LoRA round trip.
+  {
+    const uint32_t qk = (is_q || is_k) ? 0xffffffffu : 0u;
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPPL; ++j) ss += lo[j] * lo[j] + hi[j] * hi[j];
+    ss = wave_sum(ss);
+    const float rstd = do_norm ? rsqrtf(ss / (float)D + eps) : 1.f;
+#pragma unroll
+    for (int j = 0; j < kPPL; ++j) {
+      const int i = lane + j * kWave;
+      // rotation of pair i: angle = pos * inv_freq[i], the fp32 product the
+      // reference forms (inv_freq is the caller's table, scaling folded in)
+      float sn, cs;
+      sincosf(pos * (i < kPairs ? inv_freq[i] : 0.f), &sn, &cs);
+      const float a0 = lo[j] * (rstd * wlo[j]), c = hi[j] * (rstd * whi[j]);
+      const float rl = a0 * cs - c * sn, rh = c * cs + a0 * sn;
+      lo[j] = __uint_as_float((__float_as_uint(rl) & qk) | (__float_as_uint(lo[j]) & ~qk));
+      hi[j] = __uint_as_float((__float_as_uint(rh) & qk) | (__float_as_uint(hi[j]) & ~qk));
+    }
+  }
+
+  // ---- store: q to q_out, k and v into their page slot
+  T* dst;
+  if (is_q) {
+    dst = q_out + ((int64_t)b * hq + h) * D;
+  } else {
+    const bool slot_ok = p >= 0 && p < num_pages && off >= 0 && off < page_size;
+    if (!slot_ok) return;  // a slot outside the pool is skipped, never written
+    const int kvh = is_k ? h - hq : h - hq - hkv;
+    dst = (is_k ? k_cache : v_cache) + p * page_stride + off * token_stride + (int64_t)kvh * head_stride;
+  }
+#pragma unroll
+  for (int j = 0; j < kPPL; ++j) {
+    const int i = lane + j * kWave;
+    if (i < kPairs) {
+      dst[i] = from_float<T>(lo[j]);
+      dst[i + kPairs] = from_float<T>(hi[j]);
     }
   }
 }
@@ -865,7 +874,8 @@ struct QkrArgs {
 template <typename T, int D, int R>
 static void launch_qkr(const QkrArgs& a, hipStream_t s) {
   const int head_groups = (a.hq + 2 * a.hkv + kThreads / kWave - 1) / (kThreads / kWave);
-  hipLaunchKernelGGL((qk_norm_rope_append_kernel<T, D, R>), dim3(a.batch, head_groups), dim3(kThreads), 0, s,
+  auto kern = a.xs.splits > 0 ? qk_norm_rope_append_kernel<T, D, R, true> : qk_norm_rope_append_kernel<T, D, R, false>;
+  hipLaunchKernelGGL(kern, dim3(a.batch, head_groups), dim3(kThreads), 0, s,
                      (const T*)a.qkv, a.ld, (const T*)a.qn, (const T*)a.kn, a.pos, a.pid, a.off, (T*)a.q_out,
                      (T*)a.kc, (T*)a.vc, a.ps_, a.ts, a.hs, a.np, a.page_size, a.hq, a.hkv, a.invf, a.eps, a.lora,
                      a.ids, a.na, a.xs);
