@@ -365,6 +365,55 @@ int pl_qk_norm_rope_append_lora(const void* qkv, int64_t ld_qkv,
                                 const float* inv_freq, float eps, int dtype,
                                 void* stream);
 
+/*
+ * cos and sin of positions[b] * inv_freq[i] for every row b < batch and
+ * rotation pair i < half_dim, as out[b][i] = {cos, sin} (fp32).  The angles
+ * of one decode step, which every layer's RoPE shares: the same fp32 product
+ * and sincosf as pl_qk_norm_rope_append, computed once per step for
+ * pl_decode_run_qkv.  No counterpart in the reference (FlashInfer computes
+ * the angles inside apply_rope_pos_ids, projection.py:181).
+ */
+int pl_rope_cos_sin(const int64_t* positions, int batch, const float* inv_freq,
+                    int half_dim, float* out, void* stream);
+
+/*
+ * pl_decode_run with the q/k/v epilogue folded in: the kernel reads the
+ * packed projection rows qkv [batch, ld_qkv] (q heads, then k heads, then v
+ * heads, head-major, head_dim each) instead of a finished q, and
+ *   - forms each q head as pl_qk_norm_rope_append(_lora) does: the q
+ *     module's LoRA delta (lora_qkv_h[0], nullable as a whole for no LoRA),
+ *     RMSNorm with q_norm_weight (nullable), RoPE with the step's angles
+ *     rope_cos_sin (from pl_rope_cos_sin);
+ *   - appends each row's new token: k (k LoRA, k-norm, RoPE) and v (v LoRA)
+ *     of every kv head into (page_id[b], offset[b]) -- slots outside the pool
+ *     are skipped -- before attending over the row, that token included;
+ *   - attends as pl_decode_run.
+ * The plan (pl_decode_plan on the same workspace) must already count the new
+ * token.  Built for 16-bit dtypes, head_dim 128, num_qo_heads / num_kv_heads
+ * == 4 and LoRA rank 0, 8 or 16 (the three modules share it); other shapes
+ * return PL_ERR_UNSUPPORTED (use pl_qk_norm_rope_append + pl_decode_run).
+ * q differs from the two-call path by at most the rounding of the head
+ * norm's sum (another summation order).  No single counterpart in the
+ * reference: it replaces project_qkv_packed's delta, the head norm, RoPE and
+ * append (packed_ops.py:105-165, projection.py:155-190,
+ * layer_runner.py:399-412) followed by run_decode (attention_backend.py:
+ * 120-131) within one decode layer.
+ */
+int pl_decode_run_qkv(const void* qkv, int64_t ld_qkv,
+                      const pl_lora_up* lora_qkv_h, const int32_t* adapter_ids,
+                      int num_adapters, const void* q_norm_weight,
+                      const void* k_norm_weight, const float* rope_cos_sin,
+                      const int64_t* page_id, const int64_t* offset, float eps,
+                      void* k_cache, void* v_cache, int64_t page_stride,
+                      int64_t token_stride, int64_t head_stride,
+                      int64_t num_pages, const int32_t* indices,
+                      const int32_t* last_page_len, void* o,
+                      int64_t o_stride_b, int64_t o_stride_h, float* lse,
+                      int batch, int num_qo_heads, int num_kv_heads,
+                      int head_dim, int page_size, float sm_scale, int dtype,
+                      int target_items, int flags, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* No-merge multi-adapter LoRA delta                                         */
 /* ------------------------------------------------------------------------ */

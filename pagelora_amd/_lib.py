@@ -199,6 +199,26 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _f32, _i32, _vp,         # inv_freq, eps, dtype, stream
         ],
     ),
+    "pl_rope_cos_sin": (
+        _i32,
+        [_vp, _i32, _vp, _i32, _vp, _vp],  # positions, batch, inv_freq, half_dim, out, stream
+    ),
+    "pl_decode_run_qkv": (
+        _i32,
+        [
+            _vp, _i64, _vp, _vp, _i32,   # qkv, ld, lora (3 pl_lora_up), adapter_ids, num_adapters
+            _vp, _vp, _vp,               # q/k norm weights, rope cos/sin
+            _vp, _vp, _f32,              # page_id, offset, eps
+            _vp, _vp, _i64, _i64, _i64,  # k/v cache, page/token/head strides
+            _i64,                        # num_pages
+            _vp, _vp,                    # indices, last_page_len
+            _vp, _i64, _i64,             # o, strides
+            _vp,                         # lse
+            _i32, _i32, _i32, _i32, _i32,  # batch, hq, hkv, head_dim, page_size
+            _f32, _i32, _i32, _i32,      # sm_scale, dtype, target_items, flags
+            _vp, _sz, _vp,               # workspace, bytes, stream
+        ],
+    ),
     "pl_linear": (
         _i32,
         [_vp, _i64, _i32, _i32, _vp, _i64, _i32, _vp, _vp, _i64, ctypes.POINTER(LinearLora), _i32, _vp, _i32,

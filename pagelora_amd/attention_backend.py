@@ -361,6 +361,80 @@ class PagedDecodeAttention:
         _lib.check(status, "pl_decode_run")
         return out
 
+    def run_decode_qkv_into(
+        self,
+        qkv: torch.Tensor,
+        paged_kv_cache_layer,
+        out: torch.Tensor,
+        *,
+        q_norm_weight: torch.Tensor | None,
+        k_norm_weight: torch.Tensor | None,
+        rope_cos_sin: torch.Tensor,
+        page_id: torch.Tensor,
+        page_offset: torch.Tensor,
+        eps: float,
+        lora=None,
+        adapter_ids: torch.Tensor | None = None,
+        lse: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """``run_decode_into`` from the packed q/k/v projection rows
+        (pl_decode_run_qkv): the kernel forms q (LoRA delta, head norm, RoPE
+        with ``rope_cos_sin`` from ``fused_ops.rope_cos_sin``), appends each
+        row's new k/v at ``(page_id, page_offset)`` and attends.  ``lora`` is
+        the (q, k, v) ``fused_ops.LoraUp`` triple or None.  Built for 16-bit
+        caches, head_dim 128, 4 q heads per kv head, LoRA rank 0/8/16."""
+
+        from .fused_ops import _lora_args, _rows2d
+
+        plan = self._plan
+        if plan is None:
+            raise RuntimeError("plan_decode must be called before run_decode")
+        _rows2d(qkv, "qkv")
+        batch = qkv.shape[0]
+        if batch != plan["batch"]:
+            raise ValueError(f"qkv has batch {batch} but the plan has {plan['batch']}")
+        if tuple(out.shape) != (batch, self.num_qo_heads, self.head_dim) or out.stride(2) != 1 or out.dtype != qkv.dtype:
+            raise ValueError(f"out must be [{batch}, {self.num_qo_heads}, {self.head_dim}] of qkv's dtype")
+        if qkv.device.type != "cuda":
+            raise RuntimeError("run_decode needs tensors on a ROCm device")
+        k, v, page_stride, token_stride, head_stride, num_pages = _cache_geometry(
+            paged_kv_cache_layer, self.num_kv_heads, self.head_dim, self.page_size
+        )
+        if k.dtype != qkv.dtype:
+            raise ValueError(f"qkv dtype {qkv.dtype} != KV cache dtype {k.dtype}")
+        if plan["max_page"] is not None and plan["max_page"] >= num_pages:
+            raise ValueError(f"page id {plan['max_page']} is outside the {num_pages}-page KV pool")
+        for t, n in ((page_id, "page_id"), (page_offset, "page_offset")):
+            if t.dtype != torch.int64 or t.numel() != batch:
+                raise ValueError(f"{n} must be int64 [B]")
+        if (rope_cos_sin.dtype != torch.float32 or tuple(rope_cos_sin.shape) != (batch, self.head_dim // 2, 2)
+                or not rope_cos_sin.is_contiguous()):
+            raise ValueError(f"rope_cos_sin must be a contiguous fp32 [{batch}, {self.head_dim // 2}, 2] tensor")
+        if lse is not None and (lse.dtype != torch.float32 or tuple(lse.shape) != (batch, self.num_qo_heads) or not lse.is_contiguous()):
+            raise ValueError("lse must be a contiguous fp32 [B, Hq] tensor")
+        arr, ids, n = (None, None, 1)
+        if lora is not None:
+            if len(lora) != 3:
+                raise ValueError("lora must be (q, k, v)")
+            arr, ids, n = _lora_args(lora, adapter_ids, batch)
+        _, indices_buf, last_buf = self._decode_graph_buffers
+        status = self._lib.pl_decode_run_qkv(
+            qkv.data_ptr(), qkv.stride(0), arr, ids, n,
+            q_norm_weight.data_ptr() if q_norm_weight is not None else None,
+            k_norm_weight.data_ptr() if k_norm_weight is not None else None,
+            rope_cos_sin.data_ptr(), page_id.data_ptr(), page_offset.data_ptr(), float(eps),
+            k.data_ptr(), v.data_ptr(), page_stride, token_stride, head_stride, num_pages,
+            indices_buf.data_ptr(), last_buf.data_ptr(),
+            out.data_ptr(), out.stride(0), out.stride(1),
+            lse.data_ptr() if lse is not None else None,
+            batch, self.num_qo_heads, self.num_kv_heads, self.head_dim, self.page_size,
+            self.sm_scale, _lib.dtype_code(qkv.dtype), plan["target_items"], 0,
+            self.workspace_buffer.data_ptr(), self.workspace_buffer.numel(),
+            _lib.stream_handle(qkv.device),
+        )
+        _lib.check(status, "pl_decode_run_qkv")
+        return out
+
     # ------------------------------------------------------------- prefill
     def plan_prefill(
         self,

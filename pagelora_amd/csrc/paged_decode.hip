@@ -26,6 +26,7 @@
 // FlashInferAttentionBackend.run_decode (model/flashinfer/attention_backend.py
 // :120-131) obtains from FlashInfer with q/16 and sm_scale 16/sqrt(D).
 #include "pl_common.h"
+#include "lora_up.h"
 
 namespace pl {
 namespace decode {
@@ -472,7 +473,161 @@ __device__ __forceinline__ void stream_blocks(DecodeWave<T, D, G>& st, const T* 
   }
 }
 
-template <typename T, int D, int G>
+// The new token's K and V of a wave's kv head, as registers to splice into
+// the block that holds it (blk: block index, s: load instruction, row: lane
+// row; k / v: this lane's 8 dims, valid in the lanes of that row).
+struct NewToken {
+  int blk, pg, s, row;  // blk < 0: none; pg: the page the block must come from
+  uint32_t k[4], v[4];
+};
+
+// stream_blocks for the folded q/k/v epilogue: `hook` runs once the first
+// block's loads are in flight (it forms q, and for the item holding the
+// row's last page the new token's k / v, filling `nt`), and the new token's
+// K/V rows are taken from `nt` rather than from memory, so no load waits on
+// the append's stores.
+template <typename T, int D, int G, class Hook>
+__device__ __forceinline__ void stream_blocks_fused(DecodeWave<T, D, G>& st, const T* __restrict__ kc,
+                                                    const T* __restrict__ vc, int64_t page_stride,
+                                                    int64_t token_stride, int64_t lane_off,
+                                                    const int32_t* __restrict__ indices, int pbeg, int page_size,
+                                                    int64_t num_pages, int ntok, int blk0, int blk1,
+                                                    float scale_log2, int row, int first_page, Hook&& hook,
+                                                    const NewToken& nt) {
+  using WaveT = DecodeWave<T, D, G>;
+  constexpr int TPI = WaveT::TPI, NS = WaveT::NS, W = WaveT::W;
+  static_assert(W == 4, "16-bit types: 4 words per lane per token");
+  using L8 = Lane8<T>;
+  auto load_at = [&](int blk, int64_t page, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
+    const int t0 = blk * kBlockTokens;
+    const int tip = t0 - (t0 / page_size) * page_size;
+    page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);  // stay inside the pool
+    const int64_t base = page * page_stride + (int64_t)tip * token_stride + lane_off;
+    const T* kp = kc + base;
+    const T* vp = vc + base;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) L8::load(kw[s], kp + (int64_t)s * TPI * token_stride);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) L8::load(vw[s], vp + (int64_t)s * TPI * token_stride);
+  };
+  auto page_of = [&](int blk) -> int { return uniform(indices[pbeg + min(blk, blk1 - 1) * kBlockTokens / page_size]); };
+  auto splice = [&](int blk, int page, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
+    if ((blk != nt.blk) | (page != nt.pg)) return;  // wave-uniform
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      if (s == nt.s)
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          kw[s][w] = row == nt.row ? nt.k[w] : kw[s][w];
+          vw[s][w] = row == nt.row ? nt.v[w] : vw[s][w];
+        }
+  };
+  if (blk1 <= blk0) {
+    hook();
+    return;
+  }
+  uint32_t ka[NS][W], va[NS][W], kb[NS][W], vb[NS][W];
+  int pa = first_page >= 0 ? first_page : page_of(blk0), pb;
+  load_at(blk0, pa, ka, va);
+  int pid_next = page_of(blk0 + 1);
+  hook();
+  for (int i = blk0; i < blk1; i += 2) {
+    pb = pid_next;
+    pid_next = page_of(i + 2);
+    load_at(min(i + 1, blk1 - 1), pb, kb, vb);
+    __builtin_amdgcn_sched_barrier(0);
+    splice(i, pa, ka, va);
+    if ((i + 1) * kBlockTokens <= ntok)
+      st.template consume<false>(ka, va, scale_log2, row, kBlockTokens);
+    else
+      st.template consume<true>(ka, va, scale_log2, row, ntok - i * kBlockTokens);
+    if (i + 1 >= blk1) break;
+    pa = pid_next;
+    pid_next = page_of(i + 3);
+    load_at(min(i + 2, blk1 - 1), pa, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+    splice(i + 1, pb, kb, vb);
+    if ((i + 2) * kBlockTokens <= ntok)
+      st.template consume<false>(kb, vb, scale_log2, row, kBlockTokens);
+    else
+      st.template consume<true>(kb, vb, scale_log2, row, ntok - (i + 1) * kBlockTokens);
+  }
+}
+
+// Inputs of the decode run with the q/k/v epilogue folded in
+// (pl_decode_run_qkv): the packed projection rows instead of a finished q.
+struct QkvIn {
+  const void* qkv;           // [batch, ld]: q heads | k heads | v heads, head-major, D each
+  int64_t ld;
+  const void* q_norm_w;      // [D] or null
+  const void* k_norm_w;      // [D] or null
+  const float* rope;         // [batch, D/2, 2]: cos, sin of the row's position * inv_freq[i]
+  const int64_t* page_id;    // the row's new token: its page and slot in the page
+  const int64_t* page_off;
+  float eps;
+  LoraUp m[3];               // q, k, v up-projections (rank R > 0)
+  const int32_t* ids;
+  int n_adapters;
+};
+
+// One lane's 8 dims (8*col ..) of head `hh` of packed projection row b: the
+// module output (base + LoRA delta, rounded through T), the head RMSNorm
+// with weights w (none: w == nullptr) and the rotate-half RoPE (rot) -- the
+// arithmetic of qk_norm_rope_append_kernel, with the sum of squares reduced
+// over the lane's 16-lane row group and the rotation partner (the other half
+// of the head) taken from lane col ^ 8 of the group.  Every load is issued
+// unconditionally and optional terms are blended in, so none waits behind a
+// test.
+template <typename T, int R>
+__device__ __forceinline__ void qkv_head8(const QkvIn& in, int b, int hh, int mod, int mcol, int col,
+                                          const T* w, bool rot, int a_ld, bool a_ok, float (&v)[8]) {
+  constexpr int D = 128;
+  const T* src = (const T*)in.qkv + (int64_t)b * in.ld + (int64_t)hh * D + col * 8;
+  const uint4 raw = *reinterpret_cast<const uint4*>(src);
+  const uint4 wr = *reinterpret_cast<const uint4*>(w != nullptr ? w + col * 8 : src);
+  const float4* rp = reinterpret_cast<const float4*>(in.rope + ((int64_t)b * (D / 2) + (col * 8) % (D / 2)) * 2);
+  const float4 r0 = rp[0], r1 = rp[1], r2 = rp[2], r3 = rp[3];  // (cos, sin) of pairs 8*(col % 8) ..
+  unpack2<T>(raw.x, v[0], v[1]);
+  unpack2<T>(raw.y, v[2], v[3]);
+  unpack2<T>(raw.z, v[4], v[5]);
+  unpack2<T>(raw.w, v[6], v[7]);
+  if constexpr (R > 0) {
+    LoraRow<R> y;
+    load_y<T, R>(in.m[mod], b, a_ld, y);
+    float d[8];
+    lora_delta8<T, R>(in.m[mod], a_ld, mcol + col * 8, y, d);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = through<T>(v[e] + (a_ok ? d[e] : -0.f));
+  }
+  const uint32_t keep = w != nullptr ? 0xffffffffu : 0u;
+  float wf[8];
+  unpack2<T>(wr.x, wf[0], wf[1]);
+  unpack2<T>(wr.y, wf[2], wf[3]);
+  unpack2<T>(wr.z, wf[4], wf[5]);
+  unpack2<T>(wr.w, wf[6], wf[7]);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    wf[e] = __uint_as_float((__float_as_uint(wf[e]) & keep) | (0x3f800000u & ~keep));
+    ss += v[e] * v[e];
+  }
+  ss = row16_sum(ss);
+  const float rstd = w != nullptr ? rsqrtf(ss / (float)D + in.eps) : 1.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] *= rstd * wf[e];
+  const float cs[8] = {r0.x, r0.z, r1.x, r1.z, r2.x, r2.z, r3.x, r3.z};
+  const float sn[8] = {r0.y, r0.w, r1.y, r1.w, r2.y, r2.w, r3.y, r3.w};
+  const uint32_t rk = rot ? 0xffffffffu : 0u;
+  const bool lo_half = col < 8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float pe = dpp_mov<0x128>(v[e]);  // row_ror:8: lane col ^ 8 of the row group
+    const float r = lo_half ? v[e] * cs[e] - pe * sn[e] : v[e] * cs[e] + pe * sn[e];
+    v[e] = __uint_as_float((__float_as_uint(r) & rk) | (__float_as_uint(v[e]) & ~rk));
+  }
+}
+
+template <typename T, int D, int G, bool FUSED = false, int R = 0>
 __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
     const T* __restrict__ q, int64_t q_sb, int64_t q_sh, const T* __restrict__ kc,
     const T* __restrict__ vc, int64_t page_stride, int64_t token_stride, int64_t head_stride,
@@ -480,7 +635,7 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
     T* __restrict__ o, int64_t o_sb, int64_t o_sh, float* __restrict__ lse, int num_qo_heads,
     int num_kv_heads, int page_size, int64_t num_pages, float scale_log2,
     const int* __restrict__ header, const Item* __restrict__ items, int batch, int max_items,
-    float* __restrict__ part_lse, float* __restrict__ part_o) {
+    float* __restrict__ part_lse, float* __restrict__ part_o, QkvIn qin) {
   using WaveT = DecodeWave<T, D, G>;
   constexpr int LPT = WaveT::LPT;
   using L8 = Lane8<T>;
@@ -512,10 +667,12 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
 
   WaveT st;
   st.init();
+  if constexpr (!FUSED) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const T* qp = q + (int64_t)b * q_sb + (int64_t)(h * G + g) * q_sh + col * 8;
-    L8::load(st.q[g], qp);
+    for (int g = 0; g < G; ++g) {
+      const T* qp = q + (int64_t)b * q_sb + (int64_t)(h * G + g) * q_sh + col * 8;
+      L8::load(st.q[g], qp);
+    }
   }
 
   int ntok = 0;
@@ -527,8 +684,71 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
   const int nblk = (ntok + kBlockTokens - 1) / kBlockTokens;
 
   const int64_t lane_off = (int64_t)row * token_stride + (int64_t)h * head_stride + col * 8;
-  stream_blocks<T, D, G>(st, kc, vc, page_stride, token_stride, lane_off, indices, pbeg, page_size, num_pages, ntok,
-                         0, nblk, scale_log2, row, uniform(first_page));
+  if constexpr (FUSED) {
+    static_assert(G == 4 && D == 128 && sizeof(T) == 2, "the folded q/k/v epilogue is built for GQA 4, head_dim 128");
+    NewToken nt;
+    nt.blk = -1;
+    // Runs with the first block's loads in flight: q (row group r computes
+    // q head h*G + r, dims 8*col .., rounded to T as the standalone epilogue
+    // stores it; every lane then gathers the 4 heads) and, in the item
+    // holding the row's last page, the new token's k (row group 0: + LoRA,
+    // k-norm, RoPE) and v (row group 1: + LoRA) of this kv head, stored into
+    // its slot and spliced into the block that holds it.
+    auto hook = [&]() {
+      const int64_t pg = qin.page_id[b], off = qin.page_off[b];
+      const bool slot_ok = (pg >= 0) & (pg < num_pages) & (off >= 0) & (off < page_size);
+      // ids is always readable (the host points it at a dummy array for a
+      // uniform adapter) and blended in with bit operations, so its load is
+      // not moved under a test of the uniform adapter
+      const int id_raw = R > 0 ? qin.ids[b] : -1;
+      const uint32_t per_row = (uint32_t)(qin.m[0].adapter >> 31);  // all ones: per-row ids
+      const int a_in = (int)(((uint32_t)qin.m[0].adapter & ~per_row) | ((uint32_t)id_raw & per_row));
+      const bool a_ok = R > 0 && a_in >= 0 && a_in < qin.n_adapters;
+      const int a_ld = a_ok ? a_in : 0;
+      float v[8];
+      const int qh = h * G + row;
+      qkv_head8<T, R>(qin, b, qh, 0, qh * D, col, (const T*)qin.q_norm_w, true, a_ld, a_ok, v);
+      const uint32_t w4[4] = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
+                              pack2<T>(v[6], v[7])};
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) st.q[g][k] = (uint32_t)__shfl((int)w4[k], g * LPT + col);
+      if (flags & 2) {
+        const bool is_k = row == 0;
+        const int hh = (is_k ? num_qo_heads : num_qo_heads + num_kv_heads) + h;
+        qkv_head8<T, R>(qin, b, hh, is_k ? 1 : 2, h * D, col, is_k ? (const T*)qin.k_norm_w : nullptr, is_k, a_ld,
+                        a_ok, v);  // rows 2, 3 compute v again; unused
+        const uint32_t kv4[4] = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
+                                 pack2<T>(v[6], v[7])};
+        if (row < 2 && slot_ok) {
+          T* dst = const_cast<T*>(is_k ? kc : vc) + pg * page_stride + off * token_stride +
+                   (int64_t)h * head_stride + col * 8;
+          *reinterpret_cast<uint4*>(dst) = make_uint4(kv4[0], kv4[1], kv4[2], kv4[3]);
+        }
+        // A slot at the row's last token (where a decode step appends) is
+        // the item's token ntok - 1: attend over the computed k / v there.
+        // The store above is not waited for: nothing in this launch reads
+        // the slot from memory then.
+        const int lst = last_raw < 1 ? 1 : (last_raw > page_size ? page_size : last_raw);
+        const int t = ntok - 1, tt = t - (t / kBlockTokens) * kBlockTokens;
+        nt.blk = (slot_ok & (off == lst - 1) & (ntok > 0)) ? t / kBlockTokens : -1;
+        nt.pg = (int)pg;  // the block must also come from the slot's page
+        nt.s = tt / WaveT::TPI;
+        nt.row = tt - nt.s * WaveT::TPI;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          nt.k[k] = (uint32_t)__shfl((int)kv4[k], col);        // row group 0
+          nt.v[k] = (uint32_t)__shfl((int)kv4[k], LPT + col);  // row group 1
+        }
+      }
+    };
+    stream_blocks_fused<T, D, G>(st, kc, vc, page_stride, token_stride, lane_off, indices, pbeg, page_size,
+                                 num_pages, ntok, 0, nblk, scale_log2, row, uniform(first_page), hook, nt);
+  } else {
+    stream_blocks<T, D, G>(st, kc, vc, page_stride, token_stride, lane_off, indices, pbeg, page_size, num_pages,
+                           ntok, 0, nblk, scale_log2, row, uniform(first_page));
+  }
 
   st.merge_rows();
 
@@ -694,16 +914,16 @@ struct RunArgs {
   hipStream_t stream;
 };
 
-template <typename T, int D, int G>
-int launch(const RunArgs& a) {
+template <typename T, int D, int G, bool FUSED = false, int R = 0>
+int launch(const RunArgs& a, const QkvIn& qin = QkvIn{}) {
   if (!(a.flags & PL_DECODE_MERGE_ONLY)) {
     const int64_t waves = (int64_t)a.max_items * a.hkv;
     const int grid = (int)((waves + kWavesPerWG - 1) / kWavesPerWG);
-    hipLaunchKernelGGL((decode_kernel<T, D, G>), dim3(grid), dim3(kWave * kWavesPerWG), 0, a.stream,
+    hipLaunchKernelGGL((decode_kernel<T, D, G, FUSED, R>), dim3(grid), dim3(kWave * kWavesPerWG), 0, a.stream,
                        (const T*)a.q, a.q_sb, a.q_sh, (const T*)a.kc, (const T*)a.vc, a.page_stride,
                        a.token_stride, a.head_stride, a.indices, a.last, (T*)a.o, a.o_sb, a.o_sh,
                        a.lse, a.hq, a.hkv, a.page_size, a.num_pages, a.scale_log2, a.header,
-                       a.items, a.batch, a.max_items, a.part_lse, a.part_o);
+                       a.items, a.batch, a.max_items, a.part_lse, a.part_o, qin);
     PL_LAUNCH_CHECK("decode_kernel");
   }
   if (!(a.flags & PL_DECODE_SKIP_MERGE)) {
@@ -745,6 +965,17 @@ int by_dim(const RunArgs& a, int d, int g) {
   return fail(PL_ERR_UNSUPPORTED, "head_dim %d not built (64, 128, 256)", d);
 }
 
+// The folded q/k/v epilogue: 16-bit types, head_dim 128, GQA 4, LoRA rank 0/8/16.
+template <typename T>
+int by_rank_qkv(const RunArgs& a, const QkvIn& qin, int rank) {
+  switch (rank) {
+    case 0: return launch<T, 128, 4, true, 0>(a, qin);
+    case 8: return launch<T, 128, 4, true, 8>(a, qin);
+    case 16: return launch<T, 128, 4, true, 16>(a, qin);
+  }
+  return fail(PL_ERR_UNSUPPORTED, "LoRA rank %d not built for the folded q/k/v epilogue (0, 8, 16)", rank);
+}
+
 }  // namespace decode
 }  // namespace pl
 
@@ -780,14 +1011,15 @@ extern "C" int pl_decode_plan(const int32_t* indptr, int batch, int indices_capa
   return ok();
 }
 
-extern "C" int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+static int decode_run_common(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                              const void* k_cache, const void* v_cache, int64_t page_stride,
                              int64_t token_stride, int64_t head_stride, int64_t num_pages,
                              const int32_t* indices, const int32_t* last_page_len, void* o, int64_t o_stride_b,
                              int64_t o_stride_h, float* lse, int batch, int num_qo_heads,
                              int num_kv_heads, int head_dim, int page_size, float sm_scale,
                              int dtype, int target_items, int flags, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+                             size_t workspace_bytes, void* stream, const QkvIn* qin = nullptr,
+                             int qin_rank = 0) {
   if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0");
   if (batch == 0) return ok();
   if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads)
@@ -798,7 +1030,7 @@ extern "C" int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride
                 kBlockTokens);
   if (target_items <= 0) return fail(PL_ERR_INVALID, "target_items must be > 0");
   if (num_pages <= 0) return fail(PL_ERR_INVALID, "num_pages must be > 0");
-  if (!q || !k_cache || !v_cache || !indices || !last_page_len || !o || !workspace)
+  if ((!q && !qin) || !k_cache || !v_cache || !indices || !last_page_len || !o || !workspace)
     return fail(PL_ERR_INVALID, "null pointer argument");
   if (dtype != PL_DTYPE_F32 && dtype != PL_DTYPE_F16 && dtype != PL_DTYPE_BF16)
     return fail(PL_ERR_UNSUPPORTED, "dtype %d", dtype);
@@ -807,7 +1039,7 @@ extern "C" int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride
                              o_stride_b, o_stride_h};
   for (int64_t s : strides)
     if (s % 8) return fail(PL_ERR_INVALID, "every stride must be a multiple of 8 elements");
-  const void* ptrs[] = {q, k_cache, v_cache, o};
+  const void* ptrs[] = {qin ? k_cache : q, k_cache, v_cache, o};
   for (const void* p : ptrs)
     if ((uintptr_t)p % 16) return fail(PL_ERR_INVALID, "q, caches and o must be 16-byte aligned");
   const int max_items = target_items + batch;
@@ -830,10 +1062,74 @@ extern "C" int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride
   a.part_lse = (float*)(ws + L.lse); a.part_o = (float*)(ws + L.partial_o);
   a.stream = (hipStream_t)stream;
   const int g = num_qo_heads / num_kv_heads;
+  if (qin) {
+    if (head_dim != 128 || g != 4 || (dtype != PL_DTYPE_F16 && dtype != PL_DTYPE_BF16))
+      return fail(PL_ERR_UNSUPPORTED, "the folded q/k/v epilogue is built for 16-bit types, head_dim 128, GQA 4");
+    return dtype == PL_DTYPE_F16 ? by_rank_qkv<f16_t>(a, *qin, qin_rank) : by_rank_qkv<bf16_t>(a, *qin, qin_rank);
+  }
   switch (dtype) {
     case PL_DTYPE_F32: return by_dim<float>(a, head_dim, g);
     case PL_DTYPE_F16: return by_dim<f16_t>(a, head_dim, g);
     case PL_DTYPE_BF16: return by_dim<bf16_t>(a, head_dim, g);
   }
   return fail(PL_ERR_UNSUPPORTED, "dtype %d", dtype);
+}
+
+extern "C" int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                             const void* k_cache, const void* v_cache, int64_t page_stride,
+                             int64_t token_stride, int64_t head_stride, int64_t num_pages,
+                             const int32_t* indices, const int32_t* last_page_len, void* o, int64_t o_stride_b,
+                             int64_t o_stride_h, float* lse, int batch, int num_qo_heads,
+                             int num_kv_heads, int head_dim, int page_size, float sm_scale,
+                             int dtype, int target_items, int flags, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  return decode_run_common(q, q_stride_b, q_stride_h, k_cache, v_cache, page_stride, token_stride, head_stride,
+                           num_pages, indices, last_page_len, o, o_stride_b, o_stride_h, lse, batch, num_qo_heads,
+                           num_kv_heads, head_dim, page_size, sm_scale, dtype, target_items, flags, workspace,
+                           workspace_bytes, stream);
+}
+
+extern "C" int pl_decode_run_qkv(const void* qkv, int64_t ld_qkv, const pl_lora_up* lora_qkv_h,
+                                 const int32_t* adapter_ids, int num_adapters, const void* q_norm_weight,
+                                 const void* k_norm_weight, const float* rope_cos_sin, const int64_t* page_id,
+                                 const int64_t* offset, float eps, void* k_cache, void* v_cache,
+                                 int64_t page_stride, int64_t token_stride, int64_t head_stride, int64_t num_pages,
+                                 const int32_t* indices, const int32_t* last_page_len, void* o, int64_t o_stride_b,
+                                 int64_t o_stride_h, float* lse, int batch, int num_qo_heads, int num_kv_heads,
+                                 int head_dim, int page_size, float sm_scale, int dtype, int target_items, int flags,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0");
+  if (batch == 0) return ok();
+  if (!qkv || !rope_cos_sin || !page_id || !offset) return fail(PL_ERR_INVALID, "null pointer argument");
+  if (num_qo_heads <= 0 || num_kv_heads <= 0) return fail(PL_ERR_INVALID, "bad head counts");
+  const int64_t row_cols = (int64_t)(num_qo_heads + 2 * num_kv_heads) * head_dim;
+  if (ld_qkv < row_cols || ld_qkv % 8 || (uintptr_t)qkv % 16)
+    return fail(PL_ERR_INVALID, "qkv rows need ld >= %lld (a multiple of 8) and 16-byte alignment",
+                (long long)row_cols);
+  if ((uintptr_t)rope_cos_sin % 16) return fail(PL_ERR_INVALID, "rope_cos_sin must be 16-byte aligned");
+  if ((uintptr_t)q_norm_weight % 16 || (uintptr_t)k_norm_weight % 16)
+    return fail(PL_ERR_INVALID, "norm weights must be 16-byte aligned");
+  QkvIn qin{};
+  qin.qkv = qkv; qin.ld = ld_qkv; qin.q_norm_w = q_norm_weight; qin.k_norm_w = k_norm_weight;
+  qin.rope = rope_cos_sin; qin.page_id = page_id; qin.page_off = offset; qin.eps = eps;
+  // ids is read unconditionally: with a uniform adapter (no ids) it points at
+  // offset, an int64[batch] array, read as int32 and ignored
+  qin.ids = adapter_ids ? adapter_ids : reinterpret_cast<const int32_t*>(offset);
+  qin.n_adapters = num_adapters;
+  qin.m[0].adapter = -1;  // no LoRA: the kernel's adapter test is off (rank 0)
+  int rank = 0;
+  if (lora_qkv_h) {
+    if (const int st = lora_adapters_checked(lora_qkv_h, 3, adapter_ids, num_adapters, "decode q/k/v LoRA")) return st;
+    const int need[3] = {num_qo_heads * head_dim, num_kv_heads * head_dim, num_kv_heads * head_dim};
+    const char* names[3] = {"q LoRA", "k LoRA", "v LoRA"};
+    for (int m = 0; m < 3; ++m)
+      if (const int st = lora_up_checked(&lora_qkv_h[m], need[m], &qin.m[m], names[m])) return st;
+    rank = lora_qkv_h[0].rank;
+    if (lora_qkv_h[1].rank != rank || lora_qkv_h[2].rank != rank)
+      return fail(PL_ERR_INVALID, "q, k and v LoRA must share one rank");
+  }
+  return decode_run_common(nullptr, 0, 0, k_cache, v_cache, page_stride, token_stride, head_stride, num_pages,
+                           indices, last_page_len, o, o_stride_b, o_stride_h, lse, batch, num_qo_heads, num_kv_heads,
+                           head_dim, page_size, sm_scale, dtype, target_items, flags, workspace, workspace_bytes,
+                           stream, &qin, rank);
 }

@@ -179,6 +179,9 @@ class DecodeContext:
         # A captured step bakes it in (part of the graph key).
         self.uniform_adapter = -1
         self.argmax_ws: torch.Tensor | None = None  # greedy-argmax partial maxima
+        # the step's RoPE angles [B, head_dim/2, 2] when the decode layers fold
+        # the q/k/v epilogue into attention (see folded_qkv_decode)
+        self.rope_cos_sin: torch.Tensor | None = None
 
 
 # Decode-sized inputs (up to 16 tokens) take the GEMM on shuffled weights
@@ -193,6 +196,10 @@ DECODE_GEMM_MAX_TOKENS = 16
 # 4096) or qkv saves less than its consumer then pays; gate_up (1538 blocks)
 # does not need it.
 DECODE_SPLITS = {"down": 3}
+# Decode layers form q and append k/v inside the attention kernel
+# (pl_decode_run_qkv) where it is built; False keeps the separate
+# head-norm/RoPE/append kernel (tests compare the two).
+FOLD_QKV_INTO_DECODE = True
 
 
 def _project(x: torch.Tensor, lw: LayerWeights, name: str) -> "torch.Tensor | SplitOutput":
@@ -217,7 +224,7 @@ def _cols(out, n: int):
 
 def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Tensor, pending, ids: torch.Tensor,
            positions: torch.Tensor, page_id: torch.Tensor, page_offset: torch.Tensor, layer_cache: torch.Tensor,
-           page_size: int, attend, adapter: int = -1):
+           page_size: int, attend, adapter: int = -1, qkv_attend=None):
     """One decoder layer over T tokens (decode or prefill), no-merge LoRA on
     all seven modules.  ``hidden`` is the residual stream, updated in place;
     ``pending`` = (previous layer's down_proj output, its LoRA up-projection)
@@ -229,7 +236,10 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
     and the consumer kernel applies the up-projection: the q/k/v deltas in
     the head-norm/RoPE/append kernel, o's and down's in the next
     add+RMSNorm, gate's and up's in SiLU*up.  ``adapter`` >= 0 binds that
-    adapter to every token (``ids`` is then not read).
+    adapter to every token (``ids`` is then not read).  ``qkv_attend(qkv,
+    lora)``, when given, replaces the head-norm/RoPE/append kernel and
+    ``attend``: one kernel that forms q and appends k/v from the packed rows
+    while attending.
     """
     h, qd, kd, I = cfg.hidden, cfg.q_dim, cfg.kv_dim, cfg.intermediate
     a = adapter
@@ -240,13 +250,16 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
         x = fused_ops.add_rmsnorm(hidden, _cols(prev_out, h), lw.input_norm, cfg.rms_eps, lora=prev_up,
                                   adapter_ids=ids)
     qkv = _project(x, lw, "qkv")
-    q = fused_ops.qk_norm_rope_append(
-        _cols(qkv, qd + 2 * kd), lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None,
-        positions, page_id, page_offset, layer_cache, num_qo_heads=cfg.num_qo_heads,
-        num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=page_size,
-        rope_theta=cfg.rope_theta, eps=cfg.rms_eps,
-        lora=(lw.up("q", qkv, scale, a), lw.up("k", qkv, scale, a), lw.up("v", qkv, scale, a)), adapter_ids=ids)
-    attn = attend(q).view(q.shape[0], qd)
+    lora_qkv = (lw.up("q", qkv, scale, a), lw.up("k", qkv, scale, a), lw.up("v", qkv, scale, a))
+    if qkv_attend is not None and not isinstance(qkv, SplitOutput):
+        attn = qkv_attend(_cols(qkv, qd + 2 * kd), lora_qkv).view(qkv.shape[0], qd)
+    else:
+        q = fused_ops.qk_norm_rope_append(
+            _cols(qkv, qd + 2 * kd), lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None,
+            positions, page_id, page_offset, layer_cache, num_qo_heads=cfg.num_qo_heads,
+            num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=page_size,
+            rope_theta=cfg.rope_theta, eps=cfg.rms_eps, lora=lora_qkv, adapter_ids=ids)
+        attn = attend(q).view(q.shape[0], qd)
     o = _project(attn, lw, "o")
     x2 = fused_ops.add_rmsnorm(hidden, _cols(o, h), lw.post_norm, cfg.rms_eps, lora=lw.up("o", o, scale, a),
                                adapter_ids=ids)
@@ -282,8 +295,26 @@ def decode_layer_static(
         backend.run_decode_into(q, layer_cache, out)
         return out
 
+    def qkv_attend(qkv, lora):
+        out = torch.empty((qkv.shape[0], cfg.num_qo_heads, cfg.head_dim), dtype=qkv.dtype, device=qkv.device)
+        backend.run_decode_qkv_into(
+            qkv, layer_cache, out, q_norm_weight=lw.q_norm if cfg.qk_norm else None,
+            k_norm_weight=lw.k_norm if cfg.qk_norm else None, rope_cos_sin=ctx.rope_cos_sin,
+            page_id=ctx.page_id, page_offset=ctx.page_offset, eps=cfg.rms_eps, lora=lora,
+            adapter_ids=ctx.adapter_ids)
+        return out
+
     return _layer(cfg, lw, lora_scale, hidden, pending, ctx.adapter_ids, ctx.positions, ctx.page_id,
-                  ctx.page_offset, layer_cache, backend.page_size, attend, ctx.uniform_adapter)
+                  ctx.page_offset, layer_cache, backend.page_size, attend, ctx.uniform_adapter,
+                  qkv_attend if ctx.rope_cos_sin is not None else None)
+
+
+def folded_qkv_decode(cfg: DecoderConfig, dtype: torch.dtype) -> bool:
+    """Whether decode layers run the q/k/v epilogue inside the attention
+    kernel (pl_decode_run_qkv): built for 16-bit weights, head_dim 128, four
+    q heads per kv head and LoRA rank 0/8/16."""
+    return (FOLD_QKV_INTO_DECODE and dtype in (torch.bfloat16, torch.float16) and cfg.head_dim == 128
+            and cfg.num_qo_heads == 4 * cfg.num_kv_heads and cfg.lora_rank in (0, 8, 16))
 
 
 def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: PagedDecodeAttention,
@@ -295,6 +326,16 @@ def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: Page
     """
     cfg = weights.cfg
     hidden = F.embedding(ctx.tokens, weights.embed)
+    if folded_qkv_decode(cfg, weights.dtype):
+        # the step's RoPE angles, once for all layers (the first, eager call
+        # allocates the buffer, before any capture)
+        if ctx.rope_cos_sin is None:
+            ctx.rope_cos_sin = torch.empty((ctx.batch, cfg.head_dim // 2, 2), dtype=torch.float32,
+                                           device=ctx.positions.device)
+        fused_ops.rope_cos_sin(ctx.positions, head_dim=cfg.head_dim, rope_theta=cfg.rope_theta,
+                               out=ctx.rope_cos_sin)
+    else:
+        ctx.rope_cos_sin = None
     pending = None
     for li, lw in enumerate(weights.layers):
         pending = decode_layer_static(cfg, lw, weights.lora_scale, hidden, pending, pool.layer_cache(li),

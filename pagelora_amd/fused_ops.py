@@ -214,6 +214,24 @@ def rope_inv_freq(head_dim: int, theta: float, scale: float, device) -> torch.Te
     return t
 
 
+def rope_cos_sin(positions: torch.Tensor, *, head_dim: int, rope_theta: float, rope_scale: float = 1.0,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """``[B, head_dim/2, 2]`` fp32: cos and sin of ``positions[b] * inv_freq[i]``
+    (pl_rope_cos_sin) -- the RoPE angles every layer of one decode step shares,
+    for :meth:`PagedDecodeAttention.run_decode_qkv_into`."""
+    if positions.dtype != torch.int64 or positions.dim() != 1:
+        raise ValueError("positions must be int64 [B]")
+    B, half = positions.numel(), head_dim // 2
+    out = torch.empty((B, half, 2), dtype=torch.float32, device=positions.device) if out is None else out
+    if out.dtype != torch.float32 or tuple(out.shape) != (B, half, 2) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous fp32 [{B}, {half}, 2] tensor")
+    inv_freq = rope_inv_freq(head_dim, rope_theta, rope_scale, positions.device)
+    lib = _lib.load()
+    _lib.check(lib.pl_rope_cos_sin(positions.data_ptr(), B, inv_freq.data_ptr(), half, out.data_ptr(),
+                                   _lib.stream_handle(positions.device)), "pl_rope_cos_sin")
+    return out
+
+
 def qk_norm_rope_append(
     qkv: torch.Tensor,
     q_norm_weight: torch.Tensor | None,

@@ -158,13 +158,16 @@ def test_graph_replay_matches_eager(gpu_device):
 
 
 @pytest.mark.parametrize("use_graph", [False, True])
-def test_device_tables_match_host_tables(gpu_device, use_graph):
+@pytest.mark.parametrize("model", ["d64", "d128_folded"])
+def test_device_tables_match_host_tables(gpu_device, use_graph, model):
     # 40 steps carry every row (37, 49 and 33 tokens) across a page boundary;
-    # the device-grown table must give the same tokens as host packing.
+    # the device-grown table must give the same tokens as host packing (with
+    # head_dim 128 the attention kernel also forms q and appends k/v).
     steps = 40
-    w, pool, reqs, first, _ = _setup(gpu_device)
+    setup = _setup if model == "d64" else (lambda dev: _setup128(dev))
+    w, pool, reqs, first, _ = setup(gpu_device)
     ref = BatchGenerator(w, pool, workspace_mb=8, use_graph=False).generate(reqs, first, steps, [0, 1, 1])
-    w, pool, reqs, first, _ = _setup(gpu_device)
+    w, pool, reqs, first, _ = setup(gpu_device)
     gen = BatchGenerator(w, pool, workspace_mb=8, use_graph=use_graph)
     res = gen.generate(reqs, first, steps, [0, 1, 1], device_tables=True)
     assert res.used_graph == use_graph
@@ -254,3 +257,73 @@ def test_uniform_adapter_matches_per_row_ids(gpu_device, device_tables, monkeypa
         assert res.used_graph
         results.append(res.tokens)
     assert torch.equal(results[0], results[1])
+
+
+# head_dim 128 and four q heads per kv head: the shape whose decode layers
+# form q and append k/v inside the attention kernel (pl_decode_run_qkv)
+SMALL128 = DecoderConfig(num_layers=2, hidden=512, num_qo_heads=4, num_kv_heads=1, head_dim=128, intermediate=512,
+                         vocab=1000, lora_rank=16, lora_alpha=32.0)
+
+
+def _setup128(dev, seed=0):
+    w = DecoderWeights(SMALL128, n_adapters=2, device=dev, seed=seed)
+    pool = PagedKVPool(num_layers=SMALL128.num_layers, capacity_pages=64, page_size=16, num_kv_heads=1,
+                       head_dim=128, dtype=torch.bfloat16, device=dev)
+    g = torch.Generator().manual_seed(9)
+    prefix = torch.randint(0, SMALL128.vocab, (32,), generator=g)
+    prompts = [torch.randint(0, SMALL128.vocab, (n,), generator=g) for n in (5, 17, 1)]
+    reqs, first, logits = prefill_requests(w, pool, prompts, shared_prefix=prefix, adapters=[0, 1, 1])
+    return w, pool, reqs, first, logits
+
+
+def _eager_step(w, pool, reqs, first, adapters, dev):
+    gen = BatchGenerator(w, pool, workspace_mb=8, use_graph=False)
+    ctx = DecodeContext(len(reqs), dev)
+    gen._stage_inputs(ctx, reqs, adapters)
+    gen._plan(reqs)
+    ctx.tokens.copy_(first)
+    logits = decode_step_static(w, pool, gen.backend, ctx).float()
+    return logits, ctx.next_tokens.clone()
+
+
+def test_folded_qkv_step_matches_torch_reference(gpu_device):
+    from pagelora_amd import decoder
+    assert decoder.folded_qkv_decode(SMALL128, torch.bfloat16)
+    w, pool, reqs, first, _ = _setup128(gpu_device)
+    adapters = [0, 1, 1]
+    ref_cache = pool.cache.clone()
+    logits, toks = _eager_step(w, pool, reqs, first, adapters, gpu_device)
+    ref_logits, _ = _torch_reference_step(w, ref_cache, reqs, first, adapters)
+    torch.cuda.synchronize()
+    assert torch.allclose(logits, ref_logits, atol=0.1, rtol=0.01), (logits - ref_logits).abs().max()
+    _assert_same_greedy(toks, ref_logits, logits)
+    for r in reqs:  # the k/v the attention kernel appended equal the reference's index_put_
+        p, o = r.slot(r.length - 1, 16)
+        diff = (pool.cache[:, p, :, o].float() - ref_cache[:, p, :, o].float()).abs().max()
+        assert diff <= 0.05, diff
+
+
+def test_folded_qkv_matches_separate_epilogue(gpu_device, monkeypatch):
+    from pagelora_amd import decoder
+    out = []
+    for fold in (True, False):
+        monkeypatch.setattr(decoder, "FOLD_QKV_INTO_DECODE", fold)
+        w, pool, reqs, first, _ = _setup128(gpu_device)
+        out.append(_eager_step(w, pool, reqs, first, [0, 1, 1], gpu_device) + (pool.cache.clone(),))
+    (lf, tf, cf), (ls, ts, cs) = out
+    torch.cuda.synchronize()
+    # q (and the appended k) differ by at most one rounding: the head norm sums in another order
+    assert torch.allclose(lf, ls, atol=0.05, rtol=0.01), (lf - ls).abs().max()
+    _assert_same_greedy(tf, ls, lf)
+    assert torch.allclose(cf.float(), cs.float(), atol=0.05, rtol=0.02)
+
+
+def test_folded_qkv_graph_replay_matches_eager(gpu_device):
+    runs = []
+    for use_graph in (False, True):
+        w, pool, reqs, first, _ = _setup128(gpu_device)
+        gen = BatchGenerator(w, pool, workspace_mb=8, use_graph=use_graph)
+        res = gen.generate(reqs, first, steps=12, adapters=[0, 1, 1])
+        assert res.used_graph == use_graph
+        runs.append(res.tokens)
+    assert torch.equal(runs[0], runs[1])
