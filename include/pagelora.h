@@ -386,7 +386,11 @@ int pl_rope_cos_sin(const int64_t* positions, int batch, const float* inv_freq,
  *     rope_cos_sin (from pl_rope_cos_sin);
  *   - appends each row's new token: k (k LoRA, k-norm, RoPE) and v (v LoRA)
  *     of every kv head into (page_id[b], offset[b]) -- slots outside the pool
- *     are skipped -- before attending over the row, that token included;
+ *     are skipped -- and attends over the row, that token included.  The
+ *     slot is expected where a decode step puts it: the row's last token
+ *     (offset last_page_len[b] - 1 of the row's last page), whose K/V the
+ *     kernel takes from registers; a slot elsewhere is written, but this
+ *     call may read the old contents there;
  *   - attends as pl_decode_run.
  * The plan (pl_decode_plan on the same workspace) must already count the new
  * token.  Built for 16-bit dtypes, head_dim 128, num_qo_heads / num_kv_heads
