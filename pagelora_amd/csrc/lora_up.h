@@ -85,6 +85,35 @@ __device__ __forceinline__ void lora_delta8(const LoraUp& m, int a, int c0, cons
   for (int i = 0; i < 8; ++i) d[i] *= m.scale;
 }
 
+// The B pieces of 8 consecutive output columns at rank R <= 16, loaded by
+// load_cols8 and applied by dot_cols8: lora_delta8 split in two, for callers
+// that issue the loads well before the products.
+template <int R>
+struct LoraCols8 {
+  static_assert(R > 0 && R <= 16, "one pass of at most 16 ranks");
+  uint4 b[8][R / 8];
+};
+
+template <typename T, int R>
+__device__ __forceinline__ void load_cols8(const LoraUp& m, int a, int c0, LoraCols8<R>& p) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int k = 0; k < R / 8; ++k) p.b[i][k] = *lora_b_piece<T, R>(m, a, c0, i, k);
+}
+
+template <typename T, int R>
+__device__ __forceinline__ void dot_cols8(const LoraUp& m, const LoraCols8<R>& p, const LoraRow<R>& y,
+                                          float (&d)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < R / 8; ++k) acc = dot8<T>(y.v[k], p.b[i][k], acc);
+    d[i] = acc * m.scale;
+  }
+}
+
 // lora_delta8 for two modules at once (rank <= 16): both modules' B rows in
 // flight together, then the dot products.  For consumers that add two
 // modules' deltas (SiLU.up): one memory round trip instead of two.

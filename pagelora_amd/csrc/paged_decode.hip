@@ -417,13 +417,13 @@ __device__ __forceinline__ void stream_blocks(DecodeWave<T, D, G>& st, const T* 
                                               int64_t token_stride, int64_t lane_off,
                                               const int32_t* __restrict__ indices, int pbeg, int page_size,
                                               int64_t num_pages, int ntok, int blk0, int blk1, float scale_log2,
-                                              int row, int first_page = -1) {
+                                              int row, int first_page, int second_page) {
   using WaveT = DecodeWave<T, D, G>;
   constexpr int TPI = WaveT::TPI, NS = WaveT::NS, W = WaveT::W;
   using L8 = Lane8<T>;
-  // first_page >= 0: the caller already holds the page id of blk0's page
-  // (read in an earlier round trip); it serves the first block only, so the
-  // loop itself carries no extra test
+  // first_page / second_page: the page ids of blocks blk0 and blk0 + 1
+  // (clamped to the item, as page_of does), read by the caller in an earlier
+  // round trip, so the loop's first loads wait on no scalar load
   auto load_at = [&](int blk, int64_t page, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
     const int t0 = blk * kBlockTokens;
     const int tip = t0 - (t0 / page_size) * page_size;
@@ -440,13 +440,13 @@ __device__ __forceinline__ void stream_blocks(DecodeWave<T, D, G>& st, const T* 
   auto page_of = [&](int blk) -> int { return uniform(indices[pbeg + min(blk, blk1 - 1) * kBlockTokens / page_size]); };
   if (blk1 <= blk0) return;
   uint32_t ka[NS][W], va[NS][W], kb[NS][W], vb[NS][W];
-  load_at(blk0, first_page >= 0 ? first_page : page_of(blk0), ka, va);
+  load_at(blk0, first_page, ka, va);
   // Page ids run one block ahead of the K/V loads: the id a block's loads
   // need was read an iteration earlier, so no scalar load stands between a
   // wave and its next K/V loads.  (Measured against reading the id in front
   // of the loads: headline 746.5 -> 743 us, 64 x 2K GQA-4 114.2 -> 113.2 us;
   // entering the loop with both buffers in flight instead was 1-10% slower.)
-  int pid_next = page_of(blk0 + 1);
+  int pid_next = second_page;
   for (int i = blk0; i < blk1; i += 2) {
     // Prefetch the next block before consuming this one.  The index is
     // clamped instead of branched on so the load count is the same on
@@ -492,8 +492,8 @@ __device__ __forceinline__ void stream_blocks_fused(DecodeWave<T, D, G>& st, con
                                                     int64_t token_stride, int64_t lane_off,
                                                     const int32_t* __restrict__ indices, int pbeg, int page_size,
                                                     int64_t num_pages, int ntok, int blk0, int blk1,
-                                                    float scale_log2, int row, int first_page, Hook&& hook,
-                                                    const NewToken& nt) {
+                                                    float scale_log2, int row, int first_page, int second_page,
+                                                    Hook&& hook, const NewToken& nt) {
   using WaveT = DecodeWave<T, D, G>;
   constexpr int TPI = WaveT::TPI, NS = WaveT::NS, W = WaveT::W;
   static_assert(W == 4, "16-bit types: 4 words per lane per token");
@@ -527,9 +527,9 @@ __device__ __forceinline__ void stream_blocks_fused(DecodeWave<T, D, G>& st, con
     return;
   }
   uint32_t ka[NS][W], va[NS][W], kb[NS][W], vb[NS][W];
-  int pa = first_page >= 0 ? first_page : page_of(blk0), pb;
+  int pa = first_page, pb;
   load_at(blk0, pa, ka, va);
-  int pid_next = page_of(blk0 + 1);
+  int pid_next = second_page;
   hook();
   for (int i = blk0; i < blk1; i += 2) {
     pb = pid_next;
@@ -575,36 +575,61 @@ struct QkvIn {
 // with weights w (none: w == nullptr) and the rotate-half RoPE (rot) -- the
 // arithmetic of qk_norm_rope_append_kernel, with the sum of squares reduced
 // over the lane's 16-lane row group and the rotation partner (the other half
-// of the head) taken from lane col ^ 8 of the group.  Every load is issued
-// unconditionally and optional terms are blended in, so none waits behind a
-// test.
+// of the head) taken from lane col ^ 8 of the group.  In three phases, so the
+// caller can issue each group of loads as soon as its addresses are known:
+// head_base_load (the packed row, the norm weights, the step's cos / sin:
+// needs only b), head_lora_load (y and the B pieces: needs the adapter) and
+// head_finish.  Every load is issued unconditionally and optional terms are
+// blended in, so none waits behind a test.
 template <typename T, int R>
-__device__ __forceinline__ void qkv_head8(const QkvIn& in, int b, int hh, int mod, int mcol, int col,
-                                          const T* w, bool rot, int a_ld, bool a_ok, float (&v)[8]) {
+struct HeadIn {
+  uint4 raw, wr;
+  float4 r[4];  // (cos, sin) of pairs 8 * (col % 8) ..
+  LoraRow<(R > 0 ? R : 8)> y;
+  LoraCols8<(R > 0 ? R : 8)> bp;
+};
+
+template <typename T, int R>
+__device__ __forceinline__ void head_base_load(const QkvIn& in, int b, int hh, int col, const T* w,
+                                               HeadIn<T, R>& x) {
   constexpr int D = 128;
   const T* src = (const T*)in.qkv + (int64_t)b * in.ld + (int64_t)hh * D + col * 8;
-  const uint4 raw = *reinterpret_cast<const uint4*>(src);
-  const uint4 wr = *reinterpret_cast<const uint4*>(w != nullptr ? w + col * 8 : src);
+  x.raw = *reinterpret_cast<const uint4*>(src);
+  x.wr = *reinterpret_cast<const uint4*>(w != nullptr ? w + col * 8 : src);
   const float4* rp = reinterpret_cast<const float4*>(in.rope + ((int64_t)b * (D / 2) + (col * 8) % (D / 2)) * 2);
-  const float4 r0 = rp[0], r1 = rp[1], r2 = rp[2], r3 = rp[3];  // (cos, sin) of pairs 8*(col % 8) ..
-  unpack2<T>(raw.x, v[0], v[1]);
-  unpack2<T>(raw.y, v[2], v[3]);
-  unpack2<T>(raw.z, v[4], v[5]);
-  unpack2<T>(raw.w, v[6], v[7]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x.r[i] = rp[i];
+}
+
+template <typename T, int R>
+__device__ __forceinline__ void head_lora_load(const QkvIn& in, int b, int mod, int mcol, int col, int a_ld,
+                                               HeadIn<T, R>& x) {
   if constexpr (R > 0) {
-    LoraRow<R> y;
-    load_y<T, R>(in.m[mod], b, a_ld, y);
+    load_y<T, R>(in.m[mod], b, a_ld, x.y);
+    load_cols8<T, R>(in.m[mod], a_ld, mcol + col * 8, x.bp);
+  }
+}
+
+template <typename T, int R>
+__device__ __forceinline__ void head_finish(const QkvIn& in, const HeadIn<T, R>& x, int mod, int col, bool has_w,
+                                            bool rot, bool a_ok, float (&v)[8]) {
+  constexpr int D = 128;
+  unpack2<T>(x.raw.x, v[0], v[1]);
+  unpack2<T>(x.raw.y, v[2], v[3]);
+  unpack2<T>(x.raw.z, v[4], v[5]);
+  unpack2<T>(x.raw.w, v[6], v[7]);
+  if constexpr (R > 0) {
     float d[8];
-    lora_delta8<T, R>(in.m[mod], a_ld, mcol + col * 8, y, d);
+    dot_cols8<T, R>(in.m[mod], x.bp, x.y, d);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = through<T>(v[e] + (a_ok ? d[e] : -0.f));
   }
-  const uint32_t keep = w != nullptr ? 0xffffffffu : 0u;
+  const uint32_t keep = has_w ? 0xffffffffu : 0u;
   float wf[8];
-  unpack2<T>(wr.x, wf[0], wf[1]);
-  unpack2<T>(wr.y, wf[2], wf[3]);
-  unpack2<T>(wr.z, wf[4], wf[5]);
-  unpack2<T>(wr.w, wf[6], wf[7]);
+  unpack2<T>(x.wr.x, wf[0], wf[1]);
+  unpack2<T>(x.wr.y, wf[2], wf[3]);
+  unpack2<T>(x.wr.z, wf[4], wf[5]);
+  unpack2<T>(x.wr.w, wf[6], wf[7]);
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -612,11 +637,11 @@ __device__ __forceinline__ void qkv_head8(const QkvIn& in, int b, int hh, int mo
     ss += v[e] * v[e];
   }
   ss = row16_sum(ss);
-  const float rstd = w != nullptr ? rsqrtf(ss / (float)D + in.eps) : 1.f;
+  const float rstd = has_w ? rsqrtf(ss / (float)D + in.eps) : 1.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] *= rstd * wf[e];
-  const float cs[8] = {r0.x, r0.z, r1.x, r1.z, r2.x, r2.z, r3.x, r3.z};
-  const float sn[8] = {r0.y, r0.w, r1.y, r1.w, r2.y, r2.w, r3.y, r3.w};
+  const float cs[8] = {x.r[0].x, x.r[0].z, x.r[1].x, x.r[1].z, x.r[2].x, x.r[2].z, x.r[3].x, x.r[3].z};
+  const float sn[8] = {x.r[0].y, x.r[0].w, x.r[1].y, x.r[1].w, x.r[2].y, x.r[2].w, x.r[3].y, x.r[3].w};
   const uint32_t rk = rot ? 0xffffffffu : 0u;
   const bool lo_half = col < 8;
 #pragma unroll
@@ -656,18 +681,43 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
   if (!((stamp_batch == batch) & (stamp == plan_stamp(batch, max_items)) & (b >= 0) & (b < batch) & (pbeg >= 0) &
         (pend >= pbeg) & (flags >= 0) & ((flags >> 2) < max_items)))
     return;
-  // Second round trip, all at once: the row's last-page fill, the item's
-  // first page id and q (below).  The item's pages lie inside the indices
-  // buffer (the plan clamps them), so indices[pbeg] exists when pend > pbeg.
+  // Second round trip, all at once: the row's last-page fill, the page ids
+  // of the item's first two blocks and q (below).  The item's pages lie
+  // inside the indices buffer (the plan clamps them), so indices[pbeg] exists
+  // when pend > pbeg; an empty item reads its own first word instead (unused:
+  // it streams no block), so the loads need no branch.  Block 1 starts at
+  // token 16: in page pbeg + 1 when pages hold 16 tokens and the item has a
+  // second page, else in page pbeg (or it does not exist, and the stream
+  // clamps it to block 0).
   const int last_raw = last_page_len[b];
-  const int first_page = pend > pbeg ? indices[pbeg] : -1;
+  const int32_t* idx0 = pend > pbeg ? indices + pbeg : reinterpret_cast<const int32_t*>(items + item_idx);
+  const int first_page = uniform(idx0[0]);
+  const int second_page = uniform(idx0[((page_size == kBlockTokens) & (pend - pbeg >= 2)) ? 1 : 0]);
 
   const int row = lane / LPT;   // token row inside a load instruction
   const int col = lane % LPT;   // 8-element slice of the head dim
 
   WaveT st;
   st.init();
-  if constexpr (!FUSED) {
+  // The folded epilogue's loads that need only b go out with this round
+  // trip too: the adapter id, the new token's slot, and the packed rows,
+  // norm weights and cos / sin of this wave's q head (row group r: head
+  // h*G + r) and of its kv head's k (row group 0) and v (the other groups).
+  [[maybe_unused]] int id_raw = -1;
+  [[maybe_unused]] int64_t pg = -1, off = -1;
+  [[maybe_unused]] HeadIn<T, R> hq_in, hkv_in;
+  [[maybe_unused]] const bool is_k = row == 0;
+  if constexpr (FUSED) {
+    static_assert(G == 4 && D == 128 && sizeof(T) == 2, "the folded q/k/v epilogue is built for GQA 4, head_dim 128");
+    // ids is always readable (the host points it at a dummy array for a
+    // uniform adapter), so its load needs no test
+    if constexpr (R > 0) id_raw = qin.ids[b];
+    pg = qin.page_id[b];
+    off = qin.page_off[b];
+    head_base_load<T, R>(qin, b, h * G + row, col, (const T*)qin.q_norm_w, hq_in);
+    head_base_load<T, R>(qin, b, (is_k ? num_qo_heads : num_qo_heads + num_kv_heads) + h, col,
+                         is_k ? (const T*)qin.k_norm_w : nullptr, hkv_in);
+  } else {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const T* qp = q + (int64_t)b * q_sb + (int64_t)(h * G + g) * q_sh + col * 8;
@@ -675,17 +725,14 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
     }
   }
 
-  int ntok = 0;
-  if (pend > pbeg) {
-    const int last = last_raw < 1 ? 1 : (last_raw > page_size ? page_size : last_raw);
-    ntok = (pend - pbeg) * page_size - ((flags & 2) ? page_size - last : 0);
-  }
-  ntok = uniform(ntok);
+  // (no branch on pend > pbeg: a load whose only use sits in a branch is
+  // moved into it, a round trip of its own; an empty item gives <= 0)
+  const int last = last_raw < 1 ? 1 : (last_raw > page_size ? page_size : last_raw);
+  const int ntok = uniform(max(0, (pend - pbeg) * page_size - ((flags & 2) ? page_size - last : 0)));
   const int nblk = (ntok + kBlockTokens - 1) / kBlockTokens;
 
   const int64_t lane_off = (int64_t)row * token_stride + (int64_t)h * head_stride + col * 8;
   if constexpr (FUSED) {
-    static_assert(G == 4 && D == 128 && sizeof(T) == 2, "the folded q/k/v epilogue is built for GQA 4, head_dim 128");
     NewToken nt;
     nt.blk = -1;
     // Runs with the first block's loads in flight: q (row group r computes
@@ -695,19 +742,18 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
     // k-norm, RoPE) and v (row group 1: + LoRA) of this kv head, stored into
     // its slot and spliced into the block that holds it.
     auto hook = [&]() {
-      const int64_t pg = qin.page_id[b], off = qin.page_off[b];
       const bool slot_ok = (pg >= 0) & (pg < num_pages) & (off >= 0) & (off < page_size);
-      // ids is always readable (the host points it at a dummy array for a
-      // uniform adapter) and blended in with bit operations, so its load is
-      // not moved under a test of the uniform adapter
-      const int id_raw = R > 0 ? qin.ids[b] : -1;
+      // the adapter: blended with bit operations, so the id's load is not
+      // moved under a test of the uniform adapter
       const uint32_t per_row = (uint32_t)(qin.m[0].adapter >> 31);  // all ones: per-row ids
       const int a_in = (int)(((uint32_t)qin.m[0].adapter & ~per_row) | ((uint32_t)id_raw & per_row));
       const bool a_ok = R > 0 && a_in >= 0 && a_in < qin.n_adapters;
       const int a_ld = a_ok ? a_in : 0;
-      float v[8];
       const int qh = h * G + row;
-      qkv_head8<T, R>(qin, b, qh, 0, qh * D, col, (const T*)qin.q_norm_w, true, a_ld, a_ok, v);
+      head_lora_load<T, R>(qin, b, 0, qh * D, col, a_ld, hq_in);
+      __builtin_amdgcn_sched_barrier(0);
+      float v[8];
+      head_finish<T, R>(qin, hq_in, 0, col, qin.q_norm_w != nullptr, true, a_ok, v);
       const uint32_t w4[4] = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
                               pack2<T>(v[6], v[7])};
 #pragma unroll
@@ -715,10 +761,11 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
 #pragma unroll
         for (int k = 0; k < 4; ++k) st.q[g][k] = (uint32_t)__shfl((int)w4[k], g * LPT + col);
       if (flags & 2) {
-        const bool is_k = row == 0;
-        const int hh = (is_k ? num_qo_heads : num_qo_heads + num_kv_heads) + h;
-        qkv_head8<T, R>(qin, b, hh, is_k ? 1 : 2, h * D, col, is_k ? (const T*)qin.k_norm_w : nullptr, is_k, a_ld,
-                        a_ok, v);  // rows 2, 3 compute v again; unused
+        const int mod = is_k ? 1 : 2;
+        head_lora_load<T, R>(qin, b, mod, h * D, col, a_ld, hkv_in);
+        __builtin_amdgcn_sched_barrier(0);
+        head_finish<T, R>(qin, hkv_in, mod, col, is_k & (qin.k_norm_w != nullptr), is_k, a_ok,
+                          v);  // rows 2, 3 compute v again; unused
         const uint32_t kv4[4] = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
                                  pack2<T>(v[6], v[7])};
         if (row < 2 && slot_ok) {
@@ -744,10 +791,10 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
       }
     };
     stream_blocks_fused<T, D, G>(st, kc, vc, page_stride, token_stride, lane_off, indices, pbeg, page_size,
-                                 num_pages, ntok, 0, nblk, scale_log2, row, uniform(first_page), hook, nt);
+                                 num_pages, ntok, 0, nblk, scale_log2, row, first_page, second_page, hook, nt);
   } else {
     stream_blocks<T, D, G>(st, kc, vc, page_stride, token_stride, lane_off, indices, pbeg, page_size, num_pages,
-                           ntok, 0, nblk, scale_log2, row, uniform(first_page));
+                           ntok, 0, nblk, scale_log2, row, first_page, second_page);
   }
 
   st.merge_rows();
