@@ -40,20 +40,24 @@ from . import _lib
 # time of plan + decode + merge:
 #   - batch <= 32: 128 items (4 x 2114 and 1 x 32K tokens, GQA 4: 1,024 waves,
 #     one per SIMD; 256 or 64 items were 5-10% slower);
-#   - larger batches with 8 kv heads: 256 items (64 x 2048 GQA 4: 99 us
-#     against 118 us at 1,024 items; ragged 64 x U[128, 8192]: 204 vs 217 us);
+#   - GQA 4 with head_dim 128 (scores on MFMA) at any batch: 128 items
+#     (bf16, 8 kv heads: 64 x 2048 90.9 us against 92.0 at 256 items,
+#     128 x 2048 166.6 vs 170.8, 64 x 8192 325.1 vs 326.1; 192 items, an
+#     uneven count of waves per SIMD, 105.7 / 170.2 / 382.1);
+#   - other larger batches with 8 kv heads: 256 items (64 x 2048 GQA 4 on
+#     the VALU scores: 99 us against 118 us at 1,024 items; ragged
+#     64 x U[128, 8192]: 204 vs 217 us);
 #   - larger batches with >= 16 kv heads: 192 items, i.e. 6 waves per SIMD
 #     (ragged batch-64 MHA: 713.5 us against 729 us at 256 items).
-# An item count that leaves an uneven number of waves per SIMD is slower
-# (64 x 2048 GQA 4 at 192 items: 108 us).
 _ENV_TARGET_WAVES = os.environ.get("PAGELORA_DECODE_TARGET_WAVES")
 _DEFAULT_MIN_CHUNK_PAGES = int(os.environ.get("PAGELORA_DECODE_MIN_CHUNK_PAGES", "4"))
 
 
-def default_target_items(batch: int, num_kv_heads: int) -> int:
+def default_target_items(batch: int, num_kv_heads: int, num_qo_heads: int | None = None,
+                         head_dim: int | None = None) -> int:
     if _ENV_TARGET_WAVES:
         return max(1, int(_ENV_TARGET_WAVES) // num_kv_heads)
-    if batch <= 32:
+    if batch <= 32 or (num_qo_heads == 4 * num_kv_heads and head_dim == 128):
         return 128
     return 192 if num_kv_heads >= 16 else 256
 
@@ -266,7 +270,7 @@ class PagedDecodeAttention:
         if self.target_waves:
             t = max(1, self.target_waves // self.num_kv_heads)
         else:
-            t = default_target_items(batch, self.num_kv_heads)
+            t = default_target_items(batch, self.num_kv_heads, self.num_qo_heads, self.head_dim)
         cap = self.workspace_buffer.numel()
         while t > 1 and self._lib.pl_decode_workspace_size(batch, t, self.num_qo_heads, self.head_dim) > cap:
             t //= 2

@@ -14,9 +14,10 @@
 //                  (16 lanes x 16 B cover one 128-dim token row, so one
 //                  dwordx4 load instruction reads 4 token rows), scores them
 //                  against the g query heads of the kv head with v_dot2 and
-//                  DPP row reductions, and keeps an online softmax per lane
-//                  row in fp32.  Rows with one item write the output
-//                  directly; split rows write (o, lse) partials.
+//                  DPP row reductions (GQA 4 at head_dim 128 in 16-bit
+//                  types: on MFMA, DecodeWaveMfma), and keeps an online
+//                  softmax per lane row in fp32.  Rows with one item write
+//                  the output directly; split rows write (o, lse) partials.
 //   merge_kernel   one wavefront per (row, q head) of a split row: the
 //                  LSE-weighted sum of its partials.  A separate launch, so
 //                  the kernel boundary orders the partials across the eight
@@ -25,6 +26,8 @@
 // Mathematics: o = softmax(q . K^T * sm_scale) . V, as the reference's
 // FlashInferAttentionBackend.run_decode (model/flashinfer/attention_backend.py
 // :120-131) obtains from FlashInfer with q/16 and sm_scale 16/sqrt(D).
+#include <type_traits>
+
 #include "pl_common.h"
 #include "lora_up.h"
 
@@ -307,12 +310,59 @@ template <> __device__ __forceinline__ float row_sum<8>(float x) { return row8_s
 template <> __device__ __forceinline__ float row_sum<16>(float x) { return row16_sum(x); }
 template <> __device__ __forceinline__ float row_sum<32>(float x) { return row32_sum(x); }
 
+// Fold the lane rows of a wave's online-softmax states together (xor over
+// the row bits of the lane id, LPT lanes per row); afterwards every lane
+// holds the combined state for its 8 dims.
+template <int G, int LPT>
+__device__ __forceinline__ void merge_lane_rows(float (&m)[G], float (&l)[G], float (&acc)[G][8]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int off = LPT; off < kWave; off <<= 1) {
+      const float m_o = __shfl_xor(m[g], off);
+      const float l_o = __shfl_xor(l[g], off);
+      const float m_new = fmaxf(m[g], m_o);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float a_s = fast_exp2(m[g] - m_use);
+      const float a_o = fast_exp2(m_o - m_use);
+      l[g] = l[g] * a_s + l_o * a_o;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float o_o = __shfl_xor(acc[g][i], off);
+        acc[g][i] = acc[g][i] * a_s + o_o * a_o;
+      }
+      m[g] = m_new;
+    }
+  }
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// D += A . B on a 16x16x32 MFMA tile, A and B as 4 packed words per lane.
+template <typename T>
+__device__ __forceinline__ f32x4 mfma_16x16x32(const uint32_t (&a)[4], const uint32_t (&b)[4], f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mfma_16x16x32<bf16_t>(const uint32_t (&a)[4], const uint32_t (&b)[4], f32x4 c) {
+  const u32x4 av = {a[0], a[1], a[2], a[3]}, bv = {b[0], b[1], b[2], b[3]};
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
+                                                 c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma_16x16x32<f16_t>(const uint32_t (&a)[4], const uint32_t (&b)[4], f32x4 c) {
+  const u32x4 av = {a[0], a[1], a[2], a[3]}, bv = {b[0], b[1], b[2], b[3]};
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av), __builtin_bit_cast(f16x8_t, bv), c,
+                                                0, 0, 0);
+}
+
 template <typename T, int D, int G>
 struct DecodeWave {
   static constexpr int LPT = D / 8;             // lanes per token row
   static constexpr int TPI = kWave / LPT;       // token rows per load instruction
   static constexpr int NS = kBlockTokens / TPI; // loads per lane per block
   static constexpr int W = Lane8<T>::kWords;
+  static constexpr bool kMfmaScores = false;
   using L8 = Lane8<T>;
 
   uint32_t q[G][W];   // this lane's 8 dims of the g query heads
@@ -384,42 +434,153 @@ struct DecodeWave {
 
   // Fold the TPI lane rows together (xor over the row bits of the lane id).
   // Afterwards every lane holds the wave's combined state for its 8 dims.
-  __device__ __forceinline__ void merge_rows() {
+  __device__ __forceinline__ void merge_rows() { merge_lane_rows<G, LPT>(m, l, acc); }
+};
+
+// The score-on-MFMA wave for GQA groups of 4 heads, head_dim 128, 16-bit
+// types: per block of 16 tokens, S^T = K . Q^T is four
+// v_mfma_f32_16x16x32 (A: the block's K, lane l holding 8 dims of token
+// perm(l % 16); B: q, the group's 4 heads repeated over the 16 columns), in
+// place of 64 dot2 and 64 DPP reductions.  The token permutation
+// perm(m) = m / 4 + 4 * (m % 4) puts the scores of lane l's output rows
+// 4*(l/16) + i on tokens l/16 + 4i: the tokens whose V rows the lane already
+// holds in the VALU layout (row l/16, load s = i).  Lane l's scores are those
+// of head l % 4; each lane runs the online softmax of that head for its lane
+// row, and the quad's lanes (l & ~3 .. l | 3: heads 0..3 of the same tokens)
+// exchange p and the rescale factors with quad-permute DPP, so P . V stays
+// on VALU in registers as in DecodeWave.
+template <typename T, int D, int G>
+struct DecodeWaveMfma {
+  static_assert(D == 128 && G == 4 && sizeof(T) == 2, "MFMA scores: GQA 4, head_dim 128, 16-bit");
+  static constexpr int LPT = D / 8;             // V: lanes per token row
+  static constexpr int TPI = kWave / LPT;       // V: token rows per load instruction
+  static constexpr int NS = kBlockTokens / TPI; // loads per lane per block (K: one per 32 dims)
+  static constexpr int W = 4;
+  static constexpr bool kMfmaScores = true;
+  using L8 = Lane8<T>;
+
+  uint32_t qb[NS][W];  // B operand: head lane % 4, dims 32 j + 8 (lane / 16) ..
+  float mo, lo;        // online-softmax state of head lane % 4, lane row lane / 16 (log2)
+  float m[G], l[G];    // merge_rows: the state of every head
+  float acc[G][8];     // unnormalised output, this lane's 8 dims (8 * (lane % 16))
+
+  __device__ void init() {
+    mo = -INFINITY;
+    lo = 0.f;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int off = LPT; off < kWave; off <<= 1) {
-        const float m_o = __shfl_xor(m[g], off);
-        const float l_o = __shfl_xor(l[g], off);
-        const float m_new = fmaxf(m[g], m_o);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float a_s = fast_exp2(m[g] - m_use);
-        const float a_o = fast_exp2(m_o - m_use);
-        l[g] = l[g] * a_s + l_o * a_o;
+      for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+  }
+
+  // Element offset of lane `lane`'s K piece for load j = 0 within a block:
+  // token perm(lane % 16), dims 8 * (lane / 16); load j adds 32 dims.
+  __device__ static int64_t k_lane_off(int lane, int64_t token_stride) {
+    const int m16 = lane % 16;
+    return (int64_t)(m16 / 4 + 4 * (m16 % 4)) * token_stride + 8 * (lane / 16);
+  }
+  // Lane of the block that holds token t's K (its 4 loads hold dims 32 j +
+  // 8 * (lane / 16)): the lanes l with l % 16 == perm^-1(t).
+  __device__ static int k_lane_of(int t) { return 4 * (t % 4) + t / 4; }
+
+  template <int CTRL>
+  __device__ static float quad_bcast(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+  }
+
+  template <bool MASK>
+  __device__ __forceinline__ void consume(const uint32_t (&kw)[NS][W], const uint32_t (&vw)[NS][W],
+                                          float scale_log2, int row, int valid) {
+    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float o_o = __shfl_xor(acc[g][i], off);
-          acc[g][i] = acc[g][i] * a_s + o_o * a_o;
-        }
-        m[g] = m_new;
+    for (int j = 0; j < NS; ++j) sacc = mfma_16x16x32<T>(kw[j], qb[j], sacc);
+    float sc[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      sc[i] = sacc[i] * scale_log2;
+      if (MASK) sc[i] = (row + i * TPI < valid) ? sc[i] : -INFINITY;
+    }
+    float vf[NS][8];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      L8::to_f32(vw[s], vf[s]);
+      if (MASK) {
+        const bool ok = row + s * TPI < valid;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vf[s][i] = ok ? vf[s][i] : 0.f;
       }
     }
+    float mx = sc[0];
+#pragma unroll
+    for (int i = 1; i < NS; ++i) mx = fmaxf(mx, sc[i]);
+    const float m_new = fmaxf(mo, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;  // all masked so far
+    const float alpha = fast_exp2(mo - m_use);
+    mo = m_new;
+    float p[NS], psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      p[i] = fast_exp2(sc[i] - m_use);
+      psum += p[i];
+    }
+    lo = lo * alpha + psum;
+    // quad_perm:[g,g,g,g]: lane 4k + g of the quad holds head g
+    float ag[G], pg[NS][G];
+    ag[0] = quad_bcast<0x00>(alpha);
+    ag[1] = quad_bcast<0x55>(alpha);
+    ag[2] = quad_bcast<0xAA>(alpha);
+    ag[3] = quad_bcast<0xFF>(alpha);
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      pg[i][0] = quad_bcast<0x00>(p[i]);
+      pg[i][1] = quad_bcast<0x55>(p[i]);
+      pg[i][2] = quad_bcast<0xAA>(p[i]);
+      pg[i][3] = quad_bcast<0xFF>(p[i]);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        float a = acc[g][d] * ag[g];
+#pragma unroll
+        for (int i = 0; i < NS; ++i) a = fmaf(pg[i][g], vf[i][d], a);
+        acc[g][d] = a;
+      }
+  }
+
+  __device__ __forceinline__ void merge_rows() {
+    m[0] = quad_bcast<0x00>(mo);
+    m[1] = quad_bcast<0x55>(mo);
+    m[2] = quad_bcast<0xAA>(mo);
+    m[3] = quad_bcast<0xFF>(mo);
+    l[0] = quad_bcast<0x00>(lo);
+    l[1] = quad_bcast<0x55>(lo);
+    l[2] = quad_bcast<0xAA>(lo);
+    l[3] = quad_bcast<0xFF>(lo);
+    merge_lane_rows<G, LPT>(m, l, acc);
   }
 };
+
+template <typename T, int D, int G>
+using WaveFor = std::conditional_t<D == 128 && G == 4 && sizeof(T) == 2, DecodeWaveMfma<T, D, G>, DecodeWave<T, D, G>>;
 
 // Stream blocks [blk0, blk1) of an item (16 tokens each, the item's first
 // `ntok` tokens are real) through one wave's online-softmax state: each
 // block's K and V rows are loaded one block ahead of their use (two blocks
 // in flight per wave).
-template <typename T, int D, int G>
-__device__ __forceinline__ void stream_blocks(DecodeWave<T, D, G>& st, const T* __restrict__ kc,
-                                              const T* __restrict__ vc, int64_t page_stride,
-                                              int64_t token_stride, int64_t lane_off,
+// Where a lane's K and V pieces of a block lie: element offsets from the
+// block's first token row, and the step between the lane's loads.
+struct KvLanes {
+  int64_t k_off, k_step, v_off, v_step;
+};
+
+template <typename T, class WaveT>
+__device__ __forceinline__ void stream_blocks(WaveT& st, const T* __restrict__ kc, const T* __restrict__ vc,
+                                              int64_t page_stride, int64_t token_stride, const KvLanes& ln,
                                               const int32_t* __restrict__ indices, int pbeg, int page_size,
                                               int64_t num_pages, int ntok, int blk0, int blk1, float scale_log2,
                                               int row, int first_page, int second_page) {
-  using WaveT = DecodeWave<T, D, G>;
-  constexpr int TPI = WaveT::TPI, NS = WaveT::NS, W = WaveT::W;
+  constexpr int NS = WaveT::NS, W = WaveT::W;
   using L8 = Lane8<T>;
   // first_page / second_page: the page ids of blocks blk0 and blk0 + 1
   // (clamped to the item, as page_of does), read by the caller in an earlier
@@ -428,13 +589,13 @@ __device__ __forceinline__ void stream_blocks(DecodeWave<T, D, G>& st, const T* 
     const int t0 = blk * kBlockTokens;
     const int tip = t0 - (t0 / page_size) * page_size;
     page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);  // stay inside the pool
-    const int64_t base = page * page_stride + (int64_t)tip * token_stride + lane_off;
-    const T* kp = kc + base;
-    const T* vp = vc + base;
+    const int64_t base = page * page_stride + (int64_t)tip * token_stride;
+    const T* kp = kc + base + ln.k_off;
+    const T* vp = vc + base + ln.v_off;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) L8::load(kw[s], kp + (int64_t)s * TPI * token_stride);
+    for (int s = 0; s < NS; ++s) L8::load(kw[s], kp + s * ln.k_step);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) L8::load(vw[s], vp + (int64_t)s * TPI * token_stride);
+    for (int s = 0; s < NS; ++s) L8::load(vw[s], vp + s * ln.v_step);
   };
   // page id of block blk (blocks past the last re-read the last one)
   auto page_of = [&](int blk) -> int { return uniform(indices[pbeg + min(blk, blk1 - 1) * kBlockTokens / page_size]); };
@@ -479,6 +640,8 @@ __device__ __forceinline__ void stream_blocks(DecodeWave<T, D, G>& st, const T* 
 struct NewToken {
   int blk, pg, s, row;  // blk < 0: none; pg: the page the block must come from
   uint32_t k[4], v[4];
+  int klane;            // MFMA-score waves: K sits in the lanes l % 16 == klane,
+  uint32_t kq[4][4];    // load j holding dims 32 j + 8 (l / 16) ..
 };
 
 // stream_blocks for the folded q/k/v epilogue: `hook` runs once the first
@@ -486,41 +649,43 @@ struct NewToken {
 // row's last page the new token's k / v, filling `nt`), and the new token's
 // K/V rows are taken from `nt` rather than from memory, so no load waits on
 // the append's stores.
-template <typename T, int D, int G, class Hook>
-__device__ __forceinline__ void stream_blocks_fused(DecodeWave<T, D, G>& st, const T* __restrict__ kc,
-                                                    const T* __restrict__ vc, int64_t page_stride,
-                                                    int64_t token_stride, int64_t lane_off,
+template <typename T, class WaveT, class Hook>
+__device__ __forceinline__ void stream_blocks_fused(WaveT& st, const T* __restrict__ kc, const T* __restrict__ vc,
+                                                    int64_t page_stride, int64_t token_stride, const KvLanes& ln,
                                                     const int32_t* __restrict__ indices, int pbeg, int page_size,
                                                     int64_t num_pages, int ntok, int blk0, int blk1,
                                                     float scale_log2, int row, int first_page, int second_page,
                                                     Hook&& hook, const NewToken& nt) {
-  using WaveT = DecodeWave<T, D, G>;
-  constexpr int TPI = WaveT::TPI, NS = WaveT::NS, W = WaveT::W;
+  constexpr int NS = WaveT::NS, W = WaveT::W;
   static_assert(W == 4, "16-bit types: 4 words per lane per token");
   using L8 = Lane8<T>;
   auto load_at = [&](int blk, int64_t page, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
     const int t0 = blk * kBlockTokens;
     const int tip = t0 - (t0 / page_size) * page_size;
     page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);  // stay inside the pool
-    const int64_t base = page * page_stride + (int64_t)tip * token_stride + lane_off;
-    const T* kp = kc + base;
-    const T* vp = vc + base;
+    const int64_t base = page * page_stride + (int64_t)tip * token_stride;
+    const T* kp = kc + base + ln.k_off;
+    const T* vp = vc + base + ln.v_off;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) L8::load(kw[s], kp + (int64_t)s * TPI * token_stride);
+    for (int s = 0; s < NS; ++s) L8::load(kw[s], kp + s * ln.k_step);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) L8::load(vw[s], vp + (int64_t)s * TPI * token_stride);
+    for (int s = 0; s < NS; ++s) L8::load(vw[s], vp + s * ln.v_step);
   };
   auto page_of = [&](int blk) -> int { return uniform(indices[pbeg + min(blk, blk1 - 1) * kBlockTokens / page_size]); };
+  const int lane16 = threadIdx.x % 16;
   auto splice = [&](int blk, int page, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
     if ((blk != nt.blk) | (page != nt.pg)) return;  // wave-uniform
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-      if (s == nt.s)
+    for (int s = 0; s < NS; ++s) {
 #pragma unroll
-        for (int w = 0; w < W; ++w) {
-          kw[s][w] = row == nt.row ? nt.k[w] : kw[s][w];
-          vw[s][w] = row == nt.row ? nt.v[w] : vw[s][w];
-        }
+      for (int w = 0; w < W; ++w) {
+        if constexpr (WaveT::kMfmaScores)
+          kw[s][w] = lane16 == nt.klane ? nt.kq[s][w] : kw[s][w];
+        else
+          kw[s][w] = ((s == nt.s) & (row == nt.row)) ? nt.k[w] : kw[s][w];
+        vw[s][w] = ((s == nt.s) & (row == nt.row)) ? nt.v[w] : vw[s][w];
+      }
+    }
   };
   if (blk1 <= blk0) {
     hook();
@@ -661,7 +826,7 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
     int num_kv_heads, int page_size, int64_t num_pages, float scale_log2,
     const int* __restrict__ header, const Item* __restrict__ items, int batch, int max_items,
     float* __restrict__ part_lse, float* __restrict__ part_o, QkvIn qin) {
-  using WaveT = DecodeWave<T, D, G>;
+  using WaveT = WaveFor<T, D, G>;
   constexpr int LPT = WaveT::LPT;
   using L8 = Lane8<T>;
 
@@ -717,6 +882,11 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
     head_base_load<T, R>(qin, b, h * G + row, col, (const T*)qin.q_norm_w, hq_in);
     head_base_load<T, R>(qin, b, (is_k ? num_qo_heads : num_qo_heads + num_kv_heads) + h, col,
                          is_k ? (const T*)qin.k_norm_w : nullptr, hkv_in);
+  } else if constexpr (WaveT::kMfmaScores) {
+    // the B operand: head lane % 4 of the group, dims 32 j + 8 (lane / 16)
+    const T* qp = q + (int64_t)b * q_sb + (int64_t)(h * G + lane % 4) * q_sh + 8 * (lane / 16);
+#pragma unroll
+    for (int j = 0; j < WaveT::NS; ++j) L8::load(st.qb[j], qp + 32 * j);
   } else {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -731,7 +901,16 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
   const int ntok = uniform(max(0, (pend - pbeg) * page_size - ((flags & 2) ? page_size - last : 0)));
   const int nblk = (ntok + kBlockTokens - 1) / kBlockTokens;
 
-  const int64_t lane_off = (int64_t)row * token_stride + (int64_t)h * head_stride + col * 8;
+  KvLanes ln;
+  ln.v_off = (int64_t)row * token_stride + (int64_t)h * head_stride + col * 8;
+  ln.v_step = (int64_t)WaveT::TPI * token_stride;
+  if constexpr (WaveT::kMfmaScores) {
+    ln.k_off = WaveT::k_lane_off(lane, token_stride) + (int64_t)h * head_stride;
+    ln.k_step = 32;
+  } else {
+    ln.k_off = ln.v_off;
+    ln.k_step = ln.v_step;
+  }
   if constexpr (FUSED) {
     NewToken nt;
     nt.blk = -1;
@@ -756,10 +935,20 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
       head_finish<T, R>(qin, hq_in, 0, col, qin.q_norm_w != nullptr, true, a_ok, v);
       const uint32_t w4[4] = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
                               pack2<T>(v[6], v[7])};
+      if constexpr (WaveT::kMfmaScores) {
+        // B operand: head lane % 4, dims 32 j + 8 (lane / 16) .. = the
+        // 8-dim slice 4 j + lane / 16 of row group lane % 4
 #pragma unroll
-      for (int g = 0; g < G; ++g)
+        for (int j = 0; j < WaveT::NS; ++j)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) st.q[g][k] = (uint32_t)__shfl((int)w4[k], g * LPT + col);
+          for (int k = 0; k < 4; ++k)
+            st.qb[j][k] = (uint32_t)__shfl((int)w4[k], (lane % 4) * LPT + 4 * j + lane / 16);
+      } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) st.q[g][k] = (uint32_t)__shfl((int)w4[k], g * LPT + col);
+      }
       if (flags & 2) {
         const int mod = is_k ? 1 : 2;
         head_lora_load<T, R>(qin, b, mod, h * D, col, a_ld, hkv_in);
@@ -788,12 +977,19 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
           nt.k[k] = (uint32_t)__shfl((int)kv4[k], col);        // row group 0
           nt.v[k] = (uint32_t)__shfl((int)kv4[k], LPT + col);  // row group 1
         }
+        if constexpr (WaveT::kMfmaScores) {
+          nt.klane = WaveT::k_lane_of(tt);
+#pragma unroll
+          for (int j = 0; j < WaveT::NS; ++j)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) nt.kq[j][k] = (uint32_t)__shfl((int)kv4[k], 4 * j + lane / 16);
+        }
       }
     };
-    stream_blocks_fused<T, D, G>(st, kc, vc, page_stride, token_stride, lane_off, indices, pbeg, page_size,
+    stream_blocks_fused<T>(st, kc, vc, page_stride, token_stride, ln, indices, pbeg, page_size,
                                  num_pages, ntok, 0, nblk, scale_log2, row, first_page, second_page, hook, nt);
   } else {
-    stream_blocks<T, D, G>(st, kc, vc, page_stride, token_stride, lane_off, indices, pbeg, page_size, num_pages,
+    stream_blocks<T>(st, kc, vc, page_stride, token_stride, ln, indices, pbeg, page_size, num_pages,
                            ntok, 0, nblk, scale_log2, row, first_page, second_page);
   }
 
