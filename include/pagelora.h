@@ -330,6 +330,23 @@ int pl_add_rmsnorm_lora(void* residual, int64_t ldr, const void* x,
                         int hidden, float eps, int dtype, void* stream);
 
 /*
+ * pl_add_rmsnorm_lora with the module's y read from the side planes of
+ * pl_linear_shuffled_side (y_side_h: 1..64 planes, adapter a's rank-space
+ * row at columns lora_h->y_offset + a * rank; lora_h->y is ignored), x
+ * whole.  The planes are summed in order per rank, then rounded to the
+ * dtype as the reference's F.linear(x, A) output is.  16-bit dtypes,
+ * hidden <= 8192, rank 8 or 16.  Replaces the same reference code as
+ * pl_add_rmsnorm_lora.
+ */
+int pl_add_rmsnorm_lora_side(void* residual, int64_t ldr, const void* x,
+                             int64_t ldx, const pl_split_out* y_side_h,
+                             const pl_lora_up* lora_h,
+                             const int32_t* adapter_ids, int num_adapters,
+                             const void* weight, void* out, int64_t ldo,
+                             int rows, int hidden, float eps, int dtype,
+                             void* stream);
+
+/*
  * pl_silu_mul with the gate and up modules' deltas (lora_gate_up_h[0] for
  * the gate columns, [1] for the up columns) added to gate_up first.
  * Replaces project_gate_up_packed's delta + silu_and_mul
@@ -579,6 +596,27 @@ int pl_linear_shuffled_split(const void* x, int64_t ldx, int num_tokens,
                              int out_features, int splits, float* partials,
                              int64_t ld, int64_t plane_stride, int dtype,
                              void* stream);
+
+/*
+ * pl_linear_shuffled whose last out_features - main_features outputs (the
+ * LoRA A rows stacked under W) are split-K: columns c < main_features are
+ * written whole to out (no bias); the others, as in pl_linear_shuffled_split,
+ * to side_splits fp32 planes of side_partials (column c - main_features, row
+ * t at t * ld_side, planes side_plane_stride apart), computed by side_splits
+ * small workgroups per 16-column block appended to the grid.  main_features
+ * must be a multiple of 16.  With main_features a multiple of 16 x the CU
+ * count (4096 on 256 CUs) every CU streams one whole block, where one more
+ * whole block would cost some CU two.  The consumer reads y from the planes
+ * (pl_add_rmsnorm_lora_side).  No counterpart in the reference: it computes
+ * the same x . [W; A]^T as project_linear with its LoRA shrink
+ * (packed_ops.py:251-265, linear.py:226-231).
+ */
+int pl_linear_shuffled_side(const void* x, int64_t ldx, int num_tokens,
+                            int in_features, const void* shuffled,
+                            int out_features, int main_features, void* out,
+                            int64_t ldo, int side_splits, float* side_partials,
+                            int64_t ld_side, int64_t side_plane_stride,
+                            int dtype, void* stream);
 
 /*
  * Advance every row of a batched page table by one decode token, in place

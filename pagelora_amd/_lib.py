@@ -172,6 +172,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _i64, _vp, _i64, ctypes.POINTER(SplitOut), ctypes.POINTER(LoraUp), _vp, _i32, _vp, _vp, _i64, _i32,
          _i32, _f32, _i32, _vp],
     ),
+    "pl_add_rmsnorm_lora_side": (
+        _i32,
+        [_vp, _i64, _vp, _i64, ctypes.POINTER(SplitOut), ctypes.POINTER(LoraUp), _vp, _i32, _vp, _vp, _i64, _i32,
+         _i32, _f32, _i32, _vp],
+    ),
     "pl_silu_mul_lora": (_i32, [_vp, _i64, ctypes.POINTER(LoraUp), _vp, _i32, _vp, _i64, _i32, _i32, _i32, _vp]),
     "pl_qk_norm_rope_append_lora": (
         _i32,
@@ -228,6 +233,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pl_weight_shuffle": (_i32, [_vp, _i64, _i32, _i32, _vp, _sz, _i32, _vp]),
     "pl_linear_shuffled": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _vp, _vp, _i64, _i32, _vp]),
     "pl_linear_shuffled_split": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _i64, _i64, _i32, _vp]),
+    "pl_linear_shuffled_side": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _i64, _i32, _vp, _i64, _i64,
+                                       _i32, _vp]),
     "pl_lora_workspace_size": (_sz, [_i32, _i32, ctypes.POINTER(LoraModule), _i32]),
     "pl_lora_delta": (
         _i32,

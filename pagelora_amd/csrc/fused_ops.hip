@@ -24,6 +24,8 @@
 // projection.py:155-190, 248-260 (apply_rope_pos_ids non-interleaved, head
 // norm) and layer_runner.py:399-412 (the page append the fused kernel
 // replaces).  All arithmetic is fp32; each output is rounded once.
+#include <type_traits>
+
 #include "pl_common.h"
 #include "lora_up.h"
 
@@ -255,12 +257,17 @@ __device__ __forceinline__ void load8_planes(const SplitIn& sp, int64_t t, int c
 
 constexpr int kRowNormMaxHidden = 8192;
 
-template <typename T, int R, int P>
+// YS: the module's y comes from ys.splits fp32 side planes (the LoRA A rows
+// of pl_linear_shuffled_side, column y_offset + a*R of each plane): thread
+// r < R adds rank r over the planes in order (SplitOutput.sum's order), the
+// sum is shared through LDS and rounded to T.
+template <typename T, int R, int P, bool YS = false>
 __global__ __launch_bounds__(1024) void add_rmsnorm_row_kernel(
     T* __restrict__ r, int64_t ldr, const T* __restrict__ x, int64_t ldx, const T* __restrict__ w,
     T* __restrict__ out, int64_t ldo, int hidden, float eps, LoraUp lora, const int32_t* __restrict__ ids,
-    int n_adapters, SplitIn xs) {
+    int n_adapters, SplitIn xs, SplitIn ys) {
   __shared__ float s_red[1024 / kWave];
+  __shared__ float s_y[YS ? (R > 0 ? R : 1) : 1];
   const int row = blockIdx.x;
   const int a_raw = R > 0 ? (lora.adapter >= 0 ? lora.adapter : ids[row]) : -1;
   const bool live = (int)threadIdx.x * 8 < hidden;
@@ -289,7 +296,27 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_row_kernel(
       // in front of the B loads: both depend only on the id
       __builtin_amdgcn_sched_barrier(0);
       LoraRow<R> y;
-      if constexpr (P > 0) {
+      if constexpr (YS) {
+        // thread r < R adds rank r's planes in plane order, 16 loads in
+        // flight at a time (one memory round trip for up to 16 planes)
+        if ((int)threadIdx.x < R) {
+          const float* src = ys.p + (int64_t)row * ys.ld + lora.y_offset + (int64_t)a * R + threadIdx.x;
+          float tot = 0.f;
+          for (int p0 = 0; p0 < ys.splits; p0 += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = src[(int64_t)min(p0 + u, ys.splits - 1) * ys.plane];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) tot += p0 + u < ys.splits ? v[u] : 0.f;
+          }
+          s_y[threadIdx.x] = tot;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < R / 8; ++k)
+          y.v[k] = make_uint4(pack2<T>(s_y[k * 8 + 0], s_y[k * 8 + 1]), pack2<T>(s_y[k * 8 + 2], s_y[k * 8 + 3]),
+                              pack2<T>(s_y[k * 8 + 4], s_y[k * 8 + 5]), pack2<T>(s_y[k * 8 + 6], s_y[k * 8 + 7]));
+      } else if constexpr (P > 0) {
 #pragma unroll
         for (int k = 0; k < R / 8; ++k) {
           float f[8];
@@ -619,7 +646,7 @@ static void launch_row_norm_t(void* r, int64_t ldr, const void* x, int64_t ldx, 
                               int na, const SplitIn& xs, hipStream_t s) {
   const int threads = (hidden / 8 + kWave - 1) / kWave * kWave;
   hipLaunchKernelGGL((add_rmsnorm_row_kernel<T, R, P>), dim3(rows), dim3(threads), 0, s, (T*)r, ldr, (const T*)x,
-                     ldx, (const T*)w, (T*)out, ldo, hidden, eps, lu, ids, na, xs);
+                     ldx, (const T*)w, (T*)out, ldo, hidden, eps, lu, ids, na, xs, SplitIn{nullptr, 0, 0, 0});
 }
 
 template <typename T, int P>
@@ -724,6 +751,52 @@ extern "C" int pl_add_rmsnorm_lora(void* residual, int64_t ldr, const void* x, i
   if (!lora_h) return fail(PL_ERR_INVALID, "lora_h must not be null (use pl_add_rmsnorm)");
   return norm_common(true, residual, ldr, x, ldx, weight, out, ldo, rows, hidden, eps, dtype, stream, lora_h,
                      adapter_ids, num_adapters, x_split_h);
+}
+
+extern "C" int pl_add_rmsnorm_lora_side(void* residual, int64_t ldr, const void* x, int64_t ldx,
+                                        const pl_split_out* y_side_h, const pl_lora_up* lora_h,
+                                        const int32_t* adapter_ids, int num_adapters, const void* weight,
+                                        void* out, int64_t ldo, int rows, int hidden, float eps, int dtype,
+                                        void* stream) {
+  if (!lora_h || !y_side_h) return fail(PL_ERR_INVALID, "lora_h and y_side_h must not be null");
+  if (dtype != PL_DTYPE_BF16 && dtype != PL_DTYPE_F16)
+    return fail(PL_ERR_UNSUPPORTED, "pl_add_rmsnorm_lora_side dtype must be F16 or BF16 (got %d)", dtype);
+  if (rows < 0 || hidden <= 0 || hidden % 8 || hidden > kRowNormMaxHidden)
+    return fail(PL_ERR_INVALID, "hidden must be a positive multiple of 8 up to %d (got %d)", kRowNormMaxHidden,
+                hidden);
+  if (rows == 0) return ok();
+  if (!x || !weight || !out || !residual) return fail(PL_ERR_INVALID, "null pointer argument");
+  if (ldx % 8 || ldo % 8 || ldr % 8) return fail(PL_ERR_INVALID, "row strides must be multiples of 8");
+  const void* ptrs[] = {x, weight, out, residual};
+  for (const void* q : ptrs)
+    if ((uintptr_t)q % 16) return fail(PL_ERR_INVALID, "pointers must be 16-byte aligned");
+  const pl_split_out& ysh = *y_side_h;
+  if (!ysh.partials || ysh.splits < 1 || ysh.splits > 64 || ysh.ld <= 0 || ysh.plane_stride < ysh.ld * rows)
+    return fail(PL_ERR_INVALID, "y side planes: 1..64 planes of rows x ld floats, non-overlapping");
+  const SplitIn ys{ysh.partials, ysh.splits, ysh.ld, ysh.plane_stride};
+  if (const int st = adapter_check(lora_h, 1, adapter_ids, num_adapters, "add_rmsnorm LoRA")) return st;
+  LoraUp lu{};
+  if (const int st = lora_up_from(lora_h, hidden, &lu, "add_rmsnorm LoRA", &ys, num_adapters)) return st;
+  if (lu.rank != 8 && lu.rank != 16) return fail(PL_ERR_UNSUPPORTED, "side-plane y: rank 8 or 16 (got %d)", lu.rank);
+  const int threads = (hidden / 8 + kWave - 1) / kWave * kWave;
+  const SplitIn none{nullptr, 0, 0, 0};
+  hipStream_t s = (hipStream_t)stream;
+  auto go = [&](auto tag, auto rank) {
+    using T = decltype(tag);
+    constexpr int R = decltype(rank)::value;
+    hipLaunchKernelGGL((add_rmsnorm_row_kernel<T, R, 0, true>), dim3(rows), dim3(threads), 0, s, (T*)residual, ldr,
+                       (const T*)x, ldx, (const T*)weight, (T*)out, ldo, hidden, eps, lu, adapter_ids, num_adapters,
+                       none, ys);
+  };
+  if (dtype == PL_DTYPE_BF16) {
+    if (lu.rank == 8) go(bf16_t{}, std::integral_constant<int, 8>{});
+    else go(bf16_t{}, std::integral_constant<int, 16>{});
+  } else {
+    if (lu.rank == 8) go(f16_t{}, std::integral_constant<int, 8>{});
+    else go(f16_t{}, std::integral_constant<int, 16>{});
+  }
+  PL_LAUNCH_CHECK("add_rmsnorm_row_kernel");
+  return ok();
 }
 
 // Plain SiLU*up: 256 threads per workgroup; with the LoRA prologue every

@@ -70,21 +70,32 @@ __global__ void shuffle_kernel(const uint16_t* __restrict__ W, int64_t ldw, int 
 // PARTIAL: split-K over gridDim.z workgroups per row block; workgroup z sums
 // k-steps [z*K/32/splits, ..) and writes its fp32 tile to plane z of
 // `partial` (row t at t * ldp, planes plane_stride apart) instead of `out`.
-template <typename T, bool PARTIAL>
+// SIDE: row blocks below main_tiles are computed whole into `out`; the
+// blocks from main_tiles on (the LoRA A rows stacked under W) are split-K
+// over side_splits small workgroups each, appended to the grid, into fp32
+// planes of `partial` (column n - 16 * main_tiles).  A row-block count that
+// is a multiple of the CU count then stays one: one more whole block costs a
+// CU two blocks' time (o_proj, 4 tokens: 4096 rows 7.6 us, 4112 rows 10.1).
+template <typename T, bool PARTIAL, bool SIDE = false>
 __global__ __launch_bounds__(kThreads) void shuffled_gemm_kernel(const T* __restrict__ x, int64_t ldx, int tokens,
                                                                  int K, const T* __restrict__ Ws, int N,
                                                                  const T* __restrict__ bias, T* __restrict__ out,
                                                                  int64_t ldo, float* __restrict__ partial,
-                                                                 int64_t ldp, int64_t plane_stride) {
+                                                                 int64_t ldp, int64_t plane_stride,
+                                                                 int main_tiles = 0, int side_splits = 1) {
   __shared__ float s_red[kWaves][256];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int lr = lane % 16, kq = (lane / 16) * 8;
-  const int nb = blockIdx.x, t0 = blockIdx.y * 16;
+  const bool side = SIDE && (int)blockIdx.x >= main_tiles;
+  const int se_idx = (int)blockIdx.x - main_tiles;
+  const int nb = side ? main_tiles + se_idx / side_splits : (int)blockIdx.x, t0 = blockIdx.y * 16;
+  const int zs = SIDE ? (side ? se_idx % side_splits : 0) : (int)blockIdx.z;
+  const int nz = SIDE ? (side ? side_splits : 1) : (int)gridDim.z;
   const int t = t0 + lr;
   const bool t_ok = t < tokens;
   const int ksteps = K / 32;
-  const int chunk = (ksteps + gridDim.z - 1) / gridDim.z;
-  const int kb0 = min(ksteps, (int)blockIdx.z * chunk), ke0 = min(ksteps, kb0 + chunk);
+  const int chunk = (ksteps + nz - 1) / nz;
+  const int kb0 = min(ksteps, zs * chunk), ke0 = min(ksteps, kb0 + chunk);
   const int per = (ke0 - kb0 + kWaves - 1) / kWaves;
   const int sb = min(ke0, kb0 + wave * per), se = min(ke0, sb + per);
   const u32x4* wb = reinterpret_cast<const u32x4*>(Ws + (int64_t)nb * ksteps * kBlockElems) + lane;
@@ -119,7 +130,7 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_kernel(const T* __rest
   __syncthreads();
   if (wave == 0) {
     const int n = nb * 16 + lr;
-    const float bv = (!PARTIAL && bias != nullptr && n < N) ? to_float<T>(bias[n]) : 0.f;
+    const float bv = (!PARTIAL && !side && bias != nullptr && n < N) ? to_float<T>(bias[n]) : 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int cell = ((lane / 16) * 4 + i) * 16 + lr;
@@ -130,6 +141,8 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_kernel(const T* __rest
       if (n < N && tr < tokens) {
         if (PARTIAL)
           partial[(int64_t)blockIdx.z * plane_stride + (int64_t)tr * ldp + n] = sum;
+        else if (side)
+          partial[(int64_t)zs * plane_stride + (int64_t)tr * ldp + (n - main_tiles * 16)] = sum;
         else
           out[(int64_t)tr * ldo + n] = from_float<T>(sum + bv);
       }
@@ -224,6 +237,46 @@ extern "C" int pl_linear_shuffled_split(const void* x, int64_t ldx, int num_toke
     hipLaunchKernelGGL((shuffled_gemm_kernel<f16_t, true>), grid, dim3(kThreads), 0, s, (const f16_t*)x, ldx,
                        num_tokens, in_features, (const f16_t*)shuffled, out_features, nullptr, nullptr, 0,
                        partials, ld, plane_stride);
+  PL_LAUNCH_CHECK("shuffled_gemm_kernel");
+  return ok();
+}
+
+extern "C" int pl_linear_shuffled_side(const void* x, int64_t ldx, int num_tokens, int in_features,
+                                       const void* shuffled, int out_features, int main_features, void* out,
+                                       int64_t ldo, int side_splits, float* side_partials, int64_t ld_side,
+                                       int64_t side_plane_stride, int dtype, void* stream) {
+  if (num_tokens < 0 || num_tokens > PL_LINEAR_MAX_TOKENS)
+    return fail(PL_ERR_INVALID, "num_tokens must be 0..%d (got %d)", PL_LINEAR_MAX_TOKENS, num_tokens);
+  if (num_tokens == 0) return ok();
+  if (in_features <= 0 || in_features % 32 || out_features <= 0)
+    return fail(PL_ERR_INVALID, "in_features must be a positive multiple of 32 and out_features > 0");
+  if (main_features <= 0 || main_features % 16 || main_features >= out_features)
+    return fail(PL_ERR_INVALID, "main_features must be a positive multiple of 16 below out_features (got %d of %d)",
+                main_features, out_features);
+  if (side_splits < 1 || side_splits > 64 || side_splits > in_features / 32)
+    return fail(PL_ERR_INVALID, "side_splits must be 1..min(64, in_features/32) (got %d)", side_splits);
+  if (!x || !shuffled || !out || !side_partials) return fail(PL_ERR_INVALID, "null pointer argument");
+  if (ldx < in_features || ldx % 8 || (uintptr_t)x % 16 || (uintptr_t)shuffled % 16)
+    return fail(PL_ERR_INVALID, "x rows and the shuffled weight must be 16-byte aligned");
+  if (ldo < main_features) return fail(PL_ERR_INVALID, "ldo < main_features");
+  const int side_features = out_features - main_features;
+  if (ld_side < side_features || side_plane_stride < ld_side * num_tokens)
+    return fail(PL_ERR_INVALID, "side planes overlap (ld %lld, plane_stride %lld)", (long long)ld_side,
+                (long long)side_plane_stride);
+  if (dtype != PL_DTYPE_BF16 && dtype != PL_DTYPE_F16)
+    return fail(PL_ERR_UNSUPPORTED, "pl_linear_shuffled_side dtype must be F16 or BF16 (got %d)", dtype);
+  const int main_tiles = main_features / 16;
+  const int side_tiles = (out_features + 15) / 16 - main_tiles;
+  const dim3 grid(main_tiles + side_tiles * side_splits, (num_tokens + 15) / 16, 1);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == PL_DTYPE_BF16)
+    hipLaunchKernelGGL((shuffled_gemm_kernel<bf16_t, false, true>), grid, dim3(kThreads), 0, s, (const bf16_t*)x,
+                       ldx, num_tokens, in_features, (const bf16_t*)shuffled, out_features, nullptr, (bf16_t*)out,
+                       ldo, side_partials, ld_side, side_plane_stride, main_tiles, side_splits);
+  else
+    hipLaunchKernelGGL((shuffled_gemm_kernel<f16_t, false, true>), grid, dim3(kThreads), 0, s, (const f16_t*)x,
+                       ldx, num_tokens, in_features, (const f16_t*)shuffled, out_features, nullptr, (f16_t*)out,
+                       ldo, side_partials, ld_side, side_plane_stride, main_tiles, side_splits);
   PL_LAUNCH_CHECK("shuffled_gemm_kernel");
   return ok();
 }

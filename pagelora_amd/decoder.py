@@ -35,7 +35,7 @@ import torch.nn.functional as F
 from . import fused_ops
 from .attention_backend import PagedDecodeAttention
 from .kv_pool import PagedKVPool, Request
-from .linear import ShuffledWeight, SplitOutput, linear_shuffled, linear_shuffled_split
+from .linear import ShuffledWeight, SplitOutput, linear_shuffled, linear_shuffled_side, linear_shuffled_split
 from .lora import lora_linear
 
 
@@ -133,11 +133,14 @@ class LayerWeights:
             if name in self.lora:
                 self.lora_b8[name] = fused_ops.lora_b_chunk8(self.lora[name][1])
 
-    def up(self, name: str, y: torch.Tensor, scale: float, adapter: int = -1) -> fused_ops.LoraUp:
+    def up(self, name: str, y: "torch.Tensor | SideOutput", scale: float, adapter: int = -1) -> fused_ops.LoraUp:
         """The up-projection of module ``name`` reading its intermediate from ``y``
         (``adapter`` >= 0: that one adapter for every token)."""
         B = self.lora_b8.get(name)
-        return fused_ops.LoraUp(y, self.y_offset[name], self.lora[name][1] if B is None else B, scale, adapter)
+        B = self.lora[name][1] if B is None else B
+        if isinstance(y, SideOutput):
+            return fused_ops.LoraUp(y.side, self.y_offset[name] - y.main.shape[1], B, scale, adapter)
+        return fused_ops.LoraUp(y, self.y_offset[name], B, scale, adapter)
 
 
 class DecoderWeights:
@@ -189,25 +192,45 @@ class DecodeContext:
 # the narrow projections (q/k/v, o); the wide MLP projections and longer
 # inputs (prefill) take the library GEMM (torch -> hipBLASLt).
 DECODE_GEMM_MAX_TOKENS = 16
-# Split-K ways of the decode GEMM per projection.  down_proj (257 blocks of
-# 16 output columns over K = 12288) keeps too few workgroups streaming: split
-# 3 ways it drops from 25.9 to 19.4 us at 4 tokens, and the next add+RMSNorm
-# sums the fp32 planes for ~1.7 us more.  Splitting o_proj (257 blocks, K =
-# 4096) or qkv saves less than its consumer then pays; gate_up (1538 blocks)
-# does not need it.
-DECODE_SPLITS = {"down": 3}
+# Split-K ways of the decode GEMM per projection (whole output, consumers
+# sum the planes).  None by default: down_proj ran split 3 ways (257 blocks
+# of 16 outputs over K = 12288: 25.9 -> 19.4 us at 4 tokens, +1.7 us in the
+# next add+RMSNorm) until its A rows were split off instead (below); o_proj
+# and qkv save less than their consumers then pay.
+DECODE_SPLITS: dict[str, int] = {}
+# Projections whose stacked LoRA A rows are split off (pl_linear_shuffled_side)
+# at decode batch sizes, with the side planes' count: o_proj and down_proj
+# have 4096 base rows, 256 blocks of 16 (one per CU), and their A rows make a
+# 257th block that costs some CU a second whole block (4 tokens: o 7.6 ->
+# 10.1 us, down unsplit 18.8 -> 26.3 us; down split 3 ways 20.3 us).  With
+# the A rows split 16 ways by small workgroups of their own, down needs no
+# split of its base rows either.
+DECODE_SIDE_SPLITS = {"o": 16, "down": 16}
 # Decode layers form q and append k/v inside the attention kernel
 # (pl_decode_run_qkv) where it is built; False keeps the separate
 # head-norm/RoPE/append kernel (tests compare the two).
 FOLD_QKV_INTO_DECODE = True
 
 
-def _project(x: torch.Tensor, lw: LayerWeights, name: str) -> "torch.Tensor | SplitOutput":
+class SideOutput:
+    """A projection output as its base rows ``main`` [T, out] and the LoRA
+    intermediates ``side`` (split-K planes of linear_shuffled_side)."""
+
+    def __init__(self, main: torch.Tensor, side: SplitOutput) -> None:
+        self.main, self.side = main, side
+
+
+def _project(x: torch.Tensor, lw: LayerWeights, name: str) -> "torch.Tensor | SplitOutput | SideOutput":
     """x . [W; A]^T: the base output and every adapter's LoRA intermediate
-    (as split-K planes for the narrow projections at decode batch sizes)."""
+    (at decode batch sizes as split-K planes, or with the intermediates split
+    off, for the narrow projections)."""
     if x.shape[0] <= DECODE_GEMM_MAX_TOKENS:
         sw = lw.shuffled.get(name)
         if sw is not None:
+            side = DECODE_SIDE_SPLITS.get(name, 0)
+            main = lw.y_offset.get(name, sw.out_features)
+            if side and main % 16 == 0 and main < sw.out_features:
+                return SideOutput(*linear_shuffled_side(x, sw, main, side))
             splits = DECODE_SPLITS.get(name, 1)
             if splits > 1:
                 return linear_shuffled_split(x, sw, splits)
@@ -219,6 +242,8 @@ def _project(x: torch.Tensor, lw: LayerWeights, name: str) -> "torch.Tensor | Sp
 
 def _cols(out, n: int):
     """The first n columns of a projection output (split planes are passed whole)."""
+    if isinstance(out, SideOutput):
+        return out.main[:, :n]
     return out if isinstance(out, SplitOutput) else out[:, :n]
 
 

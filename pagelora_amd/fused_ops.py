@@ -143,7 +143,9 @@ def add_rmsnorm(residual: torch.Tensor, x: "torch.Tensor | SplitOutput", weight:
 
     With ``lora``, x is the base output of the module whose up-projection
     ``lora`` describes: ``residual += round(x + delta)`` (pl_add_rmsnorm_lora).
-    x may then also be a :class:`SplitOutput` (split-K planes summed here).
+    x may then also be a :class:`SplitOutput` (split-K planes summed here),
+    or x a tensor and ``lora.y`` the side planes of
+    :func:`linear.linear_shuffled_side` (pl_add_rmsnorm_lora_side).
     """
     _rows2d(residual, "residual")
     rows, hidden = residual.shape
@@ -159,6 +161,15 @@ def add_rmsnorm(residual: torch.Tensor, x: "torch.Tensor | SplitOutput", weight:
             raise ValueError("x must match residual")
     out = torch.empty_like(residual) if out is None else out
     lib = _lib.load()
+    if lora is not None and not split and isinstance(lora.y, SplitOutput):
+        # y from the side planes of linear_shuffled_side, x whole
+        arr, ids, n = _lora_args([lora], adapter_ids, rows)
+        _lib.check(lib.pl_add_rmsnorm_lora_side(residual.data_ptr(), residual.stride(0), x.data_ptr(), x.stride(0),
+                                                ctypes.byref(lora.y.struct()), arr, ids, n, weight.data_ptr(),
+                                                out.data_ptr(), out.stride(0), rows, hidden, float(eps),
+                                                _lib.dtype_code(residual.dtype), _lib.stream_handle(residual.device)),
+                   "pl_add_rmsnorm_lora_side")
+        return out
     if lora is not None:
         arr, ids, n = _lora_args([lora], adapter_ids, rows)
         xs = ctypes.byref(x.struct()) if split else None

@@ -115,3 +115,30 @@ def linear_shuffled_split(x: torch.Tensor, weight: ShuffledWeight, splits: int) 
                                             _lib.dtype_code(x.dtype), _lib.stream_handle(x.device)),
                "pl_linear_shuffled_split")
     return SplitOutput(partials, N, x.dtype)
+
+
+def linear_shuffled_side(x: torch.Tensor, weight: ShuffledWeight, main_features: int,
+                         side_splits: int) -> tuple[torch.Tensor, SplitOutput]:
+    """``x . W^T`` with the rows from ``main_features`` on (the LoRA A rows
+    stacked under W) split-K into fp32 planes: returns the first
+    ``main_features`` outputs as a ``[T, main_features]`` tensor and the rest
+    as a :class:`SplitOutput` of ``out_features - main_features`` columns
+    (``pl_linear_shuffled_side``)."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] != weight.in_features or x.dtype != weight.dtype:
+        raise ValueError(f"x must be [T, {weight.in_features}] of {weight.dtype} with unit column stride")
+    T, N = x.shape[0], weight.out_features
+    if T > _lib.PL_LINEAR_MAX_TOKENS:
+        raise ValueError(f"linear_shuffled_side takes at most {_lib.PL_LINEAR_MAX_TOKENS} tokens")
+    if main_features <= 0 or main_features % 16 or main_features >= N:
+        raise ValueError("main_features must be a positive multiple of 16 below out_features")
+    side = N - main_features
+    ld = (side + 7) // 8 * 8
+    out = torch.empty((T, main_features), dtype=x.dtype, device=x.device)
+    partials = torch.empty((side_splits, T, ld), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    _lib.check(lib.pl_linear_shuffled_side(x.data_ptr(), x.stride(0), T, weight.in_features, weight.data.data_ptr(),
+                                           N, int(main_features), out.data_ptr(), out.stride(0), int(side_splits),
+                                           partials.data_ptr(), ld, partials.stride(0), _lib.dtype_code(x.dtype),
+                                           _lib.stream_handle(x.device)),
+               "pl_linear_shuffled_side")
+    return out, SplitOutput(partials, side, x.dtype)

@@ -443,3 +443,30 @@ def test_uniform_adapter_validation(gpu_device):
     gu = torch.zeros((2, 2 * 64 + 2 * 3 * 16), dtype=torch.bfloat16, device=dev)
     with pytest.raises(ValueError):   # modules of one call bind different adapters
         fused_ops.silu_mul(gu[:, :128], lora=(fused_ops.LoraUp(gu, 128, B, 1.0, 0), fused_ops.LoraUp(gu, 176, B, 1.0, 1)))
+
+
+@pytest.mark.parametrize("planes", [1, 3, 16, 40])
+@pytest.mark.parametrize("rank", [8, 16])
+@pytest.mark.parametrize("hidden", [256, 4096])
+@pytest.mark.parametrize("bound", [False, True])
+def test_add_rmsnorm_lora_side_planes_match_summed_y(gpu_device, planes, rank, hidden, bound):
+    """pl_add_rmsnorm_lora_side (y from side planes, summed in plane order by
+    the workgroup) equals pl_add_rmsnorm_lora with y = the planes' in-order sum
+    rounded (SplitOutput.sum), bit for bit."""
+    rows = len(IDS)
+    g = torch.Generator().manual_seed(planes * 31 + rank + hidden + bound)
+    side = _random_split(g, planes, rows, N_ADAPTERS * rank, torch.bfloat16, gpu_device)
+    dense_y = side.sum()
+    x = torch.randn((rows, hidden), generator=g).to(torch.bfloat16).to(gpu_device)
+    B = (torch.randn((N_ADAPTERS, hidden, rank), generator=g) * 0.05).to(torch.bfloat16).to(gpu_device)
+    r0 = torch.randn((rows, hidden), generator=g).to(torch.bfloat16).to(gpu_device)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(gpu_device)
+    ids = None if bound else torch.tensor(IDS, dtype=torch.int32, device=gpu_device)
+    adapter = 2 if bound else -1
+    r1, r2 = r0.clone(), r0.clone()
+    out1 = fused_ops.add_rmsnorm(r1, x, w, 1e-6, lora=fused_ops.LoraUp(side, 0, B, SCALE, adapter), adapter_ids=ids)
+    out2 = fused_ops.add_rmsnorm(r2, x, w, 1e-6, lora=fused_ops.LoraUp(dense_y, 0, B, SCALE, adapter),
+                                 adapter_ids=ids)
+    torch.cuda.synchronize()
+    assert torch.equal(r1, r2) and torch.equal(out1, out2)
+    assert not torch.equal(r1, r0)

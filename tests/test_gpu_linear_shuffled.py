@@ -116,3 +116,46 @@ def test_split_planes_sum_to_the_linear(gpu_device, splits, shape, tokens):
     assert (err <= 2e-3 + REL[torch.bfloat16] * np.abs(want)).all(), f"max err {err.max():.3e}"
     if splits == 1:
         assert torch.equal(got, linear_shuffled(x.to(gpu_device), sw))
+
+
+@pytest.mark.parametrize("side_splits", [1, 3, 16])
+@pytest.mark.parametrize("shape", [(4096 + 16, 4096, 4096), (4096 + 64, 12288, 4096), (6144 + 48, 4096, 6144),
+                                   (48 + 8, 96, 48)])
+@pytest.mark.parametrize("tokens", [1, 4, 17])
+def test_side_planes_and_main_columns(gpu_device, side_splits, shape, tokens):
+    """pl_linear_shuffled_side: the main columns are pl_linear_shuffled's,
+    bit for bit (the same workgroups compute them); the side planes' in-order
+    sum, rounded, is the oracle's linear over the side rows (the same bar)."""
+    from pagelora_amd.linear import linear_shuffled_side
+
+    n, k, main = shape
+    g = torch.Generator().manual_seed(n * 3 + k + tokens + side_splits)
+    x = torch.randn((tokens, k), generator=g).to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=g) * k ** -0.5).to(torch.bfloat16)
+    sw = ShuffledWeight(w.to(gpu_device))
+    if side_splits > k // 32:
+        with pytest.raises(ValueError, match="side_splits"):
+            linear_shuffled_side(x.to(gpu_device), sw, main, side_splits)
+        return
+    out, side = linear_shuffled_side(x.to(gpu_device), sw, main, side_splits)
+    ref = linear_shuffled(x.to(gpu_device), sw)
+    torch.cuda.synchronize()
+    assert out.shape == (tokens, main)
+    assert torch.equal(out, ref[:, :main])
+    assert side.out_features == n - main and side.partials.shape == (side_splits, tokens, (n - main + 7) // 8 * 8)
+    want = _oracle_linear(x.double().numpy(), w[main:].double().numpy(), None)
+    got = side.sum().float().cpu().numpy()
+    err = np.abs(got - want)
+    assert (err <= 2e-3 + REL[torch.bfloat16] * np.abs(want)).all(), f"max err {err.max():.3e}"
+
+
+def test_side_bad_inputs_raise(gpu_device):
+    from pagelora_amd.linear import linear_shuffled_side
+
+    sw = ShuffledWeight(torch.zeros((48, 64), dtype=torch.bfloat16, device=gpu_device))
+    x = torch.zeros((4, 64), dtype=torch.bfloat16, device=gpu_device)
+    for main in (0, 8, 48, 64):  # not a positive multiple of 16 below out_features
+        with pytest.raises(ValueError, match="main_features"):
+            linear_shuffled_side(x, sw, main, 1)
+    with pytest.raises(ValueError, match="side_splits"):
+        linear_shuffled_side(x, sw, 32, 3)  # 2 k-steps
