@@ -166,13 +166,22 @@ __device__ __forceinline__ float row32_sum(float x) {  // within aligned groups 
   return x;
 }
 
+// Wave-wide reductions: DPP within each 16-lane row, then the four row
+// results read into scalar registers (no LDS round trips, the same value in
+// every lane).
+__device__ __forceinline__ float lane_value(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
 __device__ __forceinline__ float wave_max(float x) {
-  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m));
-  return x;
+  x = fmaxf(x, dpp_mov<0x128>(x));  // row_ror:8
+  x = fmaxf(x, dpp_mov<0x124>(x));  // row_ror:4
+  x = fmaxf(x, dpp_mov<0x122>(x));  // row_ror:2
+  x = fmaxf(x, dpp_mov<0x121>(x));  // row_ror:1
+  return fmaxf(fmaxf(lane_value(x, 0), lane_value(x, 16)), fmaxf(lane_value(x, 32), lane_value(x, 48)));
 }
 __device__ __forceinline__ float wave_sum(float x) {
-  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
-  return x;
+  x = row16_sum(x);
+  return (lane_value(x, 0) + lane_value(x, 16)) + (lane_value(x, 32) + lane_value(x, 48));
 }
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
