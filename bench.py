@@ -315,8 +315,8 @@ def cpu_baseline(w, budget_s):
 
 
 def cpu_small_configs():
-    """The float64 numpy oracle on the three small workloads (cfg1: batch 4 x
-    512 tokens fp32, GQA 4; cfg2: batch 1 x 2048 bf16, GQA 4; cfg4: the LoRA
+    """The float64 numpy oracle on the three small workloads (batch 4 x
+    512 tokens fp32, GQA 4; batch 1 x 2048 bf16, GQA 4; the LoRA
     delta of 64 tokens over 4 adapters and 7 modules): algorithmic GB/s, the
     median of 10 runs after 2 warm-ups, one thread."""
     import torch
@@ -335,8 +335,8 @@ def cpu_small_configs():
         return float(np.median(ts))
 
     res = {}
-    for name, B, L, dtype, kvb, seed in (("cfg1_b4_512_fp32_gqa4", 4, 512, torch.float32, 4, 1234),
-                                         ("cfg2_b1_2048_bf16_gqa4", 1, 2048, torch.bfloat16, 2, 1235)):
+    for name, B, L, dtype, kvb, seed in (("b4_512_fp32_gqa4", 4, 512, torch.float32, 4, 1234),
+                                         ("b1_2048_bf16_gqa4", 1, 2048, torch.bfloat16, 2, 1235)):
         ps, hq, hkv, d = 16, 32, 8, 128
         npg = L // ps
         gen = torch.Generator().manual_seed(seed)
@@ -360,7 +360,7 @@ def cpu_small_configs():
         mods.append((x, A, Bm))
         nb += (A.size + Bm.size) * 2 + T * fout * 4 + x.size * 2
     sec = median_s(lambda: [olora.multi_adapter_delta(x, ids, A, Bm, 2.0, intermediate="bf16") for x, A, Bm in mods])
-    res["cfg4_lora_64tok_4adapters_7modules"] = {"GBps": round(float(nb) / sec / 1e9, 4), "ms": round(sec * 1e3, 2),
+    res["lora_64tok_4adapters_7modules"] = {"GBps": round(float(nb) / sec / 1e9, 4), "ms": round(sec * 1e3, 2),
                                                  "algorithmic_bytes": int(nb)}
     res["note"] = "float64 numpy oracle, 1 thread; same algorithmic-byte definitions as the GPU legs"
     return res

@@ -56,7 +56,7 @@ def _check(out, ref, dtype, rows=None):
     return float(err.max())
 
 
-def test_cfg1_fp32_batch4_gqa4(gpu_device):
+def test_fp32_batch4_512_gqa4(gpu_device):
     # B=4, 32/8 heads, D=128, page 16, 512 tokens per row, 128 of 256 pages.
     case = ragged_case(lens=[512] * 4, hq=32, hkv=8, head_dim=128, page_size=16, dtype=torch.float32,
                        device=gpu_device, seed=1234, pool_extra=128)
@@ -65,7 +65,7 @@ def test_cfg1_fp32_batch4_gqa4(gpu_device):
     _check(out, ref, torch.float32)
 
 
-def test_cfg2_bf16_qwen3_layer_2048(gpu_device):
+def test_bf16_qwen3_layer_1x2048(gpu_device):
     case = ragged_case(lens=[2048], hq=32, hkv=8, head_dim=128, page_size=16, dtype=torch.bfloat16,
                        device=gpu_device, seed=1235, pool_extra=4096 - 128)
     out, _, _ = _run(case, 32, 8, 128, 16, torch.bfloat16, gpu_device)
@@ -181,7 +181,7 @@ def test_empty_row_gives_zeros(gpu_device):
     assert torch.isinf(lse[0]).all() and torch.isinf(lse[2]).all()
 
 
-def test_cfg3_ragged_batch64_mha_full_size(gpu_device):
+def test_ragged_batch64_mha_full_size(gpu_device):
     # Llama-2-7B shape: 32/32 heads, fp16, 64 rows with lengths U[128, 8192].
     torch.manual_seed(0)
     lens = uniform_lens(64, 128, 8192, 1236)

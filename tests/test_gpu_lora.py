@@ -23,7 +23,7 @@ def _rand(shape, std, gen, dtype=torch.bfloat16):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("out_dtype", ["f32", "same"])
-def test_cfg4_qwen3_modules_4_adapters(gpu_device, dtype, out_dtype):
+def test_qwen3_modules_64_tokens_4_adapters(gpu_device, dtype, out_dtype):
     # hidden 4096, intermediate 12288, r=16, alpha 32 (s=2), 64 tokens over 4 adapters.
     gen = torch.Generator().manual_seed(1237)
     T, H, I, r, n = 64, 4096, 12288, 16, 4
