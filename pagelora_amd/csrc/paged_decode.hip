@@ -36,7 +36,14 @@ namespace decode {
 
 constexpr int kWave = 64;
 constexpr int kBlockTokens = 16;   // tokens consumed per pipeline step
-constexpr int kWavesPerWG = 4;
+// Decode waves per workgroup (consecutive kv heads of one item).  Measured
+// on the ragged batch-64 MHA fp16 step: 1 -> 0.794 of peak, 2 -> 0.834,
+// 4 -> 0.827, 8 -> 0.810; Qwen3 layer 1 x 2048 bf16 (caches evicted):
+// 10.8 / 11.2 / 12.9 / 18.3 us.  The kernel with the folded q/k/v epilogue
+// keeps 4 (end to end at 1 x 32K tokens: 225.0 tok/s with 4, 222.8 with 2;
+// equal with 4 rows).
+template <bool FUSED>
+constexpr int waves_per_wg() { return FUSED ? 4 : 2; }
 
 struct Item {   // one split-KV work item; lives in the workspace
   int row;      // batch row, -1 = unused slot
@@ -818,7 +825,7 @@ __device__ __forceinline__ void head_finish(const QkvIn& in, const HeadIn<T, R>&
 }
 
 template <typename T, int D, int G, bool FUSED = false, int R = 0>
-__global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
+__global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
     const T* __restrict__ q, int64_t q_sb, int64_t q_sh, const T* __restrict__ kc,
     const T* __restrict__ vc, int64_t page_stride, int64_t token_stride, int64_t head_stride,
     const int32_t* __restrict__ indices, const int32_t* __restrict__ last_page_len,
@@ -831,7 +838,7 @@ __global__ __launch_bounds__(kWave * kWavesPerWG) void decode_kernel(
   using L8 = Lane8<T>;
 
   const int lane = threadIdx.x % kWave;
-  const int wave = uniform(blockIdx.x * kWavesPerWG + threadIdx.x / kWave);
+  const int wave = uniform(blockIdx.x * waves_per_wg<FUSED>() + threadIdx.x / kWave);
   const int item_idx = wave / num_kv_heads;
   const int h = wave - item_idx * num_kv_heads;
   if (item_idx >= max_items) return;
@@ -1161,8 +1168,9 @@ template <typename T, int D, int G, bool FUSED = false, int R = 0>
 int launch(const RunArgs& a, const QkvIn& qin = QkvIn{}) {
   if (!(a.flags & PL_DECODE_MERGE_ONLY)) {
     const int64_t waves = (int64_t)a.max_items * a.hkv;
-    const int grid = (int)((waves + kWavesPerWG - 1) / kWavesPerWG);
-    hipLaunchKernelGGL((decode_kernel<T, D, G, FUSED, R>), dim3(grid), dim3(kWave * kWavesPerWG), 0, a.stream,
+    constexpr int wpg = waves_per_wg<FUSED>();
+    const int grid = (int)((waves + wpg - 1) / wpg);
+    hipLaunchKernelGGL((decode_kernel<T, D, G, FUSED, R>), dim3(grid), dim3(kWave * wpg), 0, a.stream,
                        (const T*)a.q, a.q_sb, a.q_sh, (const T*)a.kc, (const T*)a.vc, a.page_stride,
                        a.token_stride, a.head_stride, a.indices, a.last, (T*)a.o, a.o_sb, a.o_sh,
                        a.lse, a.hq, a.hkv, a.page_size, a.num_pages, a.scale_log2, a.header,
