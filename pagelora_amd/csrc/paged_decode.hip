@@ -1047,9 +1047,14 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
 // partials online (running max, weight sum, weighted output); the threads'
 // states are combined with xor shuffles inside a wave and through LDS across
 // waves.  MT is one wave when the plan averages a few items per row (the
-// ragged batch-64 case: ~5), four waves when rows hold tens of items.
+// ragged batch-64 case: ~5), four waves when rows hold tens of items, eight
+// beyond 64.
 constexpr int kMergeBatch = 8;
 constexpr int kMergeFewItems = 8;  // average items per row up to which one wave merges
+// Average items per row above which eight waves merge (a row of ~128 items:
+// 1 x 32K tokens, plan + decode + merge 36.7 -> 35.7 us; at ~33 items per
+// row (4 x 2112) four waves stay 0.25 us faster).
+constexpr int kMergeManyItems = 64;
 
 struct MergeState {
   float m, w, a[8];  // log2 max, sum of weights, weighted output (8 dims)
@@ -1182,8 +1187,12 @@ int launch(const RunArgs& a, const QkvIn& qin = QkvIn{}) {
       hipLaunchKernelGGL((merge_kernel<T, D, kWave>), dim3(a.batch * a.hq), dim3(kWave), 0, a.stream,
                          a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
                          a.batch, a.hq, a.max_items);
-    else
+    else if (a.max_items <= kMergeManyItems * a.batch)
       hipLaunchKernelGGL((merge_kernel<T, D, 4 * kWave>), dim3(a.batch * a.hq), dim3(4 * kWave), 0, a.stream,
+                         a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
+                         a.batch, a.hq, a.max_items);
+    else
+      hipLaunchKernelGGL((merge_kernel<T, D, 8 * kWave>), dim3(a.batch * a.hq), dim3(8 * kWave), 0, a.stream,
                          a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
                          a.batch, a.hq, a.max_items);
     PL_LAUNCH_CHECK("merge_kernel");
