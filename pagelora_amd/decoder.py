@@ -227,7 +227,7 @@ def _project(x: torch.Tensor, lw: LayerWeights, name: str) -> "torch.Tensor | Sp
     if x.shape[0] <= DECODE_GEMM_MAX_TOKENS:
         sw = lw.shuffled.get(name)
         if sw is not None:
-            side = DECODE_SIDE_SPLITS.get(name, 0)
+            side = min(DECODE_SIDE_SPLITS.get(name, 0), sw.in_features // 32)
             main = lw.y_offset.get(name, sw.out_features)
             if side and main % 16 == 0 and main < sw.out_features:
                 return SideOutput(*linear_shuffled_side(x, sw, main, side))

@@ -328,3 +328,21 @@ def test_folded_qkv_graph_replay_matches_eager(gpu_device):
         assert res.used_graph == use_graph
         runs.append(res.tokens)
     assert torch.equal(runs[0], runs[1])
+
+
+def test_side_plane_projections_match_split_projections(gpu_device, monkeypatch):
+    """o_proj / down_proj with their LoRA A rows on side planes (the default)
+    against the earlier layout (down split 3 ways, o whole): the same logits
+    to within the rounding of y, the same greedy tokens."""
+    from pagelora_amd import decoder
+    out = []
+    for side in (True, False):
+        if not side:
+            monkeypatch.setattr(decoder, "DECODE_SIDE_SPLITS", {})
+            monkeypatch.setattr(decoder, "DECODE_SPLITS", {"down": 3})
+        w, pool, reqs, first, _ = _setup128(gpu_device)
+        out.append(_eager_step(w, pool, reqs, first, [0, 1, 1], gpu_device))
+    (ls, ts), (lp, tp) = out
+    torch.cuda.synchronize()
+    assert torch.allclose(ls, lp, atol=0.05, rtol=0.01), (ls - lp).abs().max()
+    _assert_same_greedy(ts, lp, ls)

@@ -118,11 +118,12 @@ def test_split_planes_sum_to_the_linear(gpu_device, splits, shape, tokens):
         assert torch.equal(got, linear_shuffled(x.to(gpu_device), sw))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("side_splits", [1, 3, 16])
 @pytest.mark.parametrize("shape", [(4096 + 16, 4096, 4096), (4096 + 64, 12288, 4096), (6144 + 48, 4096, 6144),
                                    (48 + 8, 96, 48)])
 @pytest.mark.parametrize("tokens", [1, 4, 17])
-def test_side_planes_and_main_columns(gpu_device, side_splits, shape, tokens):
+def test_side_planes_and_main_columns(gpu_device, side_splits, shape, tokens, dtype):
     """pl_linear_shuffled_side: the main columns are pl_linear_shuffled's,
     bit for bit (the same workgroups compute them); the side planes' in-order
     sum, rounded, is the oracle's linear over the side rows (the same bar)."""
@@ -130,8 +131,8 @@ def test_side_planes_and_main_columns(gpu_device, side_splits, shape, tokens):
 
     n, k, main = shape
     g = torch.Generator().manual_seed(n * 3 + k + tokens + side_splits)
-    x = torch.randn((tokens, k), generator=g).to(torch.bfloat16)
-    w = (torch.randn((n, k), generator=g) * k ** -0.5).to(torch.bfloat16)
+    x = torch.randn((tokens, k), generator=g).to(dtype)
+    w = (torch.randn((n, k), generator=g) * k ** -0.5).to(dtype)
     sw = ShuffledWeight(w.to(gpu_device))
     if side_splits > k // 32:
         with pytest.raises(ValueError, match="side_splits"):
@@ -146,7 +147,7 @@ def test_side_planes_and_main_columns(gpu_device, side_splits, shape, tokens):
     want = _oracle_linear(x.double().numpy(), w[main:].double().numpy(), None)
     got = side.sum().float().cpu().numpy()
     err = np.abs(got - want)
-    assert (err <= 2e-3 + REL[torch.bfloat16] * np.abs(want)).all(), f"max err {err.max():.3e}"
+    assert (err <= 2e-3 + REL[dtype] * np.abs(want)).all(), f"max err {err.max():.3e}"
 
 
 def test_side_bad_inputs_raise(gpu_device):
