@@ -15,8 +15,8 @@ Also reported: the Qwen3-8B decode-layer latency (1 row x 2048 tokens, 32/8
 heads, bf16), the per-layer LoRA delta time of 64 tokens over 4 adapters,
 end-to-end tok/s of a Qwen3-8B-shaped random-init decoder with rank-16
 no-merge LoRA under hipGraph replay (4 rows behind a 2048-token shared
-prefix; 1 row at 32768 tokens), and the CPU baseline (the float64 numpy
-oracle on a bounded sample of rows, one thread).
+prefix; 1 row at 32768 tokens), and the CPU baseline (the torch fp32 CPU
+path on every host core, on a bounded subset of the headline's rows).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
 """
@@ -54,7 +54,7 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    p.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU baseline sample budget")
     p.add_argument("--no-extra", action="store_true", help="headline workload only")
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Qwen3-8B-shaped decode legs")
     p.add_argument("--copy-calibration", action="store_true",
@@ -281,88 +281,110 @@ def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_step
     return out
 
 
+def _cpu_threads() -> int:
+    """Threads for the CPU baseline: every core this process may run on
+    (bounded by OMP_NUM_THREADS when the host sets it)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def _median_s(fn, warmup=2, runs=10):
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return float(np.median(ts))
+
+
 def cpu_baseline(w, budget_s):
-    """Time the float64 numpy oracle on whole rows of the workload until the
-    budget is spent; report algorithmic GB/s of the rows it finished."""
+    """The torch fp32 CPU path (oracle.torch_cpu) on the host's cores: paged
+    gather, fp32 upcast and softmax(q.K^T/sqrt(D)).V per row, over a bounded
+    subset of the workload's rows (as many, in row order, as fit ~budget_s
+    for 2 warm-ups + 10 timed runs); median of the 10 runs, algorithmic GB/s
+    of those rows."""
     import torch
 
     from oracle import paged_decode as opd
+    from oracle import torch_cpu as tc
 
-    q = w["q"].float().cpu().numpy()
-    indptr = w["indptr"].numpy()
-    last = w["last"].numpy()
-    order = list(range(len(last)))
-    done_bytes, spent, rows = 0, 0.0, 0
-    for b in order:
-        pages = w["indices"][indptr[b]: indptr[b + 1]].long()
-        sub = w["cache"][pages.to(w["cache"].device)].float().cpu().numpy()
-        n = len(pages)
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    cache = w["cache"].cpu()
+    q = w["q"].cpu()
+    indptr, indices, last = w["indptr"].numpy(), w["indices"].numpy(), w["last"].numpy()
+    # pick the row subset from one pass (which also warms the pages)
+    rows, spent = [], 0.0
+    for b in range(len(last)):
         t = time.perf_counter()
-        opd.paged_decode(q[b: b + 1], sub, [0, n], np.arange(n), [int(last[b])])
+        tc.paged_decode(q, cache, indptr, indices, last, rows=[b])
         spent += time.perf_counter() - t
-        done_bytes += opd.algorithmic_bytes([0, n], [int(last[b])], w["ps"], w["hq"], w["hkv"], w["d"], 2, 2)
-        rows += 1
-        if spent >= budget_s:
+        rows.append(b)
+        if spent >= budget_s / 12:
             break
+    sec = _median_s(lambda: tc.paged_decode(q, cache, indptr, indices, last, rows=rows))
+    sub_indptr = [0]
+    for b in rows:
+        sub_indptr.append(sub_indptr[-1] + int(indptr[b + 1] - indptr[b]))
+    nb = opd.algorithmic_bytes(sub_indptr, [int(last[b]) for b in rows], w["ps"], w["hq"], w["hkv"], w["d"], 2, 2)
     return {
-        "value": round(done_bytes / spent / 1e9, 3),
+        "value": round(nb / sec / 1e9, 3),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"float64 numpy oracle, {rows} of 64 rows of the same workload ({sum(w['lens'][:rows])} tokens), "
-                  f"{spent:.1f} s, host has {os.cpu_count()} cores",
+        "sample": f"torch fp32 CPU path (oracle/torch_cpu.py), {threads} threads (os.cpu_count() {os.cpu_count()}); "
+                  f"rows 0..{rows[-1]} of the 64 ({sum(w['lens'][b] for b in rows)} of {sum(w['lens'])} tokens), "
+                  f"median of 10 after 2 warm-ups: {sec * 1e3:.1f} ms per pass",
     }
 
 
 def cpu_small_configs():
-    """The float64 numpy oracle on the three small workloads (batch 4 x
-    512 tokens fp32, GQA 4; batch 1 x 2048 bf16, GQA 4; the LoRA
-    delta of 64 tokens over 4 adapters and 7 modules): algorithmic GB/s, the
-    median of 10 runs after 2 warm-ups, one thread."""
+    """The torch fp32 CPU path on the three small workloads (batch 4 x 512
+    tokens fp32, GQA 4; batch 1 x 2048 bf16, GQA 4; the LoRA delta of 64
+    tokens over 4 adapters and 7 modules): algorithmic GB/s, the median of
+    10 runs after 2 warm-ups, all threads."""
     import torch
 
-    from oracle import lora as olora
     from oracle import paged_decode as opd
+    from oracle import torch_cpu as tc
 
-    def median_s(fn):
-        for _ in range(2):
-            fn()
-        ts = []
-        for _ in range(10):
-            t = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - t)
-        return float(np.median(ts))
-
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
     res = {}
     for name, B, L, dtype, kvb, seed in (("b4_512_fp32_gqa4", 4, 512, torch.float32, 4, 1234),
                                          ("b1_2048_bf16_gqa4", 1, 2048, torch.bfloat16, 2, 1235)):
         ps, hq, hkv, d = 16, 32, 8, 128
         npg = L // ps
         gen = torch.Generator().manual_seed(seed)
-        # only the rows' own pages: the pool's other pages cost the oracle nothing
-        cache = torch.randn((B * npg, 2, ps, hkv, d), generator=gen).to(dtype).float().numpy()
-        q = torch.randn((B, hq, d), generator=gen).to(dtype).float().numpy()
-        indptr = np.arange(0, B * npg + 1, npg)
-        indices = np.arange(B * npg)
+        pool = 256 if B == 4 else 4096
+        cache = torch.randn((pool, 2, ps, hkv, d), generator=gen).to(dtype)
+        q = torch.randn((B, hq, d), generator=gen).to(dtype)
+        indices = torch.randperm(pool, generator=torch.Generator().manual_seed(seed))[: B * npg]
+        indptr = list(range(0, B * npg + 1, npg))
         last = [ps] * B
-        sec = median_s(lambda: opd.paged_decode(q, cache, indptr, indices, last))
+        sec = _median_s(lambda: tc.paged_decode(q, cache, indptr, indices, last))
         nb = opd.algorithmic_bytes(indptr, last, ps, hq, hkv, d, kvb, kvb)
-        res[name] = {"GBps": round(float(nb) / sec / 1e9, 4), "ms": round(sec * 1e3, 2), "algorithmic_bytes": int(nb)}
+        res[name] = {"GBps": round(float(nb) / sec / 1e9, 3), "ms": round(sec * 1e3, 3), "algorithmic_bytes": int(nb)}
     gen = torch.Generator().manual_seed(1237)
     T, H, I, r, n = 64, 4096, 12288, 16, 4
-    ids = torch.randint(0, n, (T,), generator=gen).tolist()
+    ids = torch.randint(0, n, (T,), generator=gen)
     mods, nb = [], 0
     for fin, fout in ((H, 4096), (H, 1024), (H, 1024), (H, 4096), (H, I), (H, I), (I, H)):
-        x = torch.randn((T, fin), generator=gen).to(torch.bfloat16).float().numpy()
-        A = (torch.randn((n, r, fin), generator=gen) / fin**0.5).to(torch.bfloat16).float().numpy()
-        Bm = (torch.randn((n, fout, r), generator=gen) * 0.01).to(torch.bfloat16).float().numpy()
+        x = torch.randn((T, fin), generator=gen).to(torch.bfloat16)
+        A = (torch.randn((n, r, fin), generator=gen) / fin**0.5).to(torch.bfloat16)
+        Bm = (torch.randn((n, fout, r), generator=gen) * 0.01).to(torch.bfloat16)
         mods.append((x, A, Bm))
-        nb += (A.size + Bm.size) * 2 + T * fout * 4 + x.size * 2
-    sec = median_s(lambda: [olora.multi_adapter_delta(x, ids, A, Bm, 2.0, intermediate="bf16") for x, A, Bm in mods])
-    res["lora_64tok_4adapters_7modules"] = {"GBps": round(float(nb) / sec / 1e9, 4), "ms": round(sec * 1e3, 2),
-                                                 "algorithmic_bytes": int(nb)}
-    res["note"] = "float64 numpy oracle, 1 thread; same algorithmic-byte definitions as the GPU legs"
+        nb += (A.numel() + Bm.numel()) * 2 + T * fout * 4 + x.numel() * 2
+    sec = _median_s(lambda: [tc.lora_delta(x, ids, A, Bm, 2.0, intermediate=torch.bfloat16) for x, A, Bm in mods])
+    res["lora_64tok_4adapters_7modules"] = {"GBps": round(float(nb) / sec / 1e9, 3), "ms": round(sec * 1e3, 3),
+                                            "algorithmic_bytes": int(nb)}
+    res["note"] = (f"torch fp32 CPU path (oracle/torch_cpu.py), {threads} threads, median of 10 after 2 warm-ups; "
+                   "same algorithmic-byte definitions as the GPU legs")
     return res
 
 

@@ -44,6 +44,17 @@ def round_to(a, dtype):
     raise ValueError(dtype)
 
 
+def linear(x, w):
+    """F.linear without bias: x W^T (the base projection and the LoRA shrink)."""
+    return _f64(x) @ _f64(w).T
+
+
+def up_projection(down, b, scale):
+    """The expand half of the delta: down B^T * scale (packed_ops.py:324-325,
+    multilora/linear.py:227-228), for the rank-space intermediate ``down``."""
+    return _f64(down) @ _f64(b).T * scale
+
+
 def lora_delta(x, a, b, scale, intermediate=None):
     """(x A^T) B^T * scale for x [T, in], A [r, in], B [out, r].
 
@@ -51,8 +62,8 @@ def lora_delta(x, a, b, scale, intermediate=None):
     reference's ``down = F.linear(x, A)`` returns it in the model dtype
     (packed_ops.py:324, 551; multilora/linear.py:227).
     """
-    down = round_to(_f64(x) @ _f64(a).T, intermediate)
-    return down @ _f64(b).T * scale
+    down = round_to(linear(x, a), intermediate)
+    return up_projection(down, b, scale)
 
 
 def lora_linear(x, w, bias, a, b, scale):

@@ -86,8 +86,13 @@ __global__ __launch_bounds__(kThreads) void skinny_linear_kernel(
   const T* xrow = x + (int64_t)(t_ok ? t : 0) * ldx;
 
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  int k = k_begin + kq;
-  for (; k + (kUnroll - 1) * 32 < k_end; k += kUnroll * 32) {
+  // Both loops step k0 uniformly over the wave (the MFMA needs every lane);
+  // lane group kq covers k0 + kq .. + 8.  The unrolled loop runs only while
+  // every group of every step is in range; in the tail a group past k_end
+  // loads zeros (K % 8 == 0, so a group is wholly in or out of range).
+  int k0 = k_begin;
+  for (; k0 + kUnroll * 32 <= k_end; k0 += kUnroll * 32) {
+    const int k = k0 + kq;
     u32x4 bw[kUnroll], ax[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
@@ -98,9 +103,11 @@ __global__ __launch_bounds__(kThreads) void skinny_linear_kernel(
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(ax[u], bw[u], acc);
   }
-  for (; k < k_end; k += 32) {  // K % 8 == 0: each lane's 8 elements are all in range
-    const u32x4 bw = n_ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + k)) : zero4();
-    const u32x4 ax = t_ok ? *reinterpret_cast<const u32x4*>(xrow + k) : zero4();
+  for (; k0 < k_end; k0 += 32) {
+    const int k = k0 + kq;
+    const bool k_ok = k < k_end;
+    const u32x4 bw = (n_ok & k_ok) ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + k)) : zero4();
+    const u32x4 ax = (t_ok & k_ok) ? *reinterpret_cast<const u32x4*>(xrow + k) : zero4();
     acc = mfma32<T>(ax, bw, acc);
   }
   // D rows = tokens 4*(lane/16)+i of the tile, column = lr

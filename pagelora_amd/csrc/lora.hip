@@ -147,11 +147,16 @@ __global__ __launch_bounds__(kShrinkThreads) void shrink_kernel(
       tok_ok[u] = ti < n_a;
       xrow[u] = x + (int64_t)(tok_ok[u] ? s_list[ti] : 0) * ldx;
     }
-    for (int k = k_begin + kq; k < k_end; k += 32) {
-      const uint4 bv = load8(arow + k, a_ok);  // in_features % 8 == 0: all 8 in range
+    // The k loop is uniform over the wave (every lane runs the same steps,
+    // as the MFMA needs); a lane whose 8-element group lies past k_end loads
+    // zeros.  in_features % 8 == 0, so a group is wholly in or out of range.
+    for (int k0 = k_begin; k0 < k_end; k0 += 32) {
+      const int k = k0 + kq;
+      const bool k_ok = k < k_end;
+      const uint4 bv = load8(arow + k, a_ok & k_ok);
 #pragma unroll
       for (int u = 0; u < kTilesPerPass; ++u) {
-        if (tt0 + u < n_tt) acc[u] = mfma32<T>(load8(xrow[u] + k, tok_ok[u]), bv, acc[u]);
+        if (tt0 + u < n_tt) acc[u] = mfma32<T>(load8(xrow[u] + k, tok_ok[u] & k_ok), bv, acc[u]);
       }
     }
     // D rows = tokens 4*(lane/16)+i of the tile, column = rank row lr.

@@ -210,6 +210,13 @@ DECODE_SIDE_SPLITS = {"o": 16, "down": 16}
 # (pl_decode_run_qkv) where it is built; False keeps the separate
 # head-norm/RoPE/append kernel (tests compare the two).
 FOLD_QKV_INTO_DECODE = True
+# Optional observer of a layer's stages, called eagerly as ``STAGE_TRACE(name,
+# value)`` with each stage's stored output (tensors, split planes) in
+# dataflow order: "hidden_in" (the residual stream on entry), "hidden" (after
+# the input add of the previous layer's down_proj output), "x", "qkv",
+# "attn", "o", "hidden_mid", "x2", "gate_up", "act", "down".  For checking a
+# decode step stage by stage; it must stay None while a graph is captured.
+STAGE_TRACE = None
 
 
 class SideOutput:
@@ -268,6 +275,9 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
     """
     h, qd, kd, I = cfg.hidden, cfg.q_dim, cfg.kv_dim, cfg.intermediate
     a = adapter
+    trace = STAGE_TRACE
+    if trace is not None:
+        trace("hidden_in", hidden)
     if pending is None:
         x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
     else:
@@ -275,6 +285,10 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
         x = fused_ops.add_rmsnorm(hidden, _cols(prev_out, h), lw.input_norm, cfg.rms_eps, lora=prev_up,
                                   adapter_ids=ids)
     qkv = _project(x, lw, "qkv")
+    if trace is not None:
+        trace("hidden", hidden)
+        trace("x", x)
+        trace("qkv", qkv)
     lora_qkv = (lw.up("q", qkv, scale, a), lw.up("k", qkv, scale, a), lw.up("v", qkv, scale, a))
     if qkv_attend is not None and not isinstance(qkv, SplitOutput):
         attn = qkv_attend(_cols(qkv, qd + 2 * kd), lora_qkv).view(qkv.shape[0], qd)
@@ -292,6 +306,10 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
     act = fused_ops.silu_mul(gu[:, : 2 * I], lora=(lw.up("gate", gu, scale, a), lw.up("up", gu, scale, a)),
                              adapter_ids=ids)
     d = _project(act, lw, "down")
+    if trace is not None:
+        for name, value in (("attn", attn), ("o", o), ("hidden_mid", hidden), ("x2", x2), ("gate_up", gu),
+                            ("act", act), ("down", d)):
+            trace(name, value)
     return d, lw.up("down", d, scale, a)
 
 

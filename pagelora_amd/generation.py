@@ -173,7 +173,8 @@ class BatchGenerator:
 
     @torch.no_grad()
     def generate(self, requests: list[Request], first_tokens: torch.Tensor, steps: int,
-                 adapters: list[int] | None = None, device_tables: bool = False) -> GenerateResult:
+                 adapters: list[int] | None = None, device_tables: bool = False,
+                 keep_logits: bool = False) -> GenerateResult:
         """Decode ``steps`` greedy tokens for rows whose prompts are prefilled.
 
         first_tokens: [B] int64 on the device, the token each row decodes
@@ -181,15 +182,18 @@ class BatchGenerator:
         ``device_tables`` the page table is uploaded once and then grown on
         the device inside the step (pl_page_table_advance); the host only
         refills the page reserve about once per page of steps.
+        ``keep_logits`` keeps every step's logits ([steps, B, vocab] on the
+        device, in ``extra["logits"]``).
         """
         if device_tables:
-            return self._generate_device_tables(requests, first_tokens, steps, adapters)
+            return self._generate_device_tables(requests, first_tokens, steps, adapters, keep_logits)
         B = len(requests)
         dev = self.pool.cache.device
         adapters = adapters or [0] * B
         uniform = self._uniform_adapter(adapters)
         history = torch.empty((steps, B), dtype=torch.int64, device=dev)
-        entry = None
+        entry = entry_key = None
+        kept = []
         ctx = DecodeContext(B, dev)
         ctx.uniform_adapter = uniform
         torch.cuda.synchronize(dev)
@@ -204,6 +208,7 @@ class BatchGenerator:
                     tc = time.perf_counter()
                     n_before = self.graphs.capture_count
                     entry = self.graphs.entry(B, uniform_adapter=uniform)
+                    entry_key = self.graphs.key(B, uniform_adapter=uniform)
                     if self.graphs.capture_count != n_before:
                         torch.cuda.synchronize(dev)
                         capture_s = time.perf_counter() - tc
@@ -215,16 +220,38 @@ class BatchGenerator:
             else:
                 self._stage_inputs(ctx, requests, adapters)
                 self._plan(requests)  # ctx.tokens holds the last pick (the step wrote it)
+                if entry is not None and self.graphs.key(B, uniform_adapter=uniform) != entry_key:
+                    # the plan moved the persistent page-table buffers (the
+                    # batch's page list outgrew them): the captured graph
+                    # reads the old ones, so take the graph of the new key
+                    tc = time.perf_counter()
+                    n_before = self.graphs.capture_count
+                    new = self.graphs.entry(B, uniform_adapter=uniform)
+                    if self.graphs.capture_count != n_before:
+                        torch.cuda.synchronize(dev)
+                        capture_s += time.perf_counter() - tc
+                    if new is None:  # capture failed: continue eagerly on the staged buffers
+                        entry = None
+                    else:
+                        for name in ("positions", "page_id", "page_offset", "adapter_ids", "tokens"):
+                            getattr(new.ctx, name).copy_(getattr(ctx, name))
+                        entry, ctx = new, new.ctx
+                    entry_key = self.graphs.key(B, uniform_adapter=uniform)
             if entry is not None:
-                self.graphs.replay(entry)
+                logits = self.graphs.replay(entry)
             else:
-                decode_step_static(self.weights, self.pool, self.backend, ctx)
+                logits = decode_step_static(self.weights, self.pool, self.backend, ctx)
             history[step].copy_(ctx.next_tokens)
+            if keep_logits:
+                kept.append(logits.clone())
         torch.cuda.synchronize(dev)
         dt = time.perf_counter() - t0 - capture_s
+        extra = {"capture_seconds": capture_s}
+        if keep_logits:
+            extra["logits"] = torch.stack(kept)
         return GenerateResult(tokens=history.t().cpu(), decode_seconds=dt, prefill_seconds=0.0, steps=steps,
                               batch=B, used_graph=entry is not None, graph_captures=self.graphs.capture_count,
-                              graph_replays=self.graphs.replay_count, extra={"capture_seconds": capture_s})
+                              graph_replays=self.graphs.replay_count, extra=extra)
 
 
     def _uniform_adapter(self, adapters) -> int:
@@ -232,7 +259,7 @@ class BatchGenerator:
         a = adapters[0] if adapters and all(x == adapters[0] for x in adapters) else -1
         return a if 0 <= a < self.weights.n_adapters else -1
 
-    def _generate_device_tables(self, requests, first_tokens, steps, adapters) -> GenerateResult:
+    def _generate_device_tables(self, requests, first_tokens, steps, adapters, keep_logits=False) -> GenerateResult:
         B = len(requests)
         dev = self.pool.cache.device
         adapters = adapters or [0] * B
@@ -262,21 +289,26 @@ class BatchGenerator:
             ctx.uniform_adapter = uniform
         ctx.adapter_ids.copy_(torch.tensor(adapters, dtype=torch.int32))
         ctx.tokens.copy_(first_tokens)
+        kept = []
         for step in range(steps):
             feeder.before_step(step)  # ctx.tokens holds the last pick (the step wrote it)
             if entry is not None:
-                self.graphs.replay(entry)
+                logits = self.graphs.replay(entry)
             else:
                 self.backend.advance_decode(reserve, ctx.positions, ctx.page_id, ctx.page_offset)
-                decode_step_static(self.weights, self.pool, self.backend, ctx)
+                logits = decode_step_static(self.weights, self.pool, self.backend, ctx)
             history[step].copy_(ctx.next_tokens)
+            if keep_logits:
+                kept.append(logits.clone())
         torch.cuda.synchronize(dev)
         dt = time.perf_counter() - t0 - capture_s
         reserve.check()
+        extra = {"capture_seconds": capture_s, "reserve_uploads": feeder.uploads}
+        if keep_logits:
+            extra["logits"] = torch.stack(kept)
         return GenerateResult(tokens=history.t().cpu(), decode_seconds=dt, prefill_seconds=0.0, steps=steps,
                               batch=B, used_graph=entry is not None, graph_captures=self.graphs.capture_count,
-                              graph_replays=self.graphs.replay_count,
-                              extra={"capture_seconds": capture_s, "reserve_uploads": feeder.uploads})
+                              graph_replays=self.graphs.replay_count, extra=extra)
 
 
 def prefill_requests(weights: DecoderWeights, pool: PagedKVPool, prompts: list[torch.Tensor],

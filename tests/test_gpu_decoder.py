@@ -346,3 +346,22 @@ def test_side_plane_projections_match_split_projections(gpu_device, monkeypatch)
     torch.cuda.synchronize()
     assert torch.allclose(ls, lp, atol=0.05, rtol=0.01), (ls - lp).abs().max()
     _assert_same_greedy(ts, lp, ls)
+
+
+def test_graph_follows_page_table_buffers_that_move(gpu_device):
+    """Host-packed tables in a small persistent buffer: the batch's page list
+    (10 pages at the start, 16-entry buffer) outgrows it mid-generation, the
+    plan moves the buffers, and generate() must switch to a graph captured on
+    the new ones.  Tokens equal the eager run's; two captures."""
+    steps = 48
+    w, pool, reqs, first, _ = _setup(gpu_device)
+    ref = BatchGenerator(w, pool, workspace_mb=8, use_graph=False).generate(reqs, first, steps, [0, 1, 1])
+    w, pool, reqs, first, _ = _setup(gpu_device)
+    gen = BatchGenerator(w, pool, workspace_mb=8, use_graph=True)
+    gen.backend.max_pages = 0  # start at the smallest pow2 capacity
+    start_pages = len(pool.tables(reqs)[1])
+    res = gen.generate(reqs, first, steps, [0, 1, 1])
+    end_pages = len(pool.tables(reqs)[1])
+    assert start_pages + 1 <= 16 < end_pages, (start_pages, end_pages)
+    assert res.used_graph and res.graph_captures == 2, res.graph_captures
+    assert torch.equal(res.tokens, ref.tokens)

@@ -29,7 +29,7 @@ def _check(got, want, dtype, atol):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("T", [1, 4, 16, 17, 64])
-@pytest.mark.parametrize("NK", [(6144, 4096), (4096, 12288), (1000, 256), (37, 64)])
+@pytest.mark.parametrize("NK", [(6144, 4096), (4096, 12288), (1000, 256), (37, 64), (48, 40), (200, 264)])
 def test_linear_matches_float64(gpu_device, dtype, T, NK):
     N, K = NK
     g = torch.Generator().manual_seed(N + K + T)
@@ -42,10 +42,12 @@ def test_linear_matches_float64(gpu_device, dtype, T, NK):
 
 
 @pytest.mark.parametrize("T", [1, 4, 16, 40])
-def test_fused_lora_expand_matches_oracle(gpu_device, T):
+@pytest.mark.parametrize("K", [512, 264])
+def test_fused_lora_expand_matches_oracle(gpu_device, T, K):
+    # K = 264: the k loops' last step holds only one 8-element group per row
     dtype = torch.bfloat16
-    g = torch.Generator().manual_seed(T)
-    K, outs, r, n = 512, (256, 64, 64), 16, 3
+    g = torch.Generator().manual_seed(T + K)
+    outs, r, n = (256, 64, 64), 16, 3
     N = sum(outs)
     x = torch.randn((T, K), generator=g).to(dtype)
     w = (torch.randn((N, K), generator=g) * 0.02).to(dtype)

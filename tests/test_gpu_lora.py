@@ -96,6 +96,31 @@ def test_negative_ids_untouched_and_rank_not_multiple_of_8(gpu_device):
         assert np.array_equal(got[neg], base.numpy()[neg])
 
 
+@pytest.mark.parametrize("fin", [40, 264, 1000])
+@pytest.mark.parametrize("T", [5, 64])
+def test_in_features_not_a_multiple_of_32(gpu_device, fin, T):
+    # the shrink's k loop runs the same 32-wide steps in every lane and
+    # zero-fills the groups past in_features (fin % 32 in {8, 8, 8})
+    gen = torch.Generator().manual_seed(fin + T)
+    n, r = 3, 16
+    ids = torch.randint(-1, n, (T,), generator=gen, dtype=torch.int32)
+    x = _rand((T, fin), 1.0, gen)
+    mods, host = [], []
+    for fout in (96, 40):
+        A = _rand((n, r, fin), fin ** -0.5, gen)
+        B = _rand((n, fout, r), 0.05, gen)
+        out = torch.zeros((T, fout), dtype=torch.float32, device=gpu_device)
+        mods.append((A.to(gpu_device), B.to(gpu_device), out, 2.0))
+        host.append((A, B))
+    lora_delta_(x.to(gpu_device), mods, ids.to(gpu_device))
+    torch.cuda.synchronize()
+    for (A, B), (_, _, out, _) in zip(host, mods):
+        want = ol.multi_adapter_delta(x.float().numpy(), ids.tolist(), A.float().numpy(), B.float().numpy(), 2.0,
+                                      intermediate="bf16")
+        err = np.abs(out.cpu().numpy() - want)
+        assert err.max() <= 2e-3, f"fin {fin}: max err {err.max():.3e}"
+
+
 def test_packed_group_equals_separate_calls(gpu_device):
     gen = torch.Generator().manual_seed(5)
     T, fin = 7, 256
