@@ -4,7 +4,8 @@
  * Every entry point is stream ordered: it enqueues work on `stream` (a
  * hipStream_t passed as void*, NULL = the legacy default stream) and returns
  * without synchronising.  None of them allocates device memory: scratch space
- * is the caller's `workspace`.  Return value: PL_OK (0) or a pl_status code;
+ * is the caller's `workspace` (pl_decode_noalloc: a fixed array the library
+ * holds per device).  Return value: PL_OK (0) or a pl_status code;
  * pl_last_error() then holds a message for the calling thread.
  *
  * Pointers are device pointers unless a parameter name ends in `_h` (host).
@@ -117,6 +118,36 @@ int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * other work or timing events between them. */
 #define PL_DECODE_SKIP_MERGE 1
 #define PL_DECODE_MERGE_ONLY 2
+
+/*
+ * Plan + run of one decode step with no caller workspace and no allocation:
+ * pl_decode_plan(indptr, ...) followed by pl_decode_run(..., flags 0), with
+ * the work list and split partials in a fixed scratch array the library
+ * holds on each device (PL_DECODE_NOALLOC_MAX_BYTES; every GPU the library
+ * runs on keeps its copy until the process ends).  Arguments are those of
+ * the two calls.  A plan that needs more scratch than the maximum
+ * (pl_decode_workspace_size(batch, target_items, num_qo_heads, head_dim))
+ * is rejected with PL_ERR_WORKSPACE before any HIP call.  `stream` must
+ * belong to the current device.  Every call on a GPU shares that GPU's
+ * scratch and re-plans into it, so calls that overlap on one GPU (other
+ * streams, other threads) race; calls ordered on one stream do not.
+ *
+ * No counterpart in the reference.  It is for callers that cannot allocate:
+ * code under hipGraph capture, tight serving loops, and harnesses that
+ * forbid hipMalloc.
+ */
+#define PL_DECODE_NOALLOC_MAX_BYTES ((size_t)16 << 20)
+int pl_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                      const void* k_cache, const void* v_cache,
+                      int64_t page_stride, int64_t token_stride,
+                      int64_t head_stride, int64_t num_pages,
+                      const int32_t* indptr, int indices_capacity,
+                      const int32_t* indices, const int32_t* last_page_len,
+                      void* o, int64_t o_stride_b, int64_t o_stride_h,
+                      float* lse, int batch, int num_qo_heads,
+                      int num_kv_heads, int head_dim, int page_size,
+                      float sm_scale, int dtype, int target_items,
+                      int min_chunk_pages, void* stream);
 
 /*
  * Write one decode token per row into its page:

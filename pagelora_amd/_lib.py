@@ -26,6 +26,7 @@ PL_LORA_MAX_MODULES = 4
 
 PL_DECODE_SKIP_MERGE = 1
 PL_DECODE_MERGE_ONLY = 2
+PL_DECODE_NOALLOC_MAX_BYTES = 16 << 20
 
 
 class ExtensionNotBuiltError(ImportError):
@@ -122,6 +123,21 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _i32, _i32, _i32, _i32, _i32,  # batch, hq, hkv, head_dim, page_size
             _f32, _i32, _i32, _i32,      # sm_scale, dtype, target_items, flags
             _vp, _sz, _vp,               # workspace, bytes, stream
+        ],
+    ),
+    "pl_decode_noalloc": (
+        _i32,
+        [
+            _vp, _i64, _i64,            # q, strides
+            _vp, _vp, _i64, _i64, _i64,  # k/v cache, page/token/head strides
+            _i64,                        # num_pages
+            _vp, _i32,                   # indptr, indices_capacity
+            _vp, _vp,                    # indices, last_page_len
+            _vp, _i64, _i64,             # o, strides
+            _vp,                         # lse
+            _i32, _i32, _i32, _i32, _i32,  # batch, hq, hkv, head_dim, page_size
+            _f32, _i32, _i32, _i32,      # sm_scale, dtype, target_items, min_chunk_pages
+            _vp,                         # stream
         ],
     ),
     "pl_kv_append": (

@@ -1393,3 +1393,80 @@ extern "C" int pl_decode_run_qkv(const void* qkv, int64_t ld_qkv, const pl_lora_
                            head_dim, page_size, sm_scale, dtype, target_items, flags, workspace, workspace_bytes,
                            stream, &qin, rank);
 }
+
+// ------------------------------------------------- allocation-free entry ---
+// pl_decode_noalloc keeps its work list and partials in this file-scope
+// device array instead of a caller workspace.  Each GPU the library runs on
+// holds its own copy for the life of the process.  In host code `scratch`
+// names a host-side stand-in, never the device memory: its device address
+// comes from hipGetSymbolAddress, once per device with that device current,
+// and only that address is handed to kernels.
+constexpr size_t kNoAllocScratchBytes = PL_DECODE_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+#include <mutex>
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch`, per device id
+}  // namespace
+
+// The device address of `scratch` on the current device (looked up on the
+// first call on that device).  `stream` must belong to the current device.
+static int scratch_of_current_device(void* stream, void** out) {
+  int dev = -1;
+  PL_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(PL_ERR_UNSUPPORTED, "device %d: the allocation-free entry serves devices 0..%d", dev,
+                kMaxScratchDevices - 1);
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    PL_HIP_CHECK(hipStreamGetDevice((hipStream_t)stream, &sdev));
+    if ((int)sdev != dev)
+      return fail(PL_ERR_INVALID, "the stream belongs to device %d but device %d is current", (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(PL_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PL_OK;
+}
+
+extern "C" int pl_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                                 const void* v_cache, int64_t page_stride, int64_t token_stride,
+                                 int64_t head_stride, int64_t num_pages, const int32_t* indptr,
+                                 int indices_capacity, const int32_t* indices, const int32_t* last_page_len,
+                                 void* o, int64_t o_stride_b, int64_t o_stride_h, float* lse, int batch,
+                                 int num_qo_heads, int num_kv_heads, int head_dim, int page_size, float sm_scale,
+                                 int dtype, int target_items, int min_chunk_pages, void* stream) {
+  if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0 (got %d)", batch);
+  if (target_items <= 0) return fail(PL_ERR_INVALID, "target_items must be > 0");
+  if (num_qo_heads <= 0 || head_dim <= 0) return fail(PL_ERR_INVALID, "bad head shape");
+  if (batch == 0) return ok();
+  // Host-side size check first: a plan that does not fit is rejected
+  // before any HIP call.
+  const size_t need = layout(batch, target_items + batch, num_qo_heads, head_dim).total;
+  if (need > kNoAllocScratchBytes)
+    return fail(PL_ERR_WORKSPACE,
+                "decode plan of %d rows x %d items x %d heads x dim %d needs %zu bytes of scratch, more than the "
+                "%zu-byte maximum of pl_decode_noalloc (use pl_decode_plan + pl_decode_run with a workspace)",
+                batch, target_items, num_qo_heads, head_dim, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (const int st = scratch_of_current_device(stream, &ws)) return st;
+  // The plan rewrites the header, the whole work list and the row table on
+  // every call, and the run reads only what this call's plan and decode
+  // kernels wrote, so nothing needs clearing between calls.
+  if (const int st = pl_decode_plan(indptr, batch, indices_capacity, num_qo_heads, head_dim, target_items,
+                                    min_chunk_pages, ws, kNoAllocScratchBytes, stream))
+    return st;
+  return pl_decode_run(q, q_stride_b, q_stride_h, k_cache, v_cache, page_stride, token_stride, head_stride,
+                       num_pages, indices, last_page_len, o, o_stride_b, o_stride_h, lse, batch, num_qo_heads,
+                       num_kv_heads, head_dim, page_size, sm_scale, dtype, target_items, 0, ws,
+                       kNoAllocScratchBytes, stream);
+}
