@@ -465,12 +465,16 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_append_kernel(
       hi[j] = i < kPairs ? to_float<T>(src[i + kPairs]) : 0.f;
     }
   }
-  // norm weights: loaded unconditionally (from the row itself when the head
-  // has none) and blended in with bit operations, so the loads are not moved
-  // under a branch behind the sum of squares
+  // norm weights: loaded unconditionally (from the head's own input when the
+  // head has none) and blended in with bit operations, so the loads are not
+  // moved under a branch behind the sum of squares.  That fallback must be
+  // readable memory of at least D elements: the head's T row, or with split-K
+  // input (no T row exists; qkv is then only a placeholder) the head's fp32
+  // values in plane 0, whose D floats hold 2D T-sized elements.
   const T* nw = is_q ? q_norm_w : (is_k ? k_norm_w : nullptr);
   const bool do_norm = nw != nullptr;
-  const T* nwp = do_norm ? nw : src;
+  const T* own = SPLIT ? reinterpret_cast<const T*>(xs.p + (int64_t)b * xs.ld + (int64_t)h * D) : src;
+  const T* nwp = do_norm ? nw : own;
   const uint32_t keep = do_norm ? 0xffffffffu : 0u;
   float wlo[kPPL], whi[kPPL];
 #pragma unroll
@@ -941,7 +945,9 @@ static int qkr_common(const void* qkv, int64_t ld_qkv, const void* q_norm_weight
   SplitIn xs{nullptr, 0, 0, 0};
   if (qkv_split) {
     if (const int st = split_from(qkv_split, row_cols, &xs, "qkv input")) return st;
-    qkv = inv_freq;  // unused: the row comes from the partial planes
+    // The row comes from the partial planes: the kernel never dereferences
+    // qkv in this mode (it must only be non-null for the checks below).
+    qkv = inv_freq;
     ld_qkv = row_cols;
   }
   if (!qkv || !positions || !page_id || !offset || !q_out || !k_cache || !v_cache || !inv_freq)

@@ -8,7 +8,9 @@ argmax (cuda_graph.py:222-234, 475-493); a capture failure disables graphs
 and the caller falls back to eager (cuda_graph.py:204-210, 420-426).
 
 The key (``DecodeGraphKey``, cuda_graph.py:76-93) differs on purpose: it has
-no ``page_table_pages`` and no host plan.  The decode plan lives on the
+no ``page_table_pages`` and no host plan, and its adapter version changes
+only when the adapter stacks move (``DecoderWeights.adapter_version``):
+writing new adapter values into a slot keeps every address a graph reads.  The decode plan lives on the
 device and the KV pool never moves, so a graph captured for a batch size
 replays for every later step while the rows grow; the reference recaptures
 on every new page.  torch's CUDAGraph is hipGraph on ROCm.
@@ -57,7 +59,6 @@ class BatchDecodeGraphRunner:
         self.pool = pool
         self.backend = backend
         self.max_entries = max_entries
-        self.adapter_version = 0
         self.disabled_reason: str | None = None
         self.capture_count = 0
         self.replay_count = 0
@@ -74,7 +75,7 @@ class BatchDecodeGraphRunner:
             cache_shape=tuple(cache.shape),
             cache_dtype=cache.dtype,
             batch=batch,
-            adapter_version=self.adapter_version,
+            adapter_version=self.weights.adapter_version,
             reserve_ptrs=ptrs,
             uniform_adapter=uniform_adapter,
         )
@@ -134,6 +135,11 @@ class BatchDecodeGraphRunner:
             if gc_was_enabled:
                 gc.enable()
         return DecodeGraphEntry(graph=graph, ctx=ctx, logits=logits)
+
+    @property
+    def adapter_version(self) -> int:
+        """The weights' adapter-layout version the graph keys carry."""
+        return self.weights.adapter_version
 
     def replay(self, entry: DecodeGraphEntry) -> torch.Tensor:
         entry.graph.replay()

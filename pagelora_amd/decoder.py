@@ -66,6 +66,92 @@ class DecoderConfig:
 QWEN3_8B = DecoderConfig()
 
 
+# Module names of the reference's adapters (HF leaf names of the wrapped
+# nn.Linear, multilora/runtime.py:95-116) -> the decoder's short names.
+MODULE_ALIASES = {"q_proj": "q", "k_proj": "k", "v_proj": "v", "o_proj": "o", "gate_proj": "gate",
+                  "up_proj": "up", "down_proj": "down"}
+MODULES = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+def projections(cfg: DecoderConfig):
+    """(projection, in_features, ((module, out_features), ...)) in the packed
+    order of the reference (q/k/v and gate/up share one input:
+    packed_ops.py:105-203)."""
+    h, qd, kd, i = cfg.hidden, cfg.q_dim, cfg.kv_dim, cfg.intermediate
+    return (("qkv", h, (("q", qd), ("k", kd), ("v", kd))), ("o", qd, (("o", h),)),
+            ("gate_up", h, (("gate", i), ("up", i))), ("down", i, (("down", h),)))
+
+
+def module_key(name: str) -> str:
+    """The decoder's name of a module given as "q", "q_proj" or "self_attn.q_proj"."""
+    leaf = name.rsplit(".", 1)[-1]
+    leaf = MODULE_ALIASES.get(leaf, leaf)
+    if leaf not in MODULES:
+        raise KeyError(f"unknown LoRA module {name!r} (known: {', '.join(MODULES)} or their *_proj names)")
+    return leaf
+
+
+class _RandomSource:
+    """Seeded random weights (N(0, 0.02) base, norms 1 +- 0.1, LoRA A with
+    std in^-1/2 and B with std 0.01, so the delta is not a no-op)."""
+
+    def __init__(self, device, dtype, gen: torch.Generator) -> None:
+        self.device, self.dtype, self.gen = device, dtype, gen
+
+    def _w(self, shape, std):
+        return (torch.randn(shape, device=self.device, dtype=torch.float32, generator=self.gen) * std).to(self.dtype)
+
+    def norm(self, name, n):
+        return (1.0 + 0.1 * torch.randn(n, device=self.device, generator=self.gen)).to(self.dtype)
+
+    def base(self, proj, modules, shape):
+        return self._w(shape, 0.02)
+
+    def lora_a(self, name, shape):
+        return self._w(shape, shape[-1] ** -0.5)
+
+    def lora_b(self, name, shape):
+        return self._w(shape, 0.01)
+
+
+class _TensorSource:
+    """Given weights: ``layer`` maps "input_norm", "post_norm", "q_norm",
+    "k_norm" and the module names to tensors ([out, in] for the modules);
+    ``adapters[slot]`` maps module names to (A [r, in], B [out, r]) or is
+    None.  A module an adapter leaves out gets a zero delta (A = B = 0)."""
+
+    def __init__(self, layer: dict, adapters, device, dtype) -> None:
+        self.layer = {(module_key(k) if k.rsplit(".", 1)[-1] in MODULE_ALIASES or k in MODULES else k): v
+                      for k, v in layer.items()}
+        self.adapters = [None if a is None else {module_key(k): v for k, v in a.items()} for a in adapters]
+        self.device, self.dtype = device, dtype
+
+    def _t(self, t, shape, what):
+        t = torch.as_tensor(t)
+        if tuple(t.shape) != tuple(shape):
+            raise ValueError(f"{what}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
+        return t.to(device=self.device, dtype=self.dtype)
+
+    def norm(self, name, n):
+        return self._t(self.layer[name], (n,), name)
+
+    def base(self, proj, modules, shape):
+        return torch.cat([self._t(self.layer[m], (out, shape[1]), m) for m, out in modules])
+
+    def _lora(self, name, shape, j, what):
+        out = torch.zeros(shape, device=self.device, dtype=self.dtype)
+        for slot, ad in enumerate(self.adapters):
+            if ad is not None and name in ad:
+                out[slot] = self._t(ad[name][j], shape[1:], f"adapter {slot} {name} {what}")
+        return out
+
+    def lora_a(self, name, shape):
+        return self._lora(name, shape, 0, "A")
+
+    def lora_b(self, name, shape):
+        return self._lora(name, shape, 1, "B")
+
+
 class LayerWeights:
     """One decoder layer: packed base weights plus stacked LoRA adapters.
 
@@ -78,42 +164,34 @@ class LayerWeights:
     every adapter's rank-space intermediate.  ``w_*`` and the A of
     ``lora[name] = (A [n, r, in], B [n, out, r])`` are views into those
     buffers; ``y_offset[name]`` is the first intermediate column of a module
-    in its projection's output.
+    in its projection's output.  Adapter slot ``a`` of module m is
+    ``lora[m][0][a]`` / ``lora[m][1][a]``.
     """
 
-    def __init__(self, cfg: DecoderConfig, n_adapters: int, device, dtype, gen: torch.Generator) -> None:
-        h, qd, kd, i, r = cfg.hidden, cfg.q_dim, cfg.kv_dim, cfg.intermediate, cfg.lora_rank
+    def __init__(self, cfg: DecoderConfig, n_adapters: int, device, dtype, gen: torch.Generator | None = None,
+                 source=None) -> None:
+        h, r = cfg.hidden, cfg.lora_rank
         n = n_adapters
-
-        def w(shape, std):
-            return (torch.randn(shape, device=device, dtype=torch.float32, generator=gen) * std).to(dtype)
-
-        self.input_norm = (1.0 + 0.1 * torch.randn(h, device=device, generator=gen)).to(dtype)
-        self.post_norm = (1.0 + 0.1 * torch.randn(h, device=device, generator=gen)).to(dtype)
-        self.q_norm = (1.0 + 0.1 * torch.randn(cfg.head_dim, device=device, generator=gen)).to(dtype)
-        self.k_norm = (1.0 + 0.1 * torch.randn(cfg.head_dim, device=device, generator=gen)).to(dtype)
+        src = source if source is not None else _RandomSource(device, dtype, gen)
+        self.cfg, self.n_adapters, self.device, self.dtype = cfg, n, device, dtype
+        self.input_norm = src.norm("input_norm", h)
+        self.post_norm = src.norm("post_norm", h)
+        self.q_norm = src.norm("q_norm", cfg.head_dim)
+        self.k_norm = src.norm("k_norm", cfg.head_dim)
         self.lora = {}
         self.y_offset = {}
-
-        def projection(out_features, fin, modules):
+        for proj, fin, modules in projections(cfg):
+            out_features = sum(o for _, o in modules)
             ext = torch.empty((out_features + len(modules) * n * r, fin), device=device, dtype=dtype)
-            ext[:out_features] = w((out_features, fin), 0.02)
+            ext[:out_features] = src.base(proj, modules, (out_features, fin))
             for j, (name, fout) in enumerate(modules):
                 row = out_features + j * n * r
                 A = ext[row:row + n * r].view(n, r, fin)
-                A.copy_(w((n, r, fin), fin ** -0.5))
-                self.lora[name] = (A, w((n, fout, r), 0.01))
+                A.copy_(src.lora_a(name, (n, r, fin)))
+                self.lora[name] = (A, src.lora_b(name, (n, fout, r)))
                 self.y_offset[name] = row
-            return ext
-
-        self.w_qkv_ext = projection(qd + 2 * kd, h, (("q", qd), ("k", kd), ("v", kd)))
-        self.w_o_ext = projection(h, qd, (("o", h),))
-        self.w_gate_up_ext = projection(2 * i, h, (("gate", i), ("up", i)))
-        self.w_down_ext = projection(h, i, (("down", h),))
-        self.w_qkv = self.w_qkv_ext[: qd + 2 * kd]
-        self.w_o = self.w_o_ext[:h]
-        self.w_gate_up = self.w_gate_up_ext[: 2 * i]
-        self.w_down = self.w_down_ext[:h]
+            setattr(self, f"w_{proj}_ext", ext)
+            setattr(self, f"w_{proj}", ext[:out_features])
         self.shuffled: dict[str, ShuffledWeight] = {}
         self.lora_b8: dict[str, torch.Tensor] = {}
 
@@ -133,6 +211,60 @@ class LayerWeights:
             if name in self.lora:
                 self.lora_b8[name] = fused_ops.lora_b_chunk8(self.lora[name][1])
 
+    def write_adapter(self, slot: int, modules: dict) -> None:
+        """Write one adapter's A/B into ``slot`` in place (every copy: the A
+        rows under W, their 16-row blocks of the shuffled weight, B and its
+        chunked copy); a module left out gets a zero delta.  Stream ordered:
+        decode steps enqueued later read the new values through the same
+        addresses, so captured graphs stay valid."""
+        if not 0 <= slot < self.n_adapters:
+            raise ValueError(f"adapter slot {slot} outside 0..{self.n_adapters - 1}")
+        r = self.cfg.lora_rank
+        given = {module_key(k): v for k, v in modules.items()}
+        for proj, fin, mods in projections(self.cfg):
+            ext = getattr(self, f"w_{proj}_ext")
+            for name, fout in mods:
+                A_stack, B_stack = self.lora[name]
+                if name in given:
+                    A, B = given[name]
+                    A = torch.as_tensor(A)
+                    B = torch.as_tensor(B)
+                    if tuple(A.shape) != (r, fin) or tuple(B.shape) != (fout, r):
+                        raise ValueError(f"{name}: A must be [{r}, {fin}] and B [{fout}, {r}], got "
+                                         f"{tuple(A.shape)} / {tuple(B.shape)}")
+                    A_stack[slot].copy_(A)
+                    B_stack[slot].copy_(B)
+                else:
+                    A_stack[slot].zero_()
+                    B_stack[slot].zero_()
+                lo = self.y_offset[name] + slot * r
+                if proj in self.shuffled:
+                    self.shuffled[proj].refresh_rows(ext, lo, lo + r)
+                if name in self.lora_b8:
+                    self.lora_b8[name][slot].copy_(fused_ops.lora_b_chunk8(B_stack[slot])[0])
+
+    def grown(self, n_adapters: int) -> "LayerWeights":
+        """A copy of this layer with ``n_adapters`` slots (the new ones zero):
+        new buffers, so graphs captured on the old ones must be recaptured."""
+        if n_adapters < self.n_adapters:
+            raise ValueError("adapter stacks only grow")
+        old = self
+        given = {"input_norm": old.input_norm, "post_norm": old.post_norm, "q_norm": old.q_norm,
+                 "k_norm": old.k_norm}
+        for proj, fin, mods in projections(self.cfg):
+            w = getattr(old, f"w_{proj}")
+            row = 0
+            for name, fout in mods:
+                given[name] = w[row:row + fout]
+                row += fout
+        adapters = [{name: (old.lora[name][0][a], old.lora[name][1][a]) for name in MODULES}
+                    for a in range(old.n_adapters)] + [None] * (n_adapters - old.n_adapters)
+        new = LayerWeights(self.cfg, n_adapters, self.device, self.dtype,
+                           source=_TensorSource(given, adapters, self.device, self.dtype))
+        if old.shuffled:
+            new.shuffle()
+        return new
+
     def up(self, name: str, y: "torch.Tensor | SideOutput", scale: float, adapter: int = -1) -> fused_ops.LoraUp:
         """The up-projection of module ``name`` reading its intermediate from ``y``
         (``adapter`` >= 0: that one adapter for every token)."""
@@ -144,25 +276,90 @@ class LayerWeights:
 
 
 class DecoderWeights:
-    """Random weights of the decoder.  ``shuffle`` (default) also builds the
-    shuffled decode-GEMM copies of every projection and of the lm_head."""
+    """Weights of the decoder: random (``DecoderWeights(cfg, seed=...)``) or
+    given (:meth:`from_tensors`).  ``shuffle`` (default) also builds the
+    shuffled decode-GEMM copies of every projection and of the lm_head.
+
+    ``adapter_version`` changes whenever the adapter stacks are reallocated
+    (:meth:`set_adapter` past the stacked slots); decode graphs key on it, as
+    the reference's captured graphs key on ``flashinfer_graph_version``
+    (multilora/runtime.py:371-375).  Writing an adapter into an existing slot
+    keeps every buffer address and needs no recapture."""
 
     def __init__(self, cfg: DecoderConfig, *, n_adapters: int = 1, device="cuda", dtype=torch.bfloat16, seed: int = 0,
-                 shuffle: bool = True):
-        gen = torch.Generator(device=device).manual_seed(seed)
+                 shuffle: bool = True, _sources=None, _top=None):
         self.cfg = cfg
         self.dtype = dtype
         self.n_adapters = n_adapters
-        self.embed = (torch.randn((cfg.vocab, cfg.hidden), device=device, generator=gen) * 0.02).to(dtype)
-        self.final_norm = (1.0 + 0.1 * torch.randn(cfg.hidden, device=device, generator=gen)).to(dtype)
-        self.lm_head = (torch.randn((cfg.vocab, cfg.hidden), device=device, generator=gen) * 0.02).to(dtype)
-        self.layers = [LayerWeights(cfg, n_adapters, device, dtype, gen) for _ in range(cfg.num_layers)]
+        self.adapter_version = 0
+        if _top is None:
+            gen = torch.Generator(device=device).manual_seed(seed)
+            self.embed = (torch.randn((cfg.vocab, cfg.hidden), device=device, generator=gen) * 0.02).to(dtype)
+            self.final_norm = (1.0 + 0.1 * torch.randn(cfg.hidden, device=device, generator=gen)).to(dtype)
+            self.lm_head = (torch.randn((cfg.vocab, cfg.hidden), device=device, generator=gen) * 0.02).to(dtype)
+            self.layers = [LayerWeights(cfg, n_adapters, device, dtype, gen) for _ in range(cfg.num_layers)]
+        else:
+            self.embed, self.final_norm, self.lm_head = _top
+            self.layers = [LayerWeights(cfg, n_adapters, device, dtype, source=src) for src in _sources]
         self.lora_scale = cfg.lora_alpha / cfg.lora_rank  # linear.py:41, 71
         self.lm_head_shuffled: ShuffledWeight | None = None
         if shuffle:
             for lw in self.layers:
                 lw.shuffle()
             self.lm_head_shuffled = ShuffledWeight(self.lm_head)
+
+    @classmethod
+    def from_tensors(cls, cfg: DecoderConfig, *, embed: torch.Tensor, final_norm: torch.Tensor,
+                     lm_head: torch.Tensor, layers: list[dict], adapters: list | None = None,
+                     n_adapters: int | None = None, device="cuda", dtype=torch.bfloat16,
+                     shuffle: bool = True) -> "DecoderWeights":
+        """Weights from given tensors.
+
+        ``layers[l]`` maps "input_norm", "post_norm", "q_norm", "k_norm" and
+        the seven module names ("q".."down", or "q_proj".."down_proj") to
+        tensors, module weights as [out, in] (nn.Linear's layout).
+        ``adapters[slot]`` is None or a mapping ``{(layer, module): (A [r, in],
+        B [out, r])}``, the reference's serve-registry layout
+        (multilora/runtime.py:257-292); its modules get the delta
+        ``alpha / r * B . (A . x)`` (linear.py:41, 226-231), the modules it
+        leaves out none.
+        """
+        adapters = list(adapters or [])
+        n = max(1, len(adapters), n_adapters or 0)
+        adapters += [None] * (n - len(adapters))
+        if len(layers) != cfg.num_layers:
+            raise ValueError(f"{len(layers)} layers given for a {cfg.num_layers}-layer config")
+        per_layer = []
+        for li in range(cfg.num_layers):
+            per_layer.append([None if a is None else {m: ab for (l, m), ab in a.items() if l == li}
+                              for a in adapters])
+        dev = torch.device(device)
+
+        def t(x, shape, what):
+            x = torch.as_tensor(x)
+            if tuple(x.shape) != shape:
+                raise ValueError(f"{what}: expected shape {shape}, got {tuple(x.shape)}")
+            return x.to(device=dev, dtype=dtype)
+
+        top = (t(embed, (cfg.vocab, cfg.hidden), "embed"), t(final_norm, (cfg.hidden,), "final_norm"),
+               t(lm_head, (cfg.vocab, cfg.hidden), "lm_head"))
+        sources = [_TensorSource(layers[li], per_layer[li], dev, dtype) for li in range(cfg.num_layers)]
+        return cls(cfg, n_adapters=n, device=dev, dtype=dtype, shuffle=shuffle, _sources=sources, _top=top)
+
+    def set_adapter(self, slot: int, adapter: dict | None) -> None:
+        """Write ``adapter`` ({(layer, module): (A, B)}, or None for a zero
+        delta) into ``slot``: in place when the slot exists (stream ordered;
+        captured graphs stay valid), else the stacks grow to ``slot + 1``
+        slots (new buffers: ``adapter_version`` changes)."""
+        if slot < 0:
+            raise ValueError("adapter slot must be >= 0")
+        if slot >= self.n_adapters:
+            self.layers = [lw.grown(slot + 1) for lw in self.layers]
+            self.n_adapters = slot + 1
+            self.adapter_version += 1
+        adapter = adapter or {}
+        for li, lw in enumerate(self.layers):
+            lw.write_adapter(slot, {m: ab for (l, m), ab in adapter.items() if l == li})
 
 
 # ------------------------------------------------------- decode (static) ---

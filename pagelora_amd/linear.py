@@ -37,6 +37,24 @@ class ShuffledWeight:
     def nbytes(self) -> int:
         return self.data.numel() * self.data.element_size()
 
+    def refresh_rows(self, weight: torch.Tensor, lo: int, hi: int) -> None:
+        """Re-shuffle rows ``lo .. hi`` of the row-major ``weight`` this copy
+        was made from (after they changed in place): the 16-row blocks that
+        hold them are rewritten, nothing else."""
+        if weight.shape != (self.out_features, self.in_features) or weight.dtype != self.dtype:
+            raise ValueError("weight must be the [out, in] tensor this copy was shuffled from")
+        if not 0 <= lo < hi <= self.out_features:
+            raise ValueError(f"rows {lo}..{hi} outside 0..{self.out_features}")
+        lo16, hi16 = lo // 16 * 16, min(-(-hi // 16) * 16, self.out_features)
+        lib = _lib.load()
+        k, es = self.in_features, weight.element_size()
+        nbytes = lib.pl_weight_shuffled_bytes(hi16 - lo16, k)
+        # row block nb starts at element nb * 16 * K of the shuffled copy
+        _lib.check(lib.pl_weight_shuffle(weight.data_ptr() + lo16 * weight.stride(0) * es, weight.stride(0),
+                                         hi16 - lo16, k, self.data.data_ptr() + lo16 * k * es, nbytes,
+                                         _lib.dtype_code(weight.dtype), _lib.stream_handle(weight.device)),
+                   "pl_weight_shuffle")
+
 
 def linear_shuffled(x: torch.Tensor, weight: ShuffledWeight, bias: torch.Tensor | None = None,
                     out: torch.Tensor | None = None) -> torch.Tensor:
