@@ -93,8 +93,10 @@ int pl_decode_plan(const int32_t* indptr, int batch, int indices_capacity,
  * log-sum-exp of the scaled scores, [batch, num_qo_heads] fp32.
  * q, caches and o share `dtype`; accumulation is fp32.
  * Requires a pl_decode_plan on the same workspace earlier on the stream.
- * head_dim: 64, 128 or 256.  num_qo_heads / num_kv_heads: 1..8.
- * page_size: a multiple of 16.
+ * head_dim: 64, 128 or 256.  num_qo_heads / num_kv_heads: any positive
+ * integer (groups above 8 run as several waves of at most 8 query heads per
+ * kv head).  page_size: 1..65536; pages of a multiple of 16 tokens take the
+ * scalar-addressed path, other sizes a per-lane page lookup.
  *
  * Replaces FlashInferAttentionBackend.run_decode / _call_run
  * (model/flashinfer/attention_backend.py:120-131, 287-292), i.e.

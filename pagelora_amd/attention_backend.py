@@ -129,12 +129,16 @@ class PagedDecodeAttention:
             raise ValueError("Q head count must be divisible by KV head count")
         self.query_rescale = 1.0
         self.sm_scale = 1.0 / math.sqrt(self.head_dim)
-        # One code path for every GQA ratio 1..8 (the reference switches to
-        # FlashInfer's tensor-core kernel for ratios outside {1,2,4,8}).
+        # One code path for every GQA ratio (the reference switches to
+        # FlashInfer's tensor-core kernel for ratios outside {1,2,4,8}); groups
+        # above 8 run as several waves of at most 8 query heads per kv head.
         self.decode_use_tensor_cores = False
         self.use_flashinfer_qk_norm = False
         self.target_waves = int(target_waves) if target_waves else None  # None: default_target_items(...)
-        self.min_chunk_pages = int(min_chunk_pages or _DEFAULT_MIN_CHUNK_PAGES)
+        # the minimum split chunk is 64 tokens (4 pages of 16) whatever the page size
+        default_chunk = _DEFAULT_MIN_CHUNK_PAGES if self.page_size >= 16 else \
+            -(-_DEFAULT_MIN_CHUNK_PAGES * 16 // max(1, self.page_size))
+        self.min_chunk_pages = int(min_chunk_pages or default_chunk)
         if self.device.type == "cuda":
             self._lib = _lib.load()  # fails loudly when the extension is not built
         else:

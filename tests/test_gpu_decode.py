@@ -129,6 +129,100 @@ def test_page_sizes(gpu_device, page_size):
     _check(out, ref, torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("page_size", [1, 2, 3, 4, 5, 8, 12, 24])
+@pytest.mark.parametrize("heads,head_dim", [((32, 8), 128), ((8, 8), 64), ((16, 2), 256), ((6, 2), 128)])
+def test_small_page_sizes(gpu_device, dtype, page_size, heads, head_dim):
+    """Pages that are not a multiple of 16 tokens: a 16-token block spans
+    several pages and each lane looks up its own rows' pages (the MFMA-score
+    wave at 32/8 heads, D=128, 16-bit; the VALU wave otherwise).  Split and
+    unsplit plans; unread slots hold NaN."""
+    hq, hkv = heads
+    seed = zlib.crc32(f"small-{dtype}-{page_size}-{hq}-{head_dim}".encode()) % 10000
+    lens = [1, page_size - 1, page_size, page_size + 1, 5 * page_size + 3, 15, 16, 17, 33, 300]
+    lens = [x for x in lens if x > 0] + uniform_lens(3, 1, 400, seed)
+    case = ragged_case(lens=lens, hq=hq, hkv=hkv, head_dim=head_dim, page_size=page_size, dtype=dtype,
+                       device=gpu_device, seed=seed, pool_extra=5)
+    ref, ref_lse = _oracle(case)
+    for tw in (8, 100000):
+        out, lse, _ = _run(case, hq, hkv, head_dim, page_size, dtype, gpu_device, lse=True, target_waves=tw,
+                           min_chunk_pages=1)
+        _check(out, ref, dtype)
+        np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=2e-3 if dtype != torch.float32 else 1e-4)
+
+
+def test_small_pages_default_chunking(gpu_device):
+    """Default plan on 2-token pages: the minimum chunk is scaled to the
+    page size (64 tokens), the rows still match the oracle."""
+    case = ragged_case(lens=[2048, 100, 1], hq=32, hkv=8, head_dim=128, page_size=2, dtype=torch.bfloat16,
+                       device=gpu_device, seed=31, pool_extra=11)
+    out, _, be = _run(case, 32, 8, 128, 2, torch.bfloat16, gpu_device)
+    assert be.min_chunk_pages == 32
+    ref, _ = _oracle(case)
+    _check(out, ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("heads", [(16, 1), (32, 2), (12, 1), (11, 1), (40, 4), (64, 4), (48, 2)])
+@pytest.mark.parametrize("page_size", [16, 4])
+def test_gqa_groups_above_8(gpu_device, dtype, heads, page_size):
+    """GQA groups of more than 8 query heads (FlashInfer routes them to its
+    tensor-core kernel, attention_backend.py:46-55): each kv head is served by
+    several waves of at most 8 query heads (16 -> 2 x 8, 12 -> 2 x 6,
+    11 -> 11 x 1, 10 -> 2 x 5, 24 -> 3 x 8)."""
+    hq, hkv = heads
+    seed = zlib.crc32(f"gqa-{dtype}-{hq}-{hkv}-{page_size}".encode()) % 10000
+    lens = [1, 17, 64, 300] + uniform_lens(4, 1, 500, seed)
+    case = ragged_case(lens=lens, hq=hq, hkv=hkv, head_dim=128, page_size=page_size, dtype=dtype,
+                       device=gpu_device, seed=seed, pool_extra=3)
+    ref, ref_lse = _oracle(case)
+    for tw in (8, 100000):
+        out, lse, _ = _run(case, hq, hkv, 128, page_size, dtype, gpu_device, lse=True, target_waves=tw,
+                           min_chunk_pages=1)
+        _check(out, ref, dtype)
+        np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=2e-3 if dtype != torch.float32 else 1e-4)
+
+
+def test_reference_page_tables_on_4_token_pages(gpu_device):
+    """The second table of test_paged_kvcache_manager.py:503-543 (page size
+    4: indptr [0,1,3], indices [2,4,5], last [4,1]) run through decode vs the
+    oracle."""
+    d, hq, hkv = 64, 4, 2
+    gen = torch.Generator().manual_seed(3)
+    cache = torch.randn((8, 2, 4, hkv, d), generator=gen).to(torch.float16)
+    q = torch.randn((2, hq, d), generator=gen).to(torch.float16)
+    indptr = torch.tensor([0, 1, 3], dtype=torch.int32)
+    indices = torch.tensor([2, 4, 5], dtype=torch.int32)
+    last = torch.tensor([4, 1], dtype=torch.int32)
+    be = PagedDecodeAttention(device=gpu_device, workspace_mb=1, num_qo_heads=hq, num_kv_heads=hkv, head_dim=d,
+                              page_size=4)
+    be.plan_decode(paged_kv_indptr=indptr, paged_kv_indices=indices, paged_kv_last_page_len=last)
+    out = be.run_decode(q.to(gpu_device), cache.to(gpu_device))[:, :, 0]
+    ref, _ = opd.paged_decode(q.float().numpy(), cache.float().numpy(), indptr.numpy(), indices.numpy(),
+                              last.numpy())
+    _check(out, ref, torch.float16)
+
+
+def test_reference_decode_vector_2_token_page(gpu_device):
+    """test_flashinfer_backend.py:157-177 on its own 2-token page: q = -1000,
+    k = 100 on both tokens, v = [1, 9]; the row that sees one token returns
+    1, the row that sees both returns their mean 5."""
+    d = 64
+    cache = torch.zeros((1, 2, 2, 1, d), dtype=torch.float32)
+    cache[0, 0, :, 0, 0] = 100.0
+    cache[0, 1, 0, 0, 0] = 1.0
+    cache[0, 1, 1, 0, 0] = 9.0
+    q = torch.zeros((2, 1, d))
+    q[:, 0, 0] = -1000.0
+    be = PagedDecodeAttention(device=gpu_device, workspace_mb=1, num_qo_heads=1, num_kv_heads=1, head_dim=d,
+                              page_size=2)
+    be.plan_decode(paged_kv_indptr=torch.tensor([0, 1, 2], dtype=torch.int32),
+                   paged_kv_indices=torch.tensor([0, 0], dtype=torch.int32),
+                   paged_kv_last_page_len=torch.tensor([1, 2], dtype=torch.int32))
+    out = be.run_decode(q.to(gpu_device), cache.to(gpu_device))
+    assert out[:, 0, 0, 0].cpu().tolist() == [1.0, 5.0]
+
+
 def test_shared_prefix_pages(gpu_device):
     # Rows listing the same physical pages (radix-shared prefix) read them concurrently.
     case = ragged_case(lens=[2048 + 64] * 4, hq=32, hkv=8, head_dim=128, page_size=16, dtype=torch.bfloat16,
