@@ -10,10 +10,11 @@ and the caller falls back to eager (cuda_graph.py:204-210, 420-426).
 The key (``DecodeGraphKey``, cuda_graph.py:76-93) differs on purpose: it has
 no ``page_table_pages`` and no host plan, and its adapter version changes
 only when the adapter stacks move (``DecoderWeights.adapter_version``):
-writing new adapter values into a slot keeps every address a graph reads.  The decode plan lives on the
-device and the KV pool never moves, so a graph captured for a batch size
-replays for every later step while the rows grow; the reference recaptures
-on every new page.  torch's CUDAGraph is hipGraph on ROCm.
+writing new adapter values into a slot keeps every address a graph reads.
+The decode plan lives on the device and the KV pool moves only when it
+grows, so a graph captured for a batch size replays for every later step
+while the rows grow; the reference recaptures on every new page.  torch's
+CUDAGraph is hipGraph on ROCm.
 """
 
 from __future__ import annotations
@@ -93,6 +94,9 @@ class BatchDecodeGraphRunner:
         if e is not None:
             self._graphs.move_to_end(k)
             return e
+        # graphs of a pool tensor that has since moved are never replayed again
+        for stale in [x for x in self._graphs if x.cache_data_ptr != k.cache_data_ptr]:
+            del self._graphs[stale]
         try:
             e = self._capture(batch, reserve, uniform_adapter)
         except Exception as exc:  # capture failure: fall back to eager for good

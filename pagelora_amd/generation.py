@@ -222,8 +222,9 @@ class BatchGenerator:
                 self._plan(requests)  # ctx.tokens holds the last pick (the step wrote it)
                 if entry is not None and self.graphs.key(B, uniform_adapter=uniform) != entry_key:
                     # the plan moved the persistent page-table buffers (the
-                    # batch's page list outgrew them): the captured graph
-                    # reads the old ones, so take the graph of the new key
+                    # batch's page list outgrew them) or the slot reservation
+                    # grew the pool: the captured graph reads the old ones,
+                    # so take the graph of the new key
                     tc = time.perf_counter()
                     n_before = self.graphs.capture_count
                     new = self.graphs.entry(B, uniform_adapter=uniform)
@@ -289,9 +290,28 @@ class BatchGenerator:
             ctx.uniform_adapter = uniform
         ctx.adapter_ids.copy_(torch.tensor(adapters, dtype=torch.int32))
         ctx.tokens.copy_(first_tokens)
+        entry_key = self.graphs.key(B, reserve, uniform) if entry is not None else None
         kept = []
         for step in range(steps):
             feeder.before_step(step)  # ctx.tokens holds the last pick (the step wrote it)
+            if entry is not None and self.graphs.key(B, reserve, uniform) != entry_key:
+                # the refill grew the pool (a new tensor, the same page ids):
+                # capture the step once more on the new pool and carry the
+                # step inputs over (positions and slots come from the
+                # in-graph advance)
+                tc = time.perf_counter()
+                n_before = self.graphs.capture_count
+                new = self.graphs.entry(B, reserve, uniform)
+                if self.graphs.capture_count != n_before:
+                    torch.cuda.synchronize(dev)
+                    capture_s += time.perf_counter() - tc
+                if new is None:  # capture failed: continue eagerly on the current buffers
+                    entry = None
+                else:
+                    for name in ("tokens", "adapter_ids"):
+                        getattr(new.ctx, name).copy_(getattr(ctx, name))
+                    entry, ctx = new, new.ctx
+                entry_key = self.graphs.key(B, reserve, uniform)
             if entry is not None:
                 logits = self.graphs.replay(entry)
             else:

@@ -5,11 +5,14 @@ tensor ``[num_layers, capacity_pages, 2, page_size, num_kv_heads, head_dim]``;
 ``pool[l]`` is the NHD layer view the decode kernels read, with K at index
 0 and V at index 1 of dim 2 (``layer_runner.py:411-412``).
 
-The MI355X pool is allocated once at its full capacity (288 GB of HBM makes
-that the normal case): the reference grows it by doubling
-(``paged_kv_store.py:543-579``), which moves the tensor and forces every
-captured decode graph to be recaptured.  A fixed pool keeps one data
-pointer for the life of the engine.
+Size the pool for the whole workload up front (288 GB of HBM makes that
+the normal case): its data pointer then stays fixed and a captured decode
+graph replays for the life of the engine.  When it does run out, it grows
+as the reference's does (``paged_kv_store.py:304-330, 543-579``): a new
+tensor of ``max(16, 2 x capacity, required)`` pages, or exactly
+``max_pages`` when capped, with the old pages copied in place, so every
+page id stays valid.  The move changes the pool's data pointer, which is
+part of every decode graph key, so the next step recaptures once.
 
 Requests own page spans (``KVBlockSpan``); rows may share prefix pages
 (``paged_kvcache_manager.py:324-333``), which are read-only to decode.
@@ -30,12 +33,15 @@ class PageAllocator:
     allocate n pages or fail atomically, free returns pages to the list).
 
     Page 0 is never handed out: it is the scratch slot that graph warm-up
-    runs append their (discarded) K/V into.
+    runs append their (discarded) K/V into.  ``grow(required_pages)``, when
+    given, is called when the free list runs short; it returns the new
+    capacity, whose pages join the free list (lowest ids handed out first).
     """
 
-    def __init__(self, capacity: int) -> None:
+    def __init__(self, capacity: int, grow=None) -> None:
         self.capacity = int(capacity)
         self._free = list(range(self.capacity - 1, 0, -1))
+        self._grow = grow
 
     @property
     def free_pages(self) -> int:
@@ -43,7 +49,11 @@ class PageAllocator:
 
     def allocate(self, n: int) -> list[int]:
         if n > len(self._free):
-            raise RuntimeError(f"paged KV pool exhausted: need {n} pages, {len(self._free)} free")
+            if self._grow is None:
+                raise RuntimeError(f"paged KV pool exhausted: need {n} pages, {len(self._free)} free")
+            new_cap = int(self._grow(self.capacity + n - len(self._free)))
+            self._free = list(range(new_cap - 1, self.capacity - 1, -1)) + self._free
+            self.capacity = new_cap
         out = [self._free.pop() for _ in range(n)]
         return out
 
@@ -80,7 +90,12 @@ class Request:
 
 
 class PagedKVPool:
-    """Fixed-capacity paged KV pool for all layers plus its allocator."""
+    """Paged KV pool for all layers plus its allocator.
+
+    ``max_pages``: 0 grows without bound (the reference's default), > 0
+    grows straight to that many pages and no further, None never grows (an
+    exhausted pool raises RuntimeError).
+    """
 
     def __init__(
         self,
@@ -92,7 +107,10 @@ class PagedKVPool:
         head_dim: int,
         dtype: torch.dtype,
         device: torch.device | str,
+        max_pages: int | None = 0,
     ) -> None:
+        if max_pages is not None and max_pages > 0 and max_pages < capacity_pages:
+            raise ValueError(f"max_pages {max_pages} < capacity_pages {capacity_pages}")
         self.num_layers = num_layers
         self.page_size = page_size
         self.num_kv_heads = num_kv_heads
@@ -100,7 +118,31 @@ class PagedKVPool:
         self.cache = torch.empty(
             (num_layers, capacity_pages, 2, page_size, num_kv_heads, head_dim), dtype=dtype, device=device
         )
-        self.allocator = PageAllocator(capacity_pages)
+        self.max_pages = max_pages
+        self.version = 0      # bumped whenever the pool tensor moves
+        self.grow_count = 0
+        self.allocator = PageAllocator(capacity_pages, grow=None if max_pages is None else self._grow)
+
+    def _grow(self, required_pages: int) -> int:
+        """Move the pool to a larger tensor, copying every page (ids unchanged)
+        (paged_kv_store.py:543-579: max(16, 2 x capacity, required), or
+        exactly max_pages when capped).  Stream-ordered: work queued earlier
+        on the current stream finishes with the old tensor first."""
+        cap = self.capacity_pages
+        if self.max_pages:
+            if required_pages > self.max_pages:
+                raise RuntimeError(f"paged KV pool capacity exceeded: {required_pages} pages > max_pages "
+                                   f"{self.max_pages}")
+            new_cap = self.max_pages
+        else:
+            new_cap = max(16, 2 * cap, required_pages)
+        old = self.cache
+        new = torch.empty((old.shape[0], new_cap) + tuple(old.shape[2:]), dtype=old.dtype, device=old.device)
+        new[:, :cap].copy_(old)
+        self.cache = new
+        self.version += 1
+        self.grow_count += 1
+        return new_cap
 
     @property
     def capacity_pages(self) -> int:

@@ -26,10 +26,10 @@ SMALL = DecoderConfig(num_layers=2, hidden=256, num_qo_heads=8, num_kv_heads=2, 
                       vocab=1000, lora_rank=16, lora_alpha=32.0)
 
 
-def _setup(dev, seed=0):
+def _setup(dev, seed=0, capacity_pages=64):
     w = DecoderWeights(SMALL, n_adapters=2, device=dev, seed=seed)
-    pool = PagedKVPool(num_layers=SMALL.num_layers, capacity_pages=64, page_size=16, num_kv_heads=2, head_dim=64,
-                       dtype=torch.bfloat16, device=dev)
+    pool = PagedKVPool(num_layers=SMALL.num_layers, capacity_pages=capacity_pages, page_size=16, num_kv_heads=2,
+                       head_dim=64, dtype=torch.bfloat16, device=dev)
     g = torch.Generator().manual_seed(7)
     prefix = torch.randint(0, SMALL.vocab, (32,), generator=g)
     prompts = [torch.randint(0, SMALL.vocab, (n,), generator=g) for n in (5, 17, 1)]
@@ -365,3 +365,34 @@ def test_graph_follows_page_table_buffers_that_move(gpu_device):
     assert start_pages + 1 <= 16 < end_pages, (start_pages, end_pages)
     assert res.used_graph and res.graph_captures == 2, res.graph_captures
     assert torch.equal(res.tokens, ref.tokens)
+
+
+@pytest.mark.parametrize("device_tables", [False, True])
+def test_pool_growth_mid_generation_matches_unconstrained(gpu_device, device_tables):
+    """A pool that runs out while rows grow (8 pages: the prompts fill 7)
+    grows to a new tensor between graph replays (paged_kv_store.py:543-579),
+    keeping every page id; the next step recaptures once on the new pool.
+    Tokens and logits equal those of a pool large enough never to grow."""
+    results = []
+    for cap in (256, 8):
+        w, pool, reqs, first, _ = _setup(gpu_device, capacity_pages=cap)
+        gen = BatchGenerator(w, pool, workspace_mb=8, use_graph=True)
+        grown_at = []
+        grow = pool.allocator._grow
+
+        def recording_grow(required, grow=grow, gen=gen, grown_at=grown_at):
+            grown_at.append(gen.graphs.replay_count)
+            return grow(required)
+
+        pool.allocator._grow = recording_grow
+        res = gen.generate(reqs, first, steps=80, adapters=[0, 1, 1], device_tables=device_tables,
+                           keep_logits=True)
+        assert res.used_graph
+        results.append((res.tokens, res.extra["logits"], grown_at, pool, res.graph_captures))
+    (t0, l0, g0, p0, c0), (t1, l1, g1, p1, c1) = results
+    assert g0 == [] and p0.grow_count == 0
+    assert p1.grow_count >= 1 and any(r > 0 for r in g1), g1  # grown between replays
+    assert p1.capacity_pages >= 16
+    assert c1 >= c0 + 1  # captured again on the grown pool
+    assert torch.equal(t0, t1)
+    assert torch.equal(l0, l1)
