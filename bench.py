@@ -188,12 +188,16 @@ def time_decode_spaced(w, steps, warmup, evict_bytes=0):
     return step, decode, merge
 
 
-def time_lora(device, steps=20):
+def time_lora(device, steps=200):
     """Per-layer no-merge LoRA delta: 64 tokens over 4 adapters, r=16, the 7
-    Qwen3-8B modules in their 4 groups (q/k/v, o, gate/up, down)."""
+    Qwen3-8B modules in their 4 groups (q/k/v, o, gate/up, down).  Each form
+    is captured in a hipGraph and replayed ``steps`` times between events:
+    the four groups in one pl_lora_delta_groups call (two launches), and one
+    pl_lora_delta call per group (eight launches).  Returns
+    (grouped ms, per-group-calls ms, algorithmic bytes) per layer."""
     import torch
 
-    from pagelora_amd.lora import lora_delta_
+    from pagelora_amd.lora import lora_delta_, lora_delta_groups_
 
     gen = torch.Generator(device=device).manual_seed(1237)
     T, H, I, r, n = 64, 4096, 12288, 16, 4
@@ -211,19 +215,32 @@ def time_lora(device, steps=20):
             nbytes += (A.numel() + B.numel()) * 2 + out.numel() * 4
         nbytes += x.numel() * 2
         groups.append((x, mods))
-    for _ in range(3):
+
+    def grouped():
+        lora_delta_groups_(groups, ids)
+
+    def per_group():
         for x, mods in groups:
             lora_delta_(x, mods, ids)
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize(device)
-    s.record()
-    for _ in range(steps):
-        for x, mods in groups:
-            lora_delta_(x, mods, ids)
-    e.record()
-    torch.cuda.synchronize(device)
-    ms = s.elapsed_time(e) / steps
-    return ms, nbytes
+
+    result = []
+    for fn in (grouped, per_group):
+        for _ in range(3):
+            fn()  # sizes the workspace before capture
+        torch.cuda.synchronize(device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        graph.replay()
+        torch.cuda.synchronize(device)
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(steps):
+            graph.replay()
+        e.record()
+        torch.cuda.synchronize(device)
+        result.append(s.elapsed_time(e) / steps)
+    return result[0], result[1], nbytes
 
 
 def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_steps=2):
@@ -455,10 +472,13 @@ def main():
         extra["qwen3_layer_b1_2048_bf16"] = leg
         del w2
         torch.cuda.empty_cache()
-        lora_ms, lora_bytes = time_lora(dev)
+        lora_ms, lora_each_ms, lora_bytes = time_lora(dev)
         extra["lora_delta_64tok_4adapters_7modules"] = {
             "us_per_layer": round(lora_ms * 1e3, 2),
             "algorithmic_GBps": round(lora_bytes / (lora_ms * 1e-3) / 1e9, 1),
+            "algorithmic_bytes": lora_bytes,
+            "form": "the layer's 4 groups in one pl_lora_delta_groups call (2 launches), hipGraph replay",
+            "us_per_layer_one_call_per_group": round(lora_each_ms * 1e3, 2),
         }
     if not args.no_extra and not args.no_e2e:
         for name, kw in E2E_LEGS.values():

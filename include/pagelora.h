@@ -493,12 +493,36 @@ typedef struct {
 /* Most modules in one group (q, k, v). */
 #define PL_LORA_MAX_MODULES 4
 
-/* Workspace bytes for one pl_lora_* call: the shrink's fp32 partial sums,
- * [k-slices][num_tokens][sum(rank) rounded up to 32], the slice count
- * depending on num_tokens and in_features.  Calls that share a workspace
- * must be stream ordered; shrink writes it, expand reads it. */
+/* Workspace bytes for pl_lora_shrink / pl_lora_expand (and pl_linear's
+ * LoRA epilogue): the shrink's fp32 partial sums, [k-slices][num_tokens]
+ * [sum(rank) rounded up to 32], the slice count depending on num_tokens and
+ * in_features.  Calls that share a workspace must be stream ordered; shrink
+ * writes it, expand reads it. */
 size_t pl_lora_workspace_size(int num_tokens, int in_features,
                               const pl_lora_module* modules_h, int num_modules);
+
+/* One group of modules sharing the input x [num_tokens, in_features] (row
+ * stride ldx), for pl_lora_delta_groups. */
+typedef struct {
+  const void* x;
+  int64_t ldx;
+  int in_features;
+  int num_modules;
+  const pl_lora_module* modules;  /* host array of num_modules */
+} pl_lora_group;
+
+/* Most groups in one pl_lora_delta_groups call (a decoder layer's four:
+ * q/k/v, o, gate/up, down). */
+#define PL_LORA_MAX_GROUPS 4
+
+/* Workspace bytes for pl_lora_delta / pl_lora_delta_groups.  The workspace
+ * of these two entry points must be zero-filled once before its first use
+ * (e.g. at allocation): the decode path keeps double-buffered intermediate
+ * accumulators and their parity there from call to call.  Keep it for these
+ * two entry points (not pl_lora_shrink, pl_lora_expand or pl_linear), one
+ * call at a time (stream-ordered).  Returns 0 for an invalid group list. */
+size_t pl_lora_delta_workspace_size(const pl_lora_group* groups_h, int num_groups,
+                                    int num_tokens, int num_adapters);
 
 /*
  * out_m[t] += scale_m * B_m[a_t] . (A_m[a_t] . x[t]) for every module m of the
@@ -516,12 +540,31 @@ size_t pl_lora_workspace_size(int num_tokens, int in_features,
  * delta term of LoRALinear.forward (multilora/linear.py:226-231).  Per-token
  * adapter ids generalise the reference's single bound adapter
  * (multilora/runtime.py:138-174).
+ *
+ * Workspace: pl_lora_delta_workspace_size of the one group, zero-filled
+ * before its first use (see there).  Up to 64 tokens and 64 adapters the
+ * call is two launches built for decode latency; otherwise the general
+ * shrink + expand pair.
  */
 int pl_lora_delta(const void* x, int64_t ldx, int num_tokens, int in_features,
                   const pl_lora_module* modules_h, int num_modules,
                   const int32_t* adapter_ids, int num_adapters, int dtype,
                   int out_dtype, void* workspace, size_t workspace_bytes,
                   void* stream);
+
+/*
+ * pl_lora_delta for up to PL_LORA_MAX_GROUPS groups with their own inputs
+ * (e.g. a decoder layer's q/k/v, o, gate/up and down deltas when their
+ * inputs are at hand together), one adapter id per token shared by all
+ * groups.  At decode sizes (<= 64 tokens, <= 64 adapters) all groups share
+ * the same two launches; otherwise they run one after another.  Groups must
+ * not write the same outputs.  No counterpart in the reference, which runs
+ * each module's delta inside its projection (packed_ops.py:105-265).
+ */
+int pl_lora_delta_groups(const pl_lora_group* groups_h, int num_groups, int num_tokens,
+                         const int32_t* adapter_ids, int num_adapters, int dtype,
+                         int out_dtype, void* workspace, size_t workspace_bytes,
+                         void* stream);
 
 /* The two stages of pl_lora_delta, for callers that overlap them with the
  * base GEMM: shrink writes the fp32 partial sums into the workspace, expand

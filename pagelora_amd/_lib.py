@@ -23,6 +23,7 @@ PL_ERR_WORKSPACE = 3
 PL_ERR_HIP = 4
 
 PL_LORA_MAX_MODULES = 4
+PL_LORA_MAX_GROUPS = 4
 
 PL_DECODE_SKIP_MERGE = 1
 PL_DECODE_MERGE_ONLY = 2
@@ -52,6 +53,18 @@ class LoraModule(ctypes.Structure):
         ("out_features", ctypes.c_int),
         ("rank", ctypes.c_int),
         ("scale", ctypes.c_float),
+    ]
+
+
+class LoraGroup(ctypes.Structure):
+    """Mirror of ``pl_lora_group``."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("ldx", ctypes.c_int64),
+        ("in_features", ctypes.c_int),
+        ("num_modules", ctypes.c_int),
+        ("modules", ctypes.POINTER(LoraModule)),
     ]
 
 
@@ -255,6 +268,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pl_lora_delta": (
         _i32,
         [_vp, _i64, _i32, _i32, ctypes.POINTER(LoraModule), _i32, _vp, _i32, _i32, _i32, _vp, _sz, _vp],
+    ),
+    "pl_lora_delta_workspace_size": (_sz, [ctypes.POINTER(LoraGroup), _i32, _i32, _i32]),
+    "pl_lora_delta_groups": (
+        _i32,
+        [ctypes.POINTER(LoraGroup), _i32, _i32, _vp, _i32, _i32, _i32, _vp, _sz, _vp],
     ),
     "pl_lora_shrink": (
         _i32,

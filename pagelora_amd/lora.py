@@ -12,9 +12,11 @@ adapter ids ``a_t`` -- the delta term of the reference's no-merge path:
 
 Here one shrink launch reads x once for the whole group and one expand
 launch accumulates every module's delta straight into its base output; the
-block-diagonal zeros are never stored or read.  Adapter selection is per
-token (the reference binds one adapter for the whole batch,
-multilora/runtime.py:138-174; a single adapter is the case ``ids == 0``).
+block-diagonal zeros are never stored or read.  ``lora_delta_groups_`` runs
+up to four groups with their own inputs in the same two launches.  Adapter
+selection is per token (the reference binds one adapter for the whole
+batch, multilora/runtime.py:138-174; a single adapter is the case
+``ids == 0``).
 """
 
 from __future__ import annotations
@@ -46,6 +48,29 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 def reserve_workspace(device: torch.device | str, nbytes: int) -> None:
     """Allocate ``nbytes`` of workspace ahead of a (possibly captured) call."""
     _workspace(torch.device(device), nbytes)
+
+
+_DELTA_WS: dict[int, torch.Tensor] = {}
+
+
+def _delta_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device workspace of pl_lora_delta(_groups): zero-filled when
+    allocated (its ticket area must start at zero; every call leaves it so)
+    and used by no other entry point; grown on demand, never inside a
+    captured graph."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _DELTA_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("LoRA workspace must be sized before graph capture (call reserve_delta_workspace)")
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _DELTA_WS[key] = ws
+    return ws
+
+
+def reserve_delta_workspace(device: torch.device | str, nbytes: int) -> None:
+    """Allocate ``nbytes`` of lora_delta_ workspace ahead of a captured call."""
+    _delta_workspace(torch.device(device), nbytes)
 
 
 def _module_structs(modules, x: torch.Tensor):
@@ -106,16 +131,59 @@ def lora_delta_(
     arr, n_adapters, out_dtype = _module_structs(modules, x)
     lib = _lib.load()
     n = len(modules)
-    nbytes = lib.pl_lora_workspace_size(x.shape[0], x.shape[1], arr, n)
+    grp = _lib.LoraGroup(x.data_ptr(), x.stride(0), x.shape[1], n, arr)
+    nbytes = lib.pl_lora_delta_workspace_size(ctypes.byref(grp), 1, x.shape[0], n_adapters)
     if nbytes == 0:
         raise ValueError(f"invalid LoRA group: {_lib.last_error()}")
-    ws = _workspace(x.device, nbytes)
+    ws = _delta_workspace(x.device, nbytes)
     status = lib.pl_lora_delta(
         x.data_ptr(), x.stride(0), x.shape[0], x.shape[1], arr, n,
         adapter_ids.data_ptr(), n_adapters, _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype),
         ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device),
     )
     _lib.check(status, "pl_lora_delta")
+
+
+def lora_delta_groups_(
+    groups: Sequence[tuple[torch.Tensor, Sequence[tuple[torch.Tensor, torch.Tensor, torch.Tensor, float]]]],
+    adapter_ids: torch.Tensor,
+) -> None:
+    """``lora_delta_`` for up to four groups ``(x, modules)`` with their own
+    inputs and the same per-token adapter ids, in one pair of launches at
+    decode sizes.  Every x has the same token count and dtype; groups must
+    not write the same outputs."""
+    if not 1 <= len(groups) <= _lib.PL_LORA_MAX_GROUPS:
+        raise ValueError(f"1..{_lib.PL_LORA_MAX_GROUPS} groups, got {len(groups)}")
+    x0 = groups[0][0]
+    T = x0.shape[0]
+    if adapter_ids.dtype != torch.int32 or adapter_ids.numel() != T or adapter_ids.device != x0.device:
+        raise ValueError("adapter_ids must be int32 [T] on the inputs' device")
+    descs = (_lib.LoraGroup * len(groups))()
+    keep = []
+    n_adapters = out_dtype = None
+    for i, (x, modules) in enumerate(groups):
+        if x.dim() != 2 or x.stride(1) != 1 or x.shape[0] != T or x.dtype != x0.dtype or x.device != x0.device:
+            raise ValueError(f"group {i}: x must be [{T}, in] with unit column stride, {x0.dtype} on {x0.device}")
+        arr, na, od = _module_structs(modules, x)
+        if n_adapters is None:
+            n_adapters, out_dtype = na, od
+        elif na != n_adapters or od != out_dtype:
+            raise ValueError("all groups need the same adapter count and output dtype")
+        keep.append(arr)
+        descs[i].x, descs[i].ldx, descs[i].in_features = x.data_ptr(), x.stride(0), x.shape[1]
+        descs[i].num_modules, descs[i].modules = len(modules), arr
+    if T == 0:
+        return
+    lib = _lib.load()
+    nbytes = lib.pl_lora_delta_workspace_size(descs, len(groups), T, n_adapters)
+    if nbytes == 0:
+        raise ValueError(f"invalid LoRA groups: {_lib.last_error()}")
+    ws = _delta_workspace(x0.device, nbytes)
+    status = lib.pl_lora_delta_groups(
+        descs, len(groups), T, adapter_ids.data_ptr(), n_adapters, _lib.dtype_code(x0.dtype),
+        _lib.dtype_code(out_dtype), ws.data_ptr(), ws.numel(), _lib.stream_handle(x0.device),
+    )
+    _lib.check(status, "pl_lora_delta_groups")
 
 
 def lora_linear(

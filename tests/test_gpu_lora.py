@@ -158,3 +158,94 @@ def test_repeated_calls_reuse_workspace(gpu_device):
     torch.cuda.synchronize()
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
+
+
+def _group(gen, T, fin, outs_ranks, n, dtype=torch.bfloat16, out_dtype=torch.float32, device=None, base=False):
+    x = _rand((T, fin), 1.0, gen, dtype)
+    mods, host = [], []
+    for fout, r in outs_ranks:
+        A = _rand((n, r, fin), fin ** -0.5, gen, dtype)
+        B = _rand((n, fout, r), 0.05, gen, dtype)
+        b0 = torch.randn((T, fout), generator=gen) if base else torch.zeros((T, fout))
+        mods.append((A.to(device), B.to(device), b0.to(out_dtype).to(device), 2.0))
+        host.append((A, B, b0.to(out_dtype).float()))
+    return x, mods, host
+
+
+def _check_group(x, ids, host, mods, dtype=torch.bfloat16, rtol=0.0):
+    inter = "bf16" if dtype == torch.bfloat16 else "f16"
+    for (A, B, b0), (_, _, out, _) in zip(host, mods):
+        want = b0.numpy() + ol.multi_adapter_delta(x.float().numpy(), ids.tolist(), A.float().numpy(),
+                                                   B.float().numpy(), 2.0, intermediate=inter)
+        got = out.float().cpu().numpy()
+        err = np.abs(got - want)
+        assert (err <= 2e-3 + rtol * np.abs(want)).all(), f"max err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("T,n", [(65, 4), (200, 3), (16, 70), (1, 65)])
+def test_general_path_beyond_decode_sizes(gpu_device, T, n):
+    # more than 64 tokens or 64 adapters: the general shrink + expand pair
+    gen = torch.Generator().manual_seed(T * 100 + n)
+    ids = torch.randint(-1, n + 1, (T,), generator=gen, dtype=torch.int32)  # includes -1 and n (both untouched)
+    x, mods, host = _group(gen, T, 512, [(96, 16), (40, 8)], n, device=gpu_device, base=True)
+    lora_delta_(x.to(gpu_device), mods, ids.to(gpu_device))
+    torch.cuda.synchronize()
+    _check_group(x, ids, host, mods)
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 17, 63, 64])
+@pytest.mark.parametrize("n", [1, 4, 64])
+def test_decode_path_tokens_and_adapters(gpu_device, T, n):
+    # the two-launch decode path at its edges: 1..64 tokens, 1..64 adapters,
+    # ids outside [0, n) untouched, ranks summing to the 128 maximum
+    gen = torch.Generator().manual_seed(T * 1000 + n)
+    ids = torch.randint(-1, n + 1, (T,), generator=gen, dtype=torch.int32)
+    x, mods, host = _group(gen, T, 1000, [(64, 32), (48, 32), (40, 32), (16, 32)], n, device=gpu_device,
+                           base=True)
+    lora_delta_(x.to(gpu_device), mods, ids.to(gpu_device))
+    torch.cuda.synchronize()
+    _check_group(x, ids, host, mods)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T", [4, 64, 100])
+def test_groups_in_one_call_equal_separate_calls(gpu_device, dtype, T):
+    """A decoder layer's four groups (Qwen3-8B modules, r=16, 4 adapters) in
+    one pl_lora_delta_groups call == four pl_lora_delta calls, bit for bit
+    (decode sizes: the same two launches; 100 tokens: one after another),
+    and the oracle on every module."""
+    from pagelora_amd.lora import lora_delta_groups_
+
+    gen = torch.Generator().manual_seed(17 + T)
+    H, I, n = 4096, 12288, 4
+    ids = torch.randint(0, n, (T,), generator=gen, dtype=torch.int32)
+    spec = [(H, [(4096, 16), (1024, 16), (1024, 16)]), (H, [(4096, 16)]), (H, [(I, 16), (I, 16)]),
+            (I, [(H, 16)])]
+    groups = [_group(gen, T, fin, outs, n, dtype=dtype, out_dtype=dtype, device=gpu_device, base=True)
+              for fin, outs in spec]
+    sep = [[(A, B, out.clone(), s) for A, B, out, s in mods] for _, mods, _ in groups]
+    lora_delta_groups_([(x.to(gpu_device), mods) for x, mods, _ in groups], ids.to(gpu_device))
+    for (x, _, _), mods in zip(groups, sep):
+        lora_delta_(x.to(gpu_device), mods, ids.to(gpu_device))
+    torch.cuda.synchronize()
+    rtol = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11
+    for (x, mods, host), smods in zip(groups, sep):
+        for (_, _, out, _), (_, _, sout, _) in zip(mods, smods):
+            assert torch.equal(out, sout)
+        _check_group(x, ids, host, mods, dtype, rtol)
+
+
+def test_delta_workspace_state_across_calls(gpu_device):
+    # the decode path keeps its double-buffered accumulators in the delta
+    # workspace between calls; calls with other layouts, ranks and token
+    # counts, and general-path calls, interleaved on the same workspace, all
+    # match the oracle
+    gen = torch.Generator().manual_seed(9)
+    for T, fin, outs in ((64, 4096, [(512, 16), (256, 16)]), (100, 512, [(64, 16)]), (3, 12288, [(128, 8)]),
+                         (20, 64, [(40, 2), (24, 6)]), (40, 264, [(64, 48)]), (64, 4096, [(512, 16), (256, 16)]),
+                         (7, 1024, [(96, 32), (32, 32), (16, 64)])):
+        ids = torch.randint(0, 4, (T,), generator=gen, dtype=torch.int32)
+        x, mods, host = _group(gen, T, fin, outs, 4, device=gpu_device)
+        lora_delta_(x.to(gpu_device), mods, ids.to(gpu_device))
+        torch.cuda.synchronize()
+        _check_group(x, ids, host, mods)
