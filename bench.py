@@ -188,6 +188,47 @@ def time_decode_spaced(w, steps, warmup, evict_bytes=0):
     return step, decode, merge
 
 
+def time_step_graph(w, steps=50, warmup=10, evict_bytes=0):
+    """One decode step (plan + decode + merge) captured in a hipGraph and
+    replayed behind a spin (warm caches) or a fill of ``evict_bytes`` (cold),
+    events only around each replay; returns the median step in us."""
+    import torch
+
+    from pagelora_amd.attention_backend import PagedDecodeAttention
+
+    dev = w["q"].device
+    be = PagedDecodeAttention(device=dev, workspace_mb=256, num_qo_heads=w["hq"], num_kv_heads=w["hkv"],
+                              head_dim=w["d"], page_size=w["ps"])
+    be.plan_decode(paged_kv_indptr=w["indptr"], paged_kv_indices=w["indices"], paged_kv_last_page_len=w["last"])
+    out = torch.empty_like(w["q"])
+
+    def step():
+        be.replan_decode()
+        be.run_decode_into(w["q"], w["cache"], out)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    junk = torch.empty(evict_bytes, dtype=torch.uint8, device=dev) if evict_bytes else None
+    ts = []
+    for i in range(warmup + steps):
+        if junk is not None:
+            junk.fill_(i & 0xFF)
+        else:
+            torch.cuda._sleep(200_000)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize(dev)
+        if i >= warmup:
+            ts.append(a.elapsed_time(b) * 1e3)
+    return float(np.median(ts))
+
+
 def time_lora(device, steps=200):
     """Per-layer no-merge LoRA delta: 64 tokens over 4 adapters, r=16, the 7
     Qwen3-8B modules in their 4 groups (q/k/v, o, gate/up, down).  Each form
@@ -249,10 +290,14 @@ def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_step
     behind a shared ``prefix_len``-token prefix in shared pages plus their own
     ``suffix_len`` random-id tokens, then ``steps`` greedy steps under hipGraph
     replay.  tok/s = generated tokens / decode seconds (the graph is captured
-    in a short warm-up call first, outside the timed region).  Timed twice:
-    with the page table packed on the host and uploaded every step, then
-    with it grown on the device inside the captured step (``tok_per_s``,
-    the default path), each after its own warm-up."""
+    in a short warm-up call first, outside the timed region).  Timed twice,
+    both from the prompts' own context (``prefix_len + suffix_len`` tokens):
+    with the page table grown on the device inside the captured step
+    (``tok_per_s``, the default path), then packed on the host and uploaded
+    every step; after each warm-up and timed call the rows are rewound to
+    the prompts (their pages stay allocated, the next call overwrites the
+    slots).  Both legs start from the prefill's greedy token, so their
+    tokens must agree (``tokens_match``)."""
     import torch
 
     from pagelora_amd.decoder import QWEN3_8B, DecoderWeights
@@ -273,12 +318,19 @@ def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_step
     torch.cuda.synchronize(device)
     prefill_s = time.perf_counter() - t
     gen = BatchGenerator(w, pool, use_graph=True)
-    warm = gen.generate(reqs, first, steps=warm_steps)
-    host = gen.generate(reqs, warm.tokens[:, -1].to(device), steps=steps)
-    context_host = reqs[0].length - steps
-    warm = gen.generate(reqs, host.tokens[:, -1].to(device), steps=warm_steps, device_tables=True)
+
+    def rewind(n):
+        for r in reqs:
+            r.length -= n
+
     context = reqs[0].length
-    res = gen.generate(reqs, warm.tokens[:, -1].to(device), steps=steps, device_tables=True)
+    gen.generate(reqs, first, steps=warm_steps, device_tables=True)
+    rewind(warm_steps)
+    res = gen.generate(reqs, first, steps=steps, device_tables=True)
+    rewind(steps)
+    gen.generate(reqs, first, steps=warm_steps)
+    rewind(warm_steps)
+    host = gen.generate(reqs, first, steps=steps)
     out = {
         "tok_per_s": round(res.decode_tokens_per_s, 1),
         "ms_per_step": round(res.decode_seconds / steps * 1e3, 3),
@@ -290,7 +342,8 @@ def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_step
         "page_table": "device (reserve uploads: %d)" % res.extra["reserve_uploads"],
         "host_tables": {"tok_per_s": round(host.decode_tokens_per_s, 1),
                         "ms_per_step": round(host.decode_seconds / steps * 1e3, 3),
-                        "context_at_start": context_host},
+                        "context_at_start": context},
+        "tokens_match": bool(torch.equal(res.tokens, host.tokens)),
         "prefill_s": round(prefill_s, 2),
     }
     del w, pool, gen
@@ -458,7 +511,10 @@ def main():
     if not args.no_extra:
         w2 = qwen3_layer_workload(dev)
         nb2 = algorithmic_bytes(w2)
-        leg = {"algorithmic_bytes": nb2, "timing": "events around each kernel, the step queued behind GPU work"}
+        leg = {"algorithmic_bytes": nb2,
+               "timing": "events around each kernel, the step queued behind GPU work; step_us_graph: the step "
+                         "(plan + decode + merge; batches of up to 16 rows launch no plan kernel) captured in a "
+                         "hipGraph, events around each replay"}
         for tag, evict in (("warm", 0), ("cold", 512 << 20)):
             st2, per2, merge2 = time_decode_spaced(w2, max(args.steps, 100), args.warmup, evict_bytes=evict)
             dk = float(np.median(per2))
@@ -467,6 +523,7 @@ def main():
                 "merge_kernel_us": round(float(np.median(merge2)) * 1e3, 2),
                 "step_us_incl_plan": round(float(np.median(st2)) * 1e3, 2),
                 "algorithmic_GBps": round(nb2 / (dk * 1e-3) / 1e9, 1),
+                "step_us_graph": round(time_step_graph(w2, evict_bytes=evict), 2),
             }
         leg["cold"]["note"] = "a 512 MiB fill before each step evicts the K/V from the L2 and the 256 MB Infinity Cache"
         extra["qwen3_layer_b1_2048_bf16"] = leg

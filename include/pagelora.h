@@ -66,6 +66,12 @@ size_t pl_decode_workspace_size(int batch, int target_items, int num_qo_heads,
  * indices buffer the run will read.
  * No host read-back: the plan runs on the stream, so it can sit inside a
  * captured hipGraph and one graph replays across steps whatever the lengths.
+ * For batches of up to 16 rows nothing is launched: the library records
+ * indptr and the split parameters against `workspace`, and the runs on that
+ * workspace derive the same chunking from indptr inside their kernels (items
+ * in row order).  indptr must then stay valid until those runs execute.
+ * PAGELORA_DECODE_PLAN_KERNEL=1 in the environment keeps the plan kernel for
+ * every batch.
  *
  * Replaces FlashInferAttentionBackend.plan_decode / _call_plan
  * (model/flashinfer/attention_backend.py:63-118, 229-285), which call

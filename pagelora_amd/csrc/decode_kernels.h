@@ -54,6 +54,94 @@ __host__ __device__ inline int plan_stamp(int batch, int max_items) {
   return (int)(0x51A70000u ^ ((unsigned)batch * 2654435761u) ^ (unsigned)max_items);
 }
 
+// ------------------------------------------------------- direct items ---
+// Batches of up to kDirectMaxBatch rows skip the plan kernel: every decode
+// wave (and every merge workgroup) derives the split from indptr itself, one
+// row per lane: the chunk size as the plan computes it, each row's chunk
+// count, their scan, and from it the row and page range of an item (or the
+// slot range of a row).  Items and slots are in row order.  Costs one load
+// of indptr in place of the item load.
+constexpr int kDirectMaxBatch = 16;
+
+struct Direct {
+  const int32_t* indptr;  // nullptr: the items come from the plan in the workspace
+  int capacity;           // indices capacity: page ranges are clamped to it, as the plan does
+  int target_items;
+  int min_chunk;
+};
+
+struct DirectScan {
+  int ip;     // this lane's clamped indptr[lane] (lanes < batch: the rows' starts)
+  int ip1;    // and indptr[lane + 1] (the rows' ends)
+  int n;      // chunks of row `lane` (lanes < batch; 0 elsewhere)
+  int incl;   // inclusive scan of n over lanes 0..15
+  int chunk;  // pages per chunk (uniform)
+  int total;  // items of the batch (uniform)
+};
+
+// a / b for 0 <= a < 2^23, 1 <= b: float quotient, then one correction step
+__device__ __forceinline__ int small_div(int a, int b) {
+  int q = (int)((float)a * __builtin_amdgcn_rcpf((float)b));
+  const int r = a - q * b;
+  q += r >= b ? 1 : 0;
+  q -= r < 0 ? 1 : 0;
+  return q;
+}
+
+__device__ __forceinline__ DirectScan direct_scan(const Direct& d, int batch) {
+  const int lane = threadIdx.x % kWave;
+  DirectScan r;
+  // both ends of row `lane` in one round trip (batch <= 16, so lanes 0..15
+  // cover every row)
+  auto clampi = [&](int v) { return v < 0 ? 0 : (v > d.capacity ? d.capacity : v); };
+  const int ip = clampi(d.indptr[lane < batch ? lane : batch]);
+  const int ip1 = clampi(d.indptr[lane < batch ? lane + 1 : batch]);
+  r.ip = ip;
+  r.ip1 = ip1;
+  const int ip0 = __builtin_amdgcn_readfirstlane(ip);
+  const int ipb = __builtin_amdgcn_readlane(ip1, batch - 1);
+  const int total_pages = ipb > ip0 ? ipb - ip0 : 0;
+  int c = (total_pages + d.target_items - 1) / d.target_items;  // uniform
+  c = c > d.min_chunk ? c : d.min_chunk;
+  r.chunk = c > 1 ? c : 1;
+  const int pages = ip1 > ip ? ip1 - ip : 0;
+  r.n = lane < batch ? (pages > 0 ? small_div(pages + r.chunk - 1, r.chunk) : 1) : 0;
+  // inclusive scan over the 16 lanes of DPP row 0 (row_shr shifts in zeros)
+  int x = r.n;
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  r.incl = x;
+  r.total = __builtin_amdgcn_readlane(x, 15);
+  return r;
+}
+
+// Row, page range and flags (single-item row, holds the last page, slot) of
+// item `item`; false past the batch's items.  Every lane of the wave calls it.
+__device__ __forceinline__ bool direct_item(const Direct& d, int batch, int item, int& b, int& pbeg, int& pend,
+                                            int& flags) {
+  const DirectScan s = direct_scan(d, batch);
+  if (item >= s.total) return false;
+  const int lane = threadIdx.x % kWave;
+  b = __builtin_amdgcn_readfirstlane(__popcll(__builtin_amdgcn_ballot_w64((lane < 16) & (s.incl <= item))));
+  const int n_b = __builtin_amdgcn_readlane(s.n, b);
+  const int first = __builtin_amdgcn_readlane(s.incl, b) - n_b;
+  const int row_beg = __builtin_amdgcn_readlane(s.ip, b);
+  const int row_end = __builtin_amdgcn_readlane(s.ip1, b);
+  pbeg = row_beg + (item - first) * s.chunk;
+  pend = min(row_end > row_beg ? row_end : row_beg, pbeg + s.chunk);
+  flags = (item << 2) | (n_b == 1 ? 1 : 0) | (pend >= row_end ? 2 : 0);
+  return true;
+}
+
+// First slot and item count of row b.  Every lane of the wave calls it.
+__device__ __forceinline__ void direct_row(const Direct& d, int batch, int b, int& first, int& n) {
+  const DirectScan s = direct_scan(d, batch);
+  n = __builtin_amdgcn_readlane(s.n, b);
+  first = __builtin_amdgcn_readlane(s.incl, b) - n;
+}
+
 // ---------------------------------------------------------------- decode ---
 // Per-type traits: how one lane's 8 elements of a token row are loaded and
 // consumed.  16-bit types: one 16-byte load; fp32: two.
@@ -739,7 +827,7 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
     T* __restrict__ o, int64_t o_sb, int64_t o_sh, float* __restrict__ lse, int num_qo_heads,
     int num_kv_heads, int page_size, int64_t num_pages, float scale_log2,
     const int* __restrict__ header, const Item* __restrict__ items, int batch, int max_items,
-    float* __restrict__ part_lse, float* __restrict__ part_o, QkvIn qin, int kv_split) {
+    float* __restrict__ part_lse, float* __restrict__ part_o, QkvIn qin, int kv_split, Direct dir) {
   static_assert(!(FUSED && SMALL), "the folded q/k/v epilogue is built for 16-token pages");
   using WaveT = WaveFor<T, D, G>;
   constexpr int LPT = WaveT::LPT;
@@ -751,17 +839,22 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
   const int h = wave - item_idx * num_kv_heads;
   const int hk = FUSED ? h : uniform(h / kv_split);  // the real kv head whose pages this wave reads
   if (item_idx >= max_items) return;
-  // The item is read together with the plan stamp (item_idx < max_items
-  // keeps the read inside the item table) and used only if the stamp
-  // matches: one combined check needs both, so both loads issue together.
-  const int stamp_batch = uniform(header[2]), stamp = uniform(header[3]);
-  const int4 iv = *reinterpret_cast<const int4*>(items + item_idx);  // the whole item in one load
-  const int b = uniform(iv.x), pbeg = uniform(iv.y), pend = uniform(iv.z), flags = uniform(iv.w);
-  // (every field takes part in the check, so no part of the item load is
-  // deferred past it)
-  if (!((stamp_batch == batch) & (stamp == plan_stamp(batch, max_items)) & (b >= 0) & (b < batch) & (pbeg >= 0) &
-        (pend >= pbeg) & (flags >= 0) & ((flags >> 2) < max_items)))
-    return;
+  int b, pbeg, pend, flags;
+  if (dir.indptr != nullptr) {  // direct items (uniform)
+    if (!direct_item(dir, batch, item_idx, b, pbeg, pend, flags)) return;
+  } else {
+    // The item is read together with the plan stamp (item_idx < max_items
+    // keeps the read inside the item table) and used only if the stamp
+    // matches: one combined check needs both, so both loads issue together.
+    const int stamp_batch = uniform(header[2]), stamp = uniform(header[3]);
+    const int4 iv = *reinterpret_cast<const int4*>(items + item_idx);  // the whole item in one load
+    b = uniform(iv.x), pbeg = uniform(iv.y), pend = uniform(iv.z), flags = uniform(iv.w);
+    // (every field takes part in the check, so no part of the item load is
+    // deferred past it)
+    if (!((stamp_batch == batch) & (stamp == plan_stamp(batch, max_items)) & (b >= 0) & (b < batch) & (pbeg >= 0) &
+          (pend >= pbeg) & (flags >= 0) & ((flags >> 2) < max_items)))
+      return;
+  }
   // Second round trip, all at once: the row's last-page fill, the page ids
   // of the item's first two blocks and q (below).  The item's pages lie
   // inside the indices buffer (the plan clamps them), so indices[pbeg] exists
@@ -994,20 +1087,26 @@ __global__ __launch_bounds__(MT) void merge_kernel(
     const int2* __restrict__ row_info, const float* __restrict__ part_lse,
     const float* __restrict__ part_o, T* __restrict__ o, int64_t o_sb, int64_t o_sh,
     float* __restrict__ lse, const int* __restrict__ header, int batch, int num_qo_heads,
-    int max_items) {
+    int max_items, Direct dir) {
   constexpr int LPT = D / 8, RPI = MT / LPT, NWV = MT / kWave;
   __shared__ float s_m[NWV][LPT], s_w[NWV][LPT], s_a[NWV][LPT][8];
   const int pair = blockIdx.x;
   if (pair >= batch * num_qo_heads) return;
   const int b = pair / num_qo_heads;
   const int hq = pair - b * num_qo_heads;
-  // One combined check that needs all three loads, so they are issued
-  // together (separate early exits would sink each load below the last).
-  const int stamp_batch = uniform(header[2]), stamp = uniform(header[3]);
-  const int2 info = row_info[b];
-  const int first = uniform(info.x), n = uniform(info.y);
-  const bool planned = (stamp_batch == batch) & (stamp == plan_stamp(batch, max_items));
-  if (!(planned & (n > 1) & (first >= 0) & (first + n <= max_items))) return;
+  int first, n;
+  if (dir.indptr != nullptr) {  // direct items (uniform): the row's slots from indptr
+    direct_row(dir, batch, b, first, n);
+    if (!((n > 1) & (first >= 0) & (first + n <= max_items))) return;
+  } else {
+    // One combined check that needs all three loads, so they are issued
+    // together (separate early exits would sink each load below the last).
+    const int stamp_batch = uniform(header[2]), stamp = uniform(header[3]);
+    const int2 info = row_info[b];
+    first = uniform(info.x), n = uniform(info.y);
+    const bool planned = (stamp_batch == batch) & (stamp == plan_stamp(batch, max_items));
+    if (!(planned & (n > 1) & (first >= 0) & (first + n <= max_items))) return;
+  }
 
   const int r = threadIdx.x / LPT, col = threadIdx.x % LPT;
   MergeState st{-INFINITY, 0.f, {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}};
@@ -1087,6 +1186,7 @@ struct RunArgs {
   int kv_split;  // virtual kv heads per real one (hkv counts the virtual heads)
   const int* header; const Item* items; int max_items; const int2* row_info;
   float* part_lse; float* part_o; int flags;
+  Direct dir;  // dir.indptr != nullptr: items derived from indptr (no plan kernel)
   hipStream_t stream;
 };
 
@@ -1100,22 +1200,22 @@ int launch(const RunArgs& a, const QkvIn& qin = QkvIn{}) {
                        (const T*)a.q, a.q_sb, a.q_sh, (const T*)a.kc, (const T*)a.vc, a.page_stride,
                        a.token_stride, a.head_stride, a.indices, a.last, (T*)a.o, a.o_sb, a.o_sh,
                        a.lse, a.hq, a.hkv, a.page_size, a.num_pages, a.scale_log2, a.header,
-                       a.items, a.batch, a.max_items, a.part_lse, a.part_o, qin, a.kv_split);
+                       a.items, a.batch, a.max_items, a.part_lse, a.part_o, qin, a.kv_split, a.dir);
     PL_LAUNCH_CHECK("decode_kernel");
   }
   if (!(a.flags & PL_DECODE_SKIP_MERGE)) {
     if (a.max_items <= kMergeFewItems * a.batch)
       hipLaunchKernelGGL((merge_kernel<T, D, kWave>), dim3(a.batch * a.hq), dim3(kWave), 0, a.stream,
                          a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
-                         a.batch, a.hq, a.max_items);
+                         a.batch, a.hq, a.max_items, a.dir);
     else if (a.max_items <= kMergeManyItems * a.batch)
       hipLaunchKernelGGL((merge_kernel<T, D, 4 * kWave>), dim3(a.batch * a.hq), dim3(4 * kWave), 0, a.stream,
                          a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
-                         a.batch, a.hq, a.max_items);
+                         a.batch, a.hq, a.max_items, a.dir);
     else
       hipLaunchKernelGGL((merge_kernel<T, D, 8 * kWave>), dim3(a.batch * a.hq), dim3(8 * kWave), 0, a.stream,
                          a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
-                         a.batch, a.hq, a.max_items);
+                         a.batch, a.hq, a.max_items, a.dir);
     PL_LAUNCH_CHECK("merge_kernel");
   }
   return ok();

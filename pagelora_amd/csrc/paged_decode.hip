@@ -26,6 +26,10 @@
 // Mathematics: o = softmax(q . K^T * sm_scale) . V, as the reference's
 // FlashInferAttentionBackend.run_decode (model/flashinfer/attention_backend.py
 // :120-131) obtains from FlashInfer with q/16 and sm_scale 16/sqrt(D).
+#include <cstdlib>
+#include <mutex>
+#include <unordered_map>
+
 #include "decode_kernels.h"
 
 namespace pl {
@@ -223,6 +227,39 @@ int run_multiple16_pages(const RunArgs& a, int dtype, int d, int g) {
 using namespace pl;
 using namespace pl::decode;
 
+// Direct-item plans (batches of up to kDirectMaxBatch rows): pl_decode_plan
+// launches nothing and records, per workspace, where the page table's indptr
+// lives and how to split it; the runs on that workspace pass it to their
+// kernels, which derive the items themselves.  The record is host state of
+// the library, read when a run is enqueued (or captured into a graph).
+// PAGELORA_DECODE_PLAN_KERNEL=1 keeps the plan kernel for every batch.
+namespace {
+struct DirectRec {
+  const int32_t* indptr;
+  int batch, capacity, target_items, min_chunk;
+};
+std::mutex g_direct_mutex;
+std::unordered_map<const void*, DirectRec> g_direct;
+
+bool direct_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("PAGELORA_DECODE_PLAN_KERNEL");
+    return !(e != nullptr && e[0] == '1');
+  }();
+  return on;
+}
+
+// The direct plan recorded for `workspace`, if it matches this run.
+Direct direct_for(const void* workspace, int batch, int target_items) {
+  Direct d{nullptr, 0, 1, 1};
+  std::lock_guard<std::mutex> lock(g_direct_mutex);
+  const auto it = g_direct.find(workspace);
+  if (it != g_direct.end() && it->second.batch == batch && it->second.target_items == target_items)
+    d = Direct{it->second.indptr, it->second.capacity, it->second.target_items, it->second.min_chunk};
+  return d;
+}
+}  // namespace
+
 extern "C" size_t pl_decode_workspace_size(int batch, int target_items, int num_qo_heads,
                                            int head_dim) {
   if (batch < 0 || target_items <= 0 || num_qo_heads <= 0 || head_dim <= 0) return 0;
@@ -244,6 +281,15 @@ extern "C" int pl_decode_plan(const int32_t* indptr, int batch, int indices_capa
   const Layout L = layout(batch, max_items, num_qo_heads, head_dim);
   if (L.total > workspace_bytes)
     return fail(PL_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, L.total);
+  const int min_chunk = min_chunk_pages < 1 ? 1 : min_chunk_pages;
+  {
+    std::lock_guard<std::mutex> lock(g_direct_mutex);
+    if (direct_enabled() && batch <= kDirectMaxBatch) {
+      g_direct[workspace] = DirectRec{indptr, batch, indices_capacity, target_items, min_chunk};
+      return ok();
+    }
+    g_direct.erase(workspace);
+  }
   char* ws = (char*)workspace;
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, indptr,
                      batch, indices_capacity, target_items, min_chunk_pages < 1 ? 1 : min_chunk_pages, max_items,
@@ -304,6 +350,7 @@ static int decode_run_common(const void* q, int64_t q_stride_b, int64_t q_stride
   a.row_info = (const int2*)(ws + L.row_info);
   a.flags = flags;
   a.part_lse = (float*)(ws + L.lse); a.part_o = (float*)(ws + L.partial_o);
+  a.dir = direct_for(workspace, batch, target_items);
   a.stream = (hipStream_t)stream;
   const int g = num_qo_heads / num_kv_heads;
   if (qin) {

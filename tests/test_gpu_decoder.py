@@ -396,3 +396,34 @@ def test_pool_growth_mid_generation_matches_unconstrained(gpu_device, device_tab
     assert c1 >= c0 + 1  # captured again on the grown pool
     assert torch.equal(t0, t1)
     assert torch.equal(l0, l1)
+
+
+def test_capture_with_collectable_pinned_staging_and_events(gpu_device):
+    """Graph capture while the cyclic collector holds garbage that owns pinned
+    host memory and HIP events (an earlier generator's staging left in a
+    reference cycle), with the collector set to run at almost every
+    allocation: the runner collects before capturing and keeps the collector
+    off while the stream captures, so no destructor makes a HIP call during
+    capture.  The captured run's tokens equal an eager run's."""
+    import gc
+
+    from pagelora_amd.generation import _PinnedRing
+
+    w, pool, reqs, first, _ = _setup(gpu_device)
+    for _ in range(8):
+        ring = _PinnedRing(2, (4096,), torch.int32)
+        for slot in range(2):
+            ring.record(slot)
+        ring.cycle = ring  # only the cyclic collector can free it
+    del ring
+    old = gc.get_threshold()
+    gc.set_threshold(1, 1, 1)
+    try:
+        gen = BatchGenerator(w, pool, workspace_mb=8, use_graph=True)
+        got = gen.generate(reqs, first, steps=6)
+    finally:
+        gc.set_threshold(*old)
+    assert got.used_graph and gen.graphs.disabled_reason is None
+    w2, pool2, reqs2, first2, _ = _setup(gpu_device)
+    want = BatchGenerator(w2, pool2, workspace_mb=8, use_graph=False).generate(reqs2, first2, steps=6)
+    assert torch.equal(got.tokens, want.tokens)
