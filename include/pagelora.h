@@ -652,6 +652,18 @@ int pl_weight_shuffle(const void* weight, int64_t ldw, int out_features,
                       int dtype, void* stream);
 
 /*
+ * The inverse of pl_weight_shuffle: rows 0 .. out_features of the row-major
+ * weight (row stride ldw, 16-byte aligned rows) from its shuffled copy.  The
+ * decoder keeps only the shuffled copy of its projection weights and runs
+ * this per layer into one reusable buffer when a library GEMM (prefill)
+ * needs the row-major form.  No counterpart in the reference, which keeps
+ * nn.Linear weights row-major.
+ */
+int pl_weight_unshuffle(const void* shuffled, size_t shuffled_bytes, int out_features,
+                        int in_features, void* weight, int64_t ldw, int dtype,
+                        void* stream);
+
+/*
  * out[t, n] = x[t] . W[n]^T (+ bias[n]) for t < num_tokens (<= 64) from the
  * shuffled weight of pl_weight_shuffle (same out_features / in_features).
  * x [num_tokens, in_features] with row stride ldx, out with ldo; fp32

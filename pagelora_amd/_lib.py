@@ -260,6 +260,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "pl_weight_shuffled_bytes": (_sz, [_i32, _i32]),
     "pl_weight_shuffle": (_i32, [_vp, _i64, _i32, _i32, _vp, _sz, _i32, _vp]),
+    "pl_weight_unshuffle": (_i32, [_vp, _sz, _i32, _i32, _vp, _i64, _i32, _vp]),
     "pl_linear_shuffled": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _vp, _vp, _i64, _i32, _vp]),
     "pl_linear_shuffled_split": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _i64, _i64, _i32, _vp]),
     "pl_linear_shuffled_side": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _i64, _i32, _vp, _i64, _i64,

@@ -67,6 +67,21 @@ __global__ void shuffle_kernel(const uint16_t* __restrict__ W, int64_t ldw, int 
   }
 }
 
+// The inverse of shuffle_kernel: one thread per 16-byte piece, rows < N
+// written back to the row-major W (row stride ldw).
+__global__ void unshuffle_kernel(const uint16_t* __restrict__ Ws, int N, int K, uint16_t* __restrict__ W,
+                                 int64_t ldw, int64_t pieces) {
+  const int ksteps = K / 32;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < pieces; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t blk = i / 64;
+    const int l = (int)(i % 64);
+    const int ks = (int)(blk % ksteps);
+    const int64_t n = (blk / ksteps) * 16 + l % 16;
+    const int k = ks * 32 + (l / 16) * 8;
+    if (n < N) *reinterpret_cast<uint4*>(W + n * ldw + k) = *reinterpret_cast<const uint4*>(Ws + i * 8);
+  }
+}
+
 // PARTIAL: split-K over gridDim.z workgroups per row block; workgroup z sums
 // k-steps [z*K/32/splits, ..) and writes its fp32 tile to plane z of
 // `partial` (row t at t * ldp, planes plane_stride apart) instead of `out`.
@@ -178,6 +193,26 @@ extern "C" int pl_weight_shuffle(const void* weight, int64_t ldw, int out_featur
   hipLaunchKernelGGL(shuffle_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)weight, ldw, out_features, in_features, (uint16_t*)shuffled, pieces);
   PL_LAUNCH_CHECK("shuffle_kernel");
+  return ok();
+}
+
+extern "C" int pl_weight_unshuffle(const void* shuffled, size_t shuffled_bytes, int out_features, int in_features,
+                                   void* weight, int64_t ldw, int dtype, void* stream) {
+  if (out_features <= 0 || in_features <= 0 || in_features % 32)
+    return fail(PL_ERR_INVALID, "out_features > 0 and in_features a positive multiple of 32 required");
+  if (dtype != PL_DTYPE_BF16 && dtype != PL_DTYPE_F16)
+    return fail(PL_ERR_UNSUPPORTED, "shuffled weights are F16 or BF16 (got %d)", dtype);
+  if (!weight || !shuffled) return fail(PL_ERR_INVALID, "null pointer argument");
+  if (ldw < in_features || ldw % 8 || (uintptr_t)weight % 16 || (uintptr_t)shuffled % 16)
+    return fail(PL_ERR_INVALID, "weight rows and the shuffled buffer must be 16-byte aligned");
+  const size_t need = pl_weight_shuffled_bytes(out_features, in_features);
+  if (shuffled_bytes < need)
+    return fail(PL_ERR_WORKSPACE, "shuffled buffer of %zu bytes < %zu needed", shuffled_bytes, need);
+  const int64_t pieces = (int64_t)need / 16;
+  const int64_t blocks = std::min<int64_t>((pieces + 255) / 256, 65536);
+  hipLaunchKernelGGL(unshuffle_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)shuffled, out_features, in_features, (uint16_t*)weight, ldw, pieces);
+  PL_LAUNCH_CHECK("unshuffle_kernel");
   return ok();
 }
 

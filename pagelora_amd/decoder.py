@@ -32,7 +32,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from . import fused_ops
+from . import _lib, fused_ops
 from .attention_backend import PagedDecodeAttention
 from .kv_pool import PagedKVPool, Request
 from .linear import ShuffledWeight, SplitOutput, linear_shuffled, linear_shuffled_side, linear_shuffled_split
@@ -180,6 +180,7 @@ class LayerWeights:
         self.k_norm = src.norm("k_norm", cfg.head_dim)
         self.lora = {}
         self.y_offset = {}
+        self.y_offset_base = {}  # base output rows of each projection
         for proj, fin, modules in projections(cfg):
             out_features = sum(o for _, o in modules)
             ext = torch.empty((out_features + len(modules) * n * r, fin), device=device, dtype=dtype)
@@ -192,16 +193,41 @@ class LayerWeights:
                 self.y_offset[name] = row
             setattr(self, f"w_{proj}_ext", ext)
             setattr(self, f"w_{proj}", ext[:out_features])
+            self.y_offset_base[proj] = out_features
         self.shuffled: dict[str, ShuffledWeight] = {}
         self.lora_b8: dict[str, torch.Tensor] = {}
+        self.single_copy = False  # True once the shuffled copies are the only ones
 
-    def shuffle(self) -> None:
+    def __getattr__(self, name: str):
+        # w_<proj>_ext / w_<proj> of a single-copy layer: unshuffled on demand
+        # (a fresh tensor; the hot paths use the shuffled copy or row_major())
+        if name.startswith("w_") and self.__dict__.get("single_copy"):
+            proj = name[2:-4] if name.endswith("_ext") else name[2:]
+            sw = self.__dict__["shuffled"].get(proj)
+            if sw is not None:
+                w = sw.unshuffle()
+                return w if name.endswith("_ext") else w[: self.__dict__["y_offset_base"][proj]]
+        raise AttributeError(f"{type(self).__name__!s} has no attribute {name!r}")
+
+    def shuffle(self, keep_row_major: bool = False) -> None:
         """Shuffled copies of the four [W; A] weights for the decode GEMM.
-        The row-major weights stay for prefill's library GEMM (and for the
-        reference-facing LoRA path); the copies double the layer's weight
-        memory in exchange for fully coalesced decode weight streaming."""
+
+        Unless ``keep_row_major``, the shuffled copy becomes the only one:
+        the row-major [W; A] buffers are released (the LoRA A stacks move to
+        tensors of their own), so the projection weights are stored once.
+        ``w_*_ext`` / ``w_*`` then return an unshuffled copy, and the library
+        GEMMs of prefill read the weight unshuffled into one buffer reused by
+        every projection (:func:`row_major`)."""
         for name in ("qkv", "o", "gate_up", "down"):
             self.shuffled[name] = ShuffledWeight(getattr(self, f"w_{name}_ext"))
+        if not keep_row_major:
+            for name in MODULES:
+                A, B = self.lora[name]
+                self.lora[name] = (A.clone(), B)
+            for proj, _, _ in projections(self.cfg):
+                delattr(self, f"w_{proj}_ext")
+                delattr(self, f"w_{proj}")
+            self.single_copy = True
         # o_proj's and down_proj's B in the chunked layout: their consumer,
         # the add+RMSNorm, reads a whole row's B in one workgroup and runs
         # 7.3 -> 4.9 us with it (Qwen3-8B shape, 4 rows).  The one-wave
@@ -222,7 +248,7 @@ class LayerWeights:
         r = self.cfg.lora_rank
         given = {module_key(k): v for k, v in modules.items()}
         for proj, fin, mods in projections(self.cfg):
-            ext = getattr(self, f"w_{proj}_ext")
+            ext = None if self.single_copy else getattr(self, f"w_{proj}_ext")
             for name, fout in mods:
                 A_stack, B_stack = self.lora[name]
                 if name in given:
@@ -238,7 +264,9 @@ class LayerWeights:
                     A_stack[slot].zero_()
                     B_stack[slot].zero_()
                 lo = self.y_offset[name] + slot * r
-                if proj in self.shuffled:
+                if self.single_copy:
+                    self.shuffled[proj].write_rows(A_stack[slot], lo)
+                elif proj in self.shuffled:
                     self.shuffled[proj].refresh_rows(ext, lo, lo + r)
                 if name in self.lora_b8:
                     self.lora_b8[name][slot].copy_(fused_ops.lora_b_chunk8(B_stack[slot])[0])
@@ -262,7 +290,7 @@ class LayerWeights:
         new = LayerWeights(self.cfg, n_adapters, self.device, self.dtype,
                            source=_TensorSource(given, adapters, self.device, self.dtype))
         if old.shuffled:
-            new.shuffle()
+            new.shuffle(keep_row_major=not old.single_copy)
         return new
 
     def up(self, name: str, y: "torch.Tensor | SideOutput", scale: float, adapter: int = -1) -> fused_ops.LoraUp:
@@ -278,7 +306,10 @@ class LayerWeights:
 class DecoderWeights:
     """Weights of the decoder: random (``DecoderWeights(cfg, seed=...)``) or
     given (:meth:`from_tensors`).  ``shuffle`` (default) also builds the
-    shuffled decode-GEMM copies of every projection and of the lm_head.
+    shuffled decode-GEMM copies of every projection and of the lm_head; the
+    projections' row-major weights are then released unless
+    ``keep_row_major`` (the lm_head stays row-major too: prefill's last-token
+    logits and decode steps of more than 16 rows read it).
 
     ``adapter_version`` changes whenever the adapter stacks are reallocated
     (:meth:`set_adapter` past the stacked slots); decode graphs key on it, as
@@ -287,7 +318,7 @@ class DecoderWeights:
     keeps every buffer address and needs no recapture."""
 
     def __init__(self, cfg: DecoderConfig, *, n_adapters: int = 1, device="cuda", dtype=torch.bfloat16, seed: int = 0,
-                 shuffle: bool = True, _sources=None, _top=None):
+                 shuffle: bool = True, keep_row_major: bool = False, _sources=None, _top=None):
         self.cfg = cfg
         self.dtype = dtype
         self.n_adapters = n_adapters
@@ -296,17 +327,34 @@ class DecoderWeights:
             gen = torch.Generator(device=device).manual_seed(seed)
             self.embed = (torch.randn((cfg.vocab, cfg.hidden), device=device, generator=gen) * 0.02).to(dtype)
             self.final_norm = (1.0 + 0.1 * torch.randn(cfg.hidden, device=device, generator=gen)).to(dtype)
-            self.lm_head = (torch.randn((cfg.vocab, cfg.hidden), device=device, generator=gen) * 0.02).to(dtype)
+            self._lm_head = (torch.randn((cfg.vocab, cfg.hidden), device=device, generator=gen) * 0.02).to(dtype)
             self.layers = [LayerWeights(cfg, n_adapters, device, dtype, gen) for _ in range(cfg.num_layers)]
         else:
-            self.embed, self.final_norm, self.lm_head = _top
+            self.embed, self.final_norm, self._lm_head = _top
             self.layers = [LayerWeights(cfg, n_adapters, device, dtype, source=src) for src in _sources]
         self.lora_scale = cfg.lora_alpha / cfg.lora_rank  # linear.py:41, 71
         self.lm_head_shuffled: ShuffledWeight | None = None
         if shuffle:
             for lw in self.layers:
-                lw.shuffle()
-            self.lm_head_shuffled = ShuffledWeight(self.lm_head)
+                lw.shuffle(keep_row_major=keep_row_major)
+            self.lm_head_shuffled = ShuffledWeight(self._lm_head)
+            if not keep_row_major:
+                self._lm_head = None
+
+    @property
+    def lm_head(self) -> torch.Tensor:
+        """The [vocab, hidden] lm_head (unshuffled on demand when only the
+        shuffled copy is kept)."""
+        return self._lm_head if self._lm_head is not None else self.lm_head_shuffled.unshuffle()
+
+    def logits(self, x: torch.Tensor) -> torch.Tensor:
+        """x . lm_head^T: the shuffled GEMM at decode sizes (up to 16 rows, or
+        64 when no row-major copy is kept), else the library GEMM on the
+        row-major weight."""
+        limit = _lib.PL_LINEAR_MAX_TOKENS if self._lm_head is None else DECODE_GEMM_MAX_TOKENS
+        if self.lm_head_shuffled is not None and x.shape[0] <= limit:
+            return linear_shuffled(x, self.lm_head_shuffled)
+        return F.linear(x, self._lm_head if self._lm_head is not None else unshuffled_scratch(self.lm_head_shuffled))
 
     @classmethod
     def from_tensors(cls, cfg: DecoderConfig, *, embed: torch.Tensor, final_norm: torch.Tensor,
@@ -428,7 +476,10 @@ def _project(x: torch.Tensor, lw: LayerWeights, name: str) -> "torch.Tensor | Sp
     """x . [W; A]^T: the base output and every adapter's LoRA intermediate
     (at decode batch sizes as split-K planes, or with the intermediates split
     off, for the narrow projections)."""
-    if x.shape[0] <= DECODE_GEMM_MAX_TOKENS:
+    # a single-copy layer keeps the shuffled GEMM up to 64 rows: unshuffling
+    # for the library GEMM would read the weight twice
+    limit = _lib.PL_LINEAR_MAX_TOKENS if lw.single_copy else DECODE_GEMM_MAX_TOKENS
+    if x.shape[0] <= limit:
         sw = lw.shuffled.get(name)
         if sw is not None:
             side = min(DECODE_SIDE_SPLITS.get(name, 0), sw.in_features // 32)
@@ -440,8 +491,31 @@ def _project(x: torch.Tensor, lw: LayerWeights, name: str) -> "torch.Tensor | Sp
                 return linear_shuffled_split(x, sw, splits)
             return linear_shuffled(x, sw)
         if name in ("qkv", "o"):
-            return lora_linear(x, getattr(lw, f"w_{name}_ext"), None, None)
-    return F.linear(x, getattr(lw, f"w_{name}_ext"))
+            return lora_linear(x, row_major(lw, name), None, None)
+    return F.linear(x, row_major(lw, name))
+
+
+_ROW_MAJOR_SCRATCH: dict = {}
+
+
+def row_major(lw: LayerWeights, name: str) -> torch.Tensor:
+    """The row-major [W; A] weight of projection ``name`` for a library GEMM:
+    the stored tensor, or for a single-copy layer the shuffled copy
+    unshuffled into a buffer shared by every projection of the device (stream
+    ordered: each use is enqueued after the previous one's GEMM)."""
+    if not lw.single_copy:
+        return getattr(lw, f"w_{name}_ext")
+    return unshuffled_scratch(lw.shuffled[name])
+
+
+def unshuffled_scratch(sw: ShuffledWeight) -> torch.Tensor:
+    """``sw`` unshuffled into the per-device row-major scratch buffer."""
+    key = (sw.data.device, sw.dtype)
+    need = sw.out_features * sw.in_features
+    buf = _ROW_MAJOR_SCRATCH.get(key)
+    if buf is None or buf.numel() < need:
+        buf = _ROW_MAJOR_SCRATCH[key] = torch.empty(need, dtype=sw.dtype, device=sw.data.device)
+    return sw.unshuffle(buf[:need].view(sw.out_features, sw.in_features))
 
 
 def _cols(out, n: int):
@@ -581,10 +655,7 @@ def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: Page
         pending = decode_layer_static(cfg, lw, weights.lora_scale, hidden, pending, pool.layer_cache(li),
                                       backend, ctx)
     x = _final_norm(weights, hidden, pending, ctx.adapter_ids)
-    if weights.lm_head_shuffled is not None and x.shape[0] <= DECODE_GEMM_MAX_TOKENS:
-        logits = linear_shuffled(x, weights.lm_head_shuffled)
-    else:
-        logits = F.linear(x, weights.lm_head)
+    logits = weights.logits(x)
     # greedy (sampling.py:8-15); the pick also becomes the next step's input token
     if ctx.argmax_ws is None:  # the first (eager) call allocates it, before any capture
         ctx.argmax_ws = fused_ops.greedy_argmax_workspace(logits.shape[0], logits.shape[1], logits.dtype,
@@ -650,5 +721,5 @@ def prefill(weights: DecoderWeights, pool: PagedKVPool, request: Request, tokens
             pending = _layer(cfg, lw, s, hidden, pending, ids, pos, page_of, off_of, cache, ps, attend,
                              adapter if 0 <= adapter < weights.n_adapters else -1)
         x = _final_norm(weights, hidden, pending, ids)
-        last_logits = F.linear(x[-1:], weights.lm_head)
+        last_logits = weights.logits(x[-1:])
     return last_logits

@@ -37,6 +37,40 @@ class ShuffledWeight:
     def nbytes(self) -> int:
         return self.data.numel() * self.data.element_size()
 
+    def unshuffle(self, out: torch.Tensor | None = None) -> torch.Tensor:
+        """The row-major ``[out_features, in_features]`` weight (into ``out``,
+        a tensor of that shape with unit column stride, when given)."""
+        n, k = self.out_features, self.in_features
+        if out is None:
+            out = torch.empty((n, k), dtype=self.dtype, device=self.data.device)
+        if out.shape != (n, k) or out.stride(1) != 1 or out.dtype != self.dtype:
+            raise ValueError(f"out must be [{n}, {k}] of {self.dtype} with unit column stride")
+        lib = _lib.load()
+        _lib.check(lib.pl_weight_unshuffle(self.data.data_ptr(), self.nbytes, n, k, out.data_ptr(), out.stride(0),
+                                           _lib.dtype_code(self.dtype), _lib.stream_handle(self.data.device)),
+                   "pl_weight_unshuffle")
+        return out
+
+    def write_rows(self, rows: torch.Tensor, lo: int) -> None:
+        """Replace rows ``lo .. lo + len(rows)`` with the row-major ``rows``
+        when no row-major copy of the whole weight is kept: the 16-row blocks
+        that hold them are unshuffled, patched and shuffled back."""
+        hi = lo + rows.shape[0]
+        if rows.dim() != 2 or rows.shape[1] != self.in_features or not 0 <= lo < hi <= self.out_features:
+            raise ValueError(f"rows must be [n, {self.in_features}] inside 0..{self.out_features}")
+        lo16, hi16 = lo // 16 * 16, min(-(-hi // 16) * 16, self.out_features)
+        k, es = self.in_features, self.data.element_size()
+        lib = _lib.load()
+        stream = _lib.stream_handle(self.data.device)
+        nbytes = lib.pl_weight_shuffled_bytes(hi16 - lo16, k)
+        block = torch.empty((hi16 - lo16, k), dtype=self.dtype, device=self.data.device)
+        base = self.data.data_ptr() + lo16 * k * es  # row block nb starts at element nb * 16 * K
+        _lib.check(lib.pl_weight_unshuffle(base, nbytes, hi16 - lo16, k, block.data_ptr(), k,
+                                           _lib.dtype_code(self.dtype), stream), "pl_weight_unshuffle")
+        block[lo - lo16: hi - lo16].copy_(rows)
+        _lib.check(lib.pl_weight_shuffle(block.data_ptr(), k, hi16 - lo16, k, base, nbytes,
+                                         _lib.dtype_code(self.dtype), stream), "pl_weight_shuffle")
+
     def refresh_rows(self, weight: torch.Tensor, lo: int, hi: int) -> None:
         """Re-shuffle rows ``lo .. hi`` of the row-major ``weight`` this copy
         was made from (after they changed in place): the 16-row blocks that
