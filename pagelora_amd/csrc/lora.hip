@@ -21,21 +21,25 @@
 // pl_lora_delta_groups take a two-launch path built for latency, for up to
 // four groups with their own inputs in the same two launches:
 //
-//   fast_shrink_kernel  grid (group, 256-element k-slice, 16 rank rows,
-//                  adapter): every load of the workgroup (ids, x of all
-//                  tokens, the A rows) issued at once, one MFMA chain per
-//                  token tile, the adapter's tokens' results added into a
-//                  64-bit fixed-point accumulator (order-independent, so
-//                  deterministic).
-//   fast_expand_kernel  grid (group, 64 output columns): the intermediate
-//                  (rounded to the input dtype into LDS), ids, B rows and
-//                  outputs in one round trip, MFMA per adapter over the
-//                  token tiles, out += scale * result; the group's last
-//                  workgroup clears the accumulator for the next call.
+//   fast_shrink_kernel  grid (group, 256-element k-slice, 16 rank rows):
+//                  each wave loads its 16 tokens' x slice once, the
+//                  workgroup stages every adapter's A tile once in LDS (in
+//                  the MFMA operand order), one MFMA chain per adapter keeps
+//                  the rows of the tokens that use it, and each (token,
+//                  rank) sum is added into a 64-bit fixed-point accumulator
+//                  (order-independent, so deterministic).
+//   fast_expand_kernel  grid (group, 128 output columns): the 32-rank tiles
+//                  of the intermediate its columns use (rounded to the input
+//                  dtype into LDS), ids, B rows and outputs in one round
+//                  trip, MFMA per adapter over the token tiles,
+//                  out += scale * result.
 //
 // Reference semantics: packed_ops.py:314-384 (packed A_cat / block-diagonal
 // B with the scale folded in), packed_ops.py:534-553 and
 // multilora/linear.py:226-231 (per-module F.linear(F.linear(x, A), B) * s).
+#include <algorithm>
+#include <type_traits>
+
 #include "pl_common.h"
 
 namespace pl {
@@ -101,11 +105,13 @@ __device__ __forceinline__ uint4 load8(const void* p, bool ok) {
 }
 
 // load8 without a branch: p must be readable whether or not ok holds (the
-// caller clamps it), the value is zeroed afterwards.  Branches around loads
-// make the compiler re-read kernel arguments inside each one.
+// caller clamps it), the value is zeroed afterwards with a mask (a select
+// lets the compiler skip the load in a branch, and a load inside a branch
+// makes every later wait on the load counter conservative).
 __device__ __forceinline__ uint4 load8_sel(const void* p, bool ok) {
   const uint4 v = *reinterpret_cast<const uint4*>(p);
-  return ok ? v : make_uint4(0, 0, 0, 0);
+  const uint32_t m = 0u - (uint32_t)ok;
+  return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
 }
 
 // Shrink: split-K.  Workgroup (k-slice, 16 rank rows, adapter) multiplies the
@@ -326,11 +332,16 @@ constexpr int kFastMaxAdapters = 64;
 constexpr int kFastKSlice = 256;      // k elements per shrink workgroup: 8 MFMA steps
 constexpr int kFastKSteps = kFastKSlice / 32;
 constexpr int kFastMaxSlices = 64;    // in_features <= 64 * kFastKSlice on this path
-constexpr int kExpandWaves = 4;  // 8 (128 columns) measured no faster: 30.2 vs 30.3 us per layer, per-group calls 60.9 vs 57.2
+constexpr int kShrinkAChunk = 4;      // adapters whose A tiles a shrink workgroup holds in LDS at once
+constexpr int kExpandWaves = 8;
 constexpr int kExpandThreads = kExpandWaves * 64;
 constexpr int kFastCols = 16 * kExpandWaves;  // output columns per expand workgroup (16 per wave)
 constexpr int kFastAChunk = 4;        // adapters whose B rows an expand wave holds at once
 constexpr int kFastTt = kFastMaxTokens / 16;
+constexpr int kFastMaxRank = 128;     // r_pad limit (make_group)
+// 16-byte accumulator pairs one expand thread stages per slot and 32-rank tile
+constexpr int kStagePairs = kFastMaxTokens * 32 / 2 / kExpandThreads;
+static_assert(kStagePairs * kExpandThreads * 2 == kFastMaxTokens * 32, "staging covers one 32-rank tile");
 // The shrink's slices meet in a signed 64-bit fixed-point accumulator with
 // 26 fraction bits: integer adds are associative, so the sum (and the
 // rounded intermediate) does not depend on the order the slices arrive in.
@@ -348,7 +359,7 @@ constexpr float kFixClamp = 2147483648.f;        // 2^31
 // with no wait inside either kernel: the kernel boundaries order the clear
 // against the reads.
 constexpr size_t kParityBytes = 256;
-constexpr size_t kAccSlotBytes = (size_t)kFastMaxTokens * 128 * sizeof(long long);
+constexpr size_t kAccSlotBytes = (size_t)kFastMaxTokens * kFastMaxRank * sizeof(long long);
 constexpr size_t kAccSlotPairs = kAccSlotBytes / 16;
 constexpr size_t kGeneralOffset = kParityBytes + 2 * PL_LORA_MAX_GROUPS * kAccSlotBytes;
 
@@ -359,9 +370,8 @@ struct FastGroup {
   int in_features;
   int ksplit;        // k-slices of kFastKSlice
   int n_rt;          // rank tiles of 16 rows holding real ranks
-  int shrink_begin;  // first shrink workgroup of the group
-  int expand_begin;  // first expand workgroup of the group
   int n_expand;      // expand workgroups of the group
+  int expand_begin;  // its first workgroup in the (flat) expand grid
   long long* acc;    // two slots of [tokens][r_pad] fixed point (kAccSlotBytes apart)
   int* parity;       // the slot this call's shrink adds into
 };
@@ -372,124 +382,301 @@ struct FastArgs {
   const int32_t* ids;
 };
 
-// Which group a flattened workgroup index belongs to (groups in order).
-template <bool SHRINK>
-__device__ __forceinline__ int group_of(const FastArgs& fa, int wg) {
-  int gi = 0;
-#pragma unroll
-  for (int i = 1; i < PL_LORA_MAX_GROUPS; ++i)
-    if (i < fa.n_groups && wg >= (SHRINK ? fa.grp[i].shrink_begin : fa.grp[i].expand_begin)) gi = i;
-  return gi;
+// A pointer rebuilt from pinned integer bits, marked as global memory first
+// (a pointer made straight from an integer compiles to flat accesses, which
+// wait on both the vector and the scalar memory counters).
+template <typename P>
+__device__ __forceinline__ P gptr(uint64_t u) {
+  using E = typename std::remove_pointer<P>::type;
+  return (P)(__attribute__((address_space(1))) E*)u;
+}
+
+// In an SGPR from here on and opaque to the compiler: every argument field
+// pinned at a kernel's top is loaded in one batch with one wait (otherwise
+// each is loaded next to its first use, a dependent round trip apiece), and
+// is never re-read from the argument segment later.
+template <typename V>
+__device__ __forceinline__ V pin(V v) {
+  if constexpr (sizeof(V) == 8) {
+    uint64_t u = __builtin_bit_cast(uint64_t, v);
+    asm volatile("" : "+s"(u));
+    return __builtin_bit_cast(V, u);
+  } else {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    asm volatile("" : "+s"(u));
+    return __builtin_bit_cast(V, u);
+  }
 }
 
 __device__ __forceinline__ long long to_fixed(float v) {
   return (long long)__builtin_rintf(fminf(fmaxf(v, -kFixClamp), kFixClamp) * kFixScale);
 }
 
-// Shrink: workgroup (group, k-slice, 16 rank rows, adapter), one 16-token
-// tile per wave.  All loads of the workgroup (ids, x of every token, the A
-// rows) go out at once, the wave runs one MFMA chain over its slice, and the
-// results of the adapter's tokens are added into the fixed-point
-// accumulator (device-scope atomics, nothing waits on them).
+// Row j of the group's concatenated A (adapter 0) as a byte offset from
+// module 0's A, plus the element stride between adapters; blended from the
+// module descriptors with bit masks (no per-lane indexing into them).
+struct ARow {
+  uint64_t off;    // bytes from m[0].A to A_m[0][j - rank_offset][0]
+  int64_t stride;  // elements between adapters a and a + 1 (rank_m * in_features)
+  bool ok;         // j is a real rank row
+};
+
+// The shrink's view of a group's modules (pinned argument fields).
+struct ShrinkMods {
+  const void* A[PL_LORA_MAX_MODULES];
+  int rank[PL_LORA_MAX_MODULES], roff[PL_LORA_MAX_MODULES];
+  int n;
+};
+
+template <typename T>
+__device__ __forceinline__ ARow a_row(const ShrinkMods& g, int j, int in_features) {
+  ARow r{0, 0, false};
+#pragma unroll
+  for (int m = 0; m < PL_LORA_MAX_MODULES; ++m) {
+    const bool in = (m < g.n) & (j >= g.roff[m]) & (j < g.roff[m] + g.rank[m]);
+    const uint64_t mask = 0 - (uint64_t)in;
+    const uint64_t row = (uint64_t)(uintptr_t)((const T*)g.A[m] + (int64_t)(j - g.roff[m]) * in_features);
+    r.off |= (row - (uint64_t)(uintptr_t)g.A[0]) & mask;
+    r.stride |= ((int64_t)g.rank[m] * in_features) & (int64_t)mask;
+    r.ok |= in;
+  }
+  return r;
+}
+
+// Shrink: workgroup (group, k-slice, 16 rank rows), one 16-token tile per
+// wave, every adapter.  The wave loads its tokens' x slice once; the
+// workgroup stages each adapter's 16 x kFastKSlice A tile once, in the MFMA
+// B-operand order, in LDS (kShrinkAChunk adapters at a time, the first
+// chunk's loads issued with x); per adapter the wave runs one MFMA chain and
+// keeps the rows of its tokens that use that adapter.  Each (token, rank)
+// result is then added into the fixed-point accumulator with one
+// device-scope atomic (nothing waits on it).
 template <typename T>
 __global__ __launch_bounds__(kShrinkThreads) void fast_shrink_kernel(FastArgs fa) {
-  const int gi = group_of<true>(fa, blockIdx.x);
-  const FastGroup& G = fa.grp[gi];
-  int local = blockIdx.x - G.shrink_begin;
-  const int a = local % fa.n_adapters;
-  local /= fa.n_adapters;
-  const int rt = local % G.n_rt;
-  const int ks = local / G.n_rt;
-  const int T_ = fa.tokens;
-  const int r_pad = G.g.r_pad;
-  const int par = *G.parity & 1;
-  long long* acc = G.acc + (par ? kAccSlotBytes / sizeof(long long) : 0);
-  long long* other = G.acc + (par ? 0 : kAccSlotBytes / sizeof(long long));
-
+  __shared__ __align__(16) uint4 s_a[kShrinkAChunk][kFastKSteps][kWave];
+  const FastGroup& G = fa.grp[blockIdx.y];  // grid (most workgroups of a group, groups)
+  // every argument field before the first address: loaded in one batch,
+  // then held in SGPRs (one asm statement takes them all, so there is one
+  // wait, and the compiler cannot re-read them from the argument segment)
+  ShrinkMods sm;
+  uint64_t a_ptr[PL_LORA_MAX_MODULES];
+#pragma unroll
+  for (int m = 0; m < PL_LORA_MAX_MODULES; ++m) {
+    a_ptr[m] = (uint64_t)(uintptr_t)G.g.m[m].A;
+    sm.rank[m] = G.g.m[m].rank;
+    sm.roff[m] = G.g.m[m].rank_offset;
+  }
+  sm.n = G.g.n;
+  int n_rt = G.n_rt, ksplit = G.ksplit, in_f = G.in_features, r_pad = G.g.r_pad, r_total = G.g.r_total;
+  int T_ = fa.tokens, n_ad = fa.n_adapters;
+  uint64_t gx_u = (uint64_t)(uintptr_t)G.x, acc_u = (uint64_t)(uintptr_t)G.acc;
+  uint64_t par_u = (uint64_t)(uintptr_t)G.parity, ids_u = (uint64_t)(uintptr_t)fa.ids;
+  int64_t ldx = G.ldx;
+  asm volatile(""
+               : "+s"(a_ptr[0]), "+s"(a_ptr[1]), "+s"(a_ptr[2]), "+s"(a_ptr[3]), "+s"(sm.rank[0]),
+                 "+s"(sm.rank[1]), "+s"(sm.rank[2]), "+s"(sm.rank[3]), "+s"(sm.roff[0]), "+s"(sm.roff[1]),
+                 "+s"(sm.roff[2]), "+s"(sm.roff[3]), "+s"(sm.n), "+s"(n_rt), "+s"(ksplit), "+s"(in_f),
+                 "+s"(r_pad), "+s"(r_total), "+s"(T_), "+s"(n_ad), "+s"(gx_u), "+s"(acc_u), "+s"(par_u),
+                 "+s"(ids_u), "+s"(ldx));
+#pragma unroll
+  for (int m = 0; m < PL_LORA_MAX_MODULES; ++m) sm.A[m] = gptr<const char*>(a_ptr[m]);
+  const void* gx = gptr<const char*>(gx_u);
+  long long* const gacc = gptr<long long*>(acc_u);
+  const int* const gpar = gptr<const int*>(par_u);
+  const int32_t* const ids = gptr<const int32_t*>(ids_u);
+  const int local = blockIdx.x;
+  if (local >= ksplit * n_rt) return;  // past the group's count (after the one argument batch)
+  const int rt = local % n_rt;
+  const int ks = local / n_rt;
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;   // token tile
   const int lr = lane % 16;
   const int kq = (lane / 16) * 8;
   const int t = wave * 16 + lr;           // the token of this lane's x row
   const bool t_ok = t < T_;
-  const int id_raw = fa.ids[t_ok ? t : 0];
-  const int id = t_ok ? id_raw : -1;
-
-  // rank row j -> its module's A row of adapter a (blended with bit masks,
-  // not branches, so the module fields come in a few batched scalar loads)
-  const int j = rt * 16 + lr;
-  const T* arow = (const T*)G.x;  // placeholder address; never dereferenced unless a_ok
-  bool a_ok = false;
-  uint64_t row_bits = 0;
-#pragma unroll
-  for (int m = 0; m < PL_LORA_MAX_MODULES; ++m) {
-    const Mod& M = G.g.m[m];
-    const bool in = (m < G.g.n) & (j >= M.rank_offset) & (j < M.rank_offset + M.rank);
-    const T* row = (const T*)M.A + ((int64_t)a * M.rank + (j - M.rank_offset)) * G.in_features;
-    row_bits |= (uint64_t)(uintptr_t)row & (0 - (uint64_t)in);
-    a_ok |= in;
-  }
-  if (a_ok) arow = (const T*)(uintptr_t)row_bits;
-  const T* xrow = (const T*)G.x + (int64_t)(t_ok ? t : 0) * G.ldx;
   const int k0 = ks * kFastKSlice;
-  // every load before the first MFMA; the k steps are uniform over the wave
-  // and a lane's 8-element group lies wholly inside or outside in_features
-  // (in_features % 8 == 0); out-of-range groups re-read the row's first
-  uint4 xv[kFastKSteps], av[kFastKSteps];
+
+  // staging role: pieces p = threadIdx.x + u * kShrinkThreads of an A tile,
+  // p -> rank row p / 32 of the tile, k elements (p % 32) * 8 .. +8; in LDS
+  // at k-step (p % 32) / 4, lane ((p % 32) % 4) * 16 + row
+  constexpr int kPieces = 16 * kFastKSlice / 8 / kShrinkThreads;  // 2
+  const T* a0p = (const T*)sm.A[0];
+  const T* arow[kPieces];
+  int64_t astride[kPieces];
+  bool aok[kPieces];
+  int lds_s[kPieces], lds_l[kPieces];
+#pragma unroll
+  for (int u = 0; u < kPieces; ++u) {
+    const int p = threadIdx.x + u * kShrinkThreads;
+    const int row = p / 32, kp = p % 32;
+    const int k = k0 + kp * 8;
+    const ARow ar = a_row<T>(sm, rt * 16 + row, in_f);
+    const bool ok = ar.ok & (k < in_f);
+    arow[u] = (const T*)((const char*)a0p + (ok ? ar.off : 0)) + (ok ? k : 0);
+    astride[u] = ok ? ar.stride : 0;
+    aok[u] = ok;
+    lds_s[u] = kp / 4;
+    lds_l[u] = (kp % 4) * 16 + row;
+  }
+  auto load_chunk = [&](int a_first, uint4 (&av)[kShrinkAChunk][kPieces]) {
+#pragma unroll
+    for (int c = 0; c < kShrinkAChunk; ++c)
+#pragma unroll
+      for (int u = 0; u < kPieces; ++u) {
+        const bool ok = aok[u] & (a_first + c < n_ad);
+        av[c][u] = load8_sel(arow[u] + (ok ? (int64_t)(a_first + c) * astride[u] : 0), ok);
+      }
+  };
+  // the first A chunk, then x of the wave's tokens (a lane's 8-element
+  // group lies wholly inside or outside in_features, in_features % 8 == 0;
+  // out-of-range groups re-read the row's first and are zeroed), then the ids
+  uint4 av[kShrinkAChunk][kPieces];
+  load_chunk(0, av);
+  const T* xrow = (const T*)gx + (int64_t)(t_ok ? t : 0) * ldx;
+  uint4 xv[kFastKSteps];
 #pragma unroll
   for (int s = 0; s < kFastKSteps; ++s) {
     const int k = k0 + s * 32 + kq;
-    const bool k_ok = k < G.in_features;
-    const int kc = k_ok ? k : 0;
-    xv[s] = load8_sel(xrow + kc, t_ok & k_ok);
-    av[s] = load8_sel(arow + kc, a_ok & k_ok);
+    const bool k_ok = k < in_f;
+    xv[s] = load8_sel(xrow + (k_ok ? k : 0), t_ok & k_ok);
   }
-  __builtin_amdgcn_sched_barrier(0);
-  f32x4 part = {0.f, 0.f, 0.f, 0.f};
+  const int id_raw = ids[t_ok ? t : 0];
+  const int id = t_ok ? id_raw : -1;
+  __builtin_amdgcn_sched_barrier(0);  // the first A chunk, x and ids in flight together
+  const int par = *gpar & 1;
+  long long* acc = gacc + (par ? kAccSlotBytes / sizeof(long long) : 0);
+  long long* other = gacc + (par ? 0 : kAccSlotBytes / sizeof(long long));
+
+  int id_tr[4];
 #pragma unroll
-  for (int s = 0; s < kFastKSteps; ++s) part = mfma32<T>(xv[s], av[s], part);
-  // D rows = tokens wave*16 + 4*(lane/16) + i, column = rank row j (ranks
-  // past r_total have zero A rows and add zero)
+  for (int i = 0; i < 4; ++i) id_tr[i] = __shfl(id, (lane / 16) * 4 + i);
+  f32x4 res = {0.f, 0.f, 0.f, 0.f};
+  for (int a0 = 0; a0 < n_ad; a0 += kShrinkAChunk) {
+    if (a0 > 0) {
+      load_chunk(a0, av);
+      __syncthreads();  // every wave is done with the previous chunk's tiles
+    }
+#pragma unroll
+    for (int c = 0; c < kShrinkAChunk; ++c)
+#pragma unroll
+      for (int u = 0; u < kPieces; ++u) s_a[c][lds_s[u]][lds_l[u]] = av[c][u];
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < kShrinkAChunk; ++c) {
+      const int a = a0 + c;
+      if (a >= n_ad) break;
+      f32x4 part = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < kFastKSteps; ++s) part = mfma32<T>(xv[s], s_a[c][s][lane], part);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) res[i] = id_tr[i] == a ? part[i] : res[i];
+    }
+  }
+  // D rows = tokens wave*16 + 4*(lane/16) + i, column = rank row j
+  const int j = rt * 16 + lr;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int r = (lane / 16) * 4 + i;
-    const int tr = wave * 16 + r;
-    const int id_tr = __shfl(id, r);
-    if (tr < T_ && id_tr == a && j < r_pad)
-      __hip_atomic_fetch_add(acc + (int64_t)tr * r_pad + j, to_fixed(part[i]), __ATOMIC_RELAXED,
+    const int tr = wave * 16 + (lane / 16) * 4 + i;
+    if (tr < T_ && id_tr[i] >= 0 && id_tr[i] < n_ad && j < r_total)
+      __hip_atomic_fetch_add(acc + (int64_t)tr * r_pad + j, to_fixed(res[i]), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
   }
   // this workgroup's share of clearing the other slot (all of it: an earlier
   // call may have used it with another layout)
-  const int n_wg = G.ksplit * G.n_rt * fa.n_adapters;
+  const int n_wg = ksplit * n_rt;
   const int per = (int)((kAccSlotPairs + n_wg - 1) / n_wg);
-  const int c_end = min((int)kAccSlotPairs, (blockIdx.x - G.shrink_begin + 1) * per);
-  for (int c = (blockIdx.x - G.shrink_begin) * per + threadIdx.x; c < c_end; c += kShrinkThreads)
+  const int c_end = min((int)kAccSlotPairs, (local + 1) * per);
+  for (int c = local * per + threadIdx.x; c < c_end; c += kShrinkThreads)
     *reinterpret_cast<longlong2*>(other + 2 * (int64_t)c) = longlong2{0, 0};
 }
 
-// Expand: workgroup (group, 64 output columns), every adapter; NKT: the
-// largest r_pad / 32 of the launch's groups.  One round trip for all of its loads:
-// the fixed-point intermediate of every token, the ids and outputs of the
-// wave's rows, the B rows of the first adapters.  The intermediate is
-// rounded to the input dtype into LDS (as the reference's F.linear returns
-// it); per adapter an MFMA over the token tiles, the result kept for the
-// rows of that adapter; out = out + scale * delta for every row with an
-// adapter.  The group's last workgroup to arrive clears the accumulator for
-// the next call (every workgroup has read it by then).
-template <typename T, typename OT, int NKT>
+// The 32-rank tiles [lo, hi] that the modules of columns c_first .. c_last
+// (inside the group's columns) use; modules are ordered by both column and
+// rank offset, so the first and last columns' modules bound the range.
+// The expand's view of a group's modules (pinned argument fields).
+struct ExpandMods {
+  uint64_t B[PL_LORA_MAX_MODULES], out[PL_LORA_MAX_MODULES];
+  int64_t ldo[PL_LORA_MAX_MODULES];
+  uint32_t scale[PL_LORA_MAX_MODULES];  // float bits
+  int rank[PL_LORA_MAX_MODULES], roff[PL_LORA_MAX_MODULES], outf[PL_LORA_MAX_MODULES], ooff[PL_LORA_MAX_MODULES];
+  int n;
+};
+
+__device__ __forceinline__ void rank_tiles(const ExpandMods& g, int c_first, int c_last, int& lo, int& hi) {
+  lo = 0;
+  hi = 0;
+#pragma unroll
+  for (int m = 0; m < PL_LORA_MAX_MODULES; ++m) {
+    const bool f = (m < g.n) & (c_first >= g.ooff[m]) & (c_first < g.ooff[m] + g.outf[m]);
+    const bool l = (m < g.n) & (c_last >= g.ooff[m]) & (c_last < g.ooff[m] + g.outf[m]);
+    lo |= (g.roff[m] / 32) & -(int)f;
+    hi |= ((g.roff[m] + g.rank[m] - 1) / 32) & -(int)l;
+  }
+}
+
+// Expand: workgroup (group, 128 output columns), every adapter; NKT: the
+// most 32-rank tiles any wave's 16 columns use (1 when every module's ranks
+// sit in one tile).  The workgroup stages only the tiles its columns use:
+// the fixed-point intermediate of every token (both slots, one of which the
+// shrink cleared), rounded to the input dtype into LDS as the reference's
+// F.linear returns it.  Those loads, the ids, the B rows of the first
+// adapters and the outputs go out together (one round trip).  Per token
+// tile and adapter an MFMA over the wave's tiles gives scale * y . B^T for
+// the wave's 16 columns, kept for the rows of that adapter; the deltas meet
+// in LDS, and each thread then adds them into two 8-column chunks of one
+// output row (16-byte loads and stores; the host routes outputs that are not
+// 16-byte aligned in 8-column chunks to the general path).
+template <typename OT>
+struct OutChunk {  // 8 consecutive outputs
+  static constexpr int kWords = 8 * sizeof(OT) / 16;
+  uint4 w[kWords];
+};
+
+template <typename T, typename OT, int NKT, bool MANY>
 __global__ __launch_bounds__(kExpandThreads) void fast_expand_kernel(FastArgs fa) {
-  constexpr int RP = NKT * 32;                         // the largest r_pad
-  constexpr int kStage = kFastMaxTokens * RP / 2 / kExpandThreads;  // 16-byte accumulator loads per thread
-  __shared__ __align__(16) uint16_t s_y[kFastMaxTokens][RP + 8];  // +8 keeps rows 16-byte aligned
-  const int gi = group_of<false>(fa, blockIdx.x);
+  __shared__ __align__(16) uint16_t s_y[kFastMaxTokens][kFastMaxRank + 8];  // +8 keeps rows 16-byte aligned
+  __shared__ __align__(16) float s_d[kFastMaxTokens][kFastCols + 4];        // +4: rows start on other banks
+  // flat grid, groups in order (a 2-D grid pads every group to the largest:
+  // the idle workgroups slow the dispatch of the rest)
+  int gi = 0;
+#pragma unroll
+  for (int i = 1; i < PL_LORA_MAX_GROUPS; ++i)
+    if (i < fa.n_groups && (int)blockIdx.x >= fa.grp[i].expand_begin) gi = i;
   const FastGroup& G = fa.grp[gi];
-  const int ct = blockIdx.x - G.expand_begin;
-  const int T_ = fa.tokens;
+  // every argument field before the first address: loaded in one batch,
+  // then held in SGPRs (the first asm statement waits for every load issued
+  // before it, and the compiler cannot re-read them from the argument segment)
+  ExpandMods em;
+#pragma unroll
+  for (int m = 0; m < PL_LORA_MAX_MODULES; ++m) {
+    const Mod& M = G.g.m[m];
+    em.B[m] = (uint64_t)(uintptr_t)M.B;
+    em.out[m] = (uint64_t)(uintptr_t)M.out;
+    em.ldo[m] = M.ldo;
+    em.scale[m] = __float_as_uint(M.scale);
+    em.rank[m] = M.rank;
+    em.roff[m] = M.rank_offset;
+    em.outf[m] = M.out_features;
+    em.ooff[m] = M.out_offset;
+  }
+  em.n = G.g.n;
+  int e_begin = G.expand_begin, r_pad = G.g.r_pad, out_total = G.g.out_total, T_ = fa.tokens, n_ad = fa.n_adapters;
+  uint64_t acc_u = (uint64_t)(uintptr_t)G.acc, par_u = (uint64_t)(uintptr_t)G.parity;
+  uint64_t ids_u = (uint64_t)(uintptr_t)fa.ids;
+  asm volatile(""
+               : "+s"(em.B[0]), "+s"(em.B[1]), "+s"(em.B[2]), "+s"(em.B[3]), "+s"(em.out[0]), "+s"(em.out[1]),
+                 "+s"(em.out[2]), "+s"(em.out[3]), "+s"(em.ldo[0]), "+s"(em.ldo[1]), "+s"(em.ldo[2]),
+                 "+s"(em.ldo[3]), "+s"(em.scale[0]), "+s"(em.scale[1]), "+s"(em.scale[2]), "+s"(em.scale[3]),
+                 "+s"(em.rank[0]), "+s"(em.rank[1]), "+s"(em.rank[2]), "+s"(em.rank[3]));
+  asm volatile(""
+               : "+s"(em.roff[0]), "+s"(em.roff[1]), "+s"(em.roff[2]), "+s"(em.roff[3]), "+s"(em.outf[0]),
+                 "+s"(em.outf[1]), "+s"(em.outf[2]), "+s"(em.outf[3]), "+s"(em.ooff[0]), "+s"(em.ooff[1]),
+                 "+s"(em.ooff[2]), "+s"(em.ooff[3]), "+s"(em.n), "+s"(e_begin), "+s"(r_pad), "+s"(out_total),
+                 "+s"(T_), "+s"(n_ad), "+s"(acc_u), "+s"(par_u), "+s"(ids_u));
+  const int32_t* const ids = gptr<const int32_t*>(ids_u);
+  const int ct = blockIdx.x - e_begin;
   const int n_tt = (T_ + 15) / 16;
-  const int n_ad = fa.n_adapters;
-  const int r_pad = G.g.r_pad;
-  const int n_kt = r_pad / 32;
+  const int c0 = ct * kFastCols;
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -497,146 +684,208 @@ __global__ __launch_bounds__(kExpandThreads) void fast_expand_kernel(FastArgs fa
   const int kq = (lane / 16) * 8;
   const int tile = ct * kExpandWaves + wave;
   const int o = tile * 16 + lr;  // this lane's output column (concatenated space)
-  const long long* accp = G.acc;
-
-  // the accumulator loads go out first (they gate the barrier): both slots,
-  // one of which the shrink cleared
-  const int n_pairs = T_ * r_pad / 2;
+  const long long* accp = gptr<const long long*>(acc_u);
   constexpr int64_t kSlot = kAccSlotBytes / sizeof(long long);
-  longlong2 av2[kStage], bv2[kStage];
+
+  // the workgroup's tiles; the first one's accumulator loads go out first
+  int kt_lo, kt_hi;
+  rank_tiles(em, c0, min(c0 + kFastCols, out_total) - 1, kt_lo, kt_hi);
+  auto stage_load = [&](int kt, longlong2 (&av)[kStagePairs], longlong2 (&bv)[kStagePairs]) {
 #pragma unroll
-  for (int u = 0; u < kStage; ++u) {
-    const int c = u * kExpandThreads + threadIdx.x;
-    const int64_t off = 2 * (int64_t)(c < n_pairs ? c : 0);
-    av2[u] = *reinterpret_cast<const longlong2*>(accp + off);
-    bv2[u] = *reinterpret_cast<const longlong2*>(accp + kSlot + off);
-  }
-  // ids of the lane's rows (4*(lane/16) + i of each tile)
-  int idr[kFastTt][4];
-#pragma unroll
-  for (int tt = 0; tt < kFastTt; ++tt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tr = tt * 16 + (lane / 16) * 4 + i;
-      const int v = fa.ids[tr < T_ ? tr : 0];
-      idr[tt][i] = tr < T_ ? v : -1;
+    for (int u = 0; u < kStagePairs; ++u) {
+      const int p = u * kExpandThreads + threadIdx.x;
+      const int tk = p / 16, j2 = kt * 32 + 2 * (p % 16);
+      const int64_t off = tk < T_ ? (int64_t)tk * r_pad + j2 : 0;
+      av[u] = *reinterpret_cast<const longlong2*>(accp + off);
+      bv[u] = *reinterpret_cast<const longlong2*>(accp + kSlot + off);
     }
+  };
+  auto stage_store = [&](int kt, const longlong2 (&av)[kStagePairs], const longlong2 (&bv)[kStagePairs]) {
+#pragma unroll
+    for (int u = 0; u < kStagePairs; ++u) {
+      const int p = u * kExpandThreads + threadIdx.x;
+      const int tk = p / 16, j2 = kt * 32 + 2 * (p % 16);
+      if (tk < T_) {
+        const long long x0 = av[u].x + bv[u].x, x1 = av[u].y + bv[u].y;
+        const uint16_t lo = __builtin_bit_cast(uint16_t, from_float<T>((float)((double)x0 * kFixInv)));
+        const uint16_t hi = __builtin_bit_cast(uint16_t, from_float<T>((float)((double)x1 * kFixInv)));
+        *reinterpret_cast<uint32_t*>(&s_y[tk][j2]) = lo | ((uint32_t)hi << 16);
+      }
+    }
+  };
+  // lane l holds token l's adapter (tokens <= 64 = the wave); -1: none.
+  // Issued first: the counter of outstanding loads drains in issue order,
+  // so the staging's wait for the accumulator then covers the ids too.
+  const int id_raw = ids[lane < T_ ? lane : 0];
+  longlong2 av2[kStagePairs], bv2[kStagePairs];
+  stage_load(kt_lo, av2, bv2);
+  __builtin_amdgcn_sched_barrier(0);  // these first: the staging then waits for them alone
+
+  // the read-modify-write role: chunks q = threadIdx.x + u * kExpandThreads,
+  // token row q / 16, columns c0 + (q % 16) * 8 .. +8, each inside one module
+  constexpr int kChunks = kFastMaxTokens * kFastCols / 8 / kExpandThreads;  // 2
+  OutChunk<OT> cur[kChunks];
+  OT* cptr[kChunks];
+  bool cok[kChunks];
+#pragma unroll
+  for (int u = 0; u < kChunks; ++u) {
+    const int q = threadIdx.x + u * kExpandThreads;
+    const int tk = q / 16, c = c0 + (q % 16) * 8;
+    uint64_t off = 0, ld = 0;
+    int ooff = 0;
+    bool in_any = false;
+#pragma unroll
+    for (int m = 0; m < PL_LORA_MAX_MODULES; ++m) {
+      const bool in = (m < em.n) & (c >= em.ooff[m]) & (c < em.ooff[m] + em.outf[m]);
+      const uint64_t mask = 0 - (uint64_t)in;
+      off |= (em.out[m] - em.out[0]) & mask;
+      ld |= (uint64_t)em.ldo[m] & mask;
+      ooff |= em.ooff[m] & (int)mask;
+      in_any |= in;
+    }
+    // the address needs no id (the id only decides the store)
+    cok[u] = in_any & (tk < T_);
+    cptr[u] = (OT*)(gptr<char*>(em.out[0]) + (cok[u] ? (int64_t)off : 0)) +
+              (cok[u] ? (int64_t)tk * (int64_t)ld + (c - ooff) : 0);
+#pragma unroll
+    for (int w = 0; w < OutChunk<OT>::kWords; ++w) cur[u].w[w] = reinterpret_cast<const uint4*>(cptr[u])[w];
+  }
 
   // The lane's module, blended from the four (uniform) module descriptors
   // with bit masks: a per-lane index into them would read the kernel
   // arguments with dependent vector loads, and a select lets the compiler
   // sink each field's load into a branch of its own (one wait apiece).
-  // Pointers are blended as byte offsets from module 0's, so they stay
-  // global-memory pointers to the compiler (no flat accesses).
-  const Mod& M0 = G.g.m[0];
+  // B is addressed as a byte offset from module 0's, so it stays a
+  // global-memory pointer to the compiler (no flat accesses).
   bool has_mod = false;
-  uint64_t b_off = 0, o_off = 0, ldo_bits = 0;
+  uint64_t b_off = 0;
   uint32_t scale_bits = 0;
   int m_rank = 0, m_roff = 0, m_out = 0, m_ooff = 0;
 #pragma unroll
   for (int m = 0; m < PL_LORA_MAX_MODULES; ++m) {
-    const Mod& M = G.g.m[m];
-    const bool in = (m < G.g.n) & (o >= M.out_offset) & (o < M.out_offset + M.out_features);
+    const bool in = (m < em.n) & (o >= em.ooff[m]) & (o < em.ooff[m] + em.outf[m]);
     const uint64_t mask = 0 - (uint64_t)in;
     has_mod |= in;
-    b_off |= ((uint64_t)(uintptr_t)M.B - (uint64_t)(uintptr_t)M0.B) & mask;
-    o_off |= ((uint64_t)(uintptr_t)M.out - (uint64_t)(uintptr_t)M0.out) & mask;
-    ldo_bits |= (uint64_t)M.ldo & mask;
-    scale_bits |= __float_as_uint(M.scale) & (uint32_t)mask;
-    m_rank |= M.rank & (int)mask;
-    m_roff |= M.rank_offset & (int)mask;
-    m_out |= M.out_features & (int)mask;
-    m_ooff |= M.out_offset & (int)mask;
+    b_off |= (em.B[m] - em.B[0]) & mask;
+    scale_bits |= em.scale[m] & (uint32_t)mask;
+    m_rank |= em.rank[m] & (int)mask;
+    m_roff |= em.roff[m] & (int)mask;
+    m_out |= em.outf[m] & (int)mask;
+    m_ooff |= em.ooff[m] & (int)mask;
   }
-  const T* bbase = (const T*)((const char*)M0.B + (int64_t)b_off);
-  // (a lane past the group's columns points at module 0's first output, which it never writes)
-  OT* out_col = (OT*)((char*)M0.out + (int64_t)o_off) + (has_mod ? o - m_ooff : 0);
-  const int64_t ldo = (int64_t)ldo_bits;
   const float scale = __uint_as_float(scale_bits);
+  // the wave's tiles: kw_lo .. kw_hi (at most NKT), none for a wave past the columns
+  int kw_lo = 0, kw_hi = -1;
+  if (tile * 16 < out_total) rank_tiles(em, tile * 16, min(tile * 16 + 16, out_total) - 1, kw_lo, kw_hi);
 
-  // B operand of adapter a for every 32-wide k tile: B_m[a][o_local][j -
+  // B operand of adapter a for the wave's tile kw_lo + k: B_m[a][o_local][j -
   // rank_offset] for j inside the column's module, zero elsewhere.  Ranks
   // and rank offsets are multiples of 8 on this path, so a lane's 8 ranks
   // lie wholly inside or outside its module.
   auto load_b = [&](int a, uint4 (&bop)[NKT]) {
     const bool a_ok = a < n_ad;
-    const T* brow = bbase + ((int64_t)(a_ok ? a : 0) * m_out + (has_mod ? o - m_ooff : 0)) * m_rank;
+    const T* brow = (const T*)(gptr<const char*>(em.B[0]) + (int64_t)b_off) +
+                    ((int64_t)(a_ok ? a : 0) * m_out + (has_mod ? o - m_ooff : 0)) * m_rank;
 #pragma unroll
-    for (int kt = 0; kt < NKT; ++kt) {
-      const int j0 = kt * 32 + kq - m_roff;  // local rank index of element 0
+    for (int k = 0; k < NKT; ++k) {
+      const int j0 = (kw_lo + k) * 32 + kq - m_roff;  // local rank index of element 0
       const bool ok = (j0 >= 0) & (j0 < m_rank) & has_mod & a_ok;
-      bop[kt] = load8_sel(brow + (ok ? j0 : 0), ok);
+      bop[k] = load8_sel(brow + (ok ? j0 : 0), ok);
     }
   };
   uint4 bop[kFastAChunk][NKT];
 #pragma unroll
   for (int u = 0; u < kFastAChunk; ++u) load_b(u, bop[u]);
-  // the wave's outputs of every token; rows that do not exist re-read a
-  // valid output whose value goes unused (no select on the loaded value: it
-  // would put each load in a branch)
-  OT cur[kFastTt][4];
-#pragma unroll
-  for (int tt = 0; tt < kFastTt; ++tt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tr = tt * 16 + (lane / 16) * 4 + i;
-      cur[tt][i] = out_col[(has_mod & (tr < T_)) ? (int64_t)tr * ldo : 0];
-    }
   __builtin_amdgcn_sched_barrier(0);  // every load of the workgroup in flight
 
-  // the intermediate into LDS: one rounding to T per value
-#pragma unroll
-  for (int u = 0; u < kStage; ++u) {
-    const int c = u * kExpandThreads + threadIdx.x;
-    if (c < n_pairs) {
-      const int tk = c / (r_pad / 2), j2 = 2 * (c % (r_pad / 2));
-      const long long x0 = av2[u].x + bv2[u].x, x1 = av2[u].y + bv2[u].y;
-      const uint16_t lo = __builtin_bit_cast(uint16_t, from_float<T>((float)((double)x0 * kFixInv)));
-      const uint16_t hi = __builtin_bit_cast(uint16_t, from_float<T>((float)((double)x1 * kFixInv)));
-      *reinterpret_cast<uint32_t*>(&s_y[tk][j2]) = lo | ((uint32_t)hi << 16);
-    }
+  // the intermediate into LDS: one rounding to T per value; further tiles
+  // (a workgroup whose columns straddle modules of different tiles) one
+  // round trip each
+  stage_store(kt_lo, av2, bv2);
+  for (int kt = kt_lo + 1; kt <= kt_hi; ++kt) {
+    stage_load(kt, av2, bv2);
+    stage_store(kt, av2, bv2);
   }
   __syncthreads();
   // the next call's shrink adds into the other slot (no expand workgroup
   // reads the parity, so the flip can go out at any time)
-  if (ct == 0 && threadIdx.x == 0) *G.parity ^= 1;
+  if (ct == 0 && threadIdx.x == 0) *gptr<int*>(par_u) ^= 1;
 
-  float delta[kFastTt][4];
+  // the adapter of the lane's y row in each token tile (row tt*16 + lr: the
+  // MFMA's A operand), and of its chunks' rows
+  const int id_lane = (lane < T_ && id_raw >= 0 && id_raw < n_ad) ? id_raw : -1;
+  int idr[kFastTt];
 #pragma unroll
-  for (int tt = 0; tt < kFastTt; ++tt)
+  for (int tt = 0; tt < kFastTt; ++tt) idr[tt] = __shfl(id_lane, tt * 16 + lr);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) delta[tt][i] = 0.f;
-  for (int a0 = 0; a0 < n_ad; a0 += kFastAChunk) {
-    if (a0 > 0) {
+  for (int u = 0; u < kChunks; ++u)
+    cok[u] = cok[u] & (__shfl(id_lane, ((int)threadIdx.x + u * kExpandThreads) / 16) >= 0);
+
+  // Per token tile and adapter: the y rows of that adapter's tokens (the
+  // others zeroed) times the adapter's B, every adapter accumulated into one
+  // MFMA result.  A row gets its own adapter's product plus exact zeros, and
+  // a row without an adapter stays zero.
+  f32x4 acc4[kFastTt];
 #pragma unroll
-      for (int u = 0; u < kFastAChunk; ++u) load_b(a0 + u, bop[u]);
-    }
+  for (int tt = 0; tt < kFastTt; ++tt) acc4[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto apply_chunk = [&](int a0, const uint4 (&bc)[kFastAChunk][NKT]) {
 #pragma unroll
-    for (int u = 0; u < kFastAChunk; ++u) {
+    for (int tt = 0; tt < kFastTt; ++tt) {
+      if (tt >= n_tt) break;
+      uint4 yv[NKT];
 #pragma unroll
-      for (int tt = 0; tt < kFastTt; ++tt) {
-        if (tt >= n_tt) break;
-        f32x4 r4 = {0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < NKT; ++k)
+        yv[k] = *reinterpret_cast<const uint4*>(&s_y[tt * 16 + lr][min(kw_lo + k, kFastMaxRank / 32 - 1) * 32 + kq]);
 #pragma unroll
-        for (int kt = 0; kt < NKT; ++kt) {
-          if (kt >= n_kt) break;  // the group's own rank tiles (uniform)
-          const uint4 yv = *reinterpret_cast<const uint4*>(&s_y[tt * 16 + lr][kt * 32 + kq]);
-          r4 = mfma32<T>(yv, bop[u][kt], r4);
+      for (int u = 0; u < kFastAChunk; ++u) {
+        const uint32_t m = 0u - (uint32_t)(idr[tt] == a0 + u);
+#pragma unroll
+        for (int k = 0; k < NKT; ++k) {
+          if (kw_lo + k > kw_hi) break;  // the wave's own tiles (uniform)
+          const uint4 ym = make_uint4(yv[k].x & m, yv[k].y & m, yv[k].z & m, yv[k].w & m);
+          acc4[tt] = mfma32<T>(ym, bc[u][k], acc4[tt]);
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) delta[tt][i] = idr[tt][i] == a0 + u ? scale * r4[i] : delta[tt][i];
       }
     }
+  };
+  apply_chunk(0, bop);
+  // MANY (more adapters than one chunk, a kernel of its own so the common
+  // case keeps its registers): a round trip per further chunk, its B rows in
+  // registers of their own
+#pragma unroll 1
+  for (int a0 = kFastAChunk; MANY && a0 < n_ad; a0 += kFastAChunk) {
+    // opaque to the compiler each pass: otherwise it hoists per-(row,
+    // adapter) comparisons out of the loop and keeps them all live
+#pragma unroll
+    for (int tt = 0; tt < kFastTt; ++tt) asm volatile("" : "+v"(idr[tt]));
+    asm volatile("" : "+v"(b_off), "+v"(m_out), "+v"(m_rank), "+v"(m_roff), "+v"(m_ooff));
+    uint4 bnext[kFastAChunk][NKT];
+#pragma unroll
+    for (int u = 0; u < kFastAChunk; ++u) load_b(a0 + u, bnext[u]);
+    apply_chunk(a0, bnext);
   }
+  // the deltas of the wave's columns into LDS, then each thread's chunks
 #pragma unroll
   for (int tt = 0; tt < kFastTt; ++tt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool mine = has_mod & (idr[tt][i] >= 0) & (idr[tt][i] < n_ad);
-      if (mine)
-        out_col[(int64_t)(tt * 16 + (lane / 16) * 4 + i) * ldo] =
-            from_float<OT>(to_float<OT>(cur[tt][i]) + delta[tt][i]);
+    for (int i = 0; i < 4; ++i) s_d[tt * 16 + (lane / 16) * 4 + i][wave * 16 + lr] = scale * acc4[tt][i];
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kChunks; ++u) {
+    const int q = threadIdx.x + u * kExpandThreads;
+    if (cok[u]) {
+      const float4 d0 = *reinterpret_cast<const float4*>(&s_d[q / 16][(q % 16) * 8]);
+      const float4 d1 = *reinterpret_cast<const float4*>(&s_d[q / 16][(q % 16) * 8 + 4]);
+      const float d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+      OutChunk<OT> r;
+      const OT* cv = reinterpret_cast<const OT*>(cur[u].w);
+      OT* rv = reinterpret_cast<OT*>(r.w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rv[e] = from_float<OT>(to_float<OT>(cv[e]) + d[e]);
+#pragma unroll
+      for (int w = 0; w < OutChunk<OT>::kWords; ++w) reinterpret_cast<uint4*>(cptr[u])[w] = r.w[w];
     }
+  }
 }
 
 // ------------------------------------------------------------ host side ---
@@ -805,7 +1054,8 @@ struct DeltaPlan {
   FastArgs fa;
   Group g[PL_LORA_MAX_GROUPS];  // general path
   size_t need;
-  int shrink_total, expand_total;
+  int shrink_x;  // shrink grid x: the most workgroups any group needs (y: groups)
+  int expand_x;  // expand grid: every group's workgroups in order
 };
 
 static int plan_delta(const pl_lora_group* groups, int n_groups, int tokens, int n_adapters, int dtype,
@@ -816,12 +1066,17 @@ static int plan_delta(const pl_lora_group* groups, int n_groups, int tokens, int
   if (tokens < 0 || tokens > kMaxTokens)
     return fail(PL_ERR_INVALID, "num_tokens must be 0..%d (got %d)", kMaxTokens, tokens);
   if (n_adapters < 1 || n_adapters > 65535) return fail(PL_ERR_INVALID, "num_adapters must be 1..65535");
-  // the decode path: decode sizes, ranks of a multiple of 8, 16-byte aligned B
+  // the decode path: decode sizes, ranks of a multiple of 8, 16-byte aligned
+  // B, outputs in 16-byte aligned 8-column chunks (out_features and ldo
+  // multiples of 8)
   P->fast = tokens <= kFastMaxTokens && n_adapters <= kFastMaxAdapters;
   for (int i = 0; i < n_groups && groups != nullptr; ++i) {
     P->fast = P->fast && groups[i].in_features <= kFastMaxSlices * kFastKSlice;
-    for (int m = 0; m < groups[i].num_modules && groups[i].modules != nullptr; ++m)
-      P->fast = P->fast && groups[i].modules[m].rank % 8 == 0 && (uintptr_t)groups[i].modules[m].B % 16 == 0;
+    for (int m = 0; m < groups[i].num_modules && groups[i].modules != nullptr; ++m) {
+      const pl_lora_module& md = groups[i].modules[m];
+      P->fast = P->fast && md.rank % 8 == 0 && (uintptr_t)md.B % 16 == 0 && md.out_features % 8 == 0 &&
+                md.ldo % 8 == 0 && (uintptr_t)md.out % 16 == 0;
+    }
   }
   size_t general = 0;
   int sb = 0, eb = 0;
@@ -841,10 +1096,9 @@ static int plan_delta(const pl_lora_group* groups, int n_groups, int tokens, int
     F.in_features = gr.in_features;
     F.ksplit = (gr.in_features + kFastKSlice - 1) / kFastKSlice;
     F.n_rt = (F.g.r_total + 15) / 16;
-    F.shrink_begin = sb;
-    F.expand_begin = eb;
     F.n_expand = (F.g.out_total + kFastCols - 1) / kFastCols;
-    sb += F.ksplit * F.n_rt * n_adapters;
+    sb = std::max(sb, F.ksplit * F.n_rt);
+    F.expand_begin = eb;
     eb += F.n_expand;
     F.parity = (int*)(ws + (size_t)i * sizeof(int));
     F.acc = (long long*)(ws + kParityBytes + (size_t)i * 2 * kAccSlotBytes);
@@ -852,8 +1106,8 @@ static int plan_delta(const pl_lora_group* groups, int n_groups, int tokens, int
   P->fa.n_groups = n_groups;
   P->fa.tokens = tokens;
   P->fa.n_adapters = n_adapters;
-  P->shrink_total = sb;
-  P->expand_total = eb;
+  P->shrink_x = sb;
+  P->expand_x = eb;
   P->need = P->fast ? kParityBytes + (size_t)n_groups * 2 * kAccSlotBytes : kGeneralOffset + general;
   (void)dtype;
   return PL_OK;
@@ -866,18 +1120,18 @@ extern "C" size_t pl_lora_delta_workspace_size(const pl_lora_group* groups_h, in
   return P.need;
 }
 
-template <typename T, int NKT>
+template <typename T, int NKT, bool MANY>
 static int launch_expand_fast(const DeltaPlan& P, int out_dtype, hipStream_t stream) {
-  const dim3 grid(P.expand_total);
+  const dim3 grid(P.expand_x);
   switch (out_dtype) {
     case PL_DTYPE_F32:
-      hipLaunchKernelGGL((fast_expand_kernel<T, float, NKT>), grid, dim3(kExpandThreads), 0, stream, P.fa);
+      hipLaunchKernelGGL((fast_expand_kernel<T, float, NKT, MANY>), grid, dim3(kExpandThreads), 0, stream, P.fa);
       break;
     case PL_DTYPE_F16:
-      hipLaunchKernelGGL((fast_expand_kernel<T, f16_t, NKT>), grid, dim3(kExpandThreads), 0, stream, P.fa);
+      hipLaunchKernelGGL((fast_expand_kernel<T, f16_t, NKT, MANY>), grid, dim3(kExpandThreads), 0, stream, P.fa);
       break;
     case PL_DTYPE_BF16:
-      hipLaunchKernelGGL((fast_expand_kernel<T, bf16_t, NKT>), grid, dim3(kExpandThreads), 0, stream, P.fa);
+      hipLaunchKernelGGL((fast_expand_kernel<T, bf16_t, NKT, MANY>), grid, dim3(kExpandThreads), 0, stream, P.fa);
       break;
     default:
       return fail(PL_ERR_UNSUPPORTED, "out_dtype %d", out_dtype);
@@ -886,12 +1140,45 @@ static int launch_expand_fast(const DeltaPlan& P, int out_dtype, hipStream_t str
   return PL_OK;
 }
 
+template <typename T, int NKT>
+static int launch_expand_fast(const DeltaPlan& P, int out_dtype, hipStream_t stream) {
+  return P.fa.n_adapters > kFastAChunk ? launch_expand_fast<T, NKT, true>(P, out_dtype, stream)
+                                       : launch_expand_fast<T, NKT, false>(P, out_dtype, stream);
+}
+
+// The most 32-rank tiles the modules of any 16 consecutive output columns
+// (one expand wave) use: a wave inside a module uses that module's tiles,
+// and only the waves holding a module's first or last column can reach into
+// a neighbour.
+static int max_wave_tiles(const Group& g) {
+  auto span = [&](int c_first, int c_last) {
+    int lo = 0, hi = 0;
+    for (int m = 0; m < g.n; ++m) {
+      const Mod& M = g.m[m];
+      if (c_first >= M.out_offset && c_first < M.out_offset + M.out_features) lo = M.rank_offset / 32;
+      if (c_last >= M.out_offset && c_last < M.out_offset + M.out_features) hi = (M.rank_offset + M.rank - 1) / 32;
+    }
+    return hi - lo + 1;
+  };
+  int best = 1;
+  for (int m = 0; m < g.n; ++m) {
+    const Mod& M = g.m[m];
+    best = std::max(best, span(M.out_offset, M.out_offset + M.out_features - 1));
+    for (const int c : {M.out_offset, M.out_offset + M.out_features - 1}) {
+      const int w0 = c / 16 * 16;
+      best = std::max(best, span(w0, std::min(w0 + 15, g.out_total - 1)));
+    }
+  }
+  return best;
+}
+
 template <typename T>
 static int launch_fast(const DeltaPlan& P, int out_dtype, hipStream_t stream) {
-  hipLaunchKernelGGL(fast_shrink_kernel<T>, dim3(P.shrink_total), dim3(kShrinkThreads), 0, stream, P.fa);
+  hipLaunchKernelGGL(fast_shrink_kernel<T>, dim3(P.shrink_x, P.fa.n_groups), dim3(kShrinkThreads), 0, stream,
+                     P.fa);
   PL_LAUNCH_CHECK("lora fast_shrink_kernel");
   int nkt = 1;
-  for (int i = 0; i < P.fa.n_groups; ++i) nkt = nkt > P.fa.grp[i].g.r_pad / 32 ? nkt : P.fa.grp[i].g.r_pad / 32;
+  for (int i = 0; i < P.fa.n_groups; ++i) nkt = std::max(nkt, max_wave_tiles(P.fa.grp[i].g));
   switch (nkt) {
     case 1: return launch_expand_fast<T, 1>(P, out_dtype, stream);
     case 2: return launch_expand_fast<T, 2>(P, out_dtype, stream);
