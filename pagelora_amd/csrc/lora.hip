@@ -28,7 +28,7 @@
 //                  the rows of the tokens that use it, and each (token,
 //                  rank) sum is added into a 64-bit fixed-point accumulator
 //                  (order-independent, so deterministic).
-//   fast_expand_kernel  grid (group, 128 output columns): the 32-rank tiles
+//   fast_expand_kernel  grid (group, 256 output columns): the 32-rank tiles
 //                  of the intermediate its columns use (rounded to the input
 //                  dtype into LDS), ids, B rows and outputs in one round
 //                  trip, MFMA per adapter over the token tiles,
@@ -333,15 +333,16 @@ constexpr int kFastKSlice = 256;      // k elements per shrink workgroup: 8 MFMA
 constexpr int kFastKSteps = kFastKSlice / 32;
 constexpr int kFastMaxSlices = 64;    // in_features <= 64 * kFastKSlice on this path
 constexpr int kShrinkAChunk = 4;      // adapters whose A tiles a shrink workgroup holds in LDS at once
-constexpr int kExpandWaves = 8;
-constexpr int kExpandThreads = kExpandWaves * 64;
-constexpr int kFastCols = 16 * kExpandWaves;  // output columns per expand workgroup (16 per wave)
+// Expand workgroups: 8 waves (128 columns) when a call needs at most one
+// workgroup per CU that way, else 16 waves (256 columns).  More workgroups
+// than CUs put two on some CUs, and those finish last: a decoder layer's
+// 38912 output columns in 304 128-column workgroups took as long as in 152
+// 256-column ones, while one group alone (16-96 workgroups) needs the narrow
+// ones to spread over the chip.
+constexpr int kExpandCUs = 256;
 constexpr int kFastAChunk = 4;        // adapters whose B rows an expand wave holds at once
 constexpr int kFastTt = kFastMaxTokens / 16;
 constexpr int kFastMaxRank = 128;     // r_pad limit (make_group)
-// 16-byte accumulator pairs one expand thread stages per slot and 32-rank tile
-constexpr int kStagePairs = kFastMaxTokens * 32 / 2 / kExpandThreads;
-static_assert(kStagePairs * kExpandThreads * 2 == kFastMaxTokens * 32, "staging covers one 32-rank tile");
 // The shrink's slices meet in a signed 64-bit fixed-point accumulator with
 // 26 fraction bits: integer adds are associative, so the sum (and the
 // rounded intermediate) does not depend on the order the slices arrive in.
@@ -614,7 +615,7 @@ __device__ __forceinline__ void rank_tiles(const ExpandMods& g, int c_first, int
   }
 }
 
-// Expand: workgroup (group, 128 output columns), every adapter; NKT: the
+// Expand: workgroup (group, 256 output columns), every adapter; NKT: the
 // most 32-rank tiles any wave's 16 columns use (1 when every module's ranks
 // sit in one tile).  The workgroup stages only the tiles its columns use:
 // the fixed-point intermediate of every token (both slots, one of which the
@@ -632,8 +633,14 @@ struct OutChunk {  // 8 consecutive outputs
   uint4 w[kWords];
 };
 
-template <typename T, typename OT, int NKT, bool MANY>
-__global__ __launch_bounds__(kExpandThreads) void fast_expand_kernel(FastArgs fa) {
+template <typename T, typename OT, int NKT, bool MANY, int EW>
+__global__ __launch_bounds__(EW * 64) void fast_expand_kernel(FastArgs fa) {
+  constexpr int kExpandWaves = EW;
+  constexpr int kExpandThreads = EW * 64;
+  constexpr int kFastCols = 16 * EW;  // output columns per workgroup (16 per wave)
+  // 16-byte accumulator pairs one thread stages per slot and 32-rank tile
+  constexpr int kStagePairs = kFastMaxTokens * 32 / 2 / kExpandThreads;
+  static_assert(kStagePairs * kExpandThreads * 2 == kFastMaxTokens * 32, "staging covers one 32-rank tile");
   __shared__ __align__(16) uint16_t s_y[kFastMaxTokens][kFastMaxRank + 8];  // +8 keeps rows 16-byte aligned
   __shared__ __align__(16) float s_d[kFastMaxTokens][kFastCols + 4];        // +4: rows start on other banks
   // flat grid, groups in order (a 2-D grid pads every group to the largest:
@@ -722,15 +729,18 @@ __global__ __launch_bounds__(kExpandThreads) void fast_expand_kernel(FastArgs fa
   __builtin_amdgcn_sched_barrier(0);  // these first: the staging then waits for them alone
 
   // the read-modify-write role: chunks q = threadIdx.x + u * kExpandThreads,
-  // token row q / 16, columns c0 + (q % 16) * 8 .. +8, each inside one module
-  constexpr int kChunks = kFastMaxTokens * kFastCols / 8 / kExpandThreads;  // 2
+  // token row q / kRowChunks, columns c0 + (q % kRowChunks) * 8 .. +8, each
+  // inside one module
+  constexpr int kRowChunks = kFastCols / 8;
+  constexpr int kChunks = kFastMaxTokens * kRowChunks / kExpandThreads;  // 2
+  static_assert(kChunks * kExpandThreads == kFastMaxTokens * kRowChunks, "every chunk has a thread");
   OutChunk<OT> cur[kChunks];
   OT* cptr[kChunks];
   bool cok[kChunks];
 #pragma unroll
   for (int u = 0; u < kChunks; ++u) {
     const int q = threadIdx.x + u * kExpandThreads;
-    const int tk = q / 16, c = c0 + (q % 16) * 8;
+    const int tk = q / kRowChunks, c = c0 + (q % kRowChunks) * 8;
     uint64_t off = 0, ld = 0;
     int ooff = 0;
     bool in_any = false;
@@ -819,7 +829,7 @@ __global__ __launch_bounds__(kExpandThreads) void fast_expand_kernel(FastArgs fa
   for (int tt = 0; tt < kFastTt; ++tt) idr[tt] = __shfl(id_lane, tt * 16 + lr);
 #pragma unroll
   for (int u = 0; u < kChunks; ++u)
-    cok[u] = cok[u] & (__shfl(id_lane, ((int)threadIdx.x + u * kExpandThreads) / 16) >= 0);
+    cok[u] = cok[u] & (__shfl(id_lane, ((int)threadIdx.x + u * kExpandThreads) / kRowChunks) >= 0);
 
   // Per token tile and adapter: the y rows of that adapter's tokens (the
   // others zeroed) times the adapter's B, every adapter accumulated into one
@@ -874,8 +884,8 @@ __global__ __launch_bounds__(kExpandThreads) void fast_expand_kernel(FastArgs fa
   for (int u = 0; u < kChunks; ++u) {
     const int q = threadIdx.x + u * kExpandThreads;
     if (cok[u]) {
-      const float4 d0 = *reinterpret_cast<const float4*>(&s_d[q / 16][(q % 16) * 8]);
-      const float4 d1 = *reinterpret_cast<const float4*>(&s_d[q / 16][(q % 16) * 8 + 4]);
+      const float4 d0 = *reinterpret_cast<const float4*>(&s_d[q / kRowChunks][(q % kRowChunks) * 8]);
+      const float4 d1 = *reinterpret_cast<const float4*>(&s_d[q / kRowChunks][(q % kRowChunks) * 8 + 4]);
       const float d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
       OutChunk<OT> r;
       const OT* cv = reinterpret_cast<const OT*>(cur[u].w);
@@ -1056,7 +1066,35 @@ struct DeltaPlan {
   size_t need;
   int shrink_x;  // shrink grid x: the most workgroups any group needs (y: groups)
   int expand_x;  // expand grid: every group's workgroups in order
+  int expand_waves;
+  int nkt;        // the most 32-rank tiles any expand wave's columns use
 };
+
+// The most 32-rank tiles the modules of any 16 consecutive output columns
+// (one expand wave) use: a wave inside a module uses that module's tiles,
+// and only the waves holding a module's first or last column can reach into
+// a neighbour.
+static int max_wave_tiles(const Group& g) {
+  auto span = [&](int c_first, int c_last) {
+    int lo = 0, hi = 0;
+    for (int m = 0; m < g.n; ++m) {
+      const Mod& M = g.m[m];
+      if (c_first >= M.out_offset && c_first < M.out_offset + M.out_features) lo = M.rank_offset / 32;
+      if (c_last >= M.out_offset && c_last < M.out_offset + M.out_features) hi = (M.rank_offset + M.rank - 1) / 32;
+    }
+    return hi - lo + 1;
+  };
+  int best = 1;
+  for (int m = 0; m < g.n; ++m) {
+    const Mod& M = g.m[m];
+    best = std::max(best, span(M.out_offset, M.out_offset + M.out_features - 1));
+    for (const int c : {M.out_offset, M.out_offset + M.out_features - 1}) {
+      const int w0 = c / 16 * 16;
+      best = std::max(best, span(w0, std::min(w0 + 15, g.out_total - 1)));
+    }
+  }
+  return best;
+}
 
 static int plan_delta(const pl_lora_group* groups, int n_groups, int tokens, int n_adapters, int dtype,
                       char* ws, DeltaPlan* P) {
@@ -1096,7 +1134,7 @@ static int plan_delta(const pl_lora_group* groups, int n_groups, int tokens, int
     F.in_features = gr.in_features;
     F.ksplit = (gr.in_features + kFastKSlice - 1) / kFastKSlice;
     F.n_rt = (F.g.r_total + 15) / 16;
-    F.n_expand = (F.g.out_total + kFastCols - 1) / kFastCols;
+    F.n_expand = (F.g.out_total + 127) / 128;  // at 8 waves; recounted below for 16
     sb = std::max(sb, F.ksplit * F.n_rt);
     F.expand_begin = eb;
     eb += F.n_expand;
@@ -1107,6 +1145,20 @@ static int plan_delta(const pl_lora_group* groups, int n_groups, int tokens, int
   P->fa.tokens = tokens;
   P->fa.n_adapters = n_adapters;
   P->shrink_x = sb;
+  P->nkt = 1;
+  for (int i = 0; i < n_groups; ++i) P->nkt = std::max(P->nkt, max_wave_tiles(P->g[i]));
+  // 16 waves of 1024 threads cap a kernel at 128 registers: waves spanning
+  // more than two 32-rank tiles would spill there, and stay at 8
+  P->expand_waves = eb > kExpandCUs && P->nkt <= 2 ? 16 : 8;
+  if (P->expand_waves == 16) {
+    eb = 0;
+    for (int i = 0; i < n_groups; ++i) {
+      FastGroup& F = P->fa.grp[i];
+      F.n_expand = (F.g.out_total + 255) / 256;
+      F.expand_begin = eb;
+      eb += F.n_expand;
+    }
+  }
   P->expand_x = eb;
   P->need = P->fast ? kParityBytes + (size_t)n_groups * 2 * kAccSlotBytes : kGeneralOffset + general;
   (void)dtype;
@@ -1120,18 +1172,18 @@ extern "C" size_t pl_lora_delta_workspace_size(const pl_lora_group* groups_h, in
   return P.need;
 }
 
-template <typename T, int NKT, bool MANY>
+template <typename T, int NKT, bool MANY, int EW>
 static int launch_expand_fast(const DeltaPlan& P, int out_dtype, hipStream_t stream) {
-  const dim3 grid(P.expand_x);
+  const dim3 grid(P.expand_x), block(EW * 64);
   switch (out_dtype) {
     case PL_DTYPE_F32:
-      hipLaunchKernelGGL((fast_expand_kernel<T, float, NKT, MANY>), grid, dim3(kExpandThreads), 0, stream, P.fa);
+      hipLaunchKernelGGL((fast_expand_kernel<T, float, NKT, MANY, EW>), grid, block, 0, stream, P.fa);
       break;
     case PL_DTYPE_F16:
-      hipLaunchKernelGGL((fast_expand_kernel<T, f16_t, NKT, MANY>), grid, dim3(kExpandThreads), 0, stream, P.fa);
+      hipLaunchKernelGGL((fast_expand_kernel<T, f16_t, NKT, MANY, EW>), grid, block, 0, stream, P.fa);
       break;
     case PL_DTYPE_BF16:
-      hipLaunchKernelGGL((fast_expand_kernel<T, bf16_t, NKT, MANY>), grid, dim3(kExpandThreads), 0, stream, P.fa);
+      hipLaunchKernelGGL((fast_expand_kernel<T, bf16_t, NKT, MANY, EW>), grid, block, 0, stream, P.fa);
       break;
     default:
       return fail(PL_ERR_UNSUPPORTED, "out_dtype %d", out_dtype);
@@ -1142,34 +1194,14 @@ static int launch_expand_fast(const DeltaPlan& P, int out_dtype, hipStream_t str
 
 template <typename T, int NKT>
 static int launch_expand_fast(const DeltaPlan& P, int out_dtype, hipStream_t stream) {
-  return P.fa.n_adapters > kFastAChunk ? launch_expand_fast<T, NKT, true>(P, out_dtype, stream)
-                                       : launch_expand_fast<T, NKT, false>(P, out_dtype, stream);
-}
-
-// The most 32-rank tiles the modules of any 16 consecutive output columns
-// (one expand wave) use: a wave inside a module uses that module's tiles,
-// and only the waves holding a module's first or last column can reach into
-// a neighbour.
-static int max_wave_tiles(const Group& g) {
-  auto span = [&](int c_first, int c_last) {
-    int lo = 0, hi = 0;
-    for (int m = 0; m < g.n; ++m) {
-      const Mod& M = g.m[m];
-      if (c_first >= M.out_offset && c_first < M.out_offset + M.out_features) lo = M.rank_offset / 32;
-      if (c_last >= M.out_offset && c_last < M.out_offset + M.out_features) hi = (M.rank_offset + M.rank - 1) / 32;
-    }
-    return hi - lo + 1;
-  };
-  int best = 1;
-  for (int m = 0; m < g.n; ++m) {
-    const Mod& M = g.m[m];
-    best = std::max(best, span(M.out_offset, M.out_offset + M.out_features - 1));
-    for (const int c : {M.out_offset, M.out_offset + M.out_features - 1}) {
-      const int w0 = c / 16 * 16;
-      best = std::max(best, span(w0, std::min(w0 + 15, g.out_total - 1)));
-    }
+  const bool many = P.fa.n_adapters > kFastAChunk;
+  if constexpr (NKT <= 2) {
+    if (P.expand_waves == 16)
+      return many ? launch_expand_fast<T, NKT, true, 16>(P, out_dtype, stream)
+                  : launch_expand_fast<T, NKT, false, 16>(P, out_dtype, stream);
   }
-  return best;
+  return many ? launch_expand_fast<T, NKT, true, 8>(P, out_dtype, stream)
+              : launch_expand_fast<T, NKT, false, 8>(P, out_dtype, stream);
 }
 
 template <typename T>
@@ -1177,15 +1209,14 @@ static int launch_fast(const DeltaPlan& P, int out_dtype, hipStream_t stream) {
   hipLaunchKernelGGL(fast_shrink_kernel<T>, dim3(P.shrink_x, P.fa.n_groups), dim3(kShrinkThreads), 0, stream,
                      P.fa);
   PL_LAUNCH_CHECK("lora fast_shrink_kernel");
-  int nkt = 1;
-  for (int i = 0; i < P.fa.n_groups; ++i) nkt = std::max(nkt, max_wave_tiles(P.fa.grp[i].g));
-  switch (nkt) {
+  // 3 tiles run as 4: a wave's loop stops at its own last tile
+  switch (P.nkt) {
     case 1: return launch_expand_fast<T, 1>(P, out_dtype, stream);
     case 2: return launch_expand_fast<T, 2>(P, out_dtype, stream);
-    case 3: return launch_expand_fast<T, 3>(P, out_dtype, stream);
+    case 3:
     case 4: return launch_expand_fast<T, 4>(P, out_dtype, stream);
   }
-  return fail(PL_ERR_UNSUPPORTED, "r_pad %d", nkt * 32);
+  return fail(PL_ERR_UNSUPPORTED, "r_pad %d", P.nkt * 32);
 }
 
 static int delta_groups_impl(const pl_lora_group* groups_h, int num_groups, int num_tokens,
