@@ -383,15 +383,6 @@ struct FastArgs {
   const int32_t* ids;
 };
 
-// A pointer rebuilt from pinned integer bits, marked as global memory first
-// (a pointer made straight from an integer compiles to flat accesses, which
-// wait on both the vector and the scalar memory counters).
-template <typename P>
-__device__ __forceinline__ P gptr(uint64_t u) {
-  using E = typename std::remove_pointer<P>::type;
-  return (P)(__attribute__((address_space(1))) E*)u;
-}
-
 // In an SGPR from here on and opaque to the compiler: every argument field
 // pinned at a kernel's top is loaded in one batch with one wait (otherwise
 // each is loaded next to its first use, a dependent round trip apiece), and
@@ -686,7 +677,7 @@ __global__ __launch_bounds__(EW * 64) void fast_expand_kernel(FastArgs fa) {
   const int c0 = ct * kFastCols;
 
   const int lane = threadIdx.x % kWave;
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform: scalar loop bounds
   const int lr = lane % 16;
   const int kq = (lane / 16) * 8;
   const int tile = ct * kExpandWaves + wave;
@@ -834,25 +825,29 @@ __global__ __launch_bounds__(EW * 64) void fast_expand_kernel(FastArgs fa) {
   // Per token tile and adapter: the y rows of that adapter's tokens (the
   // others zeroed) times the adapter's B, every adapter accumulated into one
   // MFMA result.  A row gets its own adapter's product plus exact zeros, and
-  // a row without an adapter stays zero.
+  // a row without an adapter stays zero.  Adapters outermost, so the token
+  // tiles' accumulation chains interleave.
   f32x4 acc4[kFastTt];
 #pragma unroll
   for (int tt = 0; tt < kFastTt; ++tt) acc4[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nk_w = kw_hi - kw_lo + 1;  // the wave's own tiles (uniform; 0 past the columns)
+  uint4 yv[kFastTt][NKT];
+#pragma unroll
+  for (int tt = 0; tt < kFastTt; ++tt)
+#pragma unroll
+    for (int k = 0; k < NKT; ++k)
+      yv[tt][k] = *reinterpret_cast<const uint4*>(&s_y[tt * 16 + lr][min(kw_lo + k, kFastMaxRank / 32 - 1) * 32 + kq]);
   auto apply_chunk = [&](int a0, const uint4 (&bc)[kFastAChunk][NKT]) {
 #pragma unroll
-    for (int tt = 0; tt < kFastTt; ++tt) {
-      if (tt >= n_tt) break;
-      uint4 yv[NKT];
+    for (int u = 0; u < kFastAChunk; ++u) {
 #pragma unroll
-      for (int k = 0; k < NKT; ++k)
-        yv[k] = *reinterpret_cast<const uint4*>(&s_y[tt * 16 + lr][min(kw_lo + k, kFastMaxRank / 32 - 1) * 32 + kq]);
-#pragma unroll
-      for (int u = 0; u < kFastAChunk; ++u) {
+      for (int tt = 0; tt < kFastTt; ++tt) {
+        if (tt >= n_tt) break;
         const uint32_t m = 0u - (uint32_t)(idr[tt] == a0 + u);
 #pragma unroll
         for (int k = 0; k < NKT; ++k) {
-          if (kw_lo + k > kw_hi) break;  // the wave's own tiles (uniform)
-          const uint4 ym = make_uint4(yv[k].x & m, yv[k].y & m, yv[k].z & m, yv[k].w & m);
+          if (k >= nk_w) break;
+          const uint4 ym = make_uint4(yv[tt][k].x & m, yv[tt][k].y & m, yv[tt][k].z & m, yv[tt][k].w & m);
           acc4[tt] = mfma32<T>(ym, bc[u][k], acc4[tt]);
         }
       }

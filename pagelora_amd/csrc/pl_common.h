@@ -7,10 +7,21 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <type_traits>
 
 #include "../../include/pagelora.h"
 
 namespace pl {
+
+// A pointer rebuilt from integer bits (kernel arguments held in SGPRs by an
+// empty asm statement), marked as global memory first: a pointer made
+// straight from an integer compiles to flat accesses, which wait on both the
+// vector and the scalar memory counters.
+template <typename P>
+__device__ __forceinline__ P gptr(uint64_t u) {
+  using E = typename std::remove_pointer<P>::type;
+  return (P)(__attribute__((address_space(1))) E*)u;
+}
 
 // ---------------------------------------------------------------- errors ---
 // The message buffer is per host thread, so concurrent callers on different
