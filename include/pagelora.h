@@ -548,9 +548,10 @@ size_t pl_lora_delta_workspace_size(const pl_lora_group* groups_h, int num_group
  * (multilora/runtime.py:138-174).
  *
  * Workspace: pl_lora_delta_workspace_size of the one group, zero-filled
- * before its first use (see there).  Up to 64 tokens and 64 adapters the
- * call is two launches built for decode latency; otherwise the general
- * shrink + expand pair.
+ * before its first use (see there).  Up to 64 tokens and 64 adapters, with
+ * ranks, out_features and ldo multiples of 8 and B and the outputs 16-byte
+ * aligned, the call is two launches built for decode latency; otherwise the
+ * general shrink + expand pair (same results to the stated tolerance).
  */
 int pl_lora_delta(const void* x, int64_t ldx, int num_tokens, int in_features,
                   const pl_lora_module* modules_h, int num_modules,
