@@ -61,6 +61,8 @@ def parse_args():
                    help="also run a 1 GiB device copy (for scaling rocprofv3 FETCH/WRITE_SIZE)")
     p.add_argument("--e2e-only", choices=sorted(E2E_LEGS),
                    help="run only this end-to-end decode leg and print its result (for profiling)")
+    p.add_argument("--lora-only", action="store_true",
+                   help="run only the per-layer LoRA delta timing and print its result (for profiling)")
     return p.parse_args()
 
 
@@ -494,6 +496,12 @@ def main():
     if args.e2e_only:
         name, kw = E2E_LEGS[args.e2e_only]
         print(json.dumps({"leg": name, **e2e_decode(dev, **kw)}), flush=True)
+        return
+    if args.lora_only:
+        grouped, per_group, nbytes = time_lora(dev)
+        print(json.dumps({"leg": "lora_delta_64tok_4adapters_7modules", "us_per_layer": round(grouped * 1e3, 2),
+                          "us_per_layer_one_call_per_group": round(per_group * 1e3, 2),
+                          "algorithmic_bytes": nbytes}), flush=True)
         return
     if args.copy_calibration:
         copy_calibration(dev)
