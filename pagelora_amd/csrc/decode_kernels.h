@@ -1068,6 +1068,7 @@ constexpr int kMergeFewItems = 8;  // average items per row up to which one wave
 // 1 x 32K tokens, plan + decode + merge 36.7 -> 35.7 us; at ~33 items per
 // row (4 x 2112) four waves stay 0.25 us faster).
 constexpr int kMergeManyItems = 64;
+constexpr int kMergeCUs = 256;  // MI355X
 
 struct MergeState {
   float m, w, a[8];  // log2 max, sum of weights, weighted output (8 dims)
@@ -1082,15 +1083,19 @@ struct MergeState {
   }
 };
 
-template <typename T, int D, int MT>
+// DS: the head's dims split over DS workgroups (each folds every partial of
+// its D / DS dims), for launches with few (row, head) pairs: one row of 32
+// heads is otherwise 32 workgroups, each reading 64 KB of partials alone.
+template <typename T, int D, int MT, int DS = 1>
 __global__ __launch_bounds__(MT) void merge_kernel(
     const int2* __restrict__ row_info, const float* __restrict__ part_lse,
     const float* __restrict__ part_o, T* __restrict__ o, int64_t o_sb, int64_t o_sh,
     float* __restrict__ lse, const int* __restrict__ header, int batch, int num_qo_heads,
     int max_items, Direct dir) {
-  constexpr int LPT = D / 8, RPI = MT / LPT, NWV = MT / kWave;
+  static_assert((D / 8) % DS == 0, "whole 8-dim slices per workgroup");
+  constexpr int LPT = D / 8 / DS, RPI = MT / LPT, NWV = MT / kWave;
   __shared__ float s_m[NWV][LPT], s_w[NWV][LPT], s_a[NWV][LPT][8];
-  const int pair = blockIdx.x;
+  const int pair = blockIdx.x / DS, ds = blockIdx.x % DS;
   if (pair >= batch * num_qo_heads) return;
   const int b = pair / num_qo_heads;
   const int hq = pair - b * num_qo_heads;
@@ -1109,6 +1114,7 @@ __global__ __launch_bounds__(MT) void merge_kernel(
   }
 
   const int r = threadIdx.x / LPT, col = threadIdx.x % LPT;
+  const int dcol = ds * LPT + col;  // the thread's 8-dim slice of the head
   MergeState st{-INFINITY, 0.f, {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}};
   for (int c0 = 0; c0 < n; c0 += RPI * kMergeBatch) {
     float lv[kMergeBatch];
@@ -1123,8 +1129,8 @@ __global__ __launch_bounds__(MT) void merge_kernel(
         const int c = min(c0 + r + k * RPI, n - 1);
         const int64_t slot = (int64_t)(first + c) * num_qo_heads + hq;
         lv[k] = part_lse[slot];
-        oa[k] = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8);
-        ob[k] = *reinterpret_cast<const float4*>(part_o + slot * D + col * 8 + 4);
+        oa[k] = *reinterpret_cast<const float4*>(part_o + slot * D + dcol * 8);
+        ob[k] = *reinterpret_cast<const float4*>(part_o + slot * D + dcol * 8 + 4);
       }
     }
     __builtin_amdgcn_sched_barrier(0);  // the whole batch in flight before the first fold
@@ -1166,10 +1172,10 @@ __global__ __launch_bounds__(MT) void merge_kernel(
     st.add(s_m[w][col], s_w[w][col], a_o);
   }
   const float inv = st.w > 0.f ? 1.f / st.w : 0.f;
-  T* op = o + (int64_t)b * o_sb + (int64_t)hq * o_sh + col * 8;
+  T* op = o + (int64_t)b * o_sb + (int64_t)hq * o_sh + dcol * 8;
 #pragma unroll
   for (int i = 0; i < 8; ++i) op[i] = from_float<T>(st.a[i] * inv);
-  if (lse != nullptr && col == 0) {
+  if (lse != nullptr && dcol == 0) {
     constexpr float kLn2 = 0.69314718055994530942f;
     const float m_use = st.m == -INFINITY ? 0.f : st.m;
     lse[(int64_t)b * num_qo_heads + hq] = st.w > 0.f ? (m_use + __log2f(st.w)) * kLn2 : -INFINITY;
@@ -1204,18 +1210,29 @@ int launch(const RunArgs& a, const QkvIn& qin = QkvIn{}) {
     PL_LAUNCH_CHECK("decode_kernel");
   }
   if (!(a.flags & PL_DECODE_SKIP_MERGE)) {
+    // the dim split: as far as 4 while the launch stays within one
+    // workgroup per CU (a full-chip launch gains nothing from it)
+    const int pairs = a.batch * a.hq;
+    const int ds = (D % 32 == 0 && pairs * 4 <= kMergeCUs) ? 4 : (D % 16 == 0 && pairs * 2 <= kMergeCUs) ? 2 : 1;
+    auto go = [&](auto mt, auto dsc) {
+      constexpr int MT = decltype(mt)::value, DS = decltype(dsc)::value;
+      hipLaunchKernelGGL((merge_kernel<T, D, MT, DS>), dim3(pairs * DS), dim3(MT), 0, a.stream, a.row_info,
+                         a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header, a.batch, a.hq,
+                         a.max_items, a.dir);
+    };
+    auto by_ds = [&](auto mt) {
+      if constexpr (D % 32 == 0)
+        if (ds == 4) return go(mt, std::integral_constant<int, 4>{});
+      if constexpr (D % 16 == 0)
+        if (ds == 2) return go(mt, std::integral_constant<int, 2>{});
+      go(mt, std::integral_constant<int, 1>{});
+    };
     if (a.max_items <= kMergeFewItems * a.batch)
-      hipLaunchKernelGGL((merge_kernel<T, D, kWave>), dim3(a.batch * a.hq), dim3(kWave), 0, a.stream,
-                         a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
-                         a.batch, a.hq, a.max_items, a.dir);
+      by_ds(std::integral_constant<int, kWave>{});
     else if (a.max_items <= kMergeManyItems * a.batch)
-      hipLaunchKernelGGL((merge_kernel<T, D, 4 * kWave>), dim3(a.batch * a.hq), dim3(4 * kWave), 0, a.stream,
-                         a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
-                         a.batch, a.hq, a.max_items, a.dir);
+      by_ds(std::integral_constant<int, 4 * kWave>{});
     else
-      hipLaunchKernelGGL((merge_kernel<T, D, 8 * kWave>), dim3(a.batch * a.hq), dim3(8 * kWave), 0, a.stream,
-                         a.row_info, a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header,
-                         a.batch, a.hq, a.max_items, a.dir);
+      by_ds(std::integral_constant<int, 8 * kWave>{});
     PL_LAUNCH_CHECK("merge_kernel");
   }
   return ok();
