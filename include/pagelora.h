@@ -84,6 +84,34 @@ int pl_decode_plan(const int32_t* indptr, int batch, int indices_capacity,
                    void* stream);
 
 /*
+ * pl_decode_plan for a batch whose rows all begin with the same
+ * shared_pages page ids (a shared prompt prefix held in shared pages; a
+ * multiple of prefix_chunk_pages, and fewer than every row's page count).
+ * pl_decode_run_qkv then attends the prefix once for all rows: items of
+ * prefix_chunk_pages pages, each scoring every row's query heads of one kv
+ * head as the columns of one MFMA tile, and each row's own items cover its
+ * pages after the prefix; the merge combines both.  Taken when the batch
+ * has at most 4 rows, GQA 4, head_dim 128, prefix_chunk_pages * page_size
+ * == 32 and the LoRA (if any) binds one adapter; otherwise, and in
+ * pl_decode_run, every row reads every page as after pl_decode_plan.  The
+ * results equal the unshared run's up to the order of the softmax merge.
+ * Needs the direct plan (batch <= 16, see above) and a workspace of
+ * pl_decode_workspace_size_shared bytes.  No counterpart in the reference:
+ * its decode wrapper reads a shared page once per row (FlashInfer's
+ * BatchDecodeWithPagedKVCacheWrapper, attention_backend.py:63-131).
+ */
+size_t pl_decode_workspace_size_shared(int batch, int target_items,
+                                       int num_qo_heads, int head_dim,
+                                       int shared_pages,
+                                       int prefix_chunk_pages);
+int pl_decode_plan_shared(const int32_t* indptr, int batch,
+                          int indices_capacity, int num_qo_heads,
+                          int head_dim, int target_items, int min_chunk_pages,
+                          int shared_pages, int prefix_chunk_pages,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/*
  * Batched single-token paged attention:
  *   o[b, hq] = softmax(q[b, hq] . K_b[:, hq / g]^T * sm_scale) . V_b
  * with g = num_qo_heads / num_kv_heads, K_b / V_b gathered from the pages

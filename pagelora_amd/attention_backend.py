@@ -104,7 +104,17 @@ def _cache_geometry(cache, num_kv_heads: int, head_dim: int, page_size: int):
 
 
 class PagedDecodeAttention:
-    """gfx950 paged decode attention with the FlashInferAttentionBackend surface."""
+    """gfx950 paged decode attention with the FlashInferAttentionBackend surface.
+
+    ``share_prefix``: when a host-table plan finds every row of a batch of 2..4
+    rows starting with the same pages (a shared prompt prefix), the folded
+    q/k/v run attends those pages once for all rows
+    (``pl_decode_plan_shared``); False reads them once per row.
+    """
+
+    share_prefix = True
+    # pages per prefix item: 32 tokens, one MFMA step of the prefix kernel path
+    _PREFIX_TOKENS = 32
 
     def __init__(
         self,
@@ -207,14 +217,22 @@ class PagedDecodeAttention:
             self._decode_host_uploads.append((ev, host))
 
         target_items = self._target_items(batch)
-        self._launch_plan(batch, target_items)
+        shared = 0
+        if paged_kv_indptr.device.type == "cpu":
+            shared = self._shared_prefix_pages(paged_kv_indptr, paged_kv_indices, batch, target_items)
+            if shared:
+                # the rows' own pages past the prefix are few: a few items each
+                # (a grid sized for 128 would be mostly idle workgroups)
+                target_items = min(target_items, 4 * batch)
         self._plan = {
             "batch": batch,
             "target_items": target_items,
             "q_data_type": q_data_type,
             "kv_data_type": kv_data_type,
             "max_page": max_page,
+            "shared": shared,
         }
+        self._launch_plan(batch, target_items)
 
     def replan_decode(self) -> None:
         """Re-run the device-side plan on the current buffers (same batch).
@@ -253,19 +271,56 @@ class PagedDecodeAttention:
 
     def _launch_plan(self, batch: int, target_items: int) -> None:
         indptr_buf, indices_buf, _ = self._decode_graph_buffers
-        status = self._lib.pl_decode_plan(
+        shared = (self._plan or {}).get("shared", 0)
+        pchunk = self._prefix_chunk_pages()
+        status = self._lib.pl_decode_plan_shared(
             indptr_buf.data_ptr(),
             batch,
             indices_buf.numel(),
             self.num_qo_heads,
             self.head_dim,
             target_items,
-            self.min_chunk_pages,
+            # own items as short as the prefix items when a prefix is shared
+            pchunk if shared else self.min_chunk_pages,
+            shared,
+            pchunk if shared else 1,
             self.workspace_buffer.data_ptr(),
             self.workspace_buffer.numel(),
             _lib.stream_handle(self.device),
         )
-        _lib.check(status, "pl_decode_plan")
+        _lib.check(status, "pl_decode_plan_shared")
+
+    def _prefix_chunk_pages(self) -> int:
+        return max(1, self._PREFIX_TOKENS // self.page_size)
+
+    def _shared_prefix_pages(self, indptr: torch.Tensor, indices: torch.Tensor, batch: int,
+                             target_items: int) -> int:
+        """Leading pages every row of the batch lists (whole prefix items,
+        each row keeping at least one page of its own), where the folded
+        run can share them; 0 otherwise."""
+        pchunk = self._prefix_chunk_pages()
+        if (not self.share_prefix or not 2 <= batch <= 4 or pchunk * self.page_size != self._PREFIX_TOKENS
+                or self.num_qo_heads != 4 * self.num_kv_heads or self.head_dim != 128):
+            return 0
+        ip = indptr.tolist()
+        lens = [ip[b + 1] - ip[b] for b in range(batch)]
+        limit = min(lens) - 1
+        if limit < 2 * pchunk:
+            return 0
+        import numpy as np
+
+        idx = indices.numpy()
+        first = idx[ip[0]: ip[0] + limit]
+        same = np.ones(limit, dtype=bool)
+        for b in range(1, batch):
+            same &= idx[ip[b]: ip[b] + limit] == first
+        common = limit if same.all() else int(np.argmin(same))
+        shared = common // pchunk * pchunk
+        if shared < 2 * pchunk:
+            return 0
+        need = self._lib.pl_decode_workspace_size_shared(batch, target_items, self.num_qo_heads, self.head_dim,
+                                                         shared, pchunk)
+        return shared if need <= self.workspace_buffer.numel() else 0
 
     def _target_items(self, batch: int) -> int:
         """Work items per step (target_waves / kv heads if set, else the
@@ -307,7 +362,8 @@ class PagedDecodeAttention:
         bufs = self._decode_graph_buffers
         ptrs = tuple(b.data_ptr() for b in bufs) if bufs is not None else ()
         plan = self._plan or {}
-        return (id(self), plan.get("batch"), plan.get("target_items"), ptrs, self.workspace_buffer.data_ptr())
+        return (id(self), plan.get("batch"), plan.get("target_items"), plan.get("shared", 0), ptrs,
+                self.workspace_buffer.data_ptr())
 
     # ----------------------------------------------------------------- run
     def run_decode(self, q: torch.Tensor, paged_kv_cache_layer) -> torch.Tensor:

@@ -68,15 +68,23 @@ struct Direct {
   int capacity;           // indices capacity: page ranges are clamped to it, as the plan does
   int target_items;
   int min_chunk;
+  // Shared prefix (folded q/k/v kernel only): every row's first `shared`
+  // page ids are the same pages.  They are split into prefix items of
+  // `pchunk` pages, each attended for every row at once (prefix_wave); the
+  // rows' own items cover their pages after the prefix.  Row b's partial
+  // slots are its prefix chunks, then its own items.  0: no shared prefix.
+  int shared;
+  int pchunk;
 };
 
 struct DirectScan {
   int ip;     // this lane's clamped indptr[lane] (lanes < batch: the rows' starts)
   int ip1;    // and indptr[lane + 1] (the rows' ends)
-  int n;      // chunks of row `lane` (lanes < batch; 0 elsewhere)
+  int n;      // own chunks of row `lane` (lanes < batch; 0 elsewhere)
   int incl;   // inclusive scan of n over lanes 0..15
-  int chunk;  // pages per chunk (uniform)
-  int total;  // items of the batch (uniform)
+  int chunk;  // pages per own chunk (uniform)
+  int total;  // items of the batch, prefix items included (uniform)
+  int n_pref; // prefix items (uniform; 0 without a shared prefix)
 };
 
 // a / b for 0 <= a < 2^23, 1 <= b: float quotient, then one correction step
@@ -100,12 +108,15 @@ __device__ __forceinline__ DirectScan direct_scan(const Direct& d, int batch) {
   r.ip1 = ip1;
   const int ip0 = __builtin_amdgcn_readfirstlane(ip);
   const int ipb = __builtin_amdgcn_readlane(ip1, batch - 1);
-  const int total_pages = ipb > ip0 ? ipb - ip0 : 0;
+  // the rows' own pages: past the shared prefix (every row holds more than it)
+  const int sh = d.shared;
+  const int total_pages = (ipb > ip0 ? ipb - ip0 : 0) - sh * batch;
   int c = (total_pages + d.target_items - 1) / d.target_items;  // uniform
   c = c > d.min_chunk ? c : d.min_chunk;
   r.chunk = c > 1 ? c : 1;
-  const int pages = ip1 > ip ? ip1 - ip : 0;
+  const int pages = ip1 > ip + sh ? ip1 - ip - sh : 0;
   r.n = lane < batch ? (pages > 0 ? small_div(pages + r.chunk - 1, r.chunk) : 1) : 0;
+  r.n_pref = sh > 0 ? (sh + d.pchunk - 1) / d.pchunk : 0;
   // inclusive scan over the 16 lanes of DPP row 0 (row_shr shifts in zeros)
   int x = r.n;
   x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
@@ -113,33 +124,43 @@ __device__ __forceinline__ DirectScan direct_scan(const Direct& d, int batch) {
   x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
   x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
   r.incl = x;
-  r.total = __builtin_amdgcn_readlane(x, 15);
+  r.total = __builtin_amdgcn_readlane(x, 15) + r.n_pref;
   return r;
 }
 
-// Row, page range and flags (single-item row, holds the last page, slot) of
-// item `item`; false past the batch's items.  Every lane of the wave calls it.
-__device__ __forceinline__ bool direct_item(const Direct& d, int batch, int item, int& b, int& pbeg, int& pend,
-                                            int& flags) {
-  const DirectScan s = direct_scan(d, batch);
+// Row, page range and flags (single-slot row, holds the last page, slot) of
+// own item `item` (items are numbered from the n_pref prefix items on);
+// false past the batch's items.  Every lane of the wave calls it.
+__device__ __forceinline__ bool direct_item_of(const DirectScan& s, const Direct& d, int item, int& b, int& pbeg,
+                                               int& pend, int& flags) {
   if (item >= s.total) return false;
   const int lane = threadIdx.x % kWave;
-  b = __builtin_amdgcn_readfirstlane(__popcll(__builtin_amdgcn_ballot_w64((lane < 16) & (s.incl <= item))));
+  const int own = item - s.n_pref;
+  b = __builtin_amdgcn_readfirstlane(__popcll(__builtin_amdgcn_ballot_w64((lane < 16) & (s.incl <= own))));
   const int n_b = __builtin_amdgcn_readlane(s.n, b);
   const int first = __builtin_amdgcn_readlane(s.incl, b) - n_b;
-  const int row_beg = __builtin_amdgcn_readlane(s.ip, b);
+  const int row_beg = __builtin_amdgcn_readlane(s.ip, b) + d.shared;
   const int row_end = __builtin_amdgcn_readlane(s.ip1, b);
-  pbeg = row_beg + (item - first) * s.chunk;
+  pbeg = row_beg + (own - first) * s.chunk;
   pend = min(row_end > row_beg ? row_end : row_beg, pbeg + s.chunk);
-  flags = (item << 2) | (n_b == 1 ? 1 : 0) | (pend >= row_end ? 2 : 0);
+  // row b's slots follow the earlier rows' (n_pref + own items each), its
+  // prefix chunks first
+  const int slot = (b + 1) * s.n_pref + own;
+  flags = (slot << 2) | (s.n_pref + n_b == 1 ? 1 : 0) | (pend >= row_end ? 2 : 0);
   return true;
+}
+
+__device__ __forceinline__ bool direct_item(const Direct& d, int batch, int item, int& b, int& pbeg, int& pend,
+                                            int& flags) {
+  return direct_item_of(direct_scan(d, batch), d, item, b, pbeg, pend, flags);
 }
 
 // First slot and item count of row b.  Every lane of the wave calls it.
 __device__ __forceinline__ void direct_row(const Direct& d, int batch, int b, int& first, int& n) {
   const DirectScan s = direct_scan(d, batch);
-  n = __builtin_amdgcn_readlane(s.n, b);
-  first = __builtin_amdgcn_readlane(s.incl, b) - n;
+  const int n_own = __builtin_amdgcn_readlane(s.n, b);
+  first = b * s.n_pref + __builtin_amdgcn_readlane(s.incl, b) - n_own;
+  n = s.n_pref + n_own;
 }
 
 // ---------------------------------------------------------------- decode ---
@@ -815,11 +836,208 @@ __device__ __forceinline__ void head_finish(const QkvIn& in, const HeadIn<T, R>&
   }
 }
 
+// ------------------------------------------------------ shared prefix ---
+// A prefix item: kPrefixTokens tokens of the pages every row shares, for one
+// kv head h and every row of the batch at once (batch <= 4): the 16 MFMA
+// columns are (row n / 4, query head 4h + n % 4).  The wave forms those
+// rows' q as the folded epilogue does (one bound adapter), scores
+// S^T = K . Q^T (a lane holds tokens 4*(l/16) + i of each 16-token block,
+// column l % 16), runs the fp32 online softmax per column (its four lanes
+// exchange max and sum), and forms O^T = V^T . P^T on MFMA: V is staged in
+// LDS row-major and read as pairs of head dims (tile 2a: dims 32a + 2r,
+// tile 2a+1: dims 32a + 2r + 1, r = l % 16) with byte permutes, P is split
+// into a hi and a lo part of the 16-bit type (about 16 mantissa bits).  The
+// normalised partial and its log2-sum-exp go to slot first_b + j of each
+// row b, where the merge finds them with the row's own items.
+constexpr int kPrefixTokens = 32;   // tokens per prefix item: one P.V step of 16x16x32 MFMAs
+constexpr int kPrefixMaxRows = 4;   // 16 columns / GQA 4
+
+template <typename T> __device__ __forceinline__ uint32_t pack_pv(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack_pv<bf16_t>(float a, float b) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+template <> __device__ __forceinline__ uint32_t pack_pv<f16_t>(float a, float b) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, half2_t));
+}
+
+template <typename T, int R>
+__device__ __forceinline__ void prefix_wave(const DirectScan& sc, const Direct& dir, int batch, int j, int h,
+                                            const T* __restrict__ kc, const T* __restrict__ vc,
+                                            int64_t page_stride, int64_t token_stride, int64_t head_stride,
+                                            const int32_t* __restrict__ indices, int page_size, int64_t num_pages,
+                                            float scale_log2, const QkvIn& qin, int num_qo_heads,
+                                            float* __restrict__ part_lse, float* __restrict__ part_o,
+                                            uint32_t* __restrict__ s_v, uint4 (*s_q)[4][16]) {
+  constexpr int D = 128, G = 4;
+  const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  const int rg = lane / 16, col = lane % 16;  // q formation: row group (head 4h + rg), 8-dim slice
+  const int nrows = min(batch, kPrefixMaxRows);
+  const bool live = j < sc.n_pref;  // the workgroup's last chunk group may be partial
+  // ---- wave w forms row w's q for the workgroup's kv head (the four waves
+  // share them through LDS): loads first, with the item's page ids
+  const int hq_form = h * G + rg;
+  const int a_ld = R > 0 ? qin.m[0].adapter : 0;  // the bound adapter (the host requires one)
+  const int qb_row = min(wv, nrows - 1);
+  HeadIn<T, R> x;
+  head_base_load<T, R>(qin, qb_row, hq_form, col, (const T*)qin.q_norm_w, x);
+  head_lora_load<T, R>(qin, qb_row, 0, hq_form * D, col, a_ld, x);
+  // the item's pages: tokens j*32 .. of row 0's list (every row's, up to the prefix)
+  const int ip0 = __builtin_amdgcn_readfirstlane(sc.ip);
+  const int tok0 = (live ? j : 0) * kPrefixTokens;
+  const int last_idx = dir.capacity > 0 ? dir.capacity - 1 : 0;  // page reads stay inside the indices buffer
+  const int pg_a = uniform(indices[min(ip0 + tok0 / page_size, last_idx)]);
+  const int pg_b = uniform(indices[min(ip0 + (tok0 + 16) / page_size, last_idx)]);
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    float v[8];
+    head_finish<T, R>(qin, x, 0, col, qin.q_norm_w != nullptr, true, R > 0, v);
+    if (wv < nrows)
+      s_q[wv][rg][col] = make_uint4(pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
+                                    pack2<T>(v[6], v[7]));
+  }
+  __syncthreads();
+  if (!live) return;
+  // B operand of S^T: column l % 16 = (row (l%16)/4, head l % 4), dims 32 jj + 8 (l / 16) ..
+  uint32_t qb[4][4];
+  {
+    const int qrow = min(col / 4, nrows - 1);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const uint4 t = s_q[qrow][lane % 4][4 * jj + lane / 16];
+      qb[jj][0] = t.x; qb[jj][1] = t.y; qb[jj][2] = t.z; qb[jj][3] = t.w;
+    }
+  }
+  // ---- K (A operand: token l % 16 of each block, dims 8 (l/16) + 32 jj) and
+  // V (token rows l/16 + 4 s of the 32, dims 8 (l % 16) ..) of the 32 tokens
+  auto tok_addr = [&](int t) -> int64_t {  // element offset of token t of the item, kv head h
+    const int tt = tok0 + t;
+    int64_t pg = (tt - tok0) < 16 ? pg_a : pg_b;
+    pg = pg < 0 ? 0 : (pg >= num_pages ? num_pages - 1 : pg);
+    return pg * page_stride + (int64_t)(tt % page_size) * token_stride + (int64_t)h * head_stride;
+  };
+  uint32_t kw[2][4][4];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const T* kp = kc + tok_addr(blk * 16 + col) + 8 * rg;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const uint4 t = *reinterpret_cast<const uint4*>(kp + 32 * jj);
+      kw[blk][jj][0] = t.x; kw[blk][jj][1] = t.y; kw[blk][jj][2] = t.z; kw[blk][jj][3] = t.w;
+    }
+  }
+  uint4 vr[8];
+#pragma unroll
+  for (int s2 = 0; s2 < 8; ++s2) vr[s2] = *reinterpret_cast<const uint4*>(vc + tok_addr(rg + 4 * s2) + 8 * col);
+  // ---- S^T and the softmax of each column over the 32 tokens
+  f32x4 sacc[2];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    sacc[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) sacc[blk] = mfma_16x16x32<T>(kw[blk][jj], qb[jj], sacc[blk]);
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sacc[blk][i] *= scale_log2;
+      mx = fmaxf(mx, sacc[blk][i]);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  float pv[8], ps = 0.f;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pv[blk * 4 + i] = fast_exp2(sacc[blk][i] - mx);
+      ps += pv[blk * 4 + i];
+    }
+  ps += __shfl_xor(ps, 16);
+  ps += __shfl_xor(ps, 32);
+  // ---- V into LDS (this wave's 8 KB: token row t at words 64 t ..), then O^T
+#pragma unroll
+  for (int s2 = 0; s2 < 8; ++s2)
+    *reinterpret_cast<uint4*>(s_v + (rg + 4 * s2) * 64 + 4 * col) = vr[s2];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  // P^T as the B operand: k = 8 (l/16) + e <-> token 4 (l/16) + e of block 0 (e < 4), of block 1 (e >= 4)
+  u32x4 pb_hi, pb_lo;
+  {
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hw[e] = pack_pv<T>(pv[2 * e], pv[2 * e + 1]);
+      float h0, h1;
+      unpack2<T>(hw[e], h0, h1);
+      lw[e] = pack_pv<T>(pv[2 * e] - h0, pv[2 * e + 1] - h1);
+    }
+    pb_hi = u32x4{hw[0], hw[1], hw[2], hw[3]};
+    pb_lo = u32x4{lw[0], lw[1], lw[2], lw[3]};
+  }
+  int trow[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) trow[e] = (e < 4 ? 4 * rg + e : 16 + 4 * rg + e - 4) * 64;
+  f32x4 acc[8];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    uint32_t w[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = s_v[trow[e] + 16 * a + col];
+    uint32_t alo[4], ahi[4];
+    alo[0] = __builtin_amdgcn_perm(w[1], w[0], 0x05040100u);
+    ahi[0] = __builtin_amdgcn_perm(w[1], w[0], 0x07060302u);
+    alo[1] = __builtin_amdgcn_perm(w[3], w[2], 0x05040100u);
+    ahi[1] = __builtin_amdgcn_perm(w[3], w[2], 0x07060302u);
+    alo[2] = __builtin_amdgcn_perm(w[5], w[4], 0x05040100u);
+    ahi[2] = __builtin_amdgcn_perm(w[5], w[4], 0x07060302u);
+    alo[3] = __builtin_amdgcn_perm(w[7], w[6], 0x05040100u);
+    ahi[3] = __builtin_amdgcn_perm(w[7], w[6], 0x07060302u);
+    const uint32_t phi[4] = {pb_hi[0], pb_hi[1], pb_hi[2], pb_hi[3]};
+    const uint32_t plo[4] = {pb_lo[0], pb_lo[1], pb_lo[2], pb_lo[3]};
+    acc[2 * a] = mfma_16x16x32<T>(alo, phi, f32x4{0.f, 0.f, 0.f, 0.f});
+    acc[2 * a + 1] = mfma_16x16x32<T>(ahi, phi, f32x4{0.f, 0.f, 0.f, 0.f});
+    acc[2 * a] = mfma_16x16x32<T>(alo, plo, acc[2 * a]);
+    acc[2 * a + 1] = mfma_16x16x32<T>(ahi, plo, acc[2 * a + 1]);
+  }
+  // ---- the partial of column col = lane % 16: row b, query head 4h + col % 4,
+  // dims 32a + 8 (l/16) + 2i (tile 2a) and + 1 (tile 2a + 1)
+  const int b = col / 4;
+  if (b >= nrows) return;
+  const int hq = h * G + col % 4;
+  int first = 0;
+  // row b's first slot: b * n_pref + the own items of the rows before it
+#pragma unroll
+  for (int bb = 0; bb < kPrefixMaxRows; ++bb) {
+    const int incl_bb = __builtin_amdgcn_readlane(sc.incl, bb);
+    const int n_bb = __builtin_amdgcn_readlane(sc.n, bb);
+    first = (b == bb) ? bb * sc.n_pref + incl_bb - n_bb : first;
+  }
+  const int slot = first + j;
+  const float inv = ps > 0.f ? 1.f / ps : 0.f;
+  float* op = part_o + ((int64_t)slot * num_qo_heads + hq) * D + 8 * rg;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const float o8[8] = {acc[2 * a][0] * inv, acc[2 * a + 1][0] * inv, acc[2 * a][1] * inv,
+                         acc[2 * a + 1][1] * inv, acc[2 * a][2] * inv, acc[2 * a + 1][2] * inv,
+                         acc[2 * a][3] * inv, acc[2 * a + 1][3] * inv};
+    Lane8<float>::store(op + 32 * a, o8);
+  }
+  if (rg == 0) part_lse[(int64_t)slot * num_qo_heads + hq] = ps > 0.f ? mx + __log2f(ps) : -INFINITY;
+}
+
 // SMALL: pages of a size that is not a multiple of 16 tokens (stream_blocks_small).
 // kv_split: the kernel's kv heads are virtual, kv_split of them per real kv
 // head, each serving G of that head's query heads (GQA groups above 8 run as
 // several waves of at most 8 heads); 1 otherwise.
-template <typename T, int D, int G, bool FUSED = false, int R = 0, bool SMALL = false>
+// PREFIX (FUSED): the launch has a shared prefix (prefix_wave items); its
+// own instantiation, so the prefix code's registers do not cost the plain
+// kernel occupancy.
+template <typename T, int D, int G, bool FUSED = false, int R = 0, bool SMALL = false, bool PREFIX = false>
 __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
     const T* __restrict__ q, int64_t q_sb, int64_t q_sh, const T* __restrict__ kc,
     const T* __restrict__ vc, int64_t page_stride, int64_t token_stride, int64_t head_stride,
@@ -833,15 +1051,41 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
   constexpr int LPT = WaveT::LPT;
   using L8 = Lane8<T>;
 
+  static_assert(!PREFIX || FUSED, "prefix items are built into the folded q/k/v kernel");
+  // the prefix workgroups' V tiles (one 8 KB tile per wave) and q (4 rows x 4 heads)
+  __shared__ uint32_t s_pv[PREFIX ? waves_per_wg<FUSED>() : 1][PREFIX ? kPrefixTokens * 64 : 1];
+  __shared__ uint4 s_q[PREFIX ? kPrefixMaxRows : 1][4][16];
   const int lane = threadIdx.x % kWave;
-  const int wave = uniform(blockIdx.x * waves_per_wg<FUSED>() + threadIdx.x / kWave);
+  int wave = uniform(blockIdx.x * waves_per_wg<FUSED>() + threadIdx.x / kWave);
+  int b, pbeg, pend, flags;
+  [[maybe_unused]] DirectScan sc;
+  if constexpr (PREFIX) {
+    // The first ceil(n_pref / 4) * kv-heads workgroups are prefix
+    // workgroups: workgroup g takes kv head g % hkv and prefix chunks
+    // 4 (g / hkv) + w in its waves w; the rest take the own items as usual.
+    sc = direct_scan(dir, batch);
+    const int pref_wgs = (sc.n_pref + 3) / 4 * num_kv_heads;
+    if ((int)blockIdx.x < pref_wgs) {
+      const int hh = blockIdx.x % num_kv_heads;
+      const int jj = (blockIdx.x / num_kv_heads) * 4 + threadIdx.x / kWave;
+      prefix_wave<T, R>(sc, dir, batch, jj, hh, kc, vc, page_stride, token_stride, head_stride, indices, page_size,
+                        num_pages, scale_log2, qin, num_qo_heads, part_lse, part_o, s_pv[threadIdx.x / kWave], s_q);
+      return;
+    }
+    wave = uniform((blockIdx.x - pref_wgs) * waves_per_wg<FUSED>() + threadIdx.x / kWave) +
+           sc.n_pref * num_kv_heads;
+  }
   const int item_idx = wave / num_kv_heads;
   const int h = wave - item_idx * num_kv_heads;
   const int hk = FUSED ? h : uniform(h / kv_split);  // the real kv head whose pages this wave reads
   if (item_idx >= max_items) return;
-  int b, pbeg, pend, flags;
   if (dir.indptr != nullptr) {  // direct items (uniform)
-    if (!direct_item(dir, batch, item_idx, b, pbeg, pend, flags)) return;
+    bool found;
+    if constexpr (PREFIX)
+      found = direct_item_of(sc, dir, item_idx, b, pbeg, pend, flags);
+    else
+      found = direct_item(dir, batch, item_idx, b, pbeg, pend, flags);
+    if (!found) return;
   } else {
     // The item is read together with the plan stamp (item_idx < max_items
     // keeps the read inside the item table) and used only if the stamp
@@ -1193,20 +1437,31 @@ struct RunArgs {
   const int* header; const Item* items; int max_items; const int2* row_info;
   float* part_lse; float* part_o; int flags;
   Direct dir;  // dir.indptr != nullptr: items derived from indptr (no plan kernel)
+  int grid_items;  // work items the decode grid covers (max_items, the slot count, unless a prefix is shared)
   hipStream_t stream;
 };
 
 template <typename T, int D, int G, bool FUSED = false, int R = 0, bool SMALL = false>
 int launch(const RunArgs& a, const QkvIn& qin = QkvIn{}) {
   if (!(a.flags & PL_DECODE_MERGE_ONLY)) {
-    const int64_t waves = (int64_t)a.max_items * a.hkv;
+    const int64_t waves = (int64_t)a.grid_items * a.hkv;
     constexpr int wpg = waves_per_wg<FUSED>();
     const int grid = (int)((waves + wpg - 1) / wpg);
-    hipLaunchKernelGGL((decode_kernel<T, D, G, FUSED, R, SMALL>), dim3(grid), dim3(kWave * wpg), 0, a.stream,
-                       (const T*)a.q, a.q_sb, a.q_sh, (const T*)a.kc, (const T*)a.vc, a.page_stride,
-                       a.token_stride, a.head_stride, a.indices, a.last, (T*)a.o, a.o_sb, a.o_sh,
-                       a.lse, a.hq, a.hkv, a.page_size, a.num_pages, a.scale_log2, a.header,
-                       a.items, a.batch, a.max_items, a.part_lse, a.part_o, qin, a.kv_split, a.dir);
+    auto go = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWave * wpg), 0, a.stream, (const T*)a.q, a.q_sb, a.q_sh,
+                         (const T*)a.kc, (const T*)a.vc, a.page_stride, a.token_stride, a.head_stride, a.indices,
+                         a.last, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.hq, a.hkv, a.page_size, a.num_pages,
+                         a.scale_log2, a.header, a.items, a.batch, a.max_items, a.part_lse, a.part_o, qin,
+                         a.kv_split, a.dir);
+    };
+    if constexpr (FUSED) {
+      if (a.dir.shared > 0)
+        go(decode_kernel<T, D, G, FUSED, R, SMALL, true>);
+      else
+        go(decode_kernel<T, D, G, FUSED, R, SMALL, false>);
+    } else {
+      go(decode_kernel<T, D, G, FUSED, R, SMALL, false>);
+    }
     PL_LAUNCH_CHECK("decode_kernel");
   }
   if (!(a.flags & PL_DECODE_SKIP_MERGE)) {

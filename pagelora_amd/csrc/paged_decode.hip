@@ -236,7 +236,7 @@ using namespace pl::decode;
 namespace {
 struct DirectRec {
   const int32_t* indptr;
-  int batch, capacity, target_items, min_chunk;
+  int batch, capacity, target_items, min_chunk, shared, pchunk;
 };
 std::mutex g_direct_mutex;
 std::unordered_map<const void*, DirectRec> g_direct;
@@ -251,12 +251,23 @@ bool direct_enabled() {
 
 // The direct plan recorded for `workspace`, if it matches this run.
 Direct direct_for(const void* workspace, int batch, int target_items) {
-  Direct d{nullptr, 0, 1, 1};
+  Direct d{nullptr, 0, 1, 1, 0, 1};
   std::lock_guard<std::mutex> lock(g_direct_mutex);
   const auto it = g_direct.find(workspace);
   if (it != g_direct.end() && it->second.batch == batch && it->second.target_items == target_items)
-    d = Direct{it->second.indptr, it->second.capacity, it->second.target_items, it->second.min_chunk};
+    d = Direct{it->second.indptr, it->second.capacity, it->second.target_items, it->second.min_chunk,
+               it->second.shared, it->second.pchunk};
   return d;
+}
+
+// Slot capacity (max_items) and decode grid items of a run: the plan's
+// target_items + batch, plus with a shared prefix of n_pref items one slot
+// per row for each and grid items for the prefix workgroups (four prefix
+// items of one kv head per workgroup).
+void run_sizes(int batch, int target_items, const Direct& d, int& max_items, int& grid_items) {
+  const int n_pref = d.shared > 0 ? (d.shared + d.pchunk - 1) / d.pchunk : 0;
+  max_items = target_items + batch + batch * n_pref;
+  grid_items = target_items + batch + (n_pref + 3) / 4 * 4;
 }
 }  // namespace
 
@@ -270,6 +281,30 @@ extern "C" int pl_decode_plan(const int32_t* indptr, int batch, int indices_capa
                               int num_qo_heads, int head_dim, int target_items,
                               int min_chunk_pages, void* workspace, size_t workspace_bytes,
                               void* stream) {
+  return pl_decode_plan_shared(indptr, batch, indices_capacity, num_qo_heads, head_dim, target_items,
+                               min_chunk_pages, 0, 1, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t pl_decode_workspace_size_shared(int batch, int target_items, int num_qo_heads, int head_dim,
+                                                  int shared_pages, int prefix_chunk_pages) {
+  if (batch < 0 || target_items <= 0 || num_qo_heads <= 0 || head_dim <= 0 || shared_pages < 0 ||
+      prefix_chunk_pages <= 0)
+    return 0;
+  int max_items, grid_items;
+  run_sizes(batch, target_items, Direct{nullptr, 0, 1, 1, shared_pages, prefix_chunk_pages}, max_items, grid_items);
+  return layout(batch, max_items, num_qo_heads, head_dim).total;
+}
+
+extern "C" int pl_decode_plan_shared(const int32_t* indptr, int batch, int indices_capacity,
+                                     int num_qo_heads, int head_dim, int target_items,
+                                     int min_chunk_pages, int shared_pages, int prefix_chunk_pages,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (shared_pages < 0 || prefix_chunk_pages <= 0 || (shared_pages > 0 && shared_pages % prefix_chunk_pages))
+    return fail(PL_ERR_INVALID, "shared_pages must be a multiple of prefix_chunk_pages (got %d, %d)", shared_pages,
+                prefix_chunk_pages);
+  if (shared_pages > 0 && (batch > kDirectMaxBatch || !direct_enabled()))
+    return fail(PL_ERR_UNSUPPORTED, "a shared prefix needs a batch of up to %d rows planned without the plan kernel",
+                kDirectMaxBatch);
   if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0 (got %d)", batch);
   if (target_items <= 0) return fail(PL_ERR_INVALID, "target_items must be > 0");
   if (num_qo_heads <= 0 || head_dim <= 0) return fail(PL_ERR_INVALID, "bad head shape");
@@ -278,14 +313,18 @@ extern "C" int pl_decode_plan(const int32_t* indptr, int batch, int indices_capa
   if (indptr == nullptr || workspace == nullptr) return fail(PL_ERR_INVALID, "null pointer");
   if ((uintptr_t)workspace % 256) return fail(PL_ERR_INVALID, "workspace must be 256-byte aligned");
   const int max_items = target_items + batch;
-  const Layout L = layout(batch, max_items, num_qo_heads, head_dim);
+  int shared_max_items, grid_items;
+  run_sizes(batch, target_items, Direct{nullptr, 0, 1, 1, shared_pages, prefix_chunk_pages}, shared_max_items,
+            grid_items);
+  const Layout L = layout(batch, shared_max_items, num_qo_heads, head_dim);
   if (L.total > workspace_bytes)
     return fail(PL_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, L.total);
   const int min_chunk = min_chunk_pages < 1 ? 1 : min_chunk_pages;
   {
     std::lock_guard<std::mutex> lock(g_direct_mutex);
     if (direct_enabled() && batch <= kDirectMaxBatch) {
-      g_direct[workspace] = DirectRec{indptr, batch, indices_capacity, target_items, min_chunk};
+      g_direct[workspace] =
+          DirectRec{indptr, batch, indices_capacity, target_items, min_chunk, shared_pages, prefix_chunk_pages};
       return ok();
     }
     g_direct.erase(workspace);
@@ -331,7 +370,18 @@ static int decode_run_common(const void* q, int64_t q_stride_b, int64_t q_stride
   const void* ptrs[] = {qin ? k_cache : q, k_cache, v_cache, o};
   for (const void* p : ptrs)
     if ((uintptr_t)p % 16) return fail(PL_ERR_INVALID, "q, caches and o must be 16-byte aligned");
-  const int max_items = target_items + batch;
+  Direct dir = direct_for(workspace, batch, target_items);
+  // a shared prefix is attended by prefix items in the folded q/k/v kernel
+  // only, for up to 4 rows with one bound adapter, whole 16-token blocks and
+  // one 32-token MFMA step per item; anything else reads every page per row
+  if (dir.shared > 0) {
+    const bool ok_shared = qin != nullptr && batch <= kPrefixMaxRows && page_size % kBlockTokens == 0 &&
+                           dir.pchunk * page_size == kPrefixTokens && head_dim == 128 &&
+                           num_qo_heads == 4 * num_kv_heads && (qin_rank == 0 || qin->m[0].adapter >= 0);
+    if (!ok_shared) dir.shared = 0;
+  }
+  int max_items, grid_items;
+  run_sizes(batch, target_items, dir, max_items, grid_items);
   const Layout L = layout(batch, max_items, num_qo_heads, head_dim);
   if (L.total > workspace_bytes)
     return fail(PL_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, L.total);
@@ -350,7 +400,8 @@ static int decode_run_common(const void* q, int64_t q_stride_b, int64_t q_stride
   a.row_info = (const int2*)(ws + L.row_info);
   a.flags = flags;
   a.part_lse = (float*)(ws + L.lse); a.part_o = (float*)(ws + L.partial_o);
-  a.dir = direct_for(workspace, batch, target_items);
+  a.dir = dir;
+  a.grid_items = grid_items;
   a.stream = (hipStream_t)stream;
   const int g = num_qo_heads / num_kv_heads;
   if (qin) {

@@ -30,9 +30,9 @@ HQ, HKV, D, PS = 32, 8, 128, 16
 THETA = 1e6
 
 
-def _case(device, dtype, lens, seed, rank, n_adapters, bound):
+def _case(device, dtype, lens, seed, rank, n_adapters, bound, shared=0):
     case = ragged_case(lens=lens, hq=HQ, hkv=HKV, head_dim=D, page_size=PS, dtype=dtype, device=device, seed=seed,
-                       pool_extra=4, poison=False)
+                       pool_extra=4, poison=False, shared_prefix_pages=shared)
     B = len(lens)
     gen = torch.Generator().manual_seed(seed + 1)
     cols = (HQ + 2 * HKV) * D
@@ -55,9 +55,10 @@ def _case(device, dtype, lens, seed, rank, n_adapters, bound):
     return case, qkv, qn, kn, page_id, offset, positions, lora, ids
 
 
-def _backend(case, device, tw):
+def _backend(case, device, tw, share=False):
     be = PagedDecodeAttention(device=device, workspace_mb=64, num_qo_heads=HQ, num_kv_heads=HKV, head_dim=D,
                               page_size=PS, target_waves=tw, min_chunk_pages=1)
+    be.share_prefix = share
     be.plan_decode(paged_kv_indptr=case["indptr"], paged_kv_indices=case["indices"],
                    paged_kv_last_page_len=case["last"])
     return be
@@ -118,6 +119,41 @@ def test_folded_matches_two_call_path(gpu_device, dtype, lora_mode, tw):
     assert (err <= 2e-3 + rel * np.abs(ref)).all(), f"max err {err.max():.3e}"
     # and against the two-call output: the same up to q's rounding
     assert np.abs(got - out_ref.float().cpu().numpy()).max() <= 2e-3 + 4 * rel
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("lora_mode", ["none", "bound", "ids"])
+@pytest.mark.parametrize("lens", [[2112, 2112, 2112, 2112], [700, 900, 1210], [100, 130]])
+def test_shared_prefix_matches_unshared(gpu_device, dtype, lora_mode, lens):
+    """Rows that begin with the same pages: the folded run attending the
+    prefix once for all rows (pl_decode_plan_shared: prefix items scoring
+    every row's heads as MFMA columns, P.V on MFMA) against the same run
+    reading the prefix per row, and both against the oracle fed with the
+    two-call path's q and cache (2e-3 + one output rounding).  The appended
+    k/v are the own items' and stay bit-identical.  Per-token adapters fall
+    back to the unshared run."""
+    rank, n_ad, bound = {"none": (0, 1, -1), "ids": (16, 2, -1), "bound": (16, 2, 1)}[lora_mode]
+    shared = min(lens) // PS - 1
+    case, qkv, qn, kn, page_id, offset, positions, lora, ids = _case(gpu_device, dtype, lens, 11 + len(lens), rank,
+                                                                      n_ad, bound, shared=shared)
+    be_s = _backend(case, gpu_device, None, share=True)
+    be_p = _backend(case, gpu_device, None, share=False)
+    assert be_s._plan["shared"] == shared // 2 * 2 and be_p._plan["shared"] == 0
+    cache_r, cache_s, cache_p = case["cache"].clone(), case["cache"].clone(), case["cache"].clone()
+    q_ref, _ = _two_call(case, be_p, qkv, qn, kn, page_id, offset, positions, lora, ids, cache_r)
+    out_s = _folded(case, be_s, qkv, qn, kn, page_id, offset, positions, lora, ids, cache_s)
+    out_p = _folded(case, be_p, qkv, qn, kn, page_id, offset, positions, lora, ids, cache_p)
+    torch.cuda.synchronize()
+    assert torch.equal(cache_s, cache_p)
+    rel = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11
+    ref, _ = opd.paged_decode(q_ref.float().cpu().numpy(), cache_r.float().cpu().numpy(), case["indptr"].numpy(),
+                              case["indices"].numpy(), case["last"].numpy())
+    for name, out in (("shared", out_s), ("per-row", out_p)):
+        got = out.float().cpu().numpy()
+        assert np.isfinite(got).all(), name
+        err = np.abs(got - ref)
+        assert (err <= 2e-3 + rel * np.abs(ref)).all(), f"{name}: max err {err.max():.3e}"
+    assert np.abs(out_s.float().cpu().numpy() - out_p.float().cpu().numpy()).max() <= 2e-3 + 4 * rel
 
 
 def test_out_of_pool_slot_is_skipped(gpu_device):
