@@ -1305,13 +1305,14 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
 // states are combined with xor shuffles inside a wave and through LDS across
 // waves.  MT is one wave when the plan averages a few items per row (the
 // ragged batch-64 case: ~5), four waves when rows hold tens of items, eight
-// beyond 64.
+// beyond 96.
 constexpr int kMergeBatch = 8;
 constexpr int kMergeFewItems = 8;  // average items per row up to which one wave merges
-// Average items per row above which eight waves merge (a row of ~128 items:
+// Average slots per row above which eight waves merge (a row of ~128 items:
 // 1 x 32K tokens, plan + decode + merge 36.7 -> 35.7 us; at ~33 items per
-// row (4 x 2112) four waves stay 0.25 us faster).
-constexpr int kMergeManyItems = 64;
+// row (4 x 2112) four waves stay 0.25 us faster, and at ~69 (the same rows
+// with their 2048-token prefix shared: 64 prefix chunks each) 5.2 -> 4.9 us).
+constexpr int kMergeManyItems = 96;
 constexpr int kMergeCUs = 256;  // MI355X
 
 struct MergeState {
