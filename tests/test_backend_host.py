@@ -96,3 +96,57 @@ def test_cpu_backend_refuses_to_plan_or_run_prefill():
                         paged_kv_last_page_len=_i32([2]))
     with pytest.raises(RuntimeError, match="plan_prefill"):
         be.run_prefill(torch.ones(2, 28, 128), torch.zeros(1, 2, 16, 4, 128))
+
+
+def _prefix_backend(**kw):
+    """A CPU-constructed backend with the library loaded for its size query
+    (the detection is host logic; nothing runs on a device)."""
+    from pagelora_amd import _lib
+
+    be = PagedDecodeAttention(device="cpu", workspace_mb=64, num_qo_heads=32, num_kv_heads=8, head_dim=128,
+                              page_size=16, **kw)
+    be._lib = _lib.load()
+    return be
+
+
+def _table(rows):
+    indptr = [0]
+    for r in rows:
+        indptr.append(indptr[-1] + len(r))
+    return torch.tensor(indptr, dtype=torch.int32), torch.tensor([p for r in rows for p in r], dtype=torch.int32)
+
+
+@pytest.mark.parametrize("rows,want", [
+    # 4 rows behind 10 shared pages: whole 2-page prefix items (10)
+    ([list(range(10)) + [100 + b, 200 + b] for b in range(4)], 10),
+    # an odd shared count rounds down to whole items
+    ([list(range(9)) + [100 + b] for b in range(3)], 8),
+    # every row keeps its last page (the one being appended to) as its own
+    ([list(range(12)) for _ in range(2)], 10),
+    # rows that differ from the third page on: below two items, nothing shared
+    ([[0, 1, 2 + b, 3, 4, 5] for b in range(2)], 0),
+    # one row, or more than 4: no sharing
+    ([list(range(10)) + [100]], 0),
+    ([list(range(10)) + [100 + b] for b in range(5)], 0),
+])
+def test_shared_prefix_detection(rows, want):
+    be = _prefix_backend()
+    indptr, indices = _table(rows)
+    assert be._shared_prefix_pages(indptr, indices, len(rows), 16) == want
+
+
+def test_shared_prefix_needs_gqa4_head128_and_32_token_items():
+    rows = [list(range(10)) + [100 + b] for b in range(4)]
+    indptr, indices = _table(rows)
+    be = _prefix_backend()
+    be.share_prefix = False
+    assert be._shared_prefix_pages(indptr, indices, 4, 16) == 0
+    from pagelora_amd import _lib
+    for kw in (dict(num_qo_heads=8, num_kv_heads=8, head_dim=128), dict(num_qo_heads=32, num_kv_heads=8, head_dim=64)):
+        b2 = PagedDecodeAttention(device="cpu", workspace_mb=64, page_size=16, **kw)
+        b2._lib = _lib.load()
+        assert b2._shared_prefix_pages(indptr, indices, 4, 16) == 0
+    b3 = PagedDecodeAttention(device="cpu", workspace_mb=64, num_qo_heads=32, num_kv_heads=8, head_dim=128,
+                              page_size=12)
+    b3._lib = _lib.load()
+    assert b3._shared_prefix_pages(indptr, indices, 4, 16) == 0
