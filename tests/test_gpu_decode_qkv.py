@@ -30,9 +30,10 @@ HQ, HKV, D, PS = 32, 8, 128, 16
 THETA = 1e6
 
 
-def _case(device, dtype, lens, seed, rank, n_adapters, bound, shared=0):
-    case = ragged_case(lens=lens, hq=HQ, hkv=HKV, head_dim=D, page_size=PS, dtype=dtype, device=device, seed=seed,
+def _case(device, dtype, lens, seed, rank, n_adapters, bound, shared=0, ps=PS):
+    case = ragged_case(lens=lens, hq=HQ, hkv=HKV, head_dim=D, page_size=ps, dtype=dtype, device=device, seed=seed,
                        pool_extra=4, poison=False, shared_prefix_pages=shared)
+    case["ps"] = ps
     B = len(lens)
     gen = torch.Generator().manual_seed(seed + 1)
     cols = (HQ + 2 * HKV) * D
@@ -57,7 +58,7 @@ def _case(device, dtype, lens, seed, rank, n_adapters, bound, shared=0):
 
 def _backend(case, device, tw, share=False):
     be = PagedDecodeAttention(device=device, workspace_mb=64, num_qo_heads=HQ, num_kv_heads=HKV, head_dim=D,
-                              page_size=PS, target_waves=tw, min_chunk_pages=1)
+                              page_size=case["ps"], target_waves=tw, min_chunk_pages=1)
     be.share_prefix = share
     be.plan_decode(paged_kv_indptr=case["indptr"], paged_kv_indices=case["indices"],
                    paged_kv_last_page_len=case["last"])
@@ -67,7 +68,7 @@ def _backend(case, device, tw, share=False):
 def _two_call(case, be, qkv, qn, kn, page_id, offset, positions, lora, ids, cache):
     cols = (HQ + 2 * HKV) * D
     q = fused_ops.qk_norm_rope_append(qkv[:, :cols], qn, kn, positions, page_id, offset, cache, num_qo_heads=HQ,
-                                      num_kv_heads=HKV, head_dim=D, page_size=PS, rope_theta=THETA, eps=1e-6,
+                                      num_kv_heads=HKV, head_dim=D, page_size=case["ps"], rope_theta=THETA, eps=1e-6,
                                       lora=lora, adapter_ids=ids)
     out = torch.empty_like(q)
     be.run_decode_into(q, cache, out)
@@ -123,22 +124,26 @@ def test_folded_matches_two_call_path(gpu_device, dtype, lora_mode, tw):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("lora_mode", ["none", "bound", "ids"])
-@pytest.mark.parametrize("lens", [[2112, 2112, 2112, 2112], [700, 900, 1210], [100, 130]])
-def test_shared_prefix_matches_unshared(gpu_device, dtype, lora_mode, lens):
+@pytest.mark.parametrize("lens,ps", [([2112, 2112, 2112, 2112], 16), ([700, 900, 1210], 16), ([100, 130], 16),
+                                     ([2112, 2150, 2200, 2300], 32), ([100, 130], 32), ([97, 96], 32)])
+def test_shared_prefix_matches_unshared(gpu_device, dtype, lora_mode, lens, ps):
     """Rows that begin with the same pages: the folded run attending the
-    prefix once for all rows (pl_decode_plan_shared: prefix items scoring
-    every row's heads as MFMA columns, P.V on MFMA) against the same run
-    reading the prefix per row, and both against the oracle fed with the
-    two-call path's q and cache (2e-3 + one output rounding).  The appended
-    k/v are the own items' and stay bit-identical.  Per-token adapters fall
-    back to the unshared run."""
+    prefix once for all rows (pl_decode_plan_shared: prefix items of 32
+    tokens, two 16-token pages or one 32-token page, scoring every row's
+    heads as MFMA columns, P.V on MFMA) against the same run reading the
+    prefix per row, and both against the oracle fed with the two-call
+    path's q and cache (2e-3 + one output rounding).  The appended k/v are
+    the own items' and stay bit-identical.  Per-token adapters fall back to
+    the unshared run.  [97, 96] on 32-token pages: the shorter row holds
+    exactly one page past the prefix."""
     rank, n_ad, bound = {"none": (0, 1, -1), "ids": (16, 2, -1), "bound": (16, 2, 1)}[lora_mode]
-    shared = min(lens) // PS - 1
+    shared = (min(lens) + ps - 1) // ps - 1
+    pchunk = 32 // ps
     case, qkv, qn, kn, page_id, offset, positions, lora, ids = _case(gpu_device, dtype, lens, 11 + len(lens), rank,
-                                                                      n_ad, bound, shared=shared)
+                                                                      n_ad, bound, shared=shared, ps=ps)
     be_s = _backend(case, gpu_device, None, share=True)
     be_p = _backend(case, gpu_device, None, share=False)
-    assert be_s._plan["shared"] == shared // 2 * 2 and be_p._plan["shared"] == 0
+    assert be_s._plan["shared"] == shared // pchunk * pchunk and be_p._plan["shared"] == 0
     cache_r, cache_s, cache_p = case["cache"].clone(), case["cache"].clone(), case["cache"].clone()
     q_ref, _ = _two_call(case, be_p, qkv, qn, kn, page_id, offset, positions, lora, ids, cache_r)
     out_s = _folded(case, be_s, qkv, qn, kn, page_id, offset, positions, lora, ids, cache_s)
