@@ -50,7 +50,11 @@ from . import _lib
 #   - larger batches with >= 16 kv heads: 192 items, i.e. 6 waves per SIMD
 #     (ragged batch-64 MHA: 713.5 us against 729 us at 256 items).
 _ENV_TARGET_WAVES = os.environ.get("PAGELORA_DECODE_TARGET_WAVES")
-_DEFAULT_MIN_CHUNK_PAGES = int(os.environ.get("PAGELORA_DECODE_MIN_CHUNK_PAGES", "4"))
+# The minimum chunk binds only for short rows (a chunk is otherwise
+# total / target_items pages).  1 x 2048 tokens bf16, GQA 4 (32 items at 4
+# pages, 64 at 2), plan-less step in a graph: 21.2 -> 20.2 us warm, 23.3 ->
+# 22.3 us cold at 2 pages.
+_DEFAULT_MIN_CHUNK_PAGES = int(os.environ.get("PAGELORA_DECODE_MIN_CHUNK_PAGES", "2"))
 
 
 def default_target_items(batch: int, num_kv_heads: int, num_qo_heads: int | None = None,
@@ -145,7 +149,7 @@ class PagedDecodeAttention:
         self.decode_use_tensor_cores = False
         self.use_flashinfer_qk_norm = False
         self.target_waves = int(target_waves) if target_waves else None  # None: default_target_items(...)
-        # the minimum split chunk is 64 tokens (4 pages of 16) whatever the page size
+        # the minimum split chunk is 32 tokens (2 pages of 16) whatever the page size
         default_chunk = _DEFAULT_MIN_CHUNK_PAGES if self.page_size >= 16 else \
             -(-_DEFAULT_MIN_CHUNK_PAGES * 16 // max(1, self.page_size))
         self.min_chunk_pages = int(min_chunk_pages or default_chunk)

@@ -153,11 +153,11 @@ def test_small_page_sizes(gpu_device, dtype, page_size, heads, head_dim):
 
 def test_small_pages_default_chunking(gpu_device):
     """Default plan on 2-token pages: the minimum chunk is scaled to the
-    page size (64 tokens), the rows still match the oracle."""
+    page size (32 tokens), the rows still match the oracle."""
     case = ragged_case(lens=[2048, 100, 1], hq=32, hkv=8, head_dim=128, page_size=2, dtype=torch.bfloat16,
                        device=gpu_device, seed=31, pool_extra=11)
     out, _, be = _run(case, 32, 8, 128, 2, torch.bfloat16, gpu_device)
-    assert be.min_chunk_pages == 32
+    assert be.min_chunk_pages == 16
     ref, _ = _oracle(case)
     _check(out, ref, torch.bfloat16)
 
