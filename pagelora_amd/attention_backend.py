@@ -119,6 +119,12 @@ class PagedDecodeAttention:
     share_prefix = True
     # pages per prefix item: 32 tokens, one MFMA step of the prefix kernel path
     _PREFIX_TOKENS = 32
+    # With a shared prefix: own items per row the grid is sized for, and the
+    # own items' minimum chunk in pages (None: the prefix item's).  4 rows x
+    # (2048 shared + 64+) end to end, alternating: 4 items of >= 2 pages
+    # 1000.1 tok/s, 8 of >= 2 1002.2, 8 of >= 1 1003.2, 16 of >= 1 1003.5.
+    _SHARED_OWN_ITEMS_PER_ROW = 8
+    _SHARED_OWN_MIN_CHUNK: int | None = 1
 
     def __init__(
         self,
@@ -227,7 +233,7 @@ class PagedDecodeAttention:
             if shared:
                 # the rows' own pages past the prefix are few: a few items each
                 # (a grid sized for 128 would be mostly idle workgroups)
-                target_items = min(target_items, 4 * batch)
+                target_items = min(target_items, self._SHARED_OWN_ITEMS_PER_ROW * batch)
         self._plan = {
             "batch": batch,
             "target_items": target_items,
@@ -285,7 +291,7 @@ class PagedDecodeAttention:
             self.head_dim,
             target_items,
             # own items as short as the prefix items when a prefix is shared
-            pchunk if shared else self.min_chunk_pages,
+            (self._SHARED_OWN_MIN_CHUNK or pchunk) if shared else self.min_chunk_pages,
             shared,
             pchunk if shared else 1,
             self.workspace_buffer.data_ptr(),
