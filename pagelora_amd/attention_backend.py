@@ -39,7 +39,9 @@ from . import _lib
 # pages.  The default item count was measured on MI355X (1,024 SIMDs), step
 # time of plan + decode + merge:
 #   - batch <= 32: 128 items (4 x 2114 and 1 x 32K tokens, GQA 4: 1,024 waves,
-#     one per SIMD; 256 or 64 items were 5-10% slower);
+#     one per SIMD; 256 or 64 items were 5-10% slower; re-checked end to end
+#     on the 36-layer 1 x 32K step with q/k/v folded in: 226.1 tok/s at 128
+#     items, 210.3 at 192, 215.8 at 256);
 #   - GQA 4 with head_dim 128 (scores on MFMA) at any batch: 128 items
 #     (bf16, 8 kv heads: 64 x 2048 90.9 us against 92.0 at 256 items,
 #     128 x 2048 166.6 vs 170.8, 64 x 8192 325.1 vs 326.1; 192 items, an
