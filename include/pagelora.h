@@ -67,9 +67,12 @@ size_t pl_decode_workspace_size(int batch, int target_items, int num_qo_heads,
  * No host read-back: the plan runs on the stream, so it can sit inside a
  * captured hipGraph and one graph replays across steps whatever the lengths.
  * For batches of up to 16 rows nothing is launched: the library records
- * indptr and the split parameters against `workspace`, and the runs on that
- * workspace derive the same chunking from indptr inside their kernels (items
- * in row order).  indptr must then stay valid until those runs execute.
+ * the indptr pointer and the split parameters against `workspace` (host
+ * state of the library), and the runs on that workspace derive the same
+ * chunking from indptr inside their kernels (items in row order).  indptr is
+ * then not snapshotted: the runs read it when they execute, so it must stay
+ * valid (and hold the step's row pointer) until then, and a workspace that
+ * is freed should be released with pl_decode_forget.
  * PAGELORA_DECODE_PLAN_KERNEL=1 in the environment keeps the plan kernel for
  * every batch.
  *
@@ -84,6 +87,17 @@ int pl_decode_plan(const int32_t* indptr, int batch, int indices_capacity,
                    void* stream);
 
 /*
+ * Drops the direct plan the library holds for `workspace` (see
+ * pl_decode_plan), so a later allocation at the same address cannot inherit
+ * it; runs on that workspace then need a fresh plan.  Call it before freeing
+ * a decode workspace.  Returns PL_OK whether or not a plan was held.  No
+ * counterpart in the reference: FlashInfer's wrapper keeps its plan in the
+ * wrapper object (attention_backend.py:63-118), whose lifetime is the
+ * workspace's.
+ */
+int pl_decode_forget(const void* workspace);
+
+/*
  * pl_decode_plan for a batch whose rows all begin with the same
  * shared_pages page ids (a shared prompt prefix held in shared pages; a
  * multiple of prefix_chunk_pages, and fewer than every row's page count).
@@ -96,7 +110,9 @@ int pl_decode_plan(const int32_t* indptr, int batch, int indices_capacity,
  * pl_decode_run, every row reads every page as after pl_decode_plan.  The
  * results equal the unshared run's up to the order of the softmax merge.
  * Needs the direct plan (batch <= 16, see above) and a workspace of
- * pl_decode_workspace_size_shared bytes.  No counterpart in the reference:
+ * pl_decode_workspace_size_shared bytes; a larger batch, or the plan kernel
+ * forced by PAGELORA_DECODE_PLAN_KERNEL=1, is planned as by pl_decode_plan
+ * (shared_pages ignored).  No counterpart in the reference:
  * its decode wrapper reads a shared page once per row (FlashInfer's
  * BatchDecodeWithPagedKVCacheWrapper, attention_backend.py:63-131).
  */

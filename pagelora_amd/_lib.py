@@ -126,6 +126,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pl_decode_plan": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
     "pl_decode_workspace_size_shared": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "pl_decode_plan_shared": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
+    "pl_decode_forget": (_i32, [_vp]),
     "pl_decode_run": (
         _i32,
         [

@@ -26,6 +26,7 @@ from __future__ import annotations
 import ctypes
 import math
 import os
+import weakref
 from collections import deque
 from typing import Sequence
 
@@ -166,6 +167,11 @@ class PagedDecodeAttention:
         else:
             self._lib = None
         self.workspace_buffer = torch.empty(self.workspace_mb * 1024 * 1024, dtype=torch.uint8, device=self.device)
+        if self._lib is not None:
+            # the library's direct plan for this workspace dies with it, so a
+            # later tensor at the same address starts without one
+            weakref.finalize(self.workspace_buffer, self._lib.pl_decode_forget,
+                             ctypes.c_void_p(self.workspace_buffer.data_ptr()))
         # Initial capacity of the persistent indices buffer.  A capacity that
         # covers every page a batch can list (e.g. the pool size) means the
         # buffers, and so decode_graph_signature(), never change as rows grow.

@@ -285,6 +285,12 @@ extern "C" int pl_decode_plan(const int32_t* indptr, int batch, int indices_capa
                                min_chunk_pages, 0, 1, workspace, workspace_bytes, stream);
 }
 
+extern "C" int pl_decode_forget(const void* workspace) {
+  std::lock_guard<std::mutex> lock(g_direct_mutex);
+  g_direct.erase(workspace);
+  return ok();
+}
+
 extern "C" size_t pl_decode_workspace_size_shared(int batch, int target_items, int num_qo_heads, int head_dim,
                                                   int shared_pages, int prefix_chunk_pages) {
   if (batch < 0 || target_items <= 0 || num_qo_heads <= 0 || head_dim <= 0 || shared_pages < 0 ||
@@ -302,9 +308,13 @@ extern "C" int pl_decode_plan_shared(const int32_t* indptr, int batch, int indic
   if (shared_pages < 0 || prefix_chunk_pages <= 0 || (shared_pages > 0 && shared_pages % prefix_chunk_pages))
     return fail(PL_ERR_INVALID, "shared_pages must be a multiple of prefix_chunk_pages (got %d, %d)", shared_pages,
                 prefix_chunk_pages);
-  if (shared_pages > 0 && (batch > kDirectMaxBatch || !direct_enabled()))
-    return fail(PL_ERR_UNSUPPORTED, "a shared prefix needs a batch of up to %d rows planned without the plan kernel",
-                kDirectMaxBatch);
+  // A shared prefix is attended once only on direct plans (up to
+  // kDirectMaxBatch rows, plan kernel not forced); otherwise the batch is
+  // planned unshared, every row reading its own copy of the prefix pages.
+  if (shared_pages > 0 && (batch > kDirectMaxBatch || !direct_enabled())) {
+    shared_pages = 0;
+    prefix_chunk_pages = 1;
+  }
   if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0 (got %d)", batch);
   if (target_items <= 0) return fail(PL_ERR_INVALID, "target_items must be > 0");
   if (num_qo_heads <= 0 || head_dim <= 0) return fail(PL_ERR_INVALID, "bad head shape");

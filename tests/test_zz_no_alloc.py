@@ -3,7 +3,9 @@ with the work list and split partials in the library's per-device scratch
 array, against the existing pl_decode_plan + pl_decode_run on a caller
 workspace.  Same kernels and plan, so outputs and LSE must be bit-identical;
 checked on calls in a row (each smaller than the one before, so a stale work
-list or partial would show), and a plan larger than the scratch maximum is
+list or partial would show): batches of 64 and 17 rows, planned by the plan
+kernel into the scratch, then batches of up to 16 rows, whose items the
+kernels derive from indptr.  A plan larger than the scratch maximum is
 rejected before any launch.
 """
 
@@ -13,7 +15,7 @@ import pytest
 import torch
 
 from pagelora_amd import _lib
-from tests.gpu_cases import ragged_case
+from tests.gpu_cases import ragged_case, uniform_lens
 
 pytestmark = pytest.mark.gpu
 
@@ -55,7 +57,14 @@ def test_noalloc_matches_workspace_entry(gpu_device, dtype):
     lib = _lib.load()
     stream = _lib.stream_handle(gpu_device)
     ws = torch.empty(64 << 20, dtype=torch.uint8, device=gpu_device)
+    rows64 = uniform_lens(64, 1, 1024, seed=71)
+    rows64[5] = 0
     calls = [  # (lens, target items): each call smaller than the one before
+        # more than 16 rows: the plan kernel writes the work list, row table
+        # and header into the scratch, and the next (smaller) plan must not
+        # leave any of this one's items behind
+        (rows64, 256),
+        (uniform_lens(17, 1, 3000, seed=72), 128),
         ([4100, 1, 17, 300, 2047, 16, 0, 8192], 128),
         ([32768], 128),          # one row cut into many items: partials merged from the scratch
         ([700, 33, 5], 64),
