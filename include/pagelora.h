@@ -596,6 +596,16 @@ size_t pl_lora_delta_workspace_size(const pl_lora_group* groups_h, int num_group
  * ranks, out_features and ldo multiples of 8 and B and the outputs 16-byte
  * aligned, the call is two launches built for decode latency; otherwise the
  * general shrink + expand pair (same results to the stated tolerance).
+ *
+ * Non-finite values propagate as the reference's packed product
+ * F.linear(F.linear(x, A_cat), B_bd) propagates them: a NaN or infinity in
+ * x or A makes the intermediate of that (token, rank) NaN or infinite, and
+ * the expand carries it into every output column of the group for that
+ * token (0 * inf = NaN through the block-diagonal B, as in the reference's
+ * dense B_bd).  Tokens of other adapters are not affected by x or A; a
+ * non-finite value in the B of an adapter reaches every token of the call.
+ * The decode path sums the k-split in fixed point: a finite partial of
+ * magnitude above 2^31 saturates there.
  */
 int pl_lora_delta(const void* x, int64_t ldx, int num_tokens, int in_features,
                   const pl_lora_module* modules_h, int num_modules,

@@ -229,6 +229,7 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(
   __shared__ int s_list[kMaxTokens];
   __shared__ int s_count;
   __shared__ __align__(16) uint16_t s_y[16][128 + 8];  // r_pad <= 128; +8 keeps rows 16-byte aligned
+  __shared__ int s_nf[kWaves];
   const int a = blockIdx.y;
   const int n_a = gather_tokens(ids, tokens, a, s_list, &s_count, kThreads);
   if (n_a == 0) return;
@@ -286,6 +287,7 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(
     // one thread per (valid token, rank) cell, eight independent loads in
     // flight per step; rows of absent tokens are zero
     const int valid = min(16, n_a - tt * 16);
+    bool nonfinite = false;  // this thread rounded a NaN or an infinity into the tile
     for (int c = threadIdx.x; c < 16 * g.r_pad; c += kThreads) {
       const int i = c / g.r_pad, k = c - i * g.r_pad;
       float sum = 0.f;
@@ -302,16 +304,41 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(
         }
         for (; q < ksplit; ++q) sum += pp[q * stride];
       }
-      s_y[i][k] = __builtin_bit_cast(uint16_t, from_float<T>(sum));
+      const T yt = from_float<T>(sum);
+      nonfinite |= !__builtin_isfinite(to_float<T>(yt));
+      s_y[i][k] = __builtin_bit_cast(uint16_t, yt);
     }
+    const uint64_t nf_ballot = __ballot(nonfinite);
+    if (lane == 0) s_nf[wave] = nf_ballot != 0;
     __syncthreads();
+    bool any_nonfinite = false;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) any_nonfinite |= s_nf[w] != 0;
     if (tile_ok) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (!any_nonfinite) {
 #pragma unroll
-      for (int kt = 0; kt < kMaxKt; ++kt) {  // static indices keep bop[] in registers
-        if (kt < n_kt) {
-          const uint4 av = *reinterpret_cast<const uint4*>(&s_y[lr][kt * 32 + kq]);
-          acc = mfma32<T>(av, bop[kt], acc);
+        for (int kt = 0; kt < kMaxKt; ++kt) {  // static indices keep bop[] in registers
+          if (kt < n_kt) {
+            const uint4 av = *reinterpret_cast<const uint4*>(&s_y[lr][kt * 32 + kq]);
+            acc = mfma32<T>(av, bop[kt], acc);
+          }
+        }
+      } else if (mi >= 0) {
+        // a NaN or an infinity in the tile: the contraction over the
+        // concatenated ranks would carry it into the other modules' columns
+        // through B's zeros (0 * inf = NaN), so each output is the column
+        // module's own dot product, as F.linear(F.linear(x, A_m), B_m) gives
+        const Mod& m = g.m[mi];
+        const T* brow = (const T*)m.B + ((int64_t)a * m.out_features + (o - m.out_offset)) * m.rank;
+#pragma unroll 1
+        for (int i = 0; i < 4; ++i) {
+          const int row = (lane / 16) * 4 + i;
+          float sum = 0.f;
+#pragma unroll 1
+          for (int jl = 0; jl < m.rank; ++jl)
+            sum += to_float<T>(__builtin_bit_cast(T, s_y[row][m.rank_offset + jl])) * to_float<T>(brow[jl]);
+          acc[i] = sum;
         }
       }
       if (out_col != nullptr) {
@@ -346,10 +373,17 @@ constexpr int kFastMaxRank = 128;     // r_pad limit (make_group)
 // The shrink's slices meet in a signed 64-bit fixed-point accumulator with
 // 26 fraction bits: integer adds are associative, so the sum (and the
 // rounded intermediate) does not depend on the order the slices arrive in.
-// Each partial is clamped to +-2^31 first, so 64 slices cannot overflow.
+// Each finite partial is clamped to +-2^31 first, so 64 slices cannot
+// overflow.  A non-finite partial is not added: it sets a flag bit of its
+// (token, rank) instead (kFlagNaN, kFlagPosInf, kFlagNegInf, ORed over the
+// slices) and the slot's any-flag word, and the expand turns a flagged value
+// into what a float sum of the partials gives: NaN when a NaN or both
+// infinities were seen, else the infinity.  The expand then computes the
+// outputs of a call with non-finite intermediates per module (below).
 constexpr float kFixScale = 67108864.f;          // 2^26
 constexpr double kFixInv = 1.0 / 67108864.0;
 constexpr float kFixClamp = 2147483648.f;        // 2^31
+constexpr int kFlagNaN = 1, kFlagPosInf = 2, kFlagNegInf = 4;
 // Workspace of pl_lora_delta(_groups): per group a parity word, then per
 // group two fixed-size accumulator slots, then the general path's shrink
 // partials (disjoint regions, so a general-path call never disturbs the
@@ -358,10 +392,14 @@ constexpr float kFixClamp = 2147483648.f;        // 2^31
 // reads the sum of both slots and flips the parity.  Starting from an
 // all-zero workspace, the slot a shrink adds into is therefore always zero,
 // with no wait inside either kernel: the kernel boundaries order the clear
-// against the reads.
+// against the reads.  A slot is the accumulator [tokens][r_pad] (int64),
+// the non-finite flags [tokens][r_pad] (int32) and the any-flag word.
 constexpr size_t kParityBytes = 256;
-constexpr size_t kAccSlotBytes = (size_t)kFastMaxTokens * kFastMaxRank * sizeof(long long);
+constexpr size_t kAccBytes = (size_t)kFastMaxTokens * kFastMaxRank * sizeof(long long);
+constexpr size_t kFlagBytes = (size_t)kFastMaxTokens * kFastMaxRank * sizeof(int);
+constexpr size_t kAccSlotBytes = kAccBytes + kFlagBytes + 256;
 constexpr size_t kAccSlotPairs = kAccSlotBytes / 16;
+static_assert(kAccSlotBytes % 256 == 0, "slots stay 256-byte aligned");
 constexpr size_t kGeneralOffset = kParityBytes + 2 * PL_LORA_MAX_GROUPS * kAccSlotBytes;
 
 struct FastGroup {
@@ -402,6 +440,11 @@ __device__ __forceinline__ V pin(V v) {
 
 __device__ __forceinline__ long long to_fixed(float v) {
   return (long long)__builtin_rintf(fminf(fmaxf(v, -kFixClamp), kFixClamp) * kFixScale);
+}
+
+// The flag bit of a non-finite partial.
+__device__ __forceinline__ int nonfinite_flag(float v) {
+  return __builtin_isnan(v) ? kFlagNaN : (v > 0.f ? kFlagPosInf : kFlagNegInf);
 }
 
 // Row j of the group's concatenated A (adapter 0) as a byte offset from
@@ -572,9 +615,16 @@ __global__ __launch_bounds__(kShrinkThreads) void fast_shrink_kernel(FastArgs fa
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int tr = wave * 16 + (lane / 16) * 4 + i;
-    if (tr < T_ && id_tr[i] >= 0 && id_tr[i] < n_ad && j < r_total)
-      __hip_atomic_fetch_add(acc + (int64_t)tr * r_pad + j, to_fixed(res[i]), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    if (tr < T_ && id_tr[i] >= 0 && id_tr[i] < n_ad && j < r_total) {
+      const int64_t e = (int64_t)tr * r_pad + j;
+      if (__builtin_isfinite(res[i])) {
+        __hip_atomic_fetch_add(acc + e, to_fixed(res[i]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {  // flagged instead (the expand reads the flags when the slot's any-flag is set)
+        int* flags = reinterpret_cast<int*>(reinterpret_cast<char*>(acc) + kAccBytes);
+        __hip_atomic_fetch_or(flags + e, nonfinite_flag(res[i]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_or(flags + kFlagBytes / sizeof(int), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
   // this workgroup's share of clearing the other slot (all of it: an earlier
   // call may have used it with another layout)
@@ -627,6 +677,49 @@ struct OutChunk {  // 8 consecutive outputs
   uint4 w[kWords];
 };
 
+// The value a float sum of partials gives whose non-finite ones set `flags`
+// (nonzero): NaN when a NaN or both infinities were seen, else the infinity.
+__device__ __forceinline__ float flagged_value(int flags) {
+  const bool nan = (flags & kFlagNaN) | ((flags & (kFlagPosInf | kFlagNegInf)) == (kFlagPosInf | kFlagNegInf));
+  return nan ? __builtin_nanf("") : ((flags & kFlagPosInf) ? __builtin_inff() : -__builtin_inff());
+}
+
+// A call whose rounded intermediate holds a NaN or an infinity: the MFMA's
+// contraction over the group's concatenated ranks multiplies it by the zeros
+// of B outside its module (0 * inf = NaN), so the outputs of the
+// decode-size expand are computed here instead, per module as
+// F.linear(F.linear(x, A_m), B_m) * scale does:
+//   d[e] = scale * sum_j y[j] * B[c + e][j],  j over the columns' module,
+// in fp32 with IEEE semantics, y read from the LDS tile (the values rounded
+// to T) and B from memory.  Slow, and taken only by such calls.
+template <typename T>
+__device__ __forceinline__ void module_dot(const ExpandMods& em, const uint16_t* y_row, int c, int a,
+                                           float (&d)[8]) {
+  uint64_t b_off = 0;
+  uint32_t scale_bits = 0;
+  int roff = 0, rank = 0, outf = 0, ooff = 0;
+#pragma unroll
+  for (int m = 0; m < PL_LORA_MAX_MODULES; ++m) {  // blended with masks (an index would move em to scratch)
+    const bool in = (m < em.n) & (c >= em.ooff[m]) & (c < em.ooff[m] + em.outf[m]);
+    const uint64_t mask = 0 - (uint64_t)in;
+    b_off |= (em.B[m] - em.B[0]) & mask;
+    scale_bits |= em.scale[m] & (uint32_t)mask;
+    roff |= em.roff[m] & (int)mask;
+    rank |= em.rank[m] & (int)mask;
+    outf |= em.outf[m] & (int)mask;
+    ooff |= em.ooff[m] & (int)mask;
+  }
+  const T* B = (const T*)(gptr<const char*>(em.B[0]) + (int64_t)b_off) + ((int64_t)a * outf + (c - ooff)) * rank;
+#pragma unroll 1
+  for (int e8 = 0; e8 < 8; ++e8) {
+    float sum = 0.f;
+#pragma unroll 1
+    for (int jl = 0; jl < rank; ++jl)
+      sum += to_float<T>(__builtin_bit_cast(T, y_row[roff + jl])) * to_float<T>(B[(int64_t)e8 * rank + jl]);
+    d[e8] = __uint_as_float(scale_bits) * sum;
+  }
+}
+
 template <typename T, typename OT, int NKT, bool MANY, int EW>
 __global__ __launch_bounds__(EW * 64) void fast_expand_kernel(FastArgs fa) {
   constexpr int kExpandWaves = EW;
@@ -637,6 +730,7 @@ __global__ __launch_bounds__(EW * 64) void fast_expand_kernel(FastArgs fa) {
   static_assert(kStagePairs * kExpandThreads * 2 == kFastMaxTokens * 32, "staging covers one 32-rank tile");
   __shared__ __align__(16) uint16_t s_y[kFastMaxTokens][kFastMaxRank + 8];  // +8 keeps rows 16-byte aligned
   __shared__ __align__(16) float s_d[kFastMaxTokens][kFastCols + 4];        // +4: rows start on other banks
+  __shared__ int s_nf[EW];
   // flat grid, groups in order (a 2-D grid pads every group to the largest:
   // the idle workgroups slow the dispatch of the rest)
   int gi = 0;
@@ -701,16 +795,30 @@ __global__ __launch_bounds__(EW * 64) void fast_expand_kernel(FastArgs fa) {
       bv[u] = *reinterpret_cast<const longlong2*>(accp + kSlot + off);
     }
   };
-  auto stage_store = [&](int kt, const longlong2 (&av)[kStagePairs], const longlong2 (&bv)[kStagePairs]) {
+  // the slots' non-finite flags (read only when a shrink flagged a value)
+  const int* const flg = reinterpret_cast<const int*>(reinterpret_cast<const char*>(accp) + kAccBytes);
+  constexpr int64_t kFlagSlot = kAccSlotBytes / sizeof(int);
+  bool nonfinite = false;  // this thread staged a NaN or an infinity
+  auto stage_store = [&](int kt, const longlong2 (&av)[kStagePairs], const longlong2 (&bv)[kStagePairs],
+                         bool flagged) {
 #pragma unroll
     for (int u = 0; u < kStagePairs; ++u) {
       const int p = u * kExpandThreads + threadIdx.x;
       const int tk = p / 16, j2 = kt * 32 + 2 * (p % 16);
       if (tk < T_) {
         const long long x0 = av[u].x + bv[u].x, x1 = av[u].y + bv[u].y;
-        const uint16_t lo = __builtin_bit_cast(uint16_t, from_float<T>((float)((double)x0 * kFixInv)));
-        const uint16_t hi = __builtin_bit_cast(uint16_t, from_float<T>((float)((double)x1 * kFixInv)));
-        *reinterpret_cast<uint32_t*>(&s_y[tk][j2]) = lo | ((uint32_t)hi << 16);
+        float y0 = (float)((double)x0 * kFixInv), y1 = (float)((double)x1 * kFixInv);
+        if (flagged) {  // uniform: a shrink of this call flagged a non-finite partial
+          const int64_t e = (int64_t)tk * r_pad + j2;
+          const int f0 = flg[e] | flg[kFlagSlot + e], f1 = flg[e + 1] | flg[kFlagSlot + e + 1];
+          y0 = f0 ? flagged_value(f0) : y0;
+          y1 = f1 ? flagged_value(f1) : y1;
+        }
+        const T t0 = from_float<T>(y0), t1 = from_float<T>(y1);
+        // a NaN or an infinity, also from rounding a finite value past T's range
+        nonfinite = nonfinite || !__builtin_isfinite(to_float<T>(t0)) || !__builtin_isfinite(to_float<T>(t1));
+        *reinterpret_cast<uint32_t*>(&s_y[tk][j2]) =
+            __builtin_bit_cast(uint16_t, t0) | ((uint32_t)__builtin_bit_cast(uint16_t, t1) << 16);
       }
     }
   };
@@ -720,6 +828,9 @@ __global__ __launch_bounds__(EW * 64) void fast_expand_kernel(FastArgs fa) {
   const int id_raw = ids[lane < T_ ? lane : 0];
   longlong2 av2[kStagePairs], bv2[kStagePairs];
   stage_load(kt_lo, av2, bv2);
+  // the any-flag words of both slots (nonzero only after a non-finite partial)
+  const bool flagged =
+      __builtin_amdgcn_readfirstlane(flg[kFlagBytes / sizeof(int)] | flg[kFlagSlot + kFlagBytes / sizeof(int)]) != 0;
   __builtin_amdgcn_sched_barrier(0);  // these first: the staging then waits for them alone
 
   // the read-modify-write role: chunks q = threadIdx.x + u * kExpandThreads,
@@ -805,15 +916,41 @@ __global__ __launch_bounds__(EW * 64) void fast_expand_kernel(FastArgs fa) {
   // the intermediate into LDS: one rounding to T per value; further tiles
   // (a workgroup whose columns straddle modules of different tiles) one
   // round trip each
-  stage_store(kt_lo, av2, bv2);
+  stage_store(kt_lo, av2, bv2, flagged);
   for (int kt = kt_lo + 1; kt <= kt_hi; ++kt) {
     stage_load(kt, av2, bv2);
-    stage_store(kt, av2, bv2);
+    stage_store(kt, av2, bv2, flagged);
   }
+  // whether any wave staged a non-finite value (one word per wave, no
+  // initialisation needed), read after the barrier
+  const uint64_t nf_ballot = __ballot(nonfinite);
+  if (lane == 0) s_nf[wave] = nf_ballot != 0;
   __syncthreads();
+  bool any_nonfinite = false;
+#pragma unroll
+  for (int w = 0; w < kExpandWaves; ++w) any_nonfinite |= s_nf[w] != 0;
   // the next call's shrink adds into the other slot (no expand workgroup
   // reads the parity, so the flip can go out at any time)
   if (ct == 0 && threadIdx.x == 0) *gptr<int*>(par_u) ^= 1;
+  if (any_nonfinite) {
+    // a NaN or an infinity in the staged intermediate: each output of the
+    // thread's chunks is its module's own dot product (module_dot), added to
+    // the output read again; the MFMA part is skipped.  The values of the
+    // main path are dead here, so this branch adds no registers to it.
+#pragma unroll
+    for (int u = 0; u < kChunks; ++u) {
+      const int q = threadIdx.x + u * kExpandThreads;
+      const int tk = q / kRowChunks;
+      const int a = cok[u] ? ids[tk] : -1;
+      if (a < 0 || a >= n_ad) continue;
+      float d[8];
+      module_dot<T>(em, &s_y[tk][0], c0 + (q % kRowChunks) * 8, a, d);
+      OT* const op = cptr[u];
+#pragma unroll 1
+      for (int e = 0; e < 8; ++e) op[e] = from_float<OT>(to_float<OT>(op[e]) + d[e]);
+    }
+    return;
+  }
 
   // the adapter of the lane's y row in each token tile (row tt*16 + lr: the
   // MFMA's A operand), and of its chunks' rows

@@ -249,3 +249,68 @@ def test_delta_workspace_state_across_calls(gpu_device):
         lora_delta_(x.to(gpu_device), mods, ids.to(gpu_device))
         torch.cuda.synchronize()
         _check_group(x, ids, host, mods)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T", [16, 80])  # the decode-size path, the general path
+def test_nonfinite_values_propagate_per_module(gpu_device, dtype, T):
+    """A NaN in x, infinities in A (both signs, in different k-slices) and,
+    in fp16, an intermediate that overflows when rounded: the outputs carry
+    NaN / +-inf exactly where the per-module F.linear(F.linear(x, A_m), B_m)
+    chain of multilora/linear.py:226-231 puts them (float64 oracle with IEEE
+    propagation), finite outputs stay within the bar, and the next call on
+    the workspace is bit-identical to one made before the non-finite call."""
+    gen = torch.Generator().manual_seed(900 + T)
+    n, fin = 2, 512
+    specs = [(64, 16), (32, 16), (48, 16)]  # three modules of one group (q/k/v-like)
+    ids = torch.tensor([(t % 3) - (1 if t % 7 == 6 else 0) for t in range(T)], dtype=torch.int32)
+    ids = torch.where(ids > 1, torch.zeros_like(ids), ids)  # adapters 0/1, some -1
+    ids[3], ids[5], ids[6] = 1, 1, 0
+    x = _rand((T, fin), 1.0, gen, dtype)
+    As = [_rand((n, r, fin), fin ** -0.5, gen, dtype) for _, r in specs]
+    Bs = [_rand((n, o, r), 0.05, gen, dtype) for o, r in specs]
+    x_nf, As_nf = x.clone(), [a.clone() for a in As]
+    x_nf[3, 10] = float("nan")                 # every intermediate of token 3
+    As_nf[0][1, 5, 7] = float("inf")           # module 0, adapter 1, rank 5
+    x_nf[5, 7] = 0.0                           # ... times 0: NaN for token 5
+    As_nf[2][0, 3, 20] = float("inf")          # module 2, adapter 0, rank 3: +inf and -inf
+    As_nf[2][0, 3, 300] = -float("inf")        # in different 256-element k-slices
+    x_nf[6, :] = 4.0                           # module 1, adapter 0, rank 0: 512 * 4 * 64 = 131072
+    As_nf[1][0, 0, :] = 64.0                   # (overflows when rounded to fp16, finite in bf16)
+    inter = "bf16" if dtype == torch.bfloat16 else "f16"
+
+    def run(xh, Ah):
+        outs = [torch.zeros((T, o), dtype=torch.float32, device=gpu_device) for o, _ in specs]
+        lora_delta_(xh.to(gpu_device), [(A.to(gpu_device), B.to(gpu_device), out, 2.0)
+                                        for A, B, out in zip(Ah, Bs, outs)], ids.to(gpu_device))
+        torch.cuda.synchronize()
+        return [o.cpu() for o in outs]
+
+    before = run(x, As)
+    got = run(x_nf, As_nf)
+    after = run(x, As)
+    for b, a in zip(before, after):
+        assert torch.equal(b, a), "a call after the non-finite one differs"
+    with np.errstate(invalid="ignore", over="ignore"):
+        for m, (A, B) in enumerate(zip(As_nf, Bs)):
+            want = ol.multi_adapter_delta(x_nf.float().numpy(), ids.tolist(), A.float().numpy(),
+                                          B.float().numpy(), 2.0, intermediate=inter)
+            g = got[m].numpy().astype(np.float64)
+            for kind, f in (("NaN", np.isnan), ("+inf", np.isposinf), ("-inf", np.isneginf)):
+                assert np.array_equal(f(g), f(want)), f"module {m}: {kind} positions differ"
+            # fp32 accumulation: 2e-3 plus 2^-16 of the terms' magnitude
+            # (token 6's module-1 terms reach ~2e4 in bf16)
+            mag = ol.multi_adapter_delta(np.abs(np.nan_to_num(x_nf.float().numpy())), ids.tolist(),
+                                         np.abs(np.nan_to_num(A.float().numpy(), posinf=0, neginf=0)),
+                                         np.abs(B.float().numpy()), 2.0)
+            fin_mask = np.isfinite(want)
+            err = np.abs(g[fin_mask] - want[fin_mask])
+            assert (err <= 2e-3 + 2.0**-16 * mag[fin_mask]).all(), f"module {m}: max err {err.max():.3e}"
+    # the planted values reach the outputs they should
+    assert np.isnan(got[0][3]).all() and np.isnan(got[1][3]).all() and np.isnan(got[2][3]).all()
+    assert not np.isfinite(got[0][5]).all() and np.isfinite(got[1][5]).all()
+    assert (~np.isfinite(got[2][ids.numpy() == 0])).any()
+    if dtype == torch.float16:
+        assert not np.isfinite(got[1][6]).all()
+    else:
+        assert np.isfinite(got[1][6]).all()
