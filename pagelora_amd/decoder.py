@@ -9,17 +9,21 @@ modules (packed_ops.py:105-265, multilora/linear.py:200-231):
     -> GEMM on [W_qkv; A_q; A_k; A_v]
     -> q/k/v LoRA up-projection + per-head q/k RMSNorm (projection.py:248-260)
        + RoPE (projection.py:155-190) + KV append (layer_runner.py:399-412)
-    -> paged decode attention (attention_backend.py:120-131)
+       + paged decode attention (attention_backend.py:120-131), one kernel,
+       then the split-KV merge
     -> GEMM on [W_o; A_o] -> o LoRA up-projection + residual add + RMSNorm
     -> GEMM on [W_gate_up; A_gate; A_up] -> LoRA up-projections + SiLU*up
     -> GEMM on [W_down; A_down] (its delta lands in the next layer's norm)
 
-Ten kernels per layer: the LoRA shrink rides in the base GEMM (the adapters'
-A rows stacked under W) and the expand in the kernel that consumes the
-module output, so no separate LoRA launches remain.  GEMMs are the
-decode-sized linear kernel (q/k/v, o at decode batch sizes) or the library
-GEMM (torch -> hipBLASLt); everything else runs on the library's HIP
-kernels.  Weights are random (no checkpoints are available); shapes follow
+Nine kernels per decode layer at decode batch sizes: two add+RMSNorm, four
+GEMMs on the shuffled weights (the narrow o/down ones with their LoRA A rows
+on side planes), the attention kernel with the q/k/v epilogue folded in, the
+merge and SiLU*up.  The LoRA shrink rides in the base GEMM (the adapters' A
+rows stacked under W) and the expand in the kernel that consumes the module
+output, so no separate LoRA launches remain.  Prefill, and batches beyond
+the decode GEMM's 64 rows, use the library GEMM (torch -> hipBLASLt);
+prefill forms q and appends k/v in the separate q/k norm + RoPE + append
+kernel.  Weights are random (no checkpoints are available); shapes follow
 Qwen3-8B.
 
 ``prefill`` runs the same layer over a prompt segment with the paged
@@ -459,8 +463,12 @@ FOLD_QKV_INTO_DECODE = True
 # value)`` with each stage's stored output (tensors, split planes) in
 # dataflow order: "hidden_in" (the residual stream on entry), "hidden" (after
 # the input add of the previous layer's down_proj output), "x", "qkv",
-# "attn", "o", "hidden_mid", "x2", "gate_up", "act", "down".  For checking a
-# decode step stage by stage; it must stay None while a graph is captured.
+# "attn", "o", "hidden_mid", "x2", "gate_up", "act", "down" per layer; after
+# the last layer (decode steps) "final_hidden_in" (the residual stream before
+# the final add), "final_down" (the last layer's down_proj output),
+# "final_hidden", "final_x" (after the final add + RMSNorm), "logits" and
+# "next_tokens".  For checking a decode step stage by stage; it must stay
+# None while a graph is captured.
 STAGE_TRACE = None
 
 
@@ -654,6 +662,10 @@ def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: Page
     for li, lw in enumerate(weights.layers):
         pending = decode_layer_static(cfg, lw, weights.lora_scale, hidden, pending, pool.layer_cache(li),
                                       backend, ctx)
+    trace = STAGE_TRACE
+    if trace is not None:
+        trace("final_hidden_in", hidden)
+        trace("final_down", pending[0])
     x = _final_norm(weights, hidden, pending, ctx.adapter_ids)
     logits = weights.logits(x)
     # greedy (sampling.py:8-15); the pick also becomes the next step's input token
@@ -661,6 +673,10 @@ def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: Page
         ctx.argmax_ws = fused_ops.greedy_argmax_workspace(logits.shape[0], logits.shape[1], logits.dtype,
                                                           logits.device)
     fused_ops.greedy_argmax(logits, out=ctx.next_tokens, tokens_out=ctx.tokens, workspace=ctx.argmax_ws)
+    if trace is not None:
+        for name, value in (("final_hidden", hidden), ("final_x", x), ("logits", logits),
+                            ("next_tokens", ctx.next_tokens)):
+            trace(name, value)
     return logits
 
 

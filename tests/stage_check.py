@@ -4,7 +4,10 @@ Runs one eager step of the decoder with ``decoder.STAGE_TRACE`` recording
 each stage's stored output, then applies the oracle (oracle.fused,
 oracle.lora, oracle.paged_decode) to the kernels' own stored inputs of each
 stage of layer 0 (and layer 1's input add): the stages of the reference's
-static decode layer (layer_runner.py:340-412).
+static decode layer (layer_runner.py:340-412); then the step's end: the
+final add of the last layer's down_proj output (with its LoRA
+up-projection) + RMSNorm, the lm_head logits over the vocabulary, and the
+greedy token.
 
 Bar: 2e-3 + one bf16 rounding of the output (2^-8 relative); where a stage
 rounds an intermediate before its output (the module output + LoRA delta
@@ -50,15 +53,18 @@ def check(name, got, want, carried=0.0, atol=2e-3):
 
 
 class Recorder:
-    """STAGE_TRACE target: copies of the first two layers' stage outputs."""
+    """STAGE_TRACE target: copies of the first two layers' stage outputs and
+    of the step's final stages (final add + RMSNorm, logits, greedy token)."""
 
     def __init__(self):
         self.layers = []
+        self.final = {}
 
     def __call__(self, name, value):
         if name == "hidden_in":
             self.layers.append({})
-        if len(self.layers) > 2:
+        final = name.startswith("final_") or name in ("logits", "next_tokens")
+        if len(self.layers) > 2 and not final:
             return
         if isinstance(value, SideOutput):
             value = (value.main.clone(), value.side.sum())  # planes summed in order and rounded, as consumed
@@ -66,7 +72,7 @@ class Recorder:
             value = value.sum()
         else:
             value = value.clone()
-        self.layers[-1][name] = value
+        (self.final if final else self.layers[-1])[name] = value
 
 
 def stage_check(w, pool, reqs, first, dev, slot=0, adapter=None):
@@ -94,13 +100,14 @@ def stage_check(w, pool, reqs, first, dev, slot=0, adapter=None):
     qd, kd = hq * d, hkv * d
     worst = {}
 
-    def AB(name):
+    def AB(name, layer=0):
+        lwl = w.layers[layer]
         if adapter is not None:
-            A, Bm = adapter.get((0, name), (None, None))
+            A, Bm = adapter.get((layer, name), (None, None))
             if A is None:  # a module the adapter leaves out: zero delta
-                return np.zeros((r, lw.lora[name][0].shape[-1])), np.zeros((lw.lora[name][1].shape[1], r))
+                return np.zeros((r, lwl.lora[name][0].shape[-1])), np.zeros((lwl.lora[name][1].shape[1], r))
             return _f(torch.as_tensor(A)), _f(torch.as_tensor(Bm))
-        return _f(lw.lora[name][0][slot]), _f(lw.lora[name][1][slot])
+        return _f(lwl.lora[name][0][slot]), _f(lwl.lora[name][1][slot])
 
     def ycols(name):
         c = lw.y_offset[name] + slot * r
@@ -192,5 +199,51 @@ def stage_check(w, pool, reqs, first, dev, slot=0, adapter=None):
     worst["down_residual"] = check("down_residual", _f(L1["hidden"]), _f(L1["hidden_in"]) + d_mod, np.abs(d_mod))
     worst["next_input_norm"] = check("next_input_norm", _f(L1["x"]),
                                      of.rmsnorm(_f(L1["hidden"]), _f(w.layers[1].input_norm), eps))
+    worst.update(final_stages(w, rec.final, AB, slot))
     print("[stage check] err/bound: " + ", ".join(f"{k} {v:.2f}" for k, v in worst.items()), flush=True)
+    return worst
+
+
+def final_stages(w, F, AB, slot):
+    """The step's end against the oracle, on the kernels' stored inputs: the
+    final add of the last layer's down_proj output with its LoRA
+    up-projection + RMSNorm (norm.py:27-57), the lm_head logits
+    (cuda_graph.py:245-263, generation.py:544-561) and the greedy token
+    (sampling.py:8-15: torch.argmax, first index among ties)."""
+    cfg, s, eps, r = w.cfg, w.lora_scale, w.cfg.rms_eps, w.cfg.lora_rank
+    last = cfg.num_layers - 1
+    worst = {}
+    d_out = F["final_down"]
+    if isinstance(d_out, tuple):
+        d_main, d_y = _f(d_out[0]), _f(d_out[1])[:, slot * r: (slot + 1) * r]
+    else:
+        lw = w.layers[last]
+        c = lw.y_offset["down"] + slot * r
+        d_main, d_y = _f(d_out)[:, : cfg.hidden], _f(d_out)[:, c: c + r]
+    d_mod = ol.round_bf16(d_main + ol.up_projection(d_y, AB("down", last)[1], s))
+    worst["final_residual"] = check("final_residual", _f(F["final_hidden"]), _f(F["final_hidden_in"]) + d_mod,
+                                    np.abs(d_mod))
+    worst["final_norm"] = check("final_norm", _f(F["final_x"]),
+                                of.rmsnorm(_f(F["final_hidden"]), _f(w.final_norm), eps))
+    # lm_head over the whole vocabulary in float64, 16384 rows at a time
+    # (the weight unshuffled from the decode GEMM's copy, a bit-exact
+    # inverse checked on its own)
+    x = _f(F["final_x"])
+    head = w.lm_head
+    want = np.empty((x.shape[0], head.shape[0]))
+    for lo in range(0, head.shape[0], 16384):
+        want[:, lo: lo + 16384] = ol.linear(x, _f(head[lo: lo + 16384]))
+    del head
+    logits = _f(F["logits"])
+    worst["logits"] = check("logits", logits, want)
+    # the greedy pick is the first maximum of the kernel's own logits
+    picked = F["next_tokens"].cpu().numpy().reshape(-1)
+    assert np.array_equal(picked, np.argmax(logits, axis=1)), f"greedy tokens {picked} != argmax of the logits"
+    # and the oracle's pick wherever its top-2 margin exceeds twice the bar
+    top2 = np.sort(want, axis=1)[:, -2:]
+    bar = 2e-3 + ULP * np.abs(top2[:, 1])
+    clear = top2[:, 1] - top2[:, 0] > 2 * bar
+    assert np.array_equal(picked[clear], np.argmax(want, axis=1)[clear]), "greedy tokens differ from the oracle's"
+    print(f"[stage check] greedy tokens {picked.tolist()}: the logits' first maximum; the oracle's pick on "
+          f"{int(clear.sum())} of {len(picked)} rows (the others' top-2 margin is within twice the bar)", flush=True)
     return worst

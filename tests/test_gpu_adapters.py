@@ -29,14 +29,21 @@ CFG = DecoderConfig(num_layers=2, hidden=512, num_qo_heads=4, num_kv_heads=1, he
                     vocab=1000, lora_rank=16, lora_alpha=32.0)
 
 
-def _adapter(seed, dev, modules=MODULES, scale=1.0):
+# rank 8: an adapter slot's A rows start inside a 16-row block of the
+# shuffled weight (slot 1 of a module at rows base + 8 .. + 16), so a slot
+# write patches part of a block
+CFG_R8 = DecoderConfig(num_layers=2, hidden=512, num_qo_heads=4, num_kv_heads=1, head_dim=128, intermediate=512,
+                       vocab=1000, lora_rank=8, lora_alpha=16.0)
+
+
+def _adapter(seed, dev, modules=MODULES, scale=1.0, cfg=CFG):
     g = torch.Generator().manual_seed(seed)
-    outs = {m: o for _, _, mods in projections(CFG) for m, o in mods}
-    ins = {m: fin for _, fin, mods in projections(CFG) for m, _ in mods}
-    r = CFG.lora_rank
+    outs = {m: o for _, _, mods in projections(cfg) for m, o in mods}
+    ins = {m: fin for _, fin, mods in projections(cfg) for m, _ in mods}
+    r = cfg.lora_rank
     return {(l, m): ((torch.randn((r, ins[m]), generator=g) * ins[m] ** -0.5).to(torch.bfloat16).to(dev),
                      (torch.randn((outs[m], r), generator=g) * 0.02 * scale).to(torch.bfloat16).to(dev))
-            for l in range(CFG.num_layers) for m in modules}
+            for l in range(cfg.num_layers) for m in modules}
 
 
 def _scenario(dev, use_graph):
@@ -76,22 +83,24 @@ def test_bound_adapters_graph_equals_eager(gpu_device):
     stage_check(w, pool, reqs, last, gpu_device, slot=1, adapter=tuned)
 
 
-def test_in_place_update_matches_a_fresh_shuffle(gpu_device):
-    w = DecoderWeights(CFG, n_adapters=2, device=gpu_device, seed=4)
-    new = _adapter(30, gpu_device)
+@pytest.mark.parametrize("cfg,slots", [(CFG, 2), (CFG_R8, 3)], ids=["rank16", "rank8"])
+def test_in_place_update_matches_a_fresh_shuffle(gpu_device, cfg, slots):
+    w = DecoderWeights(cfg, n_adapters=slots, device=gpu_device, seed=4)
+    new = _adapter(30, gpu_device, cfg=cfg)
     w.set_adapter(1, new)
-    adapters = [{(l, m): (lw.lora[m][0][0], lw.lora[m][1][0]) for l, lw in enumerate(w.layers) for m in MODULES},
-                new]
+    adapters = [{(l, m): (lw.lora[m][0][a], lw.lora[m][1][a]) for l, lw in enumerate(w.layers) for m in MODULES}
+                for a in range(slots)]
+    adapters[1] = new
     layers = []
     for lw in w.layers:
         d = {"input_norm": lw.input_norm, "post_norm": lw.post_norm, "q_norm": lw.q_norm, "k_norm": lw.k_norm}
-        for proj, _, mods in projections(CFG):
+        for proj, _, mods in projections(cfg):
             W, row = getattr(lw, f"w_{proj}"), 0
             for m, o in mods:
                 d[m] = W[row:row + o]
                 row += o
         layers.append(d)
-    fresh = DecoderWeights.from_tensors(CFG, embed=w.embed, final_norm=w.final_norm, lm_head=w.lm_head,
+    fresh = DecoderWeights.from_tensors(cfg, embed=w.embed, final_norm=w.final_norm, lm_head=w.lm_head,
                                         layers=layers, adapters=adapters, device=gpu_device)
     torch.cuda.synchronize()
     for a, b in zip(w.layers, fresh.layers):

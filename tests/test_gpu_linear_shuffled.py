@@ -160,3 +160,58 @@ def test_side_bad_inputs_raise(gpu_device):
             linear_shuffled_side(x, sw, main, 1)
     with pytest.raises(ValueError, match="side_splits"):
         linear_shuffled_side(x, sw, 32, 3)  # 2 k-steps
+
+
+def _oracle_chunked(x, w_dev, rows=16384):
+    """x . W^T in float64 with W copied to the host 16384 rows at a time."""
+    want = np.empty((x.shape[0], w_dev.shape[0]))
+    for lo in range(0, w_dev.shape[0], rows):
+        want[:, lo: lo + rows] = x @ w_dev[lo: lo + rows].double().cpu().numpy().T
+    return want
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 64])
+@pytest.mark.parametrize("shape", [(151936, 4096), (24608, 4096)])
+def test_linear_shuffled_decoder_shapes(gpu_device, shape, tokens):
+    """The Qwen3-8B lm_head (vocabulary 151,936: 9,496 row blocks, the
+    largest grid of the decode step) and gate_up with its two adapters' A
+    rows (24,576 + 32 rows) against the oracle's linear term, same bar."""
+    n, k = shape
+    print(f"[shuffled gemm] {n} x {k}, {tokens} tokens", flush=True)
+    g = torch.Generator(device=gpu_device).manual_seed(n + tokens)
+    w = (torch.randn((n, k), generator=g, device=gpu_device) * k ** -0.5).to(torch.bfloat16)
+    x = torch.randn((tokens, k), generator=g, device=gpu_device).to(torch.bfloat16)
+    sw = ShuffledWeight(w)
+    out = linear_shuffled(x, sw)
+    torch.cuda.synchronize()
+    want = _oracle_chunked(x.double().cpu().numpy(), w)
+    err = np.abs(out.float().cpu().numpy() - want)
+    assert (err <= 2e-3 + REL[torch.bfloat16] * np.abs(want)).all(), f"max err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(6144 + 48, 4096), (24576 + 32, 4096), (4096 + 16, 12288), (151936, 4096),
+                                   (37, 96)])
+def test_unshuffle_inverts_the_shuffle(gpu_device, shape, dtype):
+    """pl_weight_unshuffle(pl_weight_shuffle(W)) == W bit for bit at the
+    decoder's shapes (qkv, gate_up and down with their A rows, the lm_head)
+    and a ragged one, into a fresh tensor and into the decoder's shared
+    row-major scratch buffer (which the stage check's oracle weights and
+    prefill's library GEMMs read)."""
+    from pagelora_amd.decoder import unshuffled_scratch
+
+    n, k = shape
+    print(f"[unshuffle] {n} x {k} {dtype}", flush=True)
+    g = torch.Generator(device=gpu_device).manual_seed(n * 3 + k)
+    w = torch.randn((n, k), generator=g, device=gpu_device).to(dtype)
+    sw = ShuffledWeight(w)
+    fresh = sw.unshuffle()
+    assert torch.equal(fresh.view(torch.int16), w.view(torch.int16))
+    del fresh
+    scratch = unshuffled_scratch(sw)
+    assert torch.equal(scratch.view(torch.int16), w.view(torch.int16))
+    # a row-strided target (the unshuffle writes only the [n, k] view)
+    wide = torch.full((n, k + 64), 3.0, dtype=dtype, device=gpu_device)
+    sw.unshuffle(wide[:, :k])
+    assert torch.equal(wide[:, :k].view(torch.int16), w.view(torch.int16))
+    assert (wide[:, k:] == 3.0).all()
