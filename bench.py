@@ -63,6 +63,8 @@ def parse_args():
                    help="run only this end-to-end decode leg and print its result (for profiling)")
     p.add_argument("--lora-only", action="store_true",
                    help="run only the per-layer LoRA delta timing and print its result (for profiling)")
+    p.add_argument("--e2e-steps", type=int, default=None,
+                   help="decode steps of each timed end-to-end call (default 128; fewer for counter runs)")
     return p.parse_args()
 
 
@@ -321,6 +323,7 @@ def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_step
 
     cfg = QWEN3_8B
     w = DecoderWeights(cfg, n_adapters=1, device=device, seed=0)
+    print(f"[bench] e2e {rows} x ({prefix_len} shared + {suffix_len}): weights ready", file=sys.stderr, flush=True)
     ps = 16
     pages = (prefix_len + rows * (suffix_len + 2 * (steps + warm_steps) + 16)) // ps + 8 * rows + 8
     pool = PagedKVPool(num_layers=cfg.num_layers, capacity_pages=pages, page_size=ps, num_kv_heads=cfg.num_kv_heads,
@@ -332,6 +335,7 @@ def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_step
     reqs, first, _ = prefill_requests(w, pool, prompts, shared_prefix=prefix)
     torch.cuda.synchronize(device)
     prefill_s = time.perf_counter() - t
+    print(f"[bench] e2e: prefill {prefill_s:.2f} s", file=sys.stderr, flush=True)
     gen = BatchGenerator(w, pool, use_graph=True)
 
     def rewind(n):
@@ -343,6 +347,7 @@ def e2e_decode(device, *, prefix_len, suffix_len, rows, steps, seed=5, warm_step
     rewind(warm_steps)
     res = gen.generate(reqs, first, steps=steps, device_tables=True)
     rewind(steps)
+    print(f"[bench] e2e: {res.decode_tokens_per_s:.1f} tok/s with device tables", file=sys.stderr, flush=True)
     gen.generate(reqs, first, steps=warm_steps)
     rewind(warm_steps)
     host = gen.generate(reqs, first, steps=steps)
@@ -493,8 +498,11 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
+    legs = {k: (name, dict(kw, steps=args.e2e_steps or kw["steps"])) for k, (name, kw) in E2E_LEGS.items()}
+    if args.copy_calibration and (args.e2e_only or args.lora_only):
+        copy_calibration(dev)
     if args.e2e_only:
-        name, kw = E2E_LEGS[args.e2e_only]
+        name, kw = legs[args.e2e_only]
         print(json.dumps({"leg": name, **e2e_decode(dev, **kw)}), flush=True)
         return
     if args.lora_only:
@@ -560,7 +568,7 @@ def main():
             "us_per_layer_one_call_per_group": round(lora_each_ms * 1e3, 2),
         }
     if not args.no_extra and not args.no_e2e:
-        for name, kw in E2E_LEGS.values():
+        for name, kw in legs.values():
             extra[name] = e2e_decode(dev, **kw)
     line = {
         "metric": METRIC,
