@@ -31,6 +31,13 @@ import torch
 
 from .decoder import MODULES, DecoderWeights, module_key
 
+# Module paths inside a decoder layer, as the reference's wrapped modules are
+# named (layer.named_modules() of an HF Qwen3/Llama layer, runtime.py:100-115)
+# in its serve-state keys "layers.{i}.{path}.lora_serve_a|b".
+SERVE_STATE_MODULES = {"q": "self_attn.q_proj", "k": "self_attn.k_proj", "v": "self_attn.v_proj",
+                       "o": "self_attn.o_proj", "gate": "mlp.gate_proj", "up": "mlp.up_proj",
+                       "down": "mlp.down_proj"}
+
 
 class AdapterRegistry:
     """Named adapters in the slots of one :class:`DecoderWeights`.
@@ -49,6 +56,7 @@ class AdapterRegistry:
         self.adapter_versions: dict[str, int] = {name: 0 for name in logical_adapters}
         if default_logical_adapter not in self._slots:
             raise KeyError(f"Unknown logical adapter: {default_logical_adapter}")
+        self.default_logical_adapter = default_logical_adapter
         self.active_logical_adapter_name = default_logical_adapter
 
     # ------------------------------------------------------------ registry
@@ -89,6 +97,51 @@ class AdapterRegistry:
         """Write new values for a registered adapter into its slot, in place
         (captured graphs stay valid; steps enqueued afterwards use them)."""
         self.weights.set_adapter(self.slot(adapter_name), self._normalized(adapter))
+        self.adapter_versions[adapter_name] += 1
+
+    # --------------------------------------------------------- serve state
+    def export_serve_state(self, adapter_name: str) -> dict[str, torch.Tensor]:
+        """One adapter's A/B as host tensors under the reference's keys
+        "layers.{i}.{module path}.lora_serve_a" / "...lora_serve_b"
+        (runtime.py:570-579): A [r, in], B [out, r] of every layer and module."""
+        slot = self.slot(adapter_name)
+        state: dict[str, torch.Tensor] = {}
+        for li, lw in enumerate(self.weights.layers):
+            for m in MODULES:
+                prefix = f"layers.{li}.{SERVE_STATE_MODULES[m]}"
+                state[f"{prefix}.lora_serve_a"] = lw.lora[m][0][slot].detach().cpu().clone()
+                state[f"{prefix}.lora_serve_b"] = lw.lora[m][1][slot].detach().cpu().clone()
+        return state
+
+    def load_serve_state(self, adapter_name: str, state: Mapping[str, torch.Tensor]) -> None:
+        """Load an adapter from such a state dict (runtime.py:581-607): an
+        unknown name is registered first as a copy of the default adapter;
+        keys that name a known layer and module replace that A or B, every
+        other key is ignored (as the reference skips them); the values go
+        into the adapter's slot in place and its version moves on."""
+        if adapter_name not in self._slots:
+            self.register_logical_adapter(adapter_name, init_from=self.default_logical_adapter)
+        slot = self.slot(adapter_name)
+        values = {key: list(ab) for key, ab in self._values_of(slot).items()}
+        for key, tensor in state.items():
+            parts = key.split(".")
+            if len(parts) < 4 or parts[0] != "layers" or not parts[1].isdigit():
+                continue
+            leaf = parts[-1]
+            try:
+                module = module_key(".".join(parts[2:-1]))
+            except KeyError:
+                continue
+            pair = values.get((int(parts[1]), module))
+            if pair is None:
+                continue
+            if leaf == "lora_serve_a":
+                pair[0] = torch.as_tensor(tensor)
+            elif leaf == "lora_serve_b":
+                pair[1] = torch.as_tensor(tensor)
+        # set_adapter copies into the slot; the unchanged entries are views of
+        # it, so cloned first
+        self.weights.set_adapter(slot, {k: (A.clone(), B.clone()) for k, (A, B) in values.items()})
         self.adapter_versions[adapter_name] += 1
 
     @staticmethod

@@ -118,3 +118,69 @@ def test_registry_mirrors_the_runtime_api():
         reg.set_active("missing")
     with pytest.raises(ValueError):
         w.set_adapter(0, {(0, "q"): (torch.zeros(3, 64), torch.zeros(64, 3))})  # wrong rank
+
+
+def test_serve_state_export_and_load_round_trip():
+    """export_serve_state / load_serve_state (multilora/runtime.py:570-607):
+    the reference's keys, values of the adapter's slot, and a load into a new
+    name registers it and reproduces the exported state exactly."""
+    w = _weights(n=1)
+    reg = AdapterRegistry(w)
+    reg.update_adapter("general", _adapter(3))
+    state = reg.export_serve_state("general")
+    assert len(state) == CFG.num_layers * len(MODULES) * 2
+    assert "layers.0.self_attn.q_proj.lora_serve_a" in state and "layers.1.mlp.down_proj.lora_serve_b" in state
+    assert torch.equal(state["layers.1.mlp.gate_proj.lora_serve_a"], w.layers[1].lora["gate"][0][0])
+    assert torch.equal(state["layers.0.self_attn.o_proj.lora_serve_b"], w.layers[0].lora["o"][1][0])
+    v0 = w.adapter_version
+    reg.load_serve_state("tuned", state)
+    # registered from the default adapter (its version), then bumped by the load
+    assert reg.list_logical_adapters() == ["general", "tuned"]
+    assert reg.adapter_versions["tuned"] == reg.adapter_versions["general"] + 1
+    assert w.adapter_version == v0 + 1  # the stacks grew to a second slot
+    again = reg.export_serve_state("tuned")
+    assert again.keys() == state.keys()
+    for k in state:
+        assert torch.equal(again[k], state[k]), k
+
+
+def test_serve_state_load_partial_and_foreign_keys():
+    """Keys of a known layer and module replace that A or B in place; the
+    rest keep their values (a new name starts as a copy of the default
+    adapter); keys the reference would skip are skipped."""
+    w = _weights(n=2)
+    reg = AdapterRegistry(w, logical_adapters=("general", "tuned"))
+    reg.update_adapter("general", _adapter(4))
+    reg.update_adapter("tuned", _adapter(5))
+    before = reg.export_serve_state("tuned")
+    g = torch.Generator().manual_seed(6)
+    new_a = torch.randn(w.layers[1].lora["k"][0][1].shape, generator=g)
+    new_b = torch.randn(w.layers[0].lora["up"][1][1].shape, generator=g)
+    ptr = w.layers[1].lora["k"][0].data_ptr()
+    reg.load_serve_state("tuned", {
+        "layers.1.self_attn.k_proj.lora_serve_a": new_a,
+        "layers.0.mlp.up_proj.lora_serve_b": new_b,
+        "layers.0.mlp.up_proj.lora_serve_c": torch.zeros(1),   # unknown leaf
+        "layers.7.self_attn.q_proj.lora_serve_a": torch.zeros(1),  # no such layer
+        "layers.0.self_attn.rotary.lora_serve_a": torch.zeros(1),  # not a LoRA module
+        "model.embed_tokens.weight": torch.zeros(1),
+        "layers.x.mlp.up_proj.lora_serve_a": torch.zeros(1),
+    })
+    assert w.layers[1].lora["k"][0].data_ptr() == ptr  # written in place
+    after = reg.export_serve_state("tuned")
+    for k in before:
+        if k == "layers.1.self_attn.k_proj.lora_serve_a":
+            assert torch.equal(after[k], new_a)
+        elif k == "layers.0.mlp.up_proj.lora_serve_b":
+            assert torch.equal(after[k], new_b)
+        else:
+            assert torch.equal(after[k], before[k]), k
+    # "general" is untouched; a new name starts from the default adapter
+    reg.load_serve_state("third", {"layers.0.self_attn.v_proj.lora_serve_b": new_b[:, :0].new_zeros(
+        w.layers[0].lora["v"][1][0].shape)})
+    third, general = reg.export_serve_state("third"), reg.export_serve_state("general")
+    for k in general:
+        if k == "layers.0.self_attn.v_proj.lora_serve_b":
+            assert not third[k].any()
+        else:
+            assert torch.equal(third[k], general[k]), k
