@@ -42,10 +42,12 @@ class GenerateResult:
     graph_replays: int = 0
     first_logits: torch.Tensor | None = None
     extra: dict = field(default_factory=dict)
+    generated_tokens: int | None = None  # when rows retire early (EOS): the tokens actually decoded
 
     @property
     def decode_tokens_per_s(self) -> float:
-        return self.batch * self.steps / self.decode_seconds if self.decode_seconds > 0 else 0.0
+        n = self.batch * self.steps if self.generated_tokens is None else self.generated_tokens
+        return n / self.decode_seconds if self.decode_seconds > 0 else 0.0
 
 
 class _PinnedRing:
@@ -174,7 +176,7 @@ class BatchGenerator:
     @torch.no_grad()
     def generate(self, requests: list[Request], first_tokens: torch.Tensor, steps: int,
                  adapters: list[int] | None = None, device_tables: bool = False,
-                 keep_logits: bool = False) -> GenerateResult:
+                 keep_logits: bool = False, eos_token_id: int | None = None) -> GenerateResult:
         """Decode ``steps`` greedy tokens for rows whose prompts are prefilled.
 
         first_tokens: [B] int64 on the device, the token each row decodes
@@ -183,8 +185,15 @@ class BatchGenerator:
         the device inside the step (pl_page_table_advance); the host only
         refills the page reserve about once per page of steps.
         ``keep_logits`` keeps every step's logits ([steps, B, vocab] on the
-        device, in ``extra["logits"]``).
+        device, in ``extra["logits"]``).  With ``eos_token_id`` a row stops
+        at its first pick of that token (see :meth:`_generate_until_eos`).
         """
+        if eos_token_id is not None:
+            if device_tables:
+                raise ValueError("rows retiring at EOS re-plan the batch on the host every step; "
+                                 "use device_tables=False")
+            return self._generate_until_eos(requests, first_tokens, steps, adapters, int(eos_token_id),
+                                            keep_logits)
         if device_tables:
             return self._generate_device_tables(requests, first_tokens, steps, adapters, keep_logits)
         B = len(requests)
@@ -254,6 +263,87 @@ class BatchGenerator:
                               batch=B, used_graph=entry is not None, graph_captures=self.graphs.capture_count,
                               graph_replays=self.graphs.replay_count, extra=extra)
 
+
+    def _generate_until_eos(self, requests, first_tokens, steps, adapters, eos, keep_logits=False) -> GenerateResult:
+        """The reference's batched loop with rows retiring at EOS
+        (generation.py:967-1086): a row whose pick is ``eos`` keeps that token
+        as its last and is not decoded again; the others go on as a smaller
+        batch, whose graph is captured once for that batch size (the batch
+        is part of the graph key, cuda_graph.py:525-526).  A row whose first
+        token is ``eos`` is not decoded at all.  The picks come back to the
+        host every step, as the reference's sampler does.
+
+        ``tokens`` is [B, steps] with -1 after a row's last token;
+        ``extra["lengths"]`` the tokens each row decoded, ``extra["batch"]``
+        the batch size of each step, ``generated_tokens`` their sum (tok/s
+        counts those).
+        """
+        B = len(requests)
+        dev = self.pool.cache.device
+        adapters = list(adapters or [0] * B)
+        out = torch.full((B, steps), -1, dtype=torch.int64)
+        first = first_tokens.reshape(-1).cpu().tolist()
+        active = [b for b in range(B) if first[b] != eos]
+        cur = torch.tensor([first[b] for b in active], dtype=torch.int64)
+        kept = None
+        eager: dict[int, DecodeContext] = {}
+        batches: list[int] = []
+        used_graph = False
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        capture_s = 0.0
+        for step in range(steps):
+            if not active:
+                break
+            reqs = [requests[b] for b in active]
+            ads = [adapters[b] for b in active]
+            Ba, uniform = len(reqs), self._uniform_adapter(ads)
+            staging = eager.get(Ba)
+            if staging is None:
+                staging = eager[Ba] = DecodeContext(Ba, dev)
+            staging.uniform_adapter = uniform
+            self._stage_inputs(staging, reqs, ads)
+            self._plan(reqs)
+            entry = None
+            if self.use_graph:
+                tc = time.perf_counter()
+                n_before = self.graphs.capture_count
+                entry = self.graphs.entry(Ba, uniform_adapter=uniform)
+                if self.graphs.capture_count != n_before:
+                    torch.cuda.synchronize(dev)
+                    capture_s += time.perf_counter() - tc
+            if entry is not None:
+                ctx = entry.ctx
+                for name in ("positions", "page_id", "page_offset", "adapter_ids"):
+                    getattr(ctx, name).copy_(getattr(staging, name))
+            else:
+                ctx = staging
+            ctx.tokens.copy_(cur)
+            if entry is not None:
+                logits = self.graphs.replay(entry)
+                used_graph = True
+            else:
+                logits = decode_step_static(self.weights, self.pool, self.backend, ctx)
+            picks = ctx.next_tokens.cpu()
+            if keep_logits:
+                if kept is None:
+                    kept = torch.full((steps, B, logits.shape[1]), float("nan"), dtype=logits.dtype, device=dev)
+                kept[step, torch.tensor(active, device=dev)] = logits
+            out[active, step] = picks
+            batches.append(Ba)
+            go_on = picks != eos
+            active = [b for b, g in zip(active, go_on.tolist()) if g]
+            cur = picks[go_on]
+        torch.cuda.synchronize(dev)
+        dt = time.perf_counter() - t0 - capture_s
+        lengths = (out >= 0).sum(dim=1).tolist()
+        extra = {"capture_seconds": capture_s, "lengths": lengths, "batch": batches}
+        if keep_logits:
+            extra["logits"] = kept
+        return GenerateResult(tokens=out, decode_seconds=dt, prefill_seconds=0.0, steps=steps, batch=B,
+                              used_graph=used_graph, graph_captures=self.graphs.capture_count,
+                              graph_replays=self.graphs.replay_count, extra=extra,
+                              generated_tokens=int(sum(batches)))
 
     def _uniform_adapter(self, adapters) -> int:
         """The one adapter every row uses, else -1 (per-row ids)."""
