@@ -828,9 +828,9 @@ __global__ __launch_bounds__(EW * 64) void fast_expand_kernel(FastArgs fa) {
   const int id_raw = ids[lane < T_ ? lane : 0];
   longlong2 av2[kStagePairs], bv2[kStagePairs];
   stage_load(kt_lo, av2, bv2);
-  // the any-flag words of both slots (nonzero only after a non-finite partial)
-  const bool flagged =
-      __builtin_amdgcn_readfirstlane(flg[kFlagBytes / sizeof(int)] | flg[kFlagSlot + kFlagBytes / sizeof(int)]) != 0;
+  // the any-flag words of both slots (nonzero only after a non-finite
+  // partial), loaded with the accumulator and read once every load is out
+  const int any0 = flg[kFlagBytes / sizeof(int)], any1 = flg[kFlagSlot + kFlagBytes / sizeof(int)];
   __builtin_amdgcn_sched_barrier(0);  // these first: the staging then waits for them alone
 
   // the read-modify-write role: chunks q = threadIdx.x + u * kExpandThreads,
@@ -912,6 +912,7 @@ __global__ __launch_bounds__(EW * 64) void fast_expand_kernel(FastArgs fa) {
 #pragma unroll
   for (int u = 0; u < kFastAChunk; ++u) load_b(u, bop[u]);
   __builtin_amdgcn_sched_barrier(0);  // every load of the workgroup in flight
+  const bool flagged = __builtin_amdgcn_readfirstlane(any0 | any1) != 0;
 
   // the intermediate into LDS: one rounding to T per value; further tiles
   // (a workgroup whose columns straddle modules of different tiles) one
