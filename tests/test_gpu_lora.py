@@ -73,6 +73,42 @@ def test_accumulates_into_base_and_matches_merged_weights(gpu_device):
     assert np.abs(base.cpu().numpy() - want).max() <= 2e-3
 
 
+def test_qwen3_modules_match_merged_weights(gpu_device):
+    """base + B(Ax) on the seven Qwen3-8B modules (64 tokens over 4 adapters,
+    r=16, s=2) vs the merged comparator x (W + s B_a A_a)^T of each token's
+    adapter (effective_weights.py:53-129), from the same bf16 inputs.  The
+    merged form has no intermediate rounding: the difference is the bf16
+    rounding of x.A^T times |B| s, inside the 2e-3 bar."""
+    gen = torch.Generator().manual_seed(1238)
+    T, H, I, r, n = 64, 4096, 12288, 16, 4
+    ids = torch.randint(0, n, (T,), generator=gen, dtype=torch.int32)
+    ids_d = ids.to(gpu_device)
+    for fin, outs in ((H, [4096, 1024, 1024]), (H, [4096]), (H, [I, I]), (I, [H])):
+        x = _rand((T, fin), 1.0, gen)
+        xd = x.to(gpu_device)
+        mods, host = [], []
+        for fout in outs:
+            W = _rand((fout, fin), 0.02, gen)
+            A = _rand((n, r, fin), fin ** -0.5, gen)
+            B = _rand((n, fout, r), 0.01, gen)
+            base = xd.float() @ W.to(gpu_device).float().T  # fp32 base output
+            mods.append((A.to(gpu_device), B.to(gpu_device), base, 2.0))
+            host.append((W, A, B))
+        lora_delta_(xd, mods, ids_d)
+        torch.cuda.synchronize()
+        for (W, A, B), (_, _, out, _) in zip(host, mods):
+            got = out.cpu().numpy()
+            xs = x.float().numpy()
+            for a in range(n):
+                rows = (ids == a).numpy()
+                if not rows.any():
+                    continue
+                want = ol.merged_linear(xs[rows], W.float().numpy(), None, A[a].float().numpy(),
+                                        B[a].float().numpy(), 2.0)
+                err = np.abs(got[rows] - want).max()
+                assert err <= 2e-3, f"in {fin} out {W.shape[0]} adapter {a}: max err {err:.3e}"
+
+
 def test_negative_ids_untouched_and_rank_not_multiple_of_8(gpu_device):
     gen = torch.Generator().manual_seed(4)
     T, fin = 20, 64
