@@ -768,6 +768,107 @@ int pl_linear_shuffled_side(const void* x, int64_t ldx, int num_tokens,
                             int dtype, void* stream);
 
 /*
+ * The rank-space row y = x . A_a^T of a LoRA module for each token's own
+ * adapter a, as fp32 partial sums written by the kernel that produces x:
+ * y[t][r] is the sum over p = 0 .. parts-1 of partials[t * ld + p * rank + r].
+ * The consumer adds them in a fixed order, so repeated calls give the same
+ * bits.  ld >= parts * rank.
+ */
+typedef struct {
+  float* partials;
+  int64_t ld;
+  int parts;
+  int rank;
+} pl_lora_partials;
+
+/*
+ * A LoRA module's A rows inside its shuffled weight (pl_weight_shuffle of
+ * the out_features rows [W; A_0; A_1; ..], in_features wide): adapter a's
+ * rank r is row a_row0 + a * rank + r, and a_row0 + num_adapters * rank <=
+ * out_features.  adapter >= 0 binds that adapter to every token; -1 takes
+ * each token's adapter from the call's adapter_ids.  A token whose adapter
+ * lies outside [0, num_adapters) gets partials of adapter 0, which the
+ * consumer then does not apply.
+ */
+typedef struct {
+  const void* shuffled;
+  int in_features;
+  int out_features;
+  int a_row0;
+  int rank;
+  int adapter;
+} pl_lora_a_rows;
+
+/*
+ * out = RMSNorm(x) . W^T on a shuffled weight for decode batches: the norm
+ * x * rsqrt(mean(x^2) + eps) * norm_weight, rounded to dtype (the arithmetic
+ * of pl_rmsnorm), is formed by every workgroup in LDS for its tokens, so no
+ * normalized row goes through memory.  x_norm_out (nullable, row stride
+ * ld_norm_out) also receives the normalized rows.  num_tokens <= 8,
+ * in_features a multiple of 512 up to 8192 with num_tokens * in_features <=
+ * 32768.  No counterpart in the reference: it computes the input RMSNorm
+ * (model/flashinfer/norm.py:15-24) and the projection that reads it
+ * (packed_ops.py:143, 179) in one launch.
+ */
+int pl_linear_shuffled_norm(const void* x, int64_t ldx, int num_tokens,
+                            int in_features, const void* norm_weight,
+                            float eps, const void* shuffled,
+                            int out_features, void* out, int64_t ldo,
+                            void* x_norm_out, int64_t ld_norm_out, int dtype,
+                            void* stream);
+
+/*
+ * residual[t][c] += round(round(x . W^T)[t][c] + delta[t][c]) for c <
+ * out_features (rows of the shuffled weight past out_features, e.g. LoRA A
+ * rows stacked under W, are not read): the projection, its LoRA
+ * up-projection delta = scale * y . B_a^T with y from lora_y's partial sums
+ * rounded to dtype, and the residual add, rounded as the reference's module
+ * output followed by `hidden + out`.  lora / lora_y are both NULL (no
+ * delta) or both given (lora->y is ignored; rank 8 or 16); adapter ids
+ * as in pl_add_rmsnorm_lora.  out (nullable) receives round(x . W^T).
+ * num_tokens <= 16.  No counterpart in the reference: it computes
+ * project_linear with LoRALinear.forward's delta (packed_ops.py:251-265,
+ * multilora/linear.py:226-231) and the residual add that precedes the next
+ * RMSNorm (norm.py:27-57) in one launch.
+ */
+int pl_linear_shuffled_add(const void* x, int64_t ldx, int num_tokens,
+                           int in_features, const void* shuffled,
+                           int out_features, void* residual, int64_t ldr,
+                           const pl_lora_up* lora,
+                           const pl_lora_partials* lora_y,
+                           const int32_t* adapter_ids, int num_adapters,
+                           void* out, int64_t ldo, int dtype, void* stream);
+
+/*
+ * pl_decode_run_qkv whose merge also forms o_proj's LoRA shrink: the
+ * attention output of each (row, head) -- the input of o_proj -- rounded to
+ * dtype as stored, times the same columns of the row's adapter's A rows
+ * (o_lora_a, in_features = num_qo_heads * head_dim), as fp32 partial sums
+ * o_lora_y: one per (head, dim slice) of each row, parts = num_qo_heads x
+ * the merge's dim split (4 while batch * num_qo_heads * 4 <= 256, else 2
+ * while batch * num_qo_heads * 2 <= 256, else 1), for pl_linear_shuffled_add.
+ * Every row then goes through the merge, single-item rows included.  Rank 8
+ * or 16; the adapter binding follows o_lora_a->adapter with adapter_ids and
+ * num_adapters as for the q/k/v LoRA.  flags may not skip the merge.  No
+ * counterpart in the reference: it computes the first F.linear of o_proj's
+ * LoRALinear.forward delta (multilora/linear.py:226-231) inside the decode
+ * call.
+ */
+int pl_decode_run_qkv_oshrink(
+    const void* qkv, int64_t ld_qkv, const pl_lora_up* lora_qkv_h,
+    const int32_t* adapter_ids, int num_adapters, const void* q_norm_weight,
+    const void* k_norm_weight, const float* rope_cos_sin,
+    const int64_t* page_id, const int64_t* offset, float eps, void* k_cache,
+    void* v_cache, int64_t page_stride, int64_t token_stride,
+    int64_t head_stride, int64_t num_pages, const int32_t* indices,
+    const int32_t* last_page_len, void* o, int64_t o_stride_b,
+    int64_t o_stride_h, float* lse, int batch, int num_qo_heads,
+    int num_kv_heads, int head_dim, int page_size, float sm_scale, int dtype,
+    int target_items, int flags, void* workspace, size_t workspace_bytes,
+    const pl_lora_a_rows* o_lora_a, const pl_lora_partials* o_lora_y,
+    void* stream);
+
+/*
  * Advance every row of a batched page table by one decode token, in place
  * on the device (one kernel, no host table, safe to capture in a graph).
  * indptr [batch+1], indices (capacity indices_capacity entries) and

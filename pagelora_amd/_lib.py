@@ -107,6 +107,30 @@ class LoraUp(ctypes.Structure):
     ]
 
 
+class LoraPartials(ctypes.Structure):
+    """Mirror of ``pl_lora_partials``."""
+
+    _fields_ = [
+        ("partials", ctypes.c_void_p),
+        ("ld", ctypes.c_int64),
+        ("parts", ctypes.c_int),
+        ("rank", ctypes.c_int),
+    ]
+
+
+class LoraARows(ctypes.Structure):
+    """Mirror of ``pl_lora_a_rows``."""
+
+    _fields_ = [
+        ("shuffled", ctypes.c_void_p),
+        ("in_features", ctypes.c_int),
+        ("out_features", ctypes.c_int),
+        ("a_row0", ctypes.c_int),
+        ("rank", ctypes.c_int),
+        ("adapter", ctypes.c_int),
+    ]
+
+
 PL_LORA_B_ROWS = 0
 PL_LORA_B_CHUNK8 = 1
 
@@ -256,6 +280,24 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _sz, _vp,               # workspace, bytes, stream
         ],
     ),
+    "pl_decode_run_qkv_oshrink": (
+        _i32,
+        [
+            _vp, _i64, _vp, _vp, _i32,   # qkv, ld, lora (3 pl_lora_up), adapter_ids, num_adapters
+            _vp, _vp, _vp,               # q/k norm weights, rope cos/sin
+            _vp, _vp, _f32,              # page_id, offset, eps
+            _vp, _vp, _i64, _i64, _i64,  # k/v cache, page/token/head strides
+            _i64,                        # num_pages
+            _vp, _vp,                    # indices, last_page_len
+            _vp, _i64, _i64,             # o, strides
+            _vp,                         # lse
+            _i32, _i32, _i32, _i32, _i32,  # batch, hq, hkv, head_dim, page_size
+            _f32, _i32, _i32, _i32,      # sm_scale, dtype, target_items, flags
+            _vp, _sz,                    # workspace, bytes
+            ctypes.POINTER(LoraARows), ctypes.POINTER(LoraPartials),  # o_proj A rows, partials
+            _vp,                         # stream
+        ],
+    ),
     "pl_linear": (
         _i32,
         [_vp, _i64, _i32, _i32, _vp, _i64, _i32, _vp, _vp, _i64, ctypes.POINTER(LinearLora), _i32, _vp, _i32,
@@ -268,6 +310,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pl_linear_shuffled_split": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _i64, _i64, _i32, _vp]),
     "pl_linear_shuffled_side": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _i64, _i32, _vp, _i64, _i64,
                                        _i32, _vp]),
+    "pl_linear_shuffled_norm": (_i32, [_vp, _i64, _i32, _i32, _vp, _f32, _vp, _i32, _vp, _i64, _vp, _i64, _i32,
+                                       _vp]),
+    "pl_linear_shuffled_add": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _vp, _i64, ctypes.POINTER(LoraUp),
+                                      ctypes.POINTER(LoraPartials), _vp, _i32, _vp, _i64, _i32, _vp]),
     "pl_lora_workspace_size": (_sz, [_i32, _i32, ctypes.POINTER(LoraModule), _i32]),
     "pl_lora_delta": (
         _i32,

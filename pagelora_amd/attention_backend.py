@@ -458,13 +458,19 @@ class PagedDecodeAttention:
         lora=None,
         adapter_ids: torch.Tensor | None = None,
         lse: torch.Tensor | None = None,
+        o_shrink=None,
     ) -> torch.Tensor:
         """``run_decode_into`` from the packed q/k/v projection rows
         (pl_decode_run_qkv): the kernel forms q (LoRA delta, head norm, RoPE
         with ``rope_cos_sin`` from ``fused_ops.rope_cos_sin``), appends each
         row's new k/v at ``(page_id, page_offset)`` and attends.  ``lora`` is
         the (q, k, v) ``fused_ops.LoraUp`` triple or None.  Built for 16-bit
-        caches, head_dim 128, 4 q heads per kv head, LoRA rank 0/8/16."""
+        caches, head_dim 128, 4 q heads per kv head, LoRA rank 0/8/16.
+
+        ``o_shrink`` = (``_lib.LoraARows`` of o_proj, ``linear.LoraPartials``
+        [B, parts, rank], n_adapters): the merge also writes o_proj's LoRA
+        shrink partials of the attention output (pl_decode_run_qkv_oshrink);
+        ``parts`` is :meth:`oshrink_parts`."""
 
         from .fused_ops import _lora_args, _rows2d
 
@@ -500,7 +506,7 @@ class PagedDecodeAttention:
                 raise ValueError("lora must be (q, k, v)")
             arr, ids, n = _lora_args(lora, adapter_ids, batch)
         _, indices_buf, last_buf = self._decode_graph_buffers
-        status = self._lib.pl_decode_run_qkv(
+        args = (
             qkv.data_ptr(), qkv.stride(0), arr, ids, n,
             q_norm_weight.data_ptr() if q_norm_weight is not None else None,
             k_norm_weight.data_ptr() if k_norm_weight is not None else None,
@@ -512,10 +518,32 @@ class PagedDecodeAttention:
             batch, self.num_qo_heads, self.num_kv_heads, self.head_dim, self.page_size,
             self.sm_scale, _lib.dtype_code(qkv.dtype), plan["target_items"], 0,
             self.workspace_buffer.data_ptr(), self.workspace_buffer.numel(),
-            _lib.stream_handle(qkv.device),
         )
-        _lib.check(status, "pl_decode_run_qkv")
+        if o_shrink is None:
+            _lib.check(self._lib.pl_decode_run_qkv(*args, _lib.stream_handle(qkv.device)), "pl_decode_run_qkv")
+            return out
+        a_rows, parts, n_o = o_shrink
+        if parts.partials.shape[0] != batch or parts.parts != self.oshrink_parts(batch):
+            raise ValueError(f"o_proj partials must be [{batch}, {self.oshrink_parts(batch)}, rank]")
+        if lora is None:
+            if a_rows.adapter < 0 and (adapter_ids is None or adapter_ids.dtype != torch.int32
+                                       or adapter_ids.numel() != batch):
+                raise ValueError("per-row adapters need int32 adapter_ids [B]")
+            args = args[:3] + (adapter_ids.data_ptr() if adapter_ids is not None else None, int(n_o)) + args[5:]
+        elif n_o != n:
+            raise ValueError("o_proj and q/k/v must stack the same adapters")
+        p = parts.struct()
+        _lib.check(self._lib.pl_decode_run_qkv_oshrink(*args, ctypes.byref(a_rows), ctypes.byref(p),
+                                                       _lib.stream_handle(qkv.device)),
+                   "pl_decode_run_qkv_oshrink")
         return out
+
+    def oshrink_parts(self, batch: int) -> int:
+        """Partial sums per row of the o_proj shrink the merge forms: one per
+        (head, dim slice), with the merge's dim split for this batch."""
+        pairs = batch * self.num_qo_heads
+        ds = 4 if self.head_dim % 32 == 0 and pairs * 4 <= 256 else (2 if self.head_dim % 16 == 0 and pairs * 2 <= 256 else 1)
+        return self.num_qo_heads * ds
 
     # ------------------------------------------------------------- prefill
     def plan_prefill(

@@ -752,6 +752,7 @@ struct QkvIn {
   LoraUp m[3];               // q, k, v up-projections (rank R > 0)
   const int32_t* ids;
   int n_adapters;
+  int no_direct;             // 1: single-item rows publish a partial too (the merge writes them)
 };
 
 // One lane's 8 dims (8*col ..) of head `hh` of packed projection row b: the
@@ -1260,7 +1261,9 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
   st.merge_rows();
 
   constexpr float kLn2 = 0.69314718055994530942f;
-  if (flags & 1) {  // the row is one item: write the output directly
+  bool direct = flags & 1;  // the row is one item: write the output directly
+  if constexpr (FUSED) direct = direct && !qin.no_direct;
+  if (direct) {
     if (row != 0) return;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -1315,6 +1318,13 @@ constexpr int kMergeFewItems = 8;  // average items per row up to which one wave
 constexpr int kMergeManyItems = 96;
 constexpr int kMergeCUs = 256;  // MI355X
 
+// Workgroups per (row, head) of the merge: the head's dims split as far as
+// 4 while the launch stays within one workgroup per CU (a full-chip launch
+// gains nothing from it).
+__host__ __device__ constexpr int merge_dim_split(int head_dim, int pairs) {
+  return (head_dim % 32 == 0 && pairs * 4 <= kMergeCUs) ? 4 : (head_dim % 16 == 0 && pairs * 2 <= kMergeCUs) ? 2 : 1;
+}
+
 struct MergeState {
   float m, w, a[8];  // log2 max, sum of weights, weighted output (8 dims)
   __device__ __forceinline__ void add(float m_o, float w_o, const float (&a_o)[8]) {
@@ -1328,26 +1338,66 @@ struct MergeState {
   }
 };
 
+// The o_proj module's LoRA shrink, folded into the merge (decoder layers):
+// the merged output of the attention is o_proj's input, so each workgroup
+// multiplies its slice of the (row, head) output, rounded to T as stored, by
+// the same columns of the row's adapter's A rows and writes the rank-space
+// partial sums, one per (head, dim slice): part[b * ld + (hq * DS + ds) * R
+// + r].  The A rows are read from the shuffled [W_o; A_o] weight: adapter a's
+// rank r is row a_row0 + a * R + r.  An adapter outside [0, n_adapters)
+// gives adapter 0's products (its consumer does not apply them).
+struct OShrink {
+  const void* A;
+  int ksteps;       // o_proj's in_features / 32 (num_qo_heads * D / 32)
+  int a_row0;
+  int adapter;      // >= 0: every row's adapter; -1: ids[b]
+  const int32_t* ids;
+  int n_adapters;
+  float* part;
+  int64_t ld;
+};
+
 // DS: the head's dims split over DS workgroups (each folds every partial of
 // its D / DS dims), for launches with few (row, head) pairs: one row of 32
 // heads is otherwise 32 workgroups, each reading 64 KB of partials alone.
-template <typename T, int D, int MT, int DS = 1>
+// OR > 0: the OShrink products of rank OR are formed too, and single-item
+// rows (published as one partial) are merged as well.
+template <typename T, int D, int MT, int DS = 1, int OR = 0>
 __global__ __launch_bounds__(MT) void merge_kernel(
     const int2* __restrict__ row_info, const float* __restrict__ part_lse,
     const float* __restrict__ part_o, T* __restrict__ o, int64_t o_sb, int64_t o_sh,
     float* __restrict__ lse, const int* __restrict__ header, int batch, int num_qo_heads,
-    int max_items, Direct dir) {
+    int max_items, Direct dir, OShrink os) {
   static_assert((D / 8) % DS == 0, "whole 8-dim slices per workgroup");
+  static_assert(OR == 0 || OR == 8 || OR == 16, "o shrink ranks 8 or 16");
   constexpr int LPT = D / 8 / DS, RPI = MT / LPT, NWV = MT / kWave;
+  constexpr int NP = OR * LPT, PPT = OR > 0 ? (NP + MT - 1) / MT : 1;  // shrink products, per thread
+  constexpr int kMinItems = OR > 0 ? 1 : 2;
   __shared__ float s_m[NWV][LPT], s_w[NWV][LPT], s_a[NWV][LPT][8];
+  __shared__ float s_ov[OR > 0 ? LPT : 1][8];
   const int pair = blockIdx.x / DS, ds = blockIdx.x % DS;
   if (pair >= batch * num_qo_heads) return;
   const int b = pair / num_qo_heads;
   const int hq = pair - b * num_qo_heads;
+  // the A pieces first: they need only the row's adapter
+  [[maybe_unused]] uint4 ap[PPT];
+  if constexpr (OR > 0) {
+    const int a_raw = os.adapter >= 0 ? os.adapter : os.ids[b];
+    const int aa = (a_raw >= 0 && a_raw < os.n_adapters) ? a_raw : 0;
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int i = min((int)threadIdx.x + j * MT, NP - 1);
+      const int r = i / LPT, c = i - r * LPT;
+      const int64_t n = (int64_t)os.a_row0 + (int64_t)aa * OR + r;
+      const int k = hq * D + (ds * LPT + c) * 8;
+      const int64_t e = (((n / 16) * os.ksteps + k / 32) * 64 + ((k % 32) / 8) * 16 + n % 16) * 8;
+      ap[j] = *reinterpret_cast<const uint4*>((const T*)os.A + e);
+    }
+  }
   int first, n;
   if (dir.indptr != nullptr) {  // direct items (uniform): the row's slots from indptr
     direct_row(dir, batch, b, first, n);
-    if (!((n > 1) & (first >= 0) & (first + n <= max_items))) return;
+    if (!((n >= kMinItems) & (first >= 0) & (first + n <= max_items))) return;
   } else {
     // One combined check that needs all three loads, so they are issued
     // together (separate early exits would sink each load below the last).
@@ -1355,7 +1405,7 @@ __global__ __launch_bounds__(MT) void merge_kernel(
     const int2 info = row_info[b];
     first = uniform(info.x), n = uniform(info.y);
     const bool planned = (stamp_batch == batch) & (stamp == plan_stamp(batch, max_items));
-    if (!(planned & (n > 1) & (first >= 0) & (first + n <= max_items))) return;
+    if (!(planned & (n >= kMinItems) & (first >= 0) & (first + n <= max_items))) return;
   }
 
   const int r = threadIdx.x / LPT, col = threadIdx.x % LPT;
@@ -1408,22 +1458,48 @@ __global__ __launch_bounds__(MT) void merge_kernel(
     }
     __syncthreads();
   }
-  if (threadIdx.x >= LPT) return;
+  if (threadIdx.x < LPT) {
 #pragma unroll
-  for (int w = 1; w < NWV; ++w) {
-    float a_o[8];
+    for (int w = 1; w < NWV; ++w) {
+      float a_o[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) a_o[i] = s_a[w][col][i];
-    st.add(s_m[w][col], s_w[w][col], a_o);
+      for (int i = 0; i < 8; ++i) a_o[i] = s_a[w][col][i];
+      st.add(s_m[w][col], s_w[w][col], a_o);
+    }
+    const float inv = st.w > 0.f ? 1.f / st.w : 0.f;
+    T* op = o + (int64_t)b * o_sb + (int64_t)hq * o_sh + dcol * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const T v = from_float<T>(st.a[i] * inv);
+      op[i] = v;
+      if constexpr (OR > 0) s_ov[col][i] = to_float<T>(v);
+    }
+    if (lse != nullptr && dcol == 0) {
+      constexpr float kLn2 = 0.69314718055994530942f;
+      const float m_use = st.m == -INFINITY ? 0.f : st.m;
+      lse[(int64_t)b * num_qo_heads + hq] = st.w > 0.f ? (m_use + __log2f(st.w)) * kLn2 : -INFINITY;
+    }
   }
-  const float inv = st.w > 0.f ? 1.f / st.w : 0.f;
-  T* op = o + (int64_t)b * o_sb + (int64_t)hq * o_sh + dcol * 8;
+  if constexpr (OR > 0) {
+    __syncthreads();
+    // products of the A pieces with the stored output, summed over the LPT
+    // consecutive lanes of each rank (fixed butterfly order)
 #pragma unroll
-  for (int i = 0; i < 8; ++i) op[i] = from_float<T>(st.a[i] * inv);
-  if (lse != nullptr && dcol == 0) {
-    constexpr float kLn2 = 0.69314718055994530942f;
-    const float m_use = st.m == -INFINITY ? 0.f : st.m;
-    lse[(int64_t)b * num_qo_heads + hq] = st.w > 0.f ? (m_use + __log2f(st.w)) * kLn2 : -INFINITY;
+    for (int j = 0; j < PPT; ++j) {
+      const int i = (int)threadIdx.x + j * MT;
+      const int r = i / LPT, c = i - r * LPT;
+      float f[8];
+      unpack2<T>(ap[j].x, f[0], f[1]);
+      unpack2<T>(ap[j].y, f[2], f[3]);
+      unpack2<T>(ap[j].z, f[4], f[5]);
+      unpack2<T>(ap[j].w, f[6], f[7]);
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = fmaf(s_ov[c][e], f[e], acc);
+#pragma unroll
+      for (int off = LPT / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+      if (c == 0 && i < NP) os.part[(int64_t)b * os.ld + (int64_t)(hq * DS + ds) * OR + r] = acc;
+    }
   }
 }
 
@@ -1439,6 +1515,8 @@ struct RunArgs {
   float* part_lse; float* part_o; int flags;
   Direct dir;  // dir.indptr != nullptr: items derived from indptr (no plan kernel)
   int grid_items;  // work items the decode grid covers (max_items, the slot count, unless a prefix is shared)
+  OShrink os;      // os.part != nullptr: the merge forms o_proj's LoRA shrink partials (rank os_rank)
+  int os_rank;
   hipStream_t stream;
 };
 
@@ -1466,15 +1544,19 @@ int launch(const RunArgs& a, const QkvIn& qin = QkvIn{}) {
     PL_LAUNCH_CHECK("decode_kernel");
   }
   if (!(a.flags & PL_DECODE_SKIP_MERGE)) {
-    // the dim split: as far as 4 while the launch stays within one
-    // workgroup per CU (a full-chip launch gains nothing from it)
     const int pairs = a.batch * a.hq;
-    const int ds = (D % 32 == 0 && pairs * 4 <= kMergeCUs) ? 4 : (D % 16 == 0 && pairs * 2 <= kMergeCUs) ? 2 : 1;
+    const int ds = merge_dim_split(D, pairs);
     auto go = [&](auto mt, auto dsc) {
       constexpr int MT = decltype(mt)::value, DS = decltype(dsc)::value;
-      hipLaunchKernelGGL((merge_kernel<T, D, MT, DS>), dim3(pairs * DS), dim3(MT), 0, a.stream, a.row_info,
-                         a.part_lse, a.part_o, (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header, a.batch, a.hq,
-                         a.max_items, a.dir);
+      auto with = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(pairs * DS), dim3(MT), 0, a.stream, a.row_info, a.part_lse, a.part_o,
+                           (T*)a.o, a.o_sb, a.o_sh, a.lse, a.header, a.batch, a.hq, a.max_items, a.dir, a.os);
+      };
+      if constexpr (FUSED && D == 128) {
+        if (a.os.part != nullptr && a.os_rank == 16) return with(merge_kernel<T, D, MT, DS, 16>);
+        if (a.os.part != nullptr && a.os_rank == 8) return with(merge_kernel<T, D, MT, DS, 8>);
+      }
+      with(merge_kernel<T, D, MT, DS, 0>);
     };
     auto by_ds = [&](auto mt) {
       if constexpr (D % 32 == 0)

@@ -355,7 +355,7 @@ static int decode_run_common(const void* q, int64_t q_stride_b, int64_t q_stride
                              int num_kv_heads, int head_dim, int page_size, float sm_scale,
                              int dtype, int target_items, int flags, void* workspace,
                              size_t workspace_bytes, void* stream, const QkvIn* qin = nullptr,
-                             int qin_rank = 0) {
+                             int qin_rank = 0, const OShrink* os = nullptr, int os_rank = 0) {
   if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0");
   if (batch == 0) return ok();
   if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads)
@@ -412,6 +412,8 @@ static int decode_run_common(const void* q, int64_t q_stride_b, int64_t q_stride
   a.part_lse = (float*)(ws + L.lse); a.part_o = (float*)(ws + L.partial_o);
   a.dir = dir;
   a.grid_items = grid_items;
+  a.os = os ? *os : OShrink{};
+  a.os_rank = os ? os_rank : 0;
   a.stream = (hipStream_t)stream;
   const int g = num_qo_heads / num_kv_heads;
   if (qin) {
@@ -454,7 +456,7 @@ extern "C" int pl_decode_run(const void* q, int64_t q_stride_b, int64_t q_stride
                            workspace_bytes, stream);
 }
 
-extern "C" int pl_decode_run_qkv(const void* qkv, int64_t ld_qkv, const pl_lora_up* lora_qkv_h,
+static int decode_run_qkv_common(const void* qkv, int64_t ld_qkv, const pl_lora_up* lora_qkv_h,
                                  const int32_t* adapter_ids, int num_adapters, const void* q_norm_weight,
                                  const void* k_norm_weight, const float* rope_cos_sin, const int64_t* page_id,
                                  const int64_t* offset, float eps, void* k_cache, void* v_cache,
@@ -462,7 +464,8 @@ extern "C" int pl_decode_run_qkv(const void* qkv, int64_t ld_qkv, const pl_lora_
                                  const int32_t* indices, const int32_t* last_page_len, void* o, int64_t o_stride_b,
                                  int64_t o_stride_h, float* lse, int batch, int num_qo_heads, int num_kv_heads,
                                  int head_dim, int page_size, float sm_scale, int dtype, int target_items, int flags,
-                                 void* workspace, size_t workspace_bytes, void* stream) {
+                                 void* workspace, size_t workspace_bytes, void* stream,
+                                 const pl_lora_a_rows* o_a = nullptr, const pl_lora_partials* o_y = nullptr) {
   if (batch < 0) return fail(PL_ERR_INVALID, "batch must be >= 0");
   if (batch == 0) return ok();
   if (!qkv || !rope_cos_sin || !page_id || !offset) return fail(PL_ERR_INVALID, "null pointer argument");
@@ -493,10 +496,73 @@ extern "C" int pl_decode_run_qkv(const void* qkv, int64_t ld_qkv, const pl_lora_
     if (lora_qkv_h[1].rank != rank || lora_qkv_h[2].rank != rank)
       return fail(PL_ERR_INVALID, "q, k and v LoRA must share one rank");
   }
+  OShrink os{};
+  int os_rank = 0;
+  if (o_a != nullptr || o_y != nullptr) {
+    if (!o_a || !o_y) return fail(PL_ERR_INVALID, "o_proj's A rows and partials are given together");
+    if (flags & (PL_DECODE_SKIP_MERGE | PL_DECODE_MERGE_ONLY))
+      return fail(PL_ERR_INVALID, "the o_proj shrink runs in the merge: no PL_DECODE_SKIP_MERGE / MERGE_ONLY");
+    const int K = num_qo_heads * head_dim;
+    if (o_a->rank != 8 && o_a->rank != 16)
+      return fail(PL_ERR_UNSUPPORTED, "o_proj shrink rank %d not built (8, 16)", o_a->rank);
+    if (!o_a->shuffled || (uintptr_t)o_a->shuffled % 16 || o_a->in_features != K || o_a->a_row0 < 0 ||
+        (int64_t)o_a->a_row0 + (int64_t)num_adapters * o_a->rank > o_a->out_features)
+      return fail(PL_ERR_INVALID,
+                  "o_proj A rows: a 16-byte aligned shuffled weight %d wide (got %d) whose %d rows hold rows "
+                  "a_row0 (%d) .. + %d adapters x rank %d",
+                  K, o_a->in_features, o_a->out_features, o_a->a_row0, num_adapters, o_a->rank);
+    if (o_a->adapter < -1 || o_a->adapter >= num_adapters || num_adapters < 1 ||
+        (o_a->adapter < 0 && !adapter_ids))
+      return fail(PL_ERR_INVALID, "o_proj A rows: adapter %d with %d adapters (per-row ids need adapter_ids)",
+                  o_a->adapter, num_adapters);
+    // partials per row: one per (head, dim slice), the slice count the merge picks
+    const int ds = merge_dim_split(head_dim, batch * num_qo_heads);
+    if (!o_y->partials || o_y->rank != o_a->rank || o_y->parts != num_qo_heads * ds ||
+        o_y->ld < (int64_t)o_y->parts * o_y->rank)
+      return fail(PL_ERR_INVALID, "o_proj partials: rank %d, %d parts per row (num_qo_heads x %d), ld >= %d",
+                  o_a->rank, num_qo_heads * ds, ds, num_qo_heads * ds * o_a->rank);
+    os = OShrink{o_a->shuffled, K / 32, o_a->a_row0, o_a->adapter,
+                 adapter_ids ? adapter_ids : reinterpret_cast<const int32_t*>(offset), num_adapters,
+                 o_y->partials, o_y->ld};
+    os_rank = o_a->rank;
+    qin.no_direct = 1;
+  }
   return decode_run_common(nullptr, 0, 0, k_cache, v_cache, page_stride, token_stride, head_stride, num_pages,
                            indices, last_page_len, o, o_stride_b, o_stride_h, lse, batch, num_qo_heads, num_kv_heads,
                            head_dim, page_size, sm_scale, dtype, target_items, flags, workspace, workspace_bytes,
-                           stream, &qin, rank);
+                           stream, &qin, rank, os_rank ? &os : nullptr, os_rank);
+}
+
+extern "C" int pl_decode_run_qkv(const void* qkv, int64_t ld_qkv, const pl_lora_up* lora_qkv_h,
+                                 const int32_t* adapter_ids, int num_adapters, const void* q_norm_weight,
+                                 const void* k_norm_weight, const float* rope_cos_sin, const int64_t* page_id,
+                                 const int64_t* offset, float eps, void* k_cache, void* v_cache,
+                                 int64_t page_stride, int64_t token_stride, int64_t head_stride, int64_t num_pages,
+                                 const int32_t* indices, const int32_t* last_page_len, void* o, int64_t o_stride_b,
+                                 int64_t o_stride_h, float* lse, int batch, int num_qo_heads, int num_kv_heads,
+                                 int head_dim, int page_size, float sm_scale, int dtype, int target_items, int flags,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  return decode_run_qkv_common(qkv, ld_qkv, lora_qkv_h, adapter_ids, num_adapters, q_norm_weight, k_norm_weight,
+                               rope_cos_sin, page_id, offset, eps, k_cache, v_cache, page_stride, token_stride,
+                               head_stride, num_pages, indices, last_page_len, o, o_stride_b, o_stride_h, lse, batch,
+                               num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, target_items, flags,
+                               workspace, workspace_bytes, stream);
+}
+
+extern "C" int pl_decode_run_qkv_oshrink(
+    const void* qkv, int64_t ld_qkv, const pl_lora_up* lora_qkv_h, const int32_t* adapter_ids, int num_adapters,
+    const void* q_norm_weight, const void* k_norm_weight, const float* rope_cos_sin, const int64_t* page_id,
+    const int64_t* offset, float eps, void* k_cache, void* v_cache, int64_t page_stride, int64_t token_stride,
+    int64_t head_stride, int64_t num_pages, const int32_t* indices, const int32_t* last_page_len, void* o,
+    int64_t o_stride_b, int64_t o_stride_h, float* lse, int batch, int num_qo_heads, int num_kv_heads, int head_dim,
+    int page_size, float sm_scale, int dtype, int target_items, int flags, void* workspace, size_t workspace_bytes,
+    const pl_lora_a_rows* o_lora_a, const pl_lora_partials* o_lora_y, void* stream) {
+  if (!o_lora_a || !o_lora_y) return fail(PL_ERR_INVALID, "null o_proj A rows or partials");
+  return decode_run_qkv_common(qkv, ld_qkv, lora_qkv_h, adapter_ids, num_adapters, q_norm_weight, k_norm_weight,
+                               rope_cos_sin, page_id, offset, eps, k_cache, v_cache, page_stride, token_stride,
+                               head_stride, num_pages, indices, last_page_len, o, o_stride_b, o_stride_h, lse, batch,
+                               num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, target_items, flags,
+                               workspace, workspace_bytes, stream, o_lora_a, o_lora_y);
 }
 
 // ------------------------------------------------- allocation-free entry ---

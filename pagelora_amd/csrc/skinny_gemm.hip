@@ -25,6 +25,7 @@
 // LoRALinear.forward (multilora/linear.py:226-231) at decode batch sizes.
 #include <algorithm>
 
+#include "lora_up.h"
 #include "pl_common.h"
 
 namespace pl {
@@ -161,6 +162,341 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_kernel(const T* __rest
         else
           out[(int64_t)tr * ldo + n] = from_float<T>(sum + bv);
       }
+    }
+  }
+}
+
+// ------------------------------------------------------- norm prologue ---
+// out = RMSNorm(x) . W^T: the workgroup normalizes the rows of its token
+// tile into LDS (x * rsqrt(mean(x^2) + eps) * w rounded to T, as
+// rmsnorm_kernel forms it), with its waves' first batch of weight blocks
+// already in flight, and the waves then take their MFMA A operands from LDS.
+// PPT: 16-byte pieces of the tile's rows per thread (the tile's rows are
+// K / 8 * nt pieces, a multiple of 64 per row: K % 512 == 0).  The LDS rows
+// are kNormRowPad elements longer than K, so the rows of a lane group's
+// tokens start 64 bytes apart in the banks; after the main loop the same
+// LDS holds the cross-wave partial tiles.
+constexpr int kNormMaxPieces = 4;    // per thread
+constexpr int kNormRowPad = 32;      // elements
+constexpr int kNormMaxTokens = 8;
+constexpr int kRedBytes = kWaves * 256 * 4;
+
+// the tile's rows (padded), then the norm weight; the partial tiles of the
+// cross-wave sum reuse the space after the main loop
+__host__ __device__ constexpr int norm_lds_bytes(int nt, int K) {
+  return nt * (K + kNormRowPad) * 2 + K * 2 > kRedBytes ? nt * (K + kNormRowPad) * 2 + K * 2 : kRedBytes;
+}
+
+template <typename T, int PPT>
+__global__ __launch_bounds__(kThreads) void shuffled_gemm_norm_kernel(
+    const T* __restrict__ x, int64_t ldx, int tokens, int K, const T* __restrict__ nw, float eps,
+    const T* __restrict__ Ws, int N, T* __restrict__ out, int64_t ldo, T* __restrict__ xn_out, int64_t ldxn) {
+  extern __shared__ __align__(16) unsigned char s_dyn[];
+  __shared__ float s_ss[kThreads * PPT / kWave];  // one sum per 64-piece slice of a row
+  T* xs = reinterpret_cast<T*>(s_dyn);
+  float (*s_red)[256] = reinterpret_cast<float (*)[256]>(s_dyn);
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lr = lane % 16, kq = (lane / 16) * 8;
+  const int nb = blockIdx.x, t0 = blockIdx.y * 16;
+  const int nt = min(16, tokens - t0);
+  const int ksteps = K / 32;
+  const int per = (ksteps + kWaves - 1) / kWaves;
+  const int sb = min(ksteps, wave * per), se = min(ksteps, sb + per);
+  const u32x4* wb = reinterpret_cast<const u32x4*>(Ws + (int64_t)nb * ksteps * kBlockElems) + lane;
+  const int Kp = K + kNormRowPad;
+
+  // the tile's rows, PPT pieces per thread (pieces past the tile re-read
+  // piece 0), and the norm weight go to LDS as they are; the sums of squares
+  // come from the same registers (a wave's 64 pieces of pass c are one slice
+  // of one row), so no row value stays in a register across the barrier
+  const int rp = K / 8, pieces = nt * rp;
+  uint4* sw8 = reinterpret_cast<uint4*>(xs + nt * Kp);  // the norm weight, K / 8 pieces
+  uint4 hv[PPT];
+#pragma unroll
+  for (int c = 0; c < PPT; ++c) {
+    const int j = threadIdx.x + c * kThreads;
+    const int jj = j < pieces ? j : 0;
+    const int tt = jj / rp, cc = jj - tt * rp;
+    hv[c] = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + tt) * ldx + cc * 8);
+  }
+  const int wc = threadIdx.x < rp ? threadIdx.x : 0;
+  const uint4 wv = *reinterpret_cast<const uint4*>(nw + wc * 8);
+  // Then the wave's first two batches of weight blocks (its whole k-range at
+  // K = 4096), in flight while the rows are normalized.  After the rows:
+  // loads complete in order, so the rows' wait does not wait for these.
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 b[kUnroll], b1[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) b[u] = __builtin_nontemporal_load(wb + min(sb + u, ksteps - 1) * kWave);
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) b1[u] = __builtin_nontemporal_load(wb + min(sb + kUnroll + u, ksteps - 1) * kWave);
+  __builtin_amdgcn_sched_barrier(0);
+  // unconditional (threads past the K / 8 pieces rewrite piece 0 with its
+  // own value): a store under a test drags its load below the weights'
+  sw8[wc] = wv;  // rp <= kThreads: K <= 8192
+#pragma unroll
+  for (int c = 0; c < PPT; ++c) {
+    const int j = threadIdx.x + c * kThreads;
+    if (j < pieces) {
+      const int tt = j / rp, cc = j - tt * rp;
+      *reinterpret_cast<uint4*>(xs + tt * Kp + cc * 8) = hv[c];
+    }
+    float f[8];
+    unpack2<T>(hv[c].x, f[0], f[1]);
+    unpack2<T>(hv[c].y, f[2], f[3]);
+    unpack2<T>(hv[c].z, f[4], f[5]);
+    unpack2<T>(hv[c].w, f[6], f[7]);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+    ss = wave_sum(ss);
+    if (lane == 0) s_ss[wave + c * kWaves] = ss;
+  }
+  __syncthreads();
+  const int slices = rp / kWave;  // per row
+  // one piece at a time: the weight batches are live here, and two pieces'
+  // temporaries at once would raise the kernel's register count
+#pragma unroll 1
+  for (int c = 0; c < PPT; ++c) {
+    const int j = threadIdx.x + c * kThreads;
+    if (j < pieces) {
+      const int tt = j / rp, cc = j - tt * rp;
+      float tot = 0.f;
+      for (int s = 0; s < slices; ++s) tot += s_ss[tt * slices + s];
+      const float rstd = rsqrtf(tot / (float)K + eps);
+      const uint4 hw = *reinterpret_cast<const uint4*>(xs + tt * Kp + cc * 8), ww = sw8[cc];
+      auto norm2 = [&](uint32_t h2, uint32_t w2) {
+        float f0, f1, w0, w1;
+        unpack2<T>(h2, f0, f1);
+        unpack2<T>(w2, w0, w1);
+        return pack2<T>(f0 * rstd * w0, f1 * rstd * w1);
+      };
+      const uint4 o = make_uint4(norm2(hw.x, ww.x), norm2(hw.y, ww.y), norm2(hw.z, ww.z), norm2(hw.w, ww.w));
+      *reinterpret_cast<uint4*>(xs + tt * Kp + cc * 8) = o;
+      if (xn_out != nullptr && blockIdx.x == 0)
+        *reinterpret_cast<uint4*>(xn_out + (int64_t)(t0 + tt) * ldxn + cc * 8) = o;
+    }
+  }
+  __syncthreads();
+
+  // Lanes of tokens past the tile read token 0's row (their MFMA rows are
+  // never written).
+  const T* xr = xs + (lr < nt ? lr : 0) * Kp + kq;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int s = sb;
+  if (s + kUnroll <= se) {
+    u32x4 a[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) a[u] = *reinterpret_cast<const u32x4*>(xr + (s + u) * 32);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[u], b[u], acc);
+    s += kUnroll;
+    if (s + kUnroll <= se) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) a[u] = *reinterpret_cast<const u32x4*>(xr + (s + u) * 32);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[u], b1[u], acc);
+      s += kUnroll;
+    }
+  }
+  for (; s + kUnroll <= se; s += kUnroll) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) b[u] = __builtin_nontemporal_load(wb + (s + u) * kWave);
+    u32x4 a[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) a[u] = *reinterpret_cast<const u32x4*>(xr + (s + u) * 32);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[u], b[u], acc);
+  }
+  for (; s < se; ++s) {
+    const u32x4 bb = __builtin_nontemporal_load(wb + s * kWave);
+    const u32x4 a = *reinterpret_cast<const u32x4*>(xr + s * 32);
+    acc = mfma32<T>(a, bb, acc);
+  }
+  __syncthreads();  // every wave is done with the rows before the tiles reuse the LDS
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s_red[wave][((lane / 16) * 4 + i) * 16 + lr] = acc[i];
+  __syncthreads();
+  if (wave == 0) {
+    const int n = nb * 16 + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cell = ((lane / 16) * 4 + i) * 16 + lr;
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) sum += s_red[w][cell];
+      const int tr = t0 + (lane / 16) * 4 + i;
+      if (n < N && tr < tokens) out[(int64_t)tr * ldo + n] = from_float<T>(sum);
+    }
+  }
+}
+
+// --------------------------------------------- residual + LoRA epilogue ---
+// residual += round(round(x . W^T) + scale * y . B_a^T) for the first N
+// rows of the shuffled weight.  y comes as fp32 partial sums written by the
+// producer of x: flat index f = (t * (R/4) + q) * G + p (G = parts rounded up
+// to a power of two, p >= parts reading as 0) over the tile's tokens, one
+// float4 of ranks 4q .. 4q+3 per f, YPT of them per thread.  They are loaded
+// before the weights and summed while the first batch of weight blocks is in
+// flight: a butterfly over min(G, 64) lanes, then the per-wave slices of
+// groups wider than a wave in order through LDS.
+constexpr int kAddMaxYPT = 4;
+
+template <typename T, int R, int YPT>
+__global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
+    const T* __restrict__ x, int64_t ldx, int tokens, int K, const T* __restrict__ Ws, int N,
+    T* __restrict__ res, int64_t ldr, LoraUp lora, const float* __restrict__ yp, int64_t ldyp, int parts, int lg,
+    const int32_t* __restrict__ ids, int n_adapters, T* __restrict__ out, int64_t ldo) {
+  constexpr int Q = R > 0 ? R / 4 : 1;
+  __shared__ float s_red[kWaves][256];
+  // (t, q) group x slice: at most YPT * kThreads / kWave entries (G <= 64:
+  // one slice per group, nt * Q <= 64 groups; G > 64: nt * Q * G / 64)
+  __shared__ float4 s_y[R > 0 ? kAddMaxYPT * kThreads / kWave : 1];
+  __shared__ uint4 s_yr[R > 0 ? 16 * (R / 8) : 1];  // y rounded to T: token tl's ranks 8k .. at tl * R/8 + k
+  // the epilogue's inputs, loaded with the partials: the residual tile and
+  // the B pieces of the workgroup's 16 columns (token tl, column c, ranks 8k ..)
+  __shared__ float s_res[16 * 16];
+  __shared__ uint4 s_b[R > 0 ? 16 * 16 * (R / 8) : 1];
+  __shared__ int s_ok[16];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lr = lane % 16, kq = (lane / 16) * 8;
+  const int nb = blockIdx.x, t0 = blockIdx.y * 16;
+  const int nt = min(16, tokens - t0);
+  const int t = t0 + lr;
+  const bool t_ok = t < tokens;
+  const int ksteps = K / 32;
+  const int per = (ksteps + kWaves - 1) / kWaves;
+  const int sb = min(ksteps, wave * per), se = min(ksteps, sb + per);
+  const u32x4* wb = reinterpret_cast<const u32x4*>(Ws + (int64_t)nb * ksteps * kBlockElems) + lane;
+  const T* xr = x + (int64_t)(t_ok ? t : 0) * ldx + kq;
+  const int G = 1 << lg;                  // parts rounded up to a power of two
+  const int lgw = lg < 6 ? lg : 6;        // butterfly width 2^lgw lanes
+  const int slices = 1 << (lg - lgw);
+
+  // (a partial past `parts` or the tile re-reads partial 0 of token t0 and
+  // is masked to zero after the weight loads are issued: a select on the
+  // loaded value here would wait for the load first)
+  [[maybe_unused]] float4 yv[YPT];
+  [[maybe_unused]] bool yon[YPT];
+  if constexpr (R > 0) {
+#pragma unroll
+    for (int c = 0; c < YPT; ++c) {
+      const int f = threadIdx.x + c * kThreads;
+      const int p = f & (G - 1), tq = f >> lg;
+      const int tt = tq / Q, q = tq - tt * Q;
+      yon[c] = (p < parts) & (tt < nt);
+      const float* src = yp + (int64_t)(t0 + (yon[c] ? tt : 0)) * ldyp + (yon[c] ? p : 0) * R + q * 4;
+      yv[c] = *reinterpret_cast<const float4*>(src);
+    }
+  }
+  // residual tile: thread i < nt * 16 reads token i / 16, column i % 16
+  // (threads past it re-read the last entry; the stores below are
+  // unconditional, so no load waits under a test)
+  const int ri = min((int)threadIdx.x, nt * 16 - 1);
+  const T rv_ld = res[(int64_t)(t0 + ri / 16) * ldr + min(nb * 16 + ri % 16, N - 1)];
+  [[maybe_unused]] uint4 bpc;
+  [[maybe_unused]] int a_ok_ld = 0;
+  if constexpr (R > 0) {
+    constexpr int KB = R / 8;
+    const int bi = min((int)threadIdx.x, nt * 16 * KB - 1);
+    const int tl = bi / (16 * KB), col = (bi / KB) % 16, kb = bi % KB;
+    const int a_raw = lora.adapter >= 0 ? lora.adapter : ids[t0 + tl];
+    a_ok_ld = (a_raw >= 0) & (a_raw < n_adapters);
+    const int nc = min(nb * 16 + col, N - 1);
+    bpc = *lora_b_piece<T, R>(lora, a_ok_ld ? a_raw : 0, nc & ~7, nc & 7, kb);
+  }
+  u32x4 b[kUnroll], a[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int s = min(sb + u, ksteps - 1);
+    b[u] = __builtin_nontemporal_load(wb + s * kWave);
+    a[u] = *reinterpret_cast<const u32x4*>(xr + s * 32);
+  }
+  s_res[ri] = to_float<T>(rv_ld);
+  if constexpr (R > 0) {
+    constexpr int KB = R / 8;
+    const int bi = min((int)threadIdx.x, nt * 16 * KB - 1);
+    s_b[bi] = bpc;
+    if (bi % (16 * KB) == 0) s_ok[bi / (16 * KB)] = a_ok_ld;
+  }
+  if constexpr (R > 0) {
+#pragma unroll
+    for (int c = 0; c < YPT; ++c) {
+      const float m = yon[c] ? 1.f : 0.f;
+      float4 v = make_float4(yv[c].x * m, yv[c].y * m, yv[c].z * m, yv[c].w * m);
+      for (int off = 1; off < (1 << lgw); off <<= 1) {
+        v.x += __shfl_xor(v.x, off);
+        v.y += __shfl_xor(v.y, off);
+        v.z += __shfl_xor(v.z, off);
+        v.w += __shfl_xor(v.w, off);
+      }
+      const int f = threadIdx.x + c * kThreads;
+      const int p = f & (G - 1), tq = f >> lg;
+      if ((p & ((1 << lgw) - 1)) == 0 && tq < nt * Q) s_y[tq * slices + (p >> lgw)] = v;
+    }
+    __syncthreads();
+    // y of (token, 8 ranks): the slices in order, rounded to T
+    if ((int)threadIdx.x < nt * (R / 8)) {
+      const int g0 = threadIdx.x * 2;  // the two quads of ranks 8k ..
+      float4 lo = s_y[g0 * slices], hi = s_y[(g0 + 1) * slices];
+#pragma unroll 1
+      for (int sl = 1; sl < slices; ++sl) {
+        const float4 l2 = s_y[g0 * slices + sl], h2 = s_y[(g0 + 1) * slices + sl];
+        lo.x += l2.x; lo.y += l2.y; lo.z += l2.z; lo.w += l2.w;
+        hi.x += h2.x; hi.y += h2.y; hi.z += h2.z; hi.w += h2.w;
+      }
+      s_yr[threadIdx.x] = make_uint4(pack2<T>(lo.x, lo.y), pack2<T>(lo.z, lo.w), pack2<T>(hi.x, hi.y),
+                                     pack2<T>(hi.z, hi.w));
+    }
+  }
+
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int s = sb;
+  if (s + kUnroll <= se) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[u], b[u], acc);
+    s += kUnroll;
+  }
+  for (; s + kUnroll <= se; s += kUnroll) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) b[u] = __builtin_nontemporal_load(wb + (s + u) * kWave);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) a[u] = *reinterpret_cast<const u32x4*>(xr + (s + u) * 32);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[u], b[u], acc);
+  }
+  for (; s < se; ++s) {
+    const u32x4 bb = __builtin_nontemporal_load(wb + s * kWave);
+    const u32x4 aa = *reinterpret_cast<const u32x4*>(xr + s * 32);
+    acc = mfma32<T>(aa, bb, acc);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s_red[wave][((lane / 16) * 4 + i) * 16 + lr] = acc[i];
+  __syncthreads();
+  if (wave != 0) return;
+  const int n = nb * 16 + lr;
+#pragma unroll 1
+  for (int i = 0; i < 4; ++i) {
+    const int tl = (lane / 16) * 4 + i, tr = t0 + tl;
+    if (tl >= nt) break;  // uniform per 16-lane group
+    const int cell = tl * 16 + lr;
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) sum += s_red[w][cell];
+    float xa = through<T>(sum);
+    if constexpr (R > 0) {
+      constexpr int KB = R / 8;
+      float d = 0.f;
+#pragma unroll
+      for (int k = 0; k < KB; ++k) d = dot8<T>(s_yr[tl * KB + k], s_b[cell * KB + k], d);
+      d *= lora.scale;
+      xa = through<T>(xa + (s_ok[tl] ? d : -0.f));
+    }
+    if (n < N) {
+      res[(int64_t)tr * ldr + n] = from_float<T>(s_res[cell] + xa);
+      if (out != nullptr) out[(int64_t)tr * ldo + n] = from_float<T>(sum);
     }
   }
 }
@@ -314,4 +650,139 @@ extern "C" int pl_linear_shuffled_side(const void* x, int64_t ldx, int num_token
                        ldo, side_partials, ld_side, side_plane_stride, main_tiles, side_splits);
   PL_LAUNCH_CHECK("shuffled_gemm_kernel");
   return ok();
+}
+
+template <typename T, int PPT>
+static void launch_norm_gemm(const void* x, int64_t ldx, int num_tokens, int K, const void* nw, float eps,
+                             const void* Ws, int N, void* out, int64_t ldo, void* xn, int64_t ldxn, hipStream_t s) {
+  const int nt = std::min(num_tokens, 16);
+  const dim3 grid((N + 15) / 16, (num_tokens + 15) / 16);
+  hipLaunchKernelGGL((shuffled_gemm_norm_kernel<T, PPT>), grid, dim3(kThreads), norm_lds_bytes(nt, K), s,
+                     (const T*)x, ldx, num_tokens, K, (const T*)nw, eps, (const T*)Ws, N, (T*)out, ldo, (T*)xn, ldxn);
+}
+
+template <typename T>
+static int norm_gemm_t(const void* x, int64_t ldx, int num_tokens, int K, const void* nw, float eps, const void* Ws,
+                       int N, void* out, int64_t ldo, void* xn, int64_t ldxn, hipStream_t s) {
+  const int pieces = std::min(num_tokens, 16) * (K / 8);
+  if (pieces <= kThreads)
+    launch_norm_gemm<T, 1>(x, ldx, num_tokens, K, nw, eps, Ws, N, out, ldo, xn, ldxn, s);
+  else if (pieces <= 2 * kThreads)
+    launch_norm_gemm<T, 2>(x, ldx, num_tokens, K, nw, eps, Ws, N, out, ldo, xn, ldxn, s);
+  else
+    launch_norm_gemm<T, 4>(x, ldx, num_tokens, K, nw, eps, Ws, N, out, ldo, xn, ldxn, s);
+  PL_LAUNCH_CHECK("shuffled_gemm_norm_kernel");
+  return ok();
+}
+
+extern "C" int pl_linear_shuffled_norm(const void* x, int64_t ldx, int num_tokens, int in_features,
+                                       const void* norm_weight, float eps, const void* shuffled, int out_features,
+                                       void* out, int64_t ldo, void* x_norm_out, int64_t ld_norm_out, int dtype,
+                                       void* stream) {
+  if (num_tokens < 0 || num_tokens > kNormMaxTokens)
+    return fail(PL_ERR_INVALID, "num_tokens must be 0..%d (got %d)", kNormMaxTokens, num_tokens);
+  if (num_tokens == 0) return ok();
+  if (in_features <= 0 || in_features % 512 || in_features > 8192 || num_tokens * in_features > 32768)
+    return fail(PL_ERR_UNSUPPORTED,
+                "in_features must be a multiple of 512 up to 8192 with num_tokens * in_features <= 32768 "
+                "(got %d x %d)", num_tokens, in_features);
+  if (out_features <= 0) return fail(PL_ERR_INVALID, "out_features must be > 0");
+  if (!x || !norm_weight || !shuffled || !out) return fail(PL_ERR_INVALID, "null pointer argument");
+  if (ldx < in_features || ldx % 8 || (uintptr_t)x % 16 || (uintptr_t)shuffled % 16 || (uintptr_t)norm_weight % 16)
+    return fail(PL_ERR_INVALID, "x rows, the norm weight and the shuffled weight must be 16-byte aligned");
+  if (ldo < out_features) return fail(PL_ERR_INVALID, "ldo < out_features");
+  if (x_norm_out && (ld_norm_out < in_features || ld_norm_out % 8 || (uintptr_t)x_norm_out % 16))
+    return fail(PL_ERR_INVALID, "x_norm_out rows must be 16-byte aligned with ld_norm_out >= in_features");
+  if (dtype != PL_DTYPE_BF16 && dtype != PL_DTYPE_F16)
+    return fail(PL_ERR_UNSUPPORTED, "pl_linear_shuffled_norm dtype must be F16 or BF16 (got %d)", dtype);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == PL_DTYPE_BF16)
+    return norm_gemm_t<bf16_t>(x, ldx, num_tokens, in_features, norm_weight, eps, shuffled, out_features, out, ldo,
+                               x_norm_out, ld_norm_out, s);
+  return norm_gemm_t<f16_t>(x, ldx, num_tokens, in_features, norm_weight, eps, shuffled, out_features, out, ldo,
+                            x_norm_out, ld_norm_out, s);
+}
+
+template <typename T, int R, int YPT>
+static void launch_add_gemm(const void* x, int64_t ldx, int num_tokens, int K, const void* Ws, int N, void* res,
+                            int64_t ldr, const LoraUp& lu, const pl_lora_partials* yp, int lg, const int32_t* ids,
+                            int na, void* out, int64_t ldo, hipStream_t s) {
+  const dim3 grid((N + 15) / 16, (num_tokens + 15) / 16);
+  hipLaunchKernelGGL((shuffled_gemm_add_kernel<T, R, YPT>), grid, dim3(kThreads), 0, s, (const T*)x, ldx,
+                     num_tokens, K, (const T*)Ws, N, (T*)res, ldr, lu, yp ? yp->partials : nullptr,
+                     yp ? yp->ld : 0, yp ? yp->parts : 0, lg, ids, na, (T*)out, ldo);
+}
+
+template <typename T>
+static int add_gemm_t(const void* x, int64_t ldx, int num_tokens, int K, const void* Ws, int N, void* res,
+                      int64_t ldr, const LoraUp& lu, int rank, const pl_lora_partials* yp, int lg, int ypt,
+                      const int32_t* ids, int na, void* out, int64_t ldo, hipStream_t s) {
+  switch (rank) {
+    case 0: launch_add_gemm<T, 0, 1>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s); break;
+    case 8:
+      if (ypt <= 1) launch_add_gemm<T, 8, 1>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
+      else if (ypt <= 2) launch_add_gemm<T, 8, 2>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
+      else launch_add_gemm<T, 8, 4>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
+      break;
+    default:
+      if (ypt <= 1) launch_add_gemm<T, 16, 1>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
+      else if (ypt <= 2) launch_add_gemm<T, 16, 2>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
+      else launch_add_gemm<T, 16, 4>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
+      break;
+  }
+  PL_LAUNCH_CHECK("shuffled_gemm_add_kernel");
+  return ok();
+}
+
+extern "C" int pl_linear_shuffled_add(const void* x, int64_t ldx, int num_tokens, int in_features,
+                                      const void* shuffled, int out_features, void* residual, int64_t ldr,
+                                      const pl_lora_up* lora, const pl_lora_partials* lora_y,
+                                      const int32_t* adapter_ids, int num_adapters, void* out, int64_t ldo, int dtype,
+                                      void* stream) {
+  if (num_tokens < 0 || num_tokens > 16)
+    return fail(PL_ERR_INVALID, "num_tokens must be 0..16 (got %d)", num_tokens);
+  if (num_tokens == 0) return ok();
+  if (in_features <= 0 || in_features % 32 || out_features <= 0)
+    return fail(PL_ERR_INVALID, "in_features must be a positive multiple of 32 and out_features > 0");
+  if (!x || !shuffled || !residual) return fail(PL_ERR_INVALID, "null pointer argument");
+  if (ldx < in_features || ldx % 8 || (uintptr_t)x % 16 || (uintptr_t)shuffled % 16)
+    return fail(PL_ERR_INVALID, "x rows and the shuffled weight must be 16-byte aligned");
+  if (ldr < out_features || (out && ldo < out_features))
+    return fail(PL_ERR_INVALID, "residual / out rows shorter than out_features");
+  if (dtype != PL_DTYPE_BF16 && dtype != PL_DTYPE_F16)
+    return fail(PL_ERR_UNSUPPORTED, "pl_linear_shuffled_add dtype must be F16 or BF16 (got %d)", dtype);
+  if ((lora == nullptr) != (lora_y == nullptr))
+    return fail(PL_ERR_INVALID, "lora and lora_y are given together or not at all");
+  LoraUp lu{};
+  int rank = 0, G = 1, lg = 0, ypt = 1;
+  if (lora) {
+    if (const int st = lora_adapters_checked(lora, 1, adapter_ids, num_adapters, "linear_shuffled_add LoRA"))
+      return st;
+    if (!lora->B || (uintptr_t)lora->B % 16) return fail(PL_ERR_INVALID, "LoRA B must be non-null and 16-byte aligned");
+    if (lora->rank != 8 && lora->rank != 16)
+      return fail(PL_ERR_UNSUPPORTED, "pl_linear_shuffled_add: LoRA rank %d not built (8, 16)", lora->rank);
+    if (lora->out_features < out_features)
+      return fail(PL_ERR_INVALID, "LoRA B has %d output features, %d needed", lora->out_features, out_features);
+    if (lora->b_layout != PL_LORA_B_ROWS && (lora->b_layout != PL_LORA_B_CHUNK8 || lora->out_features % 8))
+      return fail(PL_ERR_INVALID, "unknown or unusable LoRA b_layout %d", lora->b_layout);
+    if (lora_y->rank != lora->rank) return fail(PL_ERR_INVALID, "lora_y rank %d != LoRA rank %d", lora_y->rank, lora->rank);
+    if (!lora_y->partials || (uintptr_t)lora_y->partials % 16 || lora_y->parts < 1 ||
+        lora_y->ld < (int64_t)lora_y->parts * lora_y->rank || lora_y->ld % 4)
+      return fail(PL_ERR_INVALID, "lora_y: 16-byte aligned partials, parts >= 1, ld >= parts * rank (a multiple of 4)");
+    rank = lora->rank;
+    while (G < lora_y->parts) G <<= 1, ++lg;
+    const int groups = std::min(num_tokens, 16) * (rank / 4);
+    const int64_t f = (int64_t)groups * G;
+    if (f > (int64_t)kAddMaxYPT * kThreads)
+      return fail(PL_ERR_UNSUPPORTED, "lora_y: %d parts for %d tokens exceed the %d partial sums a workgroup adds",
+                  lora_y->parts, num_tokens, kAddMaxYPT * kThreads * 4);
+    ypt = (int)((f + kThreads - 1) / kThreads);
+    lu = LoraUp{nullptr, 0, 0, lora->B, lora->out_features, lora->rank, lora->scale, lora->b_layout, lora->adapter};
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == PL_DTYPE_BF16)
+    return add_gemm_t<bf16_t>(x, ldx, num_tokens, in_features, shuffled, out_features, residual, ldr, lu, rank, lora_y,
+                              lg, ypt, adapter_ids, num_adapters, out, ldo, s);
+  return add_gemm_t<f16_t>(x, ldx, num_tokens, in_features, shuffled, out_features, residual, ldr, lu, rank, lora_y,
+                           lg, ypt, adapter_ids, num_adapters, out, ldo, s);
 }

@@ -39,7 +39,8 @@ import torch.nn.functional as F
 from . import _lib, fused_ops
 from .attention_backend import PagedDecodeAttention
 from .kv_pool import PagedKVPool, Request
-from .linear import ShuffledWeight, SplitOutput, linear_shuffled, linear_shuffled_side, linear_shuffled_split
+from .linear import (LoraPartials, ShuffledWeight, SplitOutput, linear_shuffled, linear_shuffled_add,
+                     linear_shuffled_norm, linear_shuffled_side, linear_shuffled_split, lora_a_rows)
 from .lora import lora_linear
 
 
@@ -459,6 +460,12 @@ DECODE_SIDE_SPLITS = {"o": 16, "down": 16}
 # (pl_decode_run_qkv) where it is built; False keeps the separate
 # head-norm/RoPE/append kernel (tests compare the two).
 FOLD_QKV_INTO_DECODE = True
+# Decode layers on the folded path fuse the post-attention add + RMSNorm away
+# where they can (see _fused_post_attention): o_proj's LoRA shrink in the
+# attention's merge, o_proj + its LoRA delta + the residual add in one GEMM,
+# the RMSNorm in the gate/up GEMM's prologue.  False keeps the add+RMSNorm
+# kernel (tests compare the two).
+FUSE_POST_ATTENTION_NORM = True
 # Optional observer of a layer's stages, called eagerly as ``STAGE_TRACE(name,
 # value)`` with each stage's stored output (tensors, split planes) in
 # dataflow order: "hidden_in" (the residual stream on entry), "hidden" (after
@@ -478,6 +485,16 @@ class SideOutput:
 
     def __init__(self, main: torch.Tensor, side: SplitOutput) -> None:
         self.main, self.side = main, side
+
+
+class PartialOutput:
+    """A projection whose output went straight into the residual stream
+    (linear_shuffled_add), traced as its base output ``main`` [T, out] (a
+    copy written for the trace) and the bound adapter's rank-space row as the
+    producer's partial sums ``partials`` (LoraPartials)."""
+
+    def __init__(self, main: torch.Tensor, partials: LoraPartials) -> None:
+        self.main, self.partials = main, partials
 
 
 def _project(x: torch.Tensor, lw: LayerWeights, name: str) -> "torch.Tensor | SplitOutput | SideOutput":
@@ -569,7 +586,20 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
         trace("x", x)
         trace("qkv", qkv)
     lora_qkv = (lw.up("q", qkv, scale, a), lw.up("k", qkv, scale, a), lw.up("v", qkv, scale, a))
-    if qkv_attend is not None and not isinstance(qkv, SplitOutput):
+    fused = qkv_attend is not None and not isinstance(qkv, SplitOutput) and _fused_post_attention(cfg, lw, x)
+    if fused:
+        T, r = x.shape[0], cfg.lora_rank
+        parts = LoraPartials(torch.empty((T, qkv_attend.oshrink_parts(T), r), dtype=torch.float32, device=x.device))
+        o_rows = lora_a_rows(lw.shuffled["o"], lw.y_offset["o"], r, a)
+        attn = qkv_attend(_cols(qkv, qd + 2 * kd), lora_qkv, (o_rows, parts, lw.n_adapters)).view(T, qd)
+        o_main = torch.empty_like(hidden) if trace is not None else None
+        # B row-major: each workgroup reads the 16 consecutive B rows of its columns
+        lo = fused_ops.LoraUp(None, 0, lw.lora["o"][1], scale, a)
+        linear_shuffled_add(attn, lw.shuffled["o"], h, hidden, lo, parts, ids, out=o_main)
+        o = PartialOutput(o_main, parts) if trace is not None else None
+        x2 = torch.empty_like(x) if trace is not None else None
+        gu = linear_shuffled_norm(hidden, lw.post_norm, cfg.rms_eps, lw.shuffled["gate_up"], x2)
+    elif qkv_attend is not None and not isinstance(qkv, SplitOutput):
         attn = qkv_attend(_cols(qkv, qd + 2 * kd), lora_qkv).view(qkv.shape[0], qd)
     else:
         q = fused_ops.qk_norm_rope_append(
@@ -578,10 +608,11 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
             num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=page_size,
             rope_theta=cfg.rope_theta, eps=cfg.rms_eps, lora=lora_qkv, adapter_ids=ids)
         attn = attend(q).view(q.shape[0], qd)
-    o = _project(attn, lw, "o")
-    x2 = fused_ops.add_rmsnorm(hidden, _cols(o, h), lw.post_norm, cfg.rms_eps, lora=lw.up("o", o, scale, a),
-                               adapter_ids=ids)
-    gu = _project(x2, lw, "gate_up")
+    if not fused:
+        o = _project(attn, lw, "o")
+        x2 = fused_ops.add_rmsnorm(hidden, _cols(o, h), lw.post_norm, cfg.rms_eps, lora=lw.up("o", o, scale, a),
+                                   adapter_ids=ids)
+        gu = _project(x2, lw, "gate_up")
     act = fused_ops.silu_mul(gu[:, : 2 * I], lora=(lw.up("gate", gu, scale, a), lw.up("up", gu, scale, a)),
                              adapter_ids=ids)
     d = _project(act, lw, "down")
@@ -590,6 +621,16 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
                             ("act", act), ("down", d)):
             trace(name, value)
     return d, lw.up("down", d, scale, a)
+
+
+def _fused_post_attention(cfg: DecoderConfig, lw: LayerWeights, x: torch.Tensor) -> bool:
+    """Whether a decode layer runs its post-attention add + RMSNorm fused
+    away: the decode-sized shuffled GEMMs for o_proj and gate/up, rank 8 or
+    16, at most 8 tokens (the RMSNorm prologue's limit) and a hidden size
+    the prologue takes."""
+    return (FUSE_POST_ATTENTION_NORM and x.shape[0] <= 8 and x.shape[0] * cfg.hidden <= 32768
+            and cfg.hidden % 512 == 0 and cfg.hidden <= 8192 and cfg.lora_rank in (8, 16)
+            and "o" in lw.shuffled and "gate_up" in lw.shuffled and lw.y_offset["o"] == cfg.hidden)
 
 
 def _final_norm(weights: "DecoderWeights", hidden: torch.Tensor, pending, ids: torch.Tensor) -> torch.Tensor:
@@ -617,14 +658,16 @@ def decode_layer_static(
         backend.run_decode_into(q, layer_cache, out)
         return out
 
-    def qkv_attend(qkv, lora):
+    def qkv_attend(qkv, lora, o_shrink=None):
         out = torch.empty((qkv.shape[0], cfg.num_qo_heads, cfg.head_dim), dtype=qkv.dtype, device=qkv.device)
         backend.run_decode_qkv_into(
             qkv, layer_cache, out, q_norm_weight=lw.q_norm if cfg.qk_norm else None,
             k_norm_weight=lw.k_norm if cfg.qk_norm else None, rope_cos_sin=ctx.rope_cos_sin,
             page_id=ctx.page_id, page_offset=ctx.page_offset, eps=cfg.rms_eps, lora=lora,
-            adapter_ids=ctx.adapter_ids)
+            adapter_ids=ctx.adapter_ids, o_shrink=o_shrink)
         return out
+
+    qkv_attend.oshrink_parts = backend.oshrink_parts
 
     return _layer(cfg, lw, lora_scale, hidden, pending, ctx.adapter_ids, ctx.positions, ctx.page_id,
                   ctx.page_offset, layer_cache, backend.page_size, attend, ctx.uniform_adapter,

@@ -9,6 +9,8 @@ replaces the base ``F.linear`` of the reference's projections
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -194,3 +196,110 @@ def linear_shuffled_side(x: torch.Tensor, weight: ShuffledWeight, main_features:
                                            _lib.stream_handle(x.device)),
                "pl_linear_shuffled_side")
     return out, SplitOutput(partials, side, x.dtype)
+
+
+class LoraPartials:
+    """fp32 partial sums ``[T, parts, rank]`` of a LoRA module's rank-space
+    row y = x . A_a^T, for each token's own adapter a, written by the kernel
+    that produces x (``pl_lora_partials``): y[t] is the sum over the parts,
+    which the consuming kernel adds in a fixed order."""
+
+    def __init__(self, partials: torch.Tensor) -> None:
+        if partials.dim() != 3 or partials.dtype != torch.float32 or not partials.is_contiguous():
+            raise ValueError("partials must be a contiguous fp32 [T, parts, rank] tensor")
+        self.partials = partials
+
+    @property
+    def rank(self) -> int:
+        return self.partials.shape[2]
+
+    @property
+    def parts(self) -> int:
+        return self.partials.shape[1]
+
+    def struct(self) -> "_lib.LoraPartials":
+        p = self.partials
+        return _lib.LoraPartials(p.data_ptr(), p.stride(0), p.shape[1], p.shape[2])
+
+    def sum(self) -> torch.Tensor:
+        """y [T, rank] in float64 (for checks)."""
+        return self.partials.double().sum(dim=1)
+
+
+def lora_a_rows(weight: ShuffledWeight, a_row0: int, rank: int, adapter: int = -1) -> "_lib.LoraARows":
+    """``pl_lora_a_rows`` of a module whose adapters' A rows sit under W in
+    the shuffled ``weight``: adapter a's rank r is row ``a_row0 + a*rank + r``."""
+    if a_row0 < 0 or a_row0 + rank > weight.out_features:
+        raise ValueError(f"A rows {a_row0}.. outside the weight's {weight.out_features} rows")
+    return _lib.LoraARows(weight.data.data_ptr(), weight.in_features, weight.out_features, int(a_row0), int(rank),
+                          int(adapter))
+
+
+def linear_shuffled_norm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weight: ShuffledWeight,
+                         x_norm_out: torch.Tensor | None = None) -> torch.Tensor:
+    """``RMSNorm(x) . W^T`` in one launch (``pl_linear_shuffled_norm``): the
+    normalized rows never go through memory (``x_norm_out``, when given,
+    receives them too)."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] != weight.in_features or x.dtype != weight.dtype:
+        raise ValueError(f"x must be [T, {weight.in_features}] of {weight.dtype} with unit column stride")
+    if norm_weight.numel() != weight.in_features or norm_weight.dtype != x.dtype or not norm_weight.is_contiguous():
+        raise ValueError("norm_weight must be a contiguous [in_features] tensor of x's dtype")
+    T, N = x.shape[0], weight.out_features
+    out = torch.empty((T, N), dtype=x.dtype, device=x.device)
+    if x_norm_out is not None and (tuple(x_norm_out.shape) != tuple(x.shape) or x_norm_out.stride(1) != 1
+                                   or x_norm_out.dtype != x.dtype):
+        raise ValueError("x_norm_out must be shaped like x with unit column stride")
+    lib = _lib.load()
+    _lib.check(lib.pl_linear_shuffled_norm(x.data_ptr(), x.stride(0), T, weight.in_features, norm_weight.data_ptr(),
+                                           float(eps), weight.data.data_ptr(), N, out.data_ptr(), out.stride(0),
+                                           x_norm_out.data_ptr() if x_norm_out is not None else None,
+                                           x_norm_out.stride(0) if x_norm_out is not None else 0,
+                                           _lib.dtype_code(x.dtype), _lib.stream_handle(x.device)),
+               "pl_linear_shuffled_norm")
+    return out
+
+
+def linear_shuffled_add(x: torch.Tensor, weight: ShuffledWeight, main_features: int, residual: torch.Tensor,
+                        lora=None, partials: LoraPartials | None = None, adapter_ids: torch.Tensor | None = None,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """``residual += round(round(x . W^T) + delta)`` over the first
+    ``main_features`` rows of ``weight`` (``pl_linear_shuffled_add``), with
+    the LoRA up-projection delta of ``lora`` (a ``fused_ops.LoraUp``; its
+    ``y`` is not read) on y from ``partials``.  ``out`` (optional) receives
+    round(x . W^T).  Returns ``residual``."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] != weight.in_features or x.dtype != weight.dtype:
+        raise ValueError(f"x must be [T, {weight.in_features}] of {weight.dtype} with unit column stride")
+    T = x.shape[0]
+    if not 0 < main_features <= weight.out_features:
+        raise ValueError("main_features must be in 1..out_features")
+    if tuple(residual.shape) != (T, main_features) or residual.stride(1) != 1 or residual.dtype != x.dtype:
+        raise ValueError(f"residual must be [{T}, {main_features}] of x's dtype with unit column stride")
+    if (lora is None) != (partials is None):
+        raise ValueError("lora and partials are given together")
+    lu = yp = None
+    ids, n = None, 1
+    if lora is not None:
+        nad, outf, r, layout = lora._b_shape()
+        if not lora.B.is_contiguous() or lora.B.dtype != x.dtype:
+            raise ValueError("LoRA B must be contiguous and of x's dtype")
+        if partials.partials.shape[0] != T:
+            raise ValueError("partials must have one row per token")
+        if lora.adapter < 0 and (adapter_ids is None or adapter_ids.dtype != torch.int32 or adapter_ids.numel() != T):
+            raise ValueError("per-token adapters need int32 adapter_ids [T]")
+        lu = _lib.LoraUp(None, 0, 0, lora.B.data_ptr(), int(outf), int(r), float(lora.scale), int(layout),
+                         int(lora.adapter))
+        yp = partials.struct()
+        n = nad
+        ids = adapter_ids.data_ptr() if adapter_ids is not None else None
+    if out is not None and (tuple(out.shape) != (T, main_features) or out.stride(1) != 1 or out.dtype != x.dtype):
+        raise ValueError("out must be shaped like residual")
+    lib = _lib.load()
+    _lib.check(lib.pl_linear_shuffled_add(x.data_ptr(), x.stride(0), T, weight.in_features, weight.data.data_ptr(),
+                                          int(main_features), residual.data_ptr(), residual.stride(0),
+                                          ctypes.byref(lu) if lu is not None else None,
+                                          ctypes.byref(yp) if yp is not None else None, ids, n,
+                                          out.data_ptr() if out is not None else None,
+                                          out.stride(0) if out is not None else 0,
+                                          _lib.dtype_code(x.dtype), _lib.stream_handle(x.device)),
+               "pl_linear_shuffled_add")
+    return residual

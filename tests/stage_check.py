@@ -29,7 +29,7 @@ from oracle import fused as of
 from oracle import lora as ol
 from oracle import paged_decode as opd
 from pagelora_amd import decoder
-from pagelora_amd.decoder import DecodeContext, SideOutput, decode_step_static
+from pagelora_amd.decoder import DecodeContext, PartialOutput, SideOutput, decode_step_static
 from pagelora_amd.generation import BatchGenerator
 from pagelora_amd.linear import SplitOutput
 
@@ -68,6 +68,9 @@ class Recorder:
             return
         if isinstance(value, SideOutput):
             value = (value.main.clone(), value.side.sum())  # planes summed in order and rounded, as consumed
+        elif isinstance(value, PartialOutput):
+            # the bound adapter's rank-space row, from the producer's partial sums
+            value = {"main": value.main.clone(), "y": value.partials.sum().cpu().numpy()}
         elif isinstance(value, SplitOutput):
             value = value.sum()
         else:
@@ -165,7 +168,9 @@ def stage_check(w, pool, reqs, first, dev, slot=0, adapter=None):
     # o_proj: base rows and the LoRA A rows' intermediate (side planes or columns)
     attn2 = attn.reshape(B, qd)
     o_out = L0["o"]
-    if isinstance(o_out, tuple):
+    if isinstance(o_out, dict):
+        o_main, o_y = _f(o_out["main"]), o_out["y"]
+    elif isinstance(o_out, tuple):
         o_main, o_y = _f(o_out[0]), _f(o_out[1])[:, slot * r: (slot + 1) * r]
     else:
         o_main, o_y = _f(o_out)[:, : cfg.hidden], _f(o_out)[:, ycols("o")]

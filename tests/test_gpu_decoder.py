@@ -319,6 +319,27 @@ def test_folded_qkv_matches_separate_epilogue(gpu_device, monkeypatch):
     assert torch.allclose(cf.float(), cs.float(), atol=0.05, rtol=0.02)
 
 
+def test_fused_post_attention_matches_add_rmsnorm(gpu_device, monkeypatch):
+    """The post-attention add + RMSNorm fused away (o_proj's shrink in the
+    merge, o_proj + delta + residual add in one GEMM, the norm in the
+    gate/up GEMM's prologue) against the add+RMSNorm kernel between separate
+    projections: the same logits to within the roundings that move (y's sum
+    order, the norm's sum of squares), the same greedy tokens, and the
+    appended K/V of layer 0 bit for bit (computed before the fused part)."""
+    from pagelora_amd import decoder
+    out = []
+    for fuse in (True, False):
+        monkeypatch.setattr(decoder, "FUSE_POST_ATTENTION_NORM", fuse)
+        w, pool, reqs, first, _ = _setup128(gpu_device)
+        out.append(_eager_step(w, pool, reqs, first, [0, 1, 1], gpu_device) + (pool.cache.clone(),))
+    (lf, tf, cf), (ls, ts, cs) = out
+    torch.cuda.synchronize()
+    assert torch.allclose(lf, ls, atol=0.05, rtol=0.01), (lf - ls).abs().max()
+    _assert_same_greedy(tf, ls, lf)
+    assert torch.equal(cf[0], cs[0])
+    assert torch.allclose(cf.float(), cs.float(), atol=0.05, rtol=0.02)
+
+
 def test_folded_qkv_graph_replay_matches_eager(gpu_device):
     runs = []
     for use_graph in (False, True):
