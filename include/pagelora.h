@@ -801,18 +801,24 @@ typedef struct {
 
 /*
  * out = RMSNorm(x) . W^T on a shuffled weight for decode batches: the norm
- * x * rsqrt(mean(x^2) + eps) * norm_weight, rounded to dtype (the arithmetic
- * of pl_rmsnorm), is formed by every workgroup in LDS for its tokens, so no
- * normalized row goes through memory.  x_norm_out (nullable, row stride
- * ld_norm_out) also receives the normalized rows.  num_tokens <= 8,
- * in_features a multiple of 512 up to 8192 with num_tokens * in_features <=
- * 32768.  No counterpart in the reference: it computes the input RMSNorm
- * (model/flashinfer/norm.py:15-24) and the projection that reads it
+ * (x * rsqrt(mean(x^2) + eps)) * norm_weight, rounded to dtype (the
+ * arithmetic of pl_rmsnorm), is formed inside the GEMM, so no normalized row
+ * goes through memory.  The sum of squares of row t comes from sq_partials
+ * when given -- sq_parts pieces sq_partials[t * ld_sq + j] added in order j =
+ * 0, 1, .., as pl_linear_shuffled_add writes them for its output -- and is
+ * otherwise formed by every workgroup from the rows (staged in LDS).
+ * x_norm_out (nullable, row stride ld_norm_out) also receives the normalized
+ * rows.  With sq_partials: num_tokens <= 16, in_features a multiple of 32 up
+ * to 8192, sq_parts <= 1024 (ld_sq a multiple of 4); without: num_tokens <=
+ * 8, in_features a multiple of 512 up to 8192 with num_tokens * in_features
+ * <= 32768.  No counterpart in the reference: it computes the RMSNorm
+ * (model/flashinfer/norm.py:15-57) and the projection that reads it
  * (packed_ops.py:143, 179) in one launch.
  */
 int pl_linear_shuffled_norm(const void* x, int64_t ldx, int num_tokens,
                             int in_features, const void* norm_weight,
-                            float eps, const void* shuffled,
+                            float eps, const float* sq_partials, int64_t ld_sq,
+                            int sq_parts, const void* shuffled,
                             int out_features, void* out, int64_t ldo,
                             void* x_norm_out, int64_t ld_norm_out, int dtype,
                             void* stream);
@@ -826,8 +832,12 @@ int pl_linear_shuffled_norm(const void* x, int64_t ldx, int num_tokens,
  * output followed by `hidden + out`.  lora / lora_y are both NULL (no
  * delta) or both given (lora->y is ignored; rank 8 or 16); adapter ids
  * as in pl_add_rmsnorm_lora.  out (nullable) receives round(x . W^T).
- * num_tokens <= 16.  No counterpart in the reference: it computes
- * project_linear with LoRALinear.forward's delta (packed_ops.py:251-265,
+ * sq_out (nullable) receives, for the next RMSNorm (pl_linear_shuffled_norm's
+ * sq_partials), the fp32 sum of squares of the new residual over each block
+ * of 16 columns: sq_out[t * ld_sq + j] for columns 16j .. 16j+15 below
+ * out_features, ld_sq >= ceil(out_features / 16).  num_tokens <= 16.  No
+ * counterpart in the reference: it computes project_linear with
+ * LoRALinear.forward's delta (packed_ops.py:251-265,
  * multilora/linear.py:226-231) and the residual add that precedes the next
  * RMSNorm (norm.py:27-57) in one launch.
  */
@@ -837,7 +847,8 @@ int pl_linear_shuffled_add(const void* x, int64_t ldx, int num_tokens,
                            const pl_lora_up* lora,
                            const pl_lora_partials* lora_y,
                            const int32_t* adapter_ids, int num_adapters,
-                           void* out, int64_t ldo, int dtype, void* stream);
+                           void* out, int64_t ldo, float* sq_out,
+                           int64_t ld_sq, int dtype, void* stream);
 
 /*
  * pl_decode_run_qkv whose merge also forms o_proj's LoRA shrink: the

@@ -310,10 +310,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pl_linear_shuffled_split": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _i64, _i64, _i32, _vp]),
     "pl_linear_shuffled_side": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _i64, _i32, _vp, _i64, _i64,
                                        _i32, _vp]),
-    "pl_linear_shuffled_norm": (_i32, [_vp, _i64, _i32, _i32, _vp, _f32, _vp, _i32, _vp, _i64, _vp, _i64, _i32,
-                                       _vp]),
+    "pl_linear_shuffled_norm": (_i32, [_vp, _i64, _i32, _i32, _vp, _f32, _vp, _i64, _i32, _vp, _i32, _vp, _i64,
+                                       _vp, _i64, _i32, _vp]),
     "pl_linear_shuffled_add": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _vp, _i64, ctypes.POINTER(LoraUp),
-                                      ctypes.POINTER(LoraPartials), _vp, _i32, _vp, _i64, _i32, _vp]),
+                                      ctypes.POINTER(LoraPartials), _vp, _i32, _vp, _i64, _vp, _i64, _i32, _vp]),
     "pl_lora_workspace_size": (_sz, [_i32, _i32, ctypes.POINTER(LoraModule), _i32]),
     "pl_lora_delta": (
         _i32,

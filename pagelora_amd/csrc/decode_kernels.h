@@ -1379,8 +1379,11 @@ __global__ __launch_bounds__(MT) void merge_kernel(
   if (pair >= batch * num_qo_heads) return;
   const int b = pair / num_qo_heads;
   const int hq = pair - b * num_qo_heads;
-  // the A pieces first: they need only the row's adapter
+  // the A pieces' addresses (they need only the row's adapter); the loads
+  // go out after the first batch of partials, so the fold does not wait
+  // for them (loads complete in order)
   [[maybe_unused]] uint4 ap[PPT];
+  [[maybe_unused]] const T* ap_src[PPT];
   if constexpr (OR > 0) {
     const int a_raw = os.adapter >= 0 ? os.adapter : os.ids[b];
     const int aa = (a_raw >= 0 && a_raw < os.n_adapters) ? a_raw : 0;
@@ -1390,8 +1393,7 @@ __global__ __launch_bounds__(MT) void merge_kernel(
       const int r = i / LPT, c = i - r * LPT;
       const int64_t n = (int64_t)os.a_row0 + (int64_t)aa * OR + r;
       const int k = hq * D + (ds * LPT + c) * 8;
-      const int64_t e = (((n / 16) * os.ksteps + k / 32) * 64 + ((k % 32) / 8) * 16 + n % 16) * 8;
-      ap[j] = *reinterpret_cast<const uint4*>((const T*)os.A + e);
+      ap_src[j] = (const T*)os.A + (((n / 16) * os.ksteps + k / 32) * 64 + ((k % 32) / 8) * 16 + n % 16) * 8;
     }
   }
   int first, n;
@@ -1426,6 +1428,12 @@ __global__ __launch_bounds__(MT) void merge_kernel(
         lv[k] = part_lse[slot];
         oa[k] = *reinterpret_cast<const float4*>(part_o + slot * D + dcol * 8);
         ob[k] = *reinterpret_cast<const float4*>(part_o + slot * D + dcol * 8 + 4);
+      }
+    }
+    if constexpr (OR > 0) {
+      if (c0 == 0) {
+#pragma unroll
+        for (int j = 0; j < PPT; ++j) ap[j] = *reinterpret_cast<const uint4*>(ap_src[j]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);  // the whole batch in flight before the first fold

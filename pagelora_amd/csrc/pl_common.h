@@ -150,6 +150,17 @@ template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
+// pack2 through the hardware round-to-nearest-even conversion
+// (v_cvt_pk_bf16_f32 for bf16): the same bits as pack2 for every non-NaN
+// value in one instruction per pair; a NaN stays a NaN (its payload bits may
+// differ).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <typename T> __device__ __forceinline__ uint32_t pack2_hw(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2_hw<bf16_t>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+template <> __device__ __forceinline__ uint32_t pack2_hw<f16_t>(float a, float b) { return pack2<f16_t>(a, b); }
+
 // ------------------------------------------------------- lane reductions ---
 // All-reduce across the 16 lanes of a DPP row with row rotations; every lane
 // of the row ends with the full result.

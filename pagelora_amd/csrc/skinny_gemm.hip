@@ -24,6 +24,7 @@
 // / project_linear (model/flashinfer/packed_ops.py:143, 179, 251-265) and
 // LoRALinear.forward (multilora/linear.py:226-231) at decode batch sizes.
 #include <algorithm>
+#include <type_traits>
 
 #include "lora_up.h"
 #include "pl_common.h"
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_norm_kernel(
         float f0, f1, w0, w1;
         unpack2<T>(h2, f0, f1);
         unpack2<T>(w2, w0, w1);
-        return pack2<T>(f0 * rstd * w0, f1 * rstd * w1);
+        return pack2_hw<T>(f0 * rstd * w0, f1 * rstd * w1);
       };
       const uint4 o = make_uint4(norm2(hw.x, ww.x), norm2(hw.y, ww.y), norm2(hw.z, ww.z), norm2(hw.w, ww.w));
       *reinterpret_cast<uint4*>(xs + tt * Kp + cc * 8) = o;
@@ -332,6 +333,132 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_norm_kernel(
   }
 }
 
+// ------------------------------------ norm from the producer's squares ---
+// out = RMSNorm(x) . W^T where the kernel that wrote x also wrote its sums
+// of squares in pieces, sq[t * ldsq + j] for j < parts
+// (pl_linear_shuffled_add's sq_out): wave t of the workgroup adds token t's
+// pieces in a fixed order (QPL float4 per lane, then the wave's DPP tree),
+// so no row goes through LDS and one barrier separates the loads from the
+// main loop.  The MFMA A operands are the rows read from global memory as
+// in shuffled_gemm_kernel, normalized in registers as rmsnorm_kernel forms
+// them, (x * rstd) * w rounded to T, with w from an LDS copy.
+template <typename T, int QPL, bool XN>
+__global__ __launch_bounds__(kThreads) void shuffled_gemm_normsq_kernel(
+    const T* __restrict__ x, int64_t ldx, int tokens, int K, const T* __restrict__ nw, float eps,
+    const float* __restrict__ sq, int64_t ldsq, int parts, const T* __restrict__ Ws, int N, T* __restrict__ out,
+    int64_t ldo, T* __restrict__ xn_out, int64_t ldxn) {
+  __shared__ float s_red[kWaves][256];
+  __shared__ uint4 s_w[8192 / 8];  // the norm weight, K / 8 pieces (K <= 8192)
+  __shared__ float s_rstd[16];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lr = lane % 16, kq = (lane / 16) * 8;
+  const int nb = blockIdx.x, t0 = blockIdx.y * 16;
+  const int nt = min(16, tokens - t0);
+  const int ksteps = K / 32;
+  const int per = (ksteps + kWaves - 1) / kWaves;
+  const int sb = min(ksteps, wave * per), se = min(ksteps, sb + per);
+  const u32x4* wb = reinterpret_cast<const u32x4*>(Ws + (int64_t)nb * ksteps * kBlockElems) + lane;
+  const int tok = lr < nt ? lr : 0;
+  const T* xr = x + (int64_t)(t0 + tok) * ldx + kq;
+
+  // the loads the barrier waits for first (they complete in order): wave w <
+  // nt takes token w's pieces (pieces past `parts` re-read piece 0 and are
+  // masked), every thread one piece of the norm weight (threads past K / 8
+  // re-read piece 0 and rewrite it with its own value)
+  const int tw = wave < nt ? wave : 0;
+  float4 qv[QPL];
+#pragma unroll
+  for (int c = 0; c < QPL; ++c) {
+    const int j = (lane + c * kWave) * 4;
+    qv[c] = *reinterpret_cast<const float4*>(sq + (int64_t)(t0 + tw) * ldsq + (j < parts ? j : 0));
+  }
+  const int wc = (int)threadIdx.x < K / 8 ? (int)threadIdx.x : 0;
+  const uint4 wv = *reinterpret_cast<const uint4*>(nw + wc * 8);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 b[kUnroll], a[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int s = min(sb + u, ksteps - 1);
+    b[u] = __builtin_nontemporal_load(wb + s * kWave);
+    a[u] = *reinterpret_cast<const u32x4*>(xr + s * 32);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  s_w[wc] = wv;
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < QPL; ++c) {
+    const int j = (lane + c * kWave) * 4;
+    ss += (j + 0 < parts ? qv[c].x : 0.f) + (j + 1 < parts ? qv[c].y : 0.f) +
+          (j + 2 < parts ? qv[c].z : 0.f) + (j + 3 < parts ? qv[c].w : 0.f);
+  }
+  ss = wave_sum(ss);
+  if (lane == 0 && wave < nt) s_rstd[wave] = rsqrtf(ss / (float)K + eps);
+  __syncthreads();
+  const float rstd = s_rstd[tok];
+  [[maybe_unused]] const bool xn_store = XN && blockIdx.x == 0 && lr < nt;
+  // x -> (x * rstd) * w rounded to T, in place
+  auto normalize = [&](u32x4& v, int s) {
+    const uint4 w8 = s_w[(s * 32 + kq) / 8];
+    auto n2 = [&](uint32_t h2, uint32_t w2) {
+      float f0, f1, w0, w1;
+      unpack2<T>(h2, f0, f1);
+      unpack2<T>(w2, w0, w1);
+      return pack2_hw<T>(f0 * rstd * w0, f1 * rstd * w1);
+    };
+    v = u32x4{n2(v.x, w8.x), n2(v.y, w8.y), n2(v.z, w8.z), n2(v.w, w8.w)};
+    if constexpr (XN)
+      if (xn_store) *reinterpret_cast<u32x4*>(xn_out + (int64_t)(t0 + lr) * ldxn + s * 32 + kq) = v;
+  };
+
+  // (one operand at a time: the scheduler would otherwise normalize the
+  // batch's four operands together and raise the kernel's register count)
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int s = sb;
+  if (s + kUnroll <= se) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      normalize(a[u], s + u);
+      acc = mfma32<T>(a[u], b[u], acc);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    s += kUnroll;
+  }
+  for (; s + kUnroll <= se; s += kUnroll) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) b[u] = __builtin_nontemporal_load(wb + (s + u) * kWave);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) a[u] = *reinterpret_cast<const u32x4*>(xr + (s + u) * 32);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      normalize(a[u], s + u);
+      acc = mfma32<T>(a[u], b[u], acc);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  for (; s < se; ++s) {
+    const u32x4 bb = __builtin_nontemporal_load(wb + s * kWave);
+    u32x4 aa = *reinterpret_cast<const u32x4*>(xr + s * 32);
+    normalize(aa, s);
+    acc = mfma32<T>(aa, bb, acc);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s_red[wave][((lane / 16) * 4 + i) * 16 + lr] = acc[i];
+  __syncthreads();
+  if (wave == 0) {
+    const int n = nb * 16 + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cell = ((lane / 16) * 4 + i) * 16 + lr;
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) sum += s_red[w][cell];
+      const int tr = t0 + (lane / 16) * 4 + i;
+      if (n < N && tr < tokens) out[(int64_t)tr * ldo + n] = from_float<T>(sum);
+    }
+  }
+}
+
 // --------------------------------------------- residual + LoRA epilogue ---
 // residual += round(round(x . W^T) + scale * y . B_a^T) for the first N
 // rows of the shuffled weight.  y comes as fp32 partial sums written by the
@@ -347,7 +474,8 @@ template <typename T, int R, int YPT>
 __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
     const T* __restrict__ x, int64_t ldx, int tokens, int K, const T* __restrict__ Ws, int N,
     T* __restrict__ res, int64_t ldr, LoraUp lora, const float* __restrict__ yp, int64_t ldyp, int parts, int lg,
-    const int32_t* __restrict__ ids, int n_adapters, T* __restrict__ out, int64_t ldo) {
+    const int32_t* __restrict__ ids, int n_adapters, T* __restrict__ out, int64_t ldo, float* __restrict__ sq_out,
+    int64_t ldsq) {
   constexpr int Q = R > 0 ? R / 4 : 1;
   __shared__ float s_red[kWaves][256];
   // (t, q) group x slice: at most YPT * kThreads / kWave entries (G <= 64:
@@ -435,20 +563,6 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
       const int p = f & (G - 1), tq = f >> lg;
       if ((p & ((1 << lgw) - 1)) == 0 && tq < nt * Q) s_y[tq * slices + (p >> lgw)] = v;
     }
-    __syncthreads();
-    // y of (token, 8 ranks): the slices in order, rounded to T
-    if ((int)threadIdx.x < nt * (R / 8)) {
-      const int g0 = threadIdx.x * 2;  // the two quads of ranks 8k ..
-      float4 lo = s_y[g0 * slices], hi = s_y[(g0 + 1) * slices];
-#pragma unroll 1
-      for (int sl = 1; sl < slices; ++sl) {
-        const float4 l2 = s_y[g0 * slices + sl], h2 = s_y[(g0 + 1) * slices + sl];
-        lo.x += l2.x; lo.y += l2.y; lo.z += l2.z; lo.w += l2.w;
-        hi.x += h2.x; hi.y += h2.y; hi.z += h2.z; hi.w += h2.w;
-      }
-      s_yr[threadIdx.x] = make_uint4(pack2<T>(lo.x, lo.y), pack2<T>(lo.z, lo.w), pack2<T>(hi.x, hi.y),
-                                     pack2<T>(hi.z, hi.w));
-    }
   }
 
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -476,6 +590,21 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
   for (int i = 0; i < 4; ++i) s_red[wave][((lane / 16) * 4 + i) * 16 + lr] = acc[i];
   __syncthreads();
   if (wave != 0) return;
+  if constexpr (R > 0) {
+    // y of (token, 8 ranks): the wave slices in order, rounded to T (the
+    // lanes' LDS writes and the reads below are one wave's, in order)
+    if (lane < nt * (R / 8)) {
+      const int g0 = lane * 2;  // the two quads of ranks 8k ..
+      float4 lo = s_y[g0 * slices], hi = s_y[(g0 + 1) * slices];
+#pragma unroll 1
+      for (int sl = 1; sl < slices; ++sl) {
+        const float4 l2 = s_y[g0 * slices + sl], h2 = s_y[(g0 + 1) * slices + sl];
+        lo.x += l2.x; lo.y += l2.y; lo.z += l2.z; lo.w += l2.w;
+        hi.x += h2.x; hi.y += h2.y; hi.z += h2.z; hi.w += h2.w;
+      }
+      s_yr[lane] = make_uint4(pack2<T>(lo.x, lo.y), pack2<T>(lo.z, lo.w), pack2<T>(hi.x, hi.y), pack2<T>(hi.z, hi.w));
+    }
+  }
   const int n = nb * 16 + lr;
 #pragma unroll 1
   for (int i = 0; i < 4; ++i) {
@@ -494,9 +623,17 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
       d *= lora.scale;
       xa = through<T>(xa + (s_ok[tl] ? d : -0.f));
     }
+    const T v = from_float<T>(s_res[cell] + xa);
     if (n < N) {
-      res[(int64_t)tr * ldr + n] = from_float<T>(s_res[cell] + xa);
+      res[(int64_t)tr * ldr + n] = v;
       if (out != nullptr) out[(int64_t)tr * ldo + n] = from_float<T>(sum);
+    }
+    if (sq_out != nullptr) {
+      // the squares of the stored residual over the block's columns (the 16
+      // lanes of this token's group), for the next RMSNorm
+      const float vf = n < N ? to_float<T>(v) : 0.f;
+      const float q = row16_sum(vf * vf);
+      if (lr == 0) sq_out[(int64_t)tr * ldsq + nb] = q;
     }
   }
 }
@@ -675,17 +812,45 @@ static int norm_gemm_t(const void* x, int64_t ldx, int num_tokens, int K, const 
   return ok();
 }
 
+template <typename T>
+static int normsq_gemm_t(const void* x, int64_t ldx, int num_tokens, int K, const void* nw, float eps,
+                         const float* sq, int64_t ldsq, int parts, const void* Ws, int N, void* out, int64_t ldo,
+                         void* xn, int64_t ldxn, hipStream_t s) {
+  const dim3 grid((N + 15) / 16, (num_tokens + 15) / 16);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, (const T*)x, ldx, num_tokens, K, (const T*)nw, eps, sq,
+                       ldsq, parts, (const T*)Ws, N, (T*)out, ldo, (T*)xn, ldxn);
+  };
+  auto by_qpl = [&](auto xn) {
+    constexpr bool XN = decltype(xn)::value;
+    if (parts <= kWave * 4)
+      go(shuffled_gemm_normsq_kernel<T, 1, XN>);
+    else if (parts <= kWave * 8)
+      go(shuffled_gemm_normsq_kernel<T, 2, XN>);
+    else
+      go(shuffled_gemm_normsq_kernel<T, 4, XN>);
+  };
+  if (xn != nullptr)
+    by_qpl(std::true_type{});
+  else
+    by_qpl(std::false_type{});
+  PL_LAUNCH_CHECK("shuffled_gemm_normsq_kernel");
+  return ok();
+}
+
 extern "C" int pl_linear_shuffled_norm(const void* x, int64_t ldx, int num_tokens, int in_features,
-                                       const void* norm_weight, float eps, const void* shuffled, int out_features,
-                                       void* out, int64_t ldo, void* x_norm_out, int64_t ld_norm_out, int dtype,
-                                       void* stream) {
-  if (num_tokens < 0 || num_tokens > kNormMaxTokens)
-    return fail(PL_ERR_INVALID, "num_tokens must be 0..%d (got %d)", kNormMaxTokens, num_tokens);
+                                       const void* norm_weight, float eps, const float* sq_partials, int64_t ld_sq,
+                                       int sq_parts, const void* shuffled, int out_features, void* out, int64_t ldo,
+                                       void* x_norm_out, int64_t ld_norm_out, int dtype, void* stream) {
+  const int max_tokens = sq_partials ? 16 : kNormMaxTokens;
+  if (num_tokens < 0 || num_tokens > max_tokens)
+    return fail(PL_ERR_INVALID, "num_tokens must be 0..%d (got %d)", max_tokens, num_tokens);
   if (num_tokens == 0) return ok();
-  if (in_features <= 0 || in_features % 512 || in_features > 8192 || num_tokens * in_features > 32768)
+  if (sq_partials ? (in_features <= 0 || in_features % 32 || in_features > 8192)
+                  : (in_features <= 0 || in_features % 512 || in_features > 8192 || num_tokens * in_features > 32768))
     return fail(PL_ERR_UNSUPPORTED,
-                "in_features must be a multiple of 512 up to 8192 with num_tokens * in_features <= 32768 "
-                "(got %d x %d)", num_tokens, in_features);
+                "in_features must be a multiple of 32 (with sq_partials) or of 512 with num_tokens * in_features <= "
+                "32768 (without), up to 8192 (got %d x %d)", num_tokens, in_features);
   if (out_features <= 0) return fail(PL_ERR_INVALID, "out_features must be > 0");
   if (!x || !norm_weight || !shuffled || !out) return fail(PL_ERR_INVALID, "null pointer argument");
   if (ldx < in_features || ldx % 8 || (uintptr_t)x % 16 || (uintptr_t)shuffled % 16 || (uintptr_t)norm_weight % 16)
@@ -696,6 +861,16 @@ extern "C" int pl_linear_shuffled_norm(const void* x, int64_t ldx, int num_token
   if (dtype != PL_DTYPE_BF16 && dtype != PL_DTYPE_F16)
     return fail(PL_ERR_UNSUPPORTED, "pl_linear_shuffled_norm dtype must be F16 or BF16 (got %d)", dtype);
   hipStream_t s = (hipStream_t)stream;
+  if (sq_partials != nullptr) {
+    if (sq_parts < 1 || sq_parts > kWave * 16 || ld_sq < sq_parts || ld_sq % 4 || (uintptr_t)sq_partials % 16)
+      return fail(PL_ERR_INVALID, "sq_partials: 1..%d parts per row, ld_sq >= parts and a multiple of 4, 16-byte "
+                  "aligned (got %d parts, ld %lld)", kWave * 16, sq_parts, (long long)ld_sq);
+    if (dtype == PL_DTYPE_BF16)
+      return normsq_gemm_t<bf16_t>(x, ldx, num_tokens, in_features, norm_weight, eps, sq_partials, ld_sq, sq_parts,
+                                   shuffled, out_features, out, ldo, x_norm_out, ld_norm_out, s);
+    return normsq_gemm_t<f16_t>(x, ldx, num_tokens, in_features, norm_weight, eps, sq_partials, ld_sq, sq_parts,
+                                shuffled, out_features, out, ldo, x_norm_out, ld_norm_out, s);
+  }
   if (dtype == PL_DTYPE_BF16)
     return norm_gemm_t<bf16_t>(x, ldx, num_tokens, in_features, norm_weight, eps, shuffled, out_features, out, ldo,
                                x_norm_out, ld_norm_out, s);
@@ -706,28 +881,28 @@ extern "C" int pl_linear_shuffled_norm(const void* x, int64_t ldx, int num_token
 template <typename T, int R, int YPT>
 static void launch_add_gemm(const void* x, int64_t ldx, int num_tokens, int K, const void* Ws, int N, void* res,
                             int64_t ldr, const LoraUp& lu, const pl_lora_partials* yp, int lg, const int32_t* ids,
-                            int na, void* out, int64_t ldo, hipStream_t s) {
+                            int na, void* out, int64_t ldo, float* sq, int64_t ldsq, hipStream_t s) {
   const dim3 grid((N + 15) / 16, (num_tokens + 15) / 16);
   hipLaunchKernelGGL((shuffled_gemm_add_kernel<T, R, YPT>), grid, dim3(kThreads), 0, s, (const T*)x, ldx,
                      num_tokens, K, (const T*)Ws, N, (T*)res, ldr, lu, yp ? yp->partials : nullptr,
-                     yp ? yp->ld : 0, yp ? yp->parts : 0, lg, ids, na, (T*)out, ldo);
+                     yp ? yp->ld : 0, yp ? yp->parts : 0, lg, ids, na, (T*)out, ldo, sq, ldsq);
 }
 
 template <typename T>
 static int add_gemm_t(const void* x, int64_t ldx, int num_tokens, int K, const void* Ws, int N, void* res,
                       int64_t ldr, const LoraUp& lu, int rank, const pl_lora_partials* yp, int lg, int ypt,
-                      const int32_t* ids, int na, void* out, int64_t ldo, hipStream_t s) {
+                      const int32_t* ids, int na, void* out, int64_t ldo, float* sq, int64_t ldsq, hipStream_t s) {
   switch (rank) {
-    case 0: launch_add_gemm<T, 0, 1>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s); break;
+    case 0: launch_add_gemm<T, 0, 1>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, sq, ldsq, s); break;
     case 8:
-      if (ypt <= 1) launch_add_gemm<T, 8, 1>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
-      else if (ypt <= 2) launch_add_gemm<T, 8, 2>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
-      else launch_add_gemm<T, 8, 4>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
+      if (ypt <= 1) launch_add_gemm<T, 8, 1>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, sq, ldsq, s);
+      else if (ypt <= 2) launch_add_gemm<T, 8, 2>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, sq, ldsq, s);
+      else launch_add_gemm<T, 8, 4>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, sq, ldsq, s);
       break;
     default:
-      if (ypt <= 1) launch_add_gemm<T, 16, 1>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
-      else if (ypt <= 2) launch_add_gemm<T, 16, 2>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
-      else launch_add_gemm<T, 16, 4>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, s);
+      if (ypt <= 1) launch_add_gemm<T, 16, 1>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, sq, ldsq, s);
+      else if (ypt <= 2) launch_add_gemm<T, 16, 2>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, sq, ldsq, s);
+      else launch_add_gemm<T, 16, 4>(x, ldx, num_tokens, K, Ws, N, res, ldr, lu, yp, lg, ids, na, out, ldo, sq, ldsq, s);
       break;
   }
   PL_LAUNCH_CHECK("shuffled_gemm_add_kernel");
@@ -737,8 +912,8 @@ static int add_gemm_t(const void* x, int64_t ldx, int num_tokens, int K, const v
 extern "C" int pl_linear_shuffled_add(const void* x, int64_t ldx, int num_tokens, int in_features,
                                       const void* shuffled, int out_features, void* residual, int64_t ldr,
                                       const pl_lora_up* lora, const pl_lora_partials* lora_y,
-                                      const int32_t* adapter_ids, int num_adapters, void* out, int64_t ldo, int dtype,
-                                      void* stream) {
+                                      const int32_t* adapter_ids, int num_adapters, void* out, int64_t ldo,
+                                      float* sq_out, int64_t ld_sq, int dtype, void* stream) {
   if (num_tokens < 0 || num_tokens > 16)
     return fail(PL_ERR_INVALID, "num_tokens must be 0..16 (got %d)", num_tokens);
   if (num_tokens == 0) return ok();
@@ -749,6 +924,8 @@ extern "C" int pl_linear_shuffled_add(const void* x, int64_t ldx, int num_tokens
     return fail(PL_ERR_INVALID, "x rows and the shuffled weight must be 16-byte aligned");
   if (ldr < out_features || (out && ldo < out_features))
     return fail(PL_ERR_INVALID, "residual / out rows shorter than out_features");
+  if (sq_out && ld_sq < (out_features + 15) / 16)
+    return fail(PL_ERR_INVALID, "sq_out rows need ld_sq >= %d (one sum per 16 columns)", (out_features + 15) / 16);
   if (dtype != PL_DTYPE_BF16 && dtype != PL_DTYPE_F16)
     return fail(PL_ERR_UNSUPPORTED, "pl_linear_shuffled_add dtype must be F16 or BF16 (got %d)", dtype);
   if ((lora == nullptr) != (lora_y == nullptr))
@@ -782,7 +959,7 @@ extern "C" int pl_linear_shuffled_add(const void* x, int64_t ldx, int num_tokens
   hipStream_t s = (hipStream_t)stream;
   if (dtype == PL_DTYPE_BF16)
     return add_gemm_t<bf16_t>(x, ldx, num_tokens, in_features, shuffled, out_features, residual, ldr, lu, rank, lora_y,
-                              lg, ypt, adapter_ids, num_adapters, out, ldo, s);
+                              lg, ypt, adapter_ids, num_adapters, out, ldo, sq_out, ld_sq, s);
   return add_gemm_t<f16_t>(x, ldx, num_tokens, in_features, shuffled, out_features, residual, ldr, lu, rank, lora_y,
-                           lg, ypt, adapter_ids, num_adapters, out, ldo, s);
+                           lg, ypt, adapter_ids, num_adapters, out, ldo, sq_out, ld_sq, s);
 }

@@ -236,10 +236,11 @@ def lora_a_rows(weight: ShuffledWeight, a_row0: int, rank: int, adapter: int = -
 
 
 def linear_shuffled_norm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weight: ShuffledWeight,
-                         x_norm_out: torch.Tensor | None = None) -> torch.Tensor:
+                         x_norm_out: torch.Tensor | None = None, sq: torch.Tensor | None = None) -> torch.Tensor:
     """``RMSNorm(x) . W^T`` in one launch (``pl_linear_shuffled_norm``): the
     normalized rows never go through memory (``x_norm_out``, when given,
-    receives them too)."""
+    receives them too).  ``sq`` [T, parts] fp32: the rows' sums of squares in
+    pieces, from the GEMM that wrote x (:func:`linear_shuffled_add`)."""
     if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] != weight.in_features or x.dtype != weight.dtype:
         raise ValueError(f"x must be [T, {weight.in_features}] of {weight.dtype} with unit column stride")
     if norm_weight.numel() != weight.in_features or norm_weight.dtype != x.dtype or not norm_weight.is_contiguous():
@@ -249,9 +250,13 @@ def linear_shuffled_norm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     if x_norm_out is not None and (tuple(x_norm_out.shape) != tuple(x.shape) or x_norm_out.stride(1) != 1
                                    or x_norm_out.dtype != x.dtype):
         raise ValueError("x_norm_out must be shaped like x with unit column stride")
+    if sq is not None and (sq.dim() != 2 or sq.shape[0] != T or sq.dtype != torch.float32 or sq.stride(1) != 1):
+        raise ValueError("sq must be fp32 [T, parts] with unit column stride")
     lib = _lib.load()
     _lib.check(lib.pl_linear_shuffled_norm(x.data_ptr(), x.stride(0), T, weight.in_features, norm_weight.data_ptr(),
-                                           float(eps), weight.data.data_ptr(), N, out.data_ptr(), out.stride(0),
+                                           float(eps), sq.data_ptr() if sq is not None else None,
+                                           sq.stride(0) if sq is not None else 0, sq.shape[1] if sq is not None else 0,
+                                           weight.data.data_ptr(), N, out.data_ptr(), out.stride(0),
                                            x_norm_out.data_ptr() if x_norm_out is not None else None,
                                            x_norm_out.stride(0) if x_norm_out is not None else 0,
                                            _lib.dtype_code(x.dtype), _lib.stream_handle(x.device)),
@@ -261,12 +266,14 @@ def linear_shuffled_norm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
 
 def linear_shuffled_add(x: torch.Tensor, weight: ShuffledWeight, main_features: int, residual: torch.Tensor,
                         lora=None, partials: LoraPartials | None = None, adapter_ids: torch.Tensor | None = None,
-                        out: torch.Tensor | None = None) -> torch.Tensor:
+                        out: torch.Tensor | None = None, sq_out: torch.Tensor | None = None) -> torch.Tensor:
     """``residual += round(round(x . W^T) + delta)`` over the first
     ``main_features`` rows of ``weight`` (``pl_linear_shuffled_add``), with
     the LoRA up-projection delta of ``lora`` (a ``fused_ops.LoraUp``; its
     ``y`` is not read) on y from ``partials``.  ``out`` (optional) receives
-    round(x . W^T).  Returns ``residual``."""
+    round(x . W^T); ``sq_out`` (optional, fp32 [T, >= main_features / 16])
+    the new residual's sums of squares per 16 columns.  Returns
+    ``residual``."""
     if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] != weight.in_features or x.dtype != weight.dtype:
         raise ValueError(f"x must be [T, {weight.in_features}] of {weight.dtype} with unit column stride")
     T = x.shape[0]
@@ -293,6 +300,9 @@ def linear_shuffled_add(x: torch.Tensor, weight: ShuffledWeight, main_features: 
         ids = adapter_ids.data_ptr() if adapter_ids is not None else None
     if out is not None and (tuple(out.shape) != (T, main_features) or out.stride(1) != 1 or out.dtype != x.dtype):
         raise ValueError("out must be shaped like residual")
+    if sq_out is not None and (sq_out.dim() != 2 or sq_out.shape[0] != T or sq_out.shape[1] < -(-main_features // 16)
+                               or sq_out.dtype != torch.float32 or sq_out.stride(1) != 1):
+        raise ValueError(f"sq_out must be fp32 [T, >= {-(-main_features // 16)}] with unit column stride")
     lib = _lib.load()
     _lib.check(lib.pl_linear_shuffled_add(x.data_ptr(), x.stride(0), T, weight.in_features, weight.data.data_ptr(),
                                           int(main_features), residual.data_ptr(), residual.stride(0),
@@ -300,6 +310,8 @@ def linear_shuffled_add(x: torch.Tensor, weight: ShuffledWeight, main_features: 
                                           ctypes.byref(yp) if yp is not None else None, ids, n,
                                           out.data_ptr() if out is not None else None,
                                           out.stride(0) if out is not None else 0,
+                                          sq_out.data_ptr() if sq_out is not None else None,
+                                          sq_out.stride(0) if sq_out is not None else 0,
                                           _lib.dtype_code(x.dtype), _lib.stream_handle(x.device)),
                "pl_linear_shuffled_add")
     return residual

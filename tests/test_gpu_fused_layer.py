@@ -65,6 +65,47 @@ def test_norm_gemm(gpu_device, dtype, tokens, shape):
     assert torch.equal(out, ref), "the GEMM on the LDS rows differs from the GEMM on the reported rows"
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("tokens", [1, 4, 9, 16])
+@pytest.mark.parametrize("shape,parts", [((24608, 4096), 256), ((6192, 4096), 256), ((48, 1024), 37),
+                                         ((1000, 2048), 600)])
+def test_norm_gemm_from_squares(gpu_device, dtype, tokens, shape, parts):
+    """The sums of squares given in pieces (as pl_linear_shuffled_add writes
+    them): the normalized rows against the float64 RMSNorm, the output bit
+    for bit against pl_linear_shuffled on those rows."""
+    n, k = shape
+    g = torch.Generator().manual_seed(n + k + tokens + parts)
+    x = (torch.randn((tokens, k), generator=g) * 3).to(dtype)
+    w = (1 + 0.1 * torch.randn(k, generator=g)).to(dtype)
+    W = (torch.randn((n, k), generator=g) * k ** -0.5).to(dtype)
+    xf = x.double().numpy()
+    sq = np.zeros((tokens, (parts + 3) // 4 * 4), dtype=np.float32)
+    edges = np.linspace(0, k, parts + 1).astype(int)
+    for j in range(parts):
+        sq[:, j] = (xf[:, edges[j]:edges[j + 1]] ** 2).sum(axis=1)
+    sw = ShuffledWeight(W.to(gpu_device))
+    xd = x.to(gpu_device)
+    xn = torch.empty_like(xd)
+    sqd = torch.from_numpy(sq).to(gpu_device)[:, :parts] if parts % 4 == 0 else torch.from_numpy(sq).to(gpu_device)
+    if parts % 4:
+        # the pieces are read 4 at a time: the row pitch is a multiple of 4, the count `parts`
+        out = torch.empty((tokens, n), dtype=dtype, device=gpu_device)
+        lib = _lib.load()
+        _lib.check(lib.pl_linear_shuffled_norm(xd.data_ptr(), xd.stride(0), tokens, k, w.to(gpu_device).data_ptr(),
+                                               1e-6, sqd.data_ptr(), sqd.stride(0), parts, sw.data.data_ptr(), n,
+                                               out.data_ptr(), out.stride(0), xn.data_ptr(), xn.stride(0),
+                                               _lib.dtype_code(dtype), _lib.stream_handle(xd.device)),
+                   "pl_linear_shuffled_norm")
+    else:
+        out = linear_shuffled_norm(xd, w.to(gpu_device), 1e-6, sw, x_norm_out=xn, sq=sqd)
+    ref = linear_shuffled(xn, sw)
+    torch.cuda.synchronize()
+    want = of.rmsnorm(xf, _np(w), 1e-6)
+    err = np.abs(_np(xn) - want)
+    assert (err <= REL[dtype] * np.abs(want) + 1e-6).all(), f"norm: max err {err.max():.3e}"
+    assert torch.equal(out, ref), "the GEMM on the normalized operands differs from the GEMM on the reported rows"
+
+
 def test_norm_gemm_strided_rows(gpu_device):
     """x as a column slice of a wider buffer; no x_norm_out."""
     g = torch.Generator().manual_seed(5)
@@ -106,11 +147,18 @@ def test_add_gemm(gpu_device, dtype, tokens, parts, rank, mode):
     res = hid.to(gpu_device)
     base = torch.empty_like(res)
     ids_d = ids.to(gpu_device)
+    sq = torch.full((tokens, 260), float("nan"), device=gpu_device)
     linear_shuffled_add(x.to(gpu_device), sw, 4096, res, lora, LoraPartials(yp.to(gpu_device)),
-                        ids_d if bound < 0 else None, out=base)
+                        ids_d if bound < 0 else None, out=base, sq_out=sq)
     ref = linear_shuffled(x.to(gpu_device), sw)[:, :4096]
     torch.cuda.synchronize()
     assert torch.equal(base, ref), "base output differs from pl_linear_shuffled"
+    # the squares of the stored residual per 16 columns (fp32 sums of 16 terms)
+    r64 = _np(res).reshape(tokens, 256, 16)
+    sq_want = (r64 ** 2).sum(axis=2)
+    sq_got = sq[:, :256].double().cpu().numpy()
+    assert (np.abs(sq_got - sq_want) <= 1e-5 * sq_want + 1e-30).all(), "sums of squares"
+    assert torch.isnan(sq[:, 256:]).all(), "sq_out written past its blocks"
     rel = REL[dtype]
     y = yp.double().sum(dim=1).numpy()
     ok_id = np.array([bound] * tokens) if bound >= 0 else ids.numpy()
