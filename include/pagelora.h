@@ -880,6 +880,25 @@ int pl_decode_run_qkv_oshrink(
     void* stream);
 
 /*
+ * pl_silu_mul_lora that also forms down_proj's LoRA shrink: the stored
+ * output act (down_proj's input), times the same columns of the row's
+ * adapter's A rows (down_lora_a, in_features = inter, binding the gate / up
+ * modules' adapter), as fp32 partial sums down_lora_y with one part per 512
+ * columns (parts = ceil(inter / 512); ld a multiple of 4), for
+ * pl_linear_shuffled_add.  16-bit dtypes, gate / up rank up to 16, down rank
+ * 8 or 16, inter a multiple of 32.  No counterpart in the reference: it
+ * computes the first F.linear of down_proj's LoRALinear.forward delta
+ * (multilora/linear.py:226-231) with silu_and_mul (packed_ops.py:230-239).
+ */
+int pl_silu_mul_lora_shrink(const void* gate_up, int64_t ldg,
+                            const pl_lora_up* lora_gate_up_h,
+                            const int32_t* adapter_ids, int num_adapters,
+                            void* out, int64_t ldo, int rows, int inter,
+                            const pl_lora_a_rows* down_lora_a,
+                            const pl_lora_partials* down_lora_y, int dtype,
+                            void* stream);
+
+/*
  * Advance every row of a batched page table by one decode token, in place
  * on the device (one kernel, no host table, safe to capture in a graph).
  * indptr [batch+1], indices (capacity indices_capacity entries) and

@@ -234,6 +234,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i32, _f32, _i32, _vp],
     ),
     "pl_silu_mul_lora": (_i32, [_vp, _i64, ctypes.POINTER(LoraUp), _vp, _i32, _vp, _i64, _i32, _i32, _i32, _vp]),
+    "pl_silu_mul_lora_shrink": (_i32, [_vp, _i64, ctypes.POINTER(LoraUp), _vp, _i32, _vp, _i64, _i32, _i32,
+                                       ctypes.POINTER(LoraARows), ctypes.POINTER(LoraPartials), _i32, _vp]),
     "pl_qk_norm_rope_append_lora": (
         _i32,
         [

@@ -420,6 +420,88 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const T* __restrict_
   store_row8<T>(out + row * ldo + chunk * 8, o);
 }
 
+// silu_mul_kernel (one wave per workgroup, LoRA rank R on gate / up) that
+// also forms down_proj's LoRA shrink: the product of the stored output (the
+// down projection's input) with the same columns of the row's adapter's
+// down A rows, read from the shuffled [W_down; A_down] weight (adapter a's
+// rank r is row a_row0 + a * OR + r), summed over the wave's 512 columns in
+// a fixed order and written as one partial per workgroup:
+// part[row * ldp + blockIdx.x * OR + r].  An adapter outside [0,
+// n_adapters) gives adapter 0's products (the consumer does not apply them).
+struct DownShrink {
+  const void* A;
+  int ksteps;  // inter / 32
+  int a_row0;
+  float* part;
+  int64_t ldp;
+};
+
+template <typename T, int R, int OR>
+__global__ __launch_bounds__(kWave) void silu_mul_shrink_kernel(const T* __restrict__ gu, int64_t ldg,
+                                                                T* __restrict__ out, int64_t ldo, int inter, LoraUp lg,
+                                                                LoraUp lu, const int32_t* __restrict__ ids,
+                                                                int n_adapters, DownShrink ds) {
+  static_assert(R > 0 && R <= 16 && (OR == 8 || OR == 16), "gate / up rank up to 16, down rank 8 or 16");
+  const int row = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int chunk_raw = blockIdx.x * kWave + lane;
+  const bool live = chunk_raw * 8 < inter;
+  const int chunk = live ? chunk_raw : inter / 8 - 1;  // idle lanes redo the last chunk, contributing nothing
+  const int a = lg.adapter >= 0 ? lg.adapter : ids[row];
+  const bool a_ok = a >= 0 && a < n_adapters;
+  const int a_ld = a_ok ? a : 0;
+  float g[8], u[8], o[8];
+  load_row8<T>(gu + row * ldg + chunk * 8, g);
+  load_row8<T>(gu + row * ldg + inter + chunk * 8, u);
+  LoraRow<R> yg, yu;
+  load_y<T, R>(lg, row, a_ld, yg);
+  load_y<T, R>(lu, row, a_ld, yu);
+  // the down A pieces: ranks 0 .. OR-1 of columns chunk*8 .. +8 (OR
+  // consecutive 16-byte pieces of one shuffled block when a_row0 + a*OR is
+  // a multiple of 16)
+  uint4 ap[OR];
+  {
+    const int k = chunk * 8;
+#pragma unroll
+    for (int r = 0; r < OR; ++r) {
+      const int64_t n = (int64_t)ds.a_row0 + (int64_t)a_ld * OR + r;
+      const int64_t e = (((n / 16) * ds.ksteps + k / 32) * 64 + ((k % 32) / 8) * 16 + n % 16) * 8;
+      ap[r] = *reinterpret_cast<const uint4*>((const T*)ds.A + e);
+    }
+  }
+  float dg[8], du[8];
+  lora_delta8_pair<T, R>(lg, lu, a_ld, chunk * 8, yg, yu, dg, du);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    g[i] = through<T>(g[i] + (a_ok ? dg[i] : -0.f));
+    u[i] = through<T>(u[i] + (a_ok ? du[i] : -0.f));
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = g[i] / (1.f + expf(-g[i])) * u[i];
+  if (live) store_row8<T>(out + row * ldo + chunk * 8, o);
+  // the shrink of the stored values
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = live ? through<T>(o[i]) : 0.f;
+  float p[OR];
+#pragma unroll
+  for (int r = 0; r < OR; ++r) {
+    float f[8];
+    unpack2<T>(ap[r].x, f[0], f[1]);
+    unpack2<T>(ap[r].y, f[2], f[3]);
+    unpack2<T>(ap[r].z, f[4], f[5]);
+    unpack2<T>(ap[r].w, f[6], f[7]);
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc = fmaf(o[i], f[i], acc);
+    p[r] = wave_sum(acc);
+  }
+  if (lane == 0) {
+    float* dst = ds.part + (int64_t)row * ds.ldp + (int64_t)blockIdx.x * OR;
+#pragma unroll
+    for (int r = 0; r < OR; r += 4) *reinterpret_cast<float4*>(dst + r) = make_float4(p[r], p[r + 1], p[r + 2], p[r + 3]);
+  }
+}
+
 // R > 0: the q, k and v modules' up-projections (rank R); their columns are
 // head-major within each module.
 struct QkvLora {
@@ -862,6 +944,62 @@ static int silu_common(const void* gate_up, int64_t ldg, void* out, int64_t ldo,
 extern "C" int pl_silu_mul(const void* gate_up, int64_t ldg, void* out, int64_t ldo, int rows, int inter,
                            int dtype, void* stream) {
   return silu_common(gate_up, ldg, out, ldo, rows, inter, dtype, stream, nullptr, nullptr, 0);
+}
+
+extern "C" int pl_silu_mul_lora_shrink(const void* gate_up, int64_t ldg, const pl_lora_up* lora_gate_up_h,
+                                       const int32_t* adapter_ids, int num_adapters, void* out, int64_t ldo, int rows,
+                                       int inter, const pl_lora_a_rows* down_lora_a,
+                                       const pl_lora_partials* down_lora_y, int dtype, void* stream) {
+  if (rows < 0 || inter <= 0 || inter % 32) return fail(PL_ERR_INVALID, "inter must be a positive multiple of 32");
+  if (rows == 0) return ok();
+  if (!gate_up || !out || !lora_gate_up_h || !down_lora_a || !down_lora_y)
+    return fail(PL_ERR_INVALID, "null pointer argument");
+  if (ldg % 8 || ldo % 8 || (uintptr_t)gate_up % 16 || (uintptr_t)out % 16)
+    return fail(PL_ERR_INVALID, "16-byte aligned rows required");
+  if (dtype != PL_DTYPE_F16 && dtype != PL_DTYPE_BF16)
+    return fail(PL_ERR_UNSUPPORTED, "pl_silu_mul_lora_shrink dtype must be F16 or BF16 (got %d)", dtype);
+  if (const int st = adapter_check(lora_gate_up_h, 2, adapter_ids, num_adapters, "silu_mul LoRA")) return st;
+  LoraUp lg{}, lu{};
+  if (const int st = lora_up_from(&lora_gate_up_h[0], inter, &lg, "silu_mul gate LoRA")) return st;
+  if (const int st = lora_up_from(&lora_gate_up_h[1], inter, &lu, "silu_mul up LoRA")) return st;
+  if (lg.rank != lu.rank || lg.rank > 16)
+    return fail(PL_ERR_UNSUPPORTED, "gate and up LoRA: one rank up to 16 (got %d, %d)", lg.rank, lu.rank);
+  const pl_lora_a_rows& da = *down_lora_a;
+  const pl_lora_partials& dy = *down_lora_y;
+  if (da.rank != 8 && da.rank != 16) return fail(PL_ERR_UNSUPPORTED, "down_proj shrink rank %d not built (8, 16)", da.rank);
+  if (da.adapter != lora_gate_up_h[0].adapter)
+    return fail(PL_ERR_INVALID, "down_proj's A rows must bind the gate / up modules' adapter");
+  if (!da.shuffled || (uintptr_t)da.shuffled % 16 || da.in_features != inter || da.a_row0 < 0 ||
+      (int64_t)da.a_row0 + (int64_t)num_adapters * da.rank > da.out_features)
+    return fail(PL_ERR_INVALID, "down_proj A rows: a 16-byte aligned shuffled weight %d wide (got %d) whose %d rows "
+                "hold rows a_row0 (%d) .. + %d adapters x rank %d", inter, da.in_features, da.out_features, da.a_row0,
+                num_adapters, da.rank);
+  const int parts = (inter / 8 + kWave - 1) / kWave;
+  if (!dy.partials || (uintptr_t)dy.partials % 16 || dy.rank != da.rank || dy.parts != parts ||
+      dy.ld < (int64_t)parts * dy.rank || dy.ld % 4)
+    return fail(PL_ERR_INVALID, "down_proj partials: rank %d, %d parts per row (one per 512 columns), ld >= %d and a "
+                "multiple of 4, 16-byte aligned", da.rank, parts, parts * da.rank);
+  const DownShrink dsh{da.shuffled, inter / 32, da.a_row0, dy.partials, dy.ld};
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(parts, rows);
+  auto go = [&](auto t, auto r, auto orr) {
+    using T = decltype(t);
+    constexpr int R = decltype(r)::value, OR = decltype(orr)::value;
+    hipLaunchKernelGGL((silu_mul_shrink_kernel<T, R, OR>), grid, dim3(kWave), 0, s, (const T*)gate_up, ldg, (T*)out,
+                       ldo, inter, lg, lu, adapter_ids, num_adapters, dsh);
+  };
+  auto by_or = [&](auto t, auto r) {
+    if (da.rank == 8) go(t, r, std::integral_constant<int, 8>{});
+    else go(t, r, std::integral_constant<int, 16>{});
+  };
+  auto by_r = [&](auto t) {
+    if (lg.rank == 8) by_or(t, std::integral_constant<int, 8>{});
+    else by_or(t, std::integral_constant<int, 16>{});
+  };
+  if (dtype == PL_DTYPE_BF16) by_r(bf16_t{});
+  else by_r(f16_t{});
+  PL_LAUNCH_CHECK("silu_mul_shrink_kernel");
+  return ok();
 }
 
 extern "C" int pl_silu_mul_lora(const void* gate_up, int64_t ldg, const pl_lora_up* lora_gate_up_h,

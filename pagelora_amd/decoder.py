@@ -15,12 +15,16 @@ modules (packed_ops.py:105-265, multilora/linear.py:200-231):
     -> GEMM on [W_gate_up; A_gate; A_up] -> LoRA up-projections + SiLU*up
     -> GEMM on [W_down; A_down] (its delta lands in the next layer's norm)
 
-Nine kernels per decode layer at decode batch sizes: two add+RMSNorm, four
-GEMMs on the shuffled weights (the narrow o/down ones with their LoRA A rows
-on side planes), the attention kernel with the q/k/v epilogue folded in, the
-merge and SiLU*up.  The LoRA shrink rides in the base GEMM (the adapters' A
-rows stacked under W) and the expand in the kernel that consumes the module
-output, so no separate LoRA launches remain.  Prefill, and batches beyond
+Seven kernels per decode layer at decode batch sizes: four GEMMs on the
+shuffled weights, the attention kernel with the q/k/v epilogue folded in,
+the merge and SiLU*up.  The RMSNorms run in the prologues of the q/k/v and
+gate/up GEMMs; o_proj and down_proj add their output and LoRA delta into
+the residual stream in their epilogues.  The q/k/v and gate/up LoRA shrink
+rides in the base GEMM (the adapters' A rows stacked under W) and the
+expand in the kernel that consumes the module output; o_proj's shrink runs
+in the attention's merge and down_proj's in SiLU*up, so no separate LoRA
+launches remain.  (With the fusion off, or past 16 rows: two add+RMSNorm
+kernels and the o/down GEMMs with their A rows on side planes, nine.)  Prefill, and batches beyond
 the decode GEMM's 64 rows, use the library GEMM (torch -> hipBLASLt);
 prefill forms q and appends k/v in the separate q/k norm + RoPE + append
 kernel.  Weights are random (no checkpoints are available); shapes follow
@@ -460,19 +464,21 @@ DECODE_SIDE_SPLITS = {"o": 16, "down": 16}
 # (pl_decode_run_qkv) where it is built; False keeps the separate
 # head-norm/RoPE/append kernel (tests compare the two).
 FOLD_QKV_INTO_DECODE = True
-# Decode layers on the folded path fuse the post-attention add + RMSNorm away
-# where they can (see _fused_post_attention): o_proj's LoRA shrink in the
-# attention's merge, o_proj + its LoRA delta + the residual add in one GEMM,
-# the RMSNorm in the gate/up GEMM's prologue.  False keeps the add+RMSNorm
-# kernel (tests compare the two).
-FUSE_POST_ATTENTION_NORM = True
+# Decode layers on the folded path fuse the add + RMSNorm launches away
+# where they can (see _layer): FUSE_NORMS the post-attention one (and the
+# input RMSNorm into the q/k/v GEMM), FUSE_DOWN_NORM also the one after
+# down_proj.  False keeps the add+RMSNorm kernel (tests compare the two).
+FUSE_NORMS = True
+FUSE_DOWN_NORM = True
 # Optional observer of a layer's stages, called eagerly as ``STAGE_TRACE(name,
-# value)`` with each stage's stored output (tensors, split planes) in
-# dataflow order: "hidden_in" (the residual stream on entry), "hidden" (after
-# the input add of the previous layer's down_proj output), "x", "qkv",
-# "attn", "o", "hidden_mid", "x2", "gate_up", "act", "down" per layer; after
-# the last layer (decode steps) "final_hidden_in" (the residual stream before
-# the final add), "final_down" (the last layer's down_proj output),
+# value)`` with each stage's stored output (tensors, split planes, partial
+# outputs) in dataflow order: "hidden_in" (the residual stream on entry),
+# "hidden" (after the input add of the previous layer's down_proj output,
+# when this layer does that add), "x", "qkv", "attn", "o", "hidden_mid",
+# "x2", "gate_up", "act", "down" per layer (with the norms fused into the
+# GEMMs, "x" and "x2" are the normalized rows the GEMMs report); after the
+# last layer (decode steps) "final_hidden_in" (the residual stream before
+# the last down_proj output is added), "final_down" (that output),
 # "final_hidden", "final_x" (after the final add + RMSNorm), "logits" and
 # "next_tokens".  For checking a decode step stage by stage; it must stay
 # None while a graph is captured.
@@ -556,9 +562,10 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
     """One decoder layer over T tokens (decode or prefill), no-merge LoRA on
     all seven modules.  ``hidden`` is the residual stream, updated in place;
     ``pending`` = (previous layer's down_proj output, its LoRA up-projection)
-    or None, folded into this layer's input add+RMSNorm.  ``attend(q)``
-    returns attention over the pages as [T, Hq, D].  Returns this layer's
-    pending pair.
+    to fold into this layer's input add+RMSNorm, a :class:`FusedPending`
+    when the previous layer already added it into ``hidden``, or None.
+    ``attend(q)`` returns attention over the pages as [T, Hq, D].  Returns
+    this layer's pending value.
 
     Per projection, one GEMM on [W; A] yields base output + LoRA intermediate
     and the consumer kernel applies the up-projection: the q/k/v deltas in
@@ -568,80 +575,146 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
     lora)``, when given, replaces the head-norm/RoPE/append kernel and
     ``attend``: one kernel that forms q and appends k/v from the packed rows
     while attending.
+
+    Decode layers on that folded path take the add + RMSNorm launches out
+    where :func:`_fused_norms` allows: o_proj's LoRA shrink runs in the
+    attention's merge and down_proj's in SiLU*up (as partial sums), o_proj
+    and down_proj each add their output and LoRA delta into the residual
+    stream in the GEMM's epilogue (pl_linear_shuffled_add), and the RMSNorms
+    run in the prologue of the q/k/v and gate/up GEMMs
+    (pl_linear_shuffled_norm).
     """
     h, qd, kd, I = cfg.hidden, cfg.q_dim, cfg.kv_dim, cfg.intermediate
+    T, r = hidden.shape[0], cfg.lora_rank
     a = adapter
     trace = STAGE_TRACE
     if trace is not None:
         trace("hidden_in", hidden)
-    if pending is None:
-        x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
+    fused = qkv_attend is not None and _fused_norms(cfg, lw, T)
+    if isinstance(pending, FusedPending) or (pending is None and fused and _norm_prologue(cfg, T)):
+        # the residual stream is complete: RMSNorm in the q/k/v GEMM
+        x = torch.empty_like(hidden) if trace is not None else None
+        sq = pending.sq if isinstance(pending, FusedPending) else None
+        qkv = linear_shuffled_norm(hidden, lw.input_norm, cfg.rms_eps, lw.shuffled["qkv"], x, sq=sq)
     else:
-        prev_out, prev_up = pending
-        x = fused_ops.add_rmsnorm(hidden, _cols(prev_out, h), lw.input_norm, cfg.rms_eps, lora=prev_up,
-                                  adapter_ids=ids)
-    qkv = _project(x, lw, "qkv")
+        if pending is None:
+            x = fused_ops.rmsnorm(hidden, lw.input_norm, cfg.rms_eps)
+        else:
+            prev_out, prev_up = pending
+            x = fused_ops.add_rmsnorm(hidden, _cols(prev_out, h), lw.input_norm, cfg.rms_eps, lora=prev_up,
+                                      adapter_ids=ids)
+        qkv = _project(x, lw, "qkv")
+        if trace is not None:
+            trace("hidden", hidden)
     if trace is not None:
-        trace("hidden", hidden)
         trace("x", x)
         trace("qkv", qkv)
     lora_qkv = (lw.up("q", qkv, scale, a), lw.up("k", qkv, scale, a), lw.up("v", qkv, scale, a))
-    fused = qkv_attend is not None and not isinstance(qkv, SplitOutput) and _fused_post_attention(cfg, lw, x)
+    fused = fused and not isinstance(qkv, SplitOutput)
     if fused:
-        T, r = x.shape[0], cfg.lora_rank
-        parts = LoraPartials(torch.empty((T, qkv_attend.oshrink_parts(T), r), dtype=torch.float32, device=x.device))
+        parts = LoraPartials(torch.empty((T, qkv_attend.oshrink_parts(T), r), dtype=torch.float32,
+                                         device=hidden.device))
         o_rows = lora_a_rows(lw.shuffled["o"], lw.y_offset["o"], r, a)
         attn = qkv_attend(_cols(qkv, qd + 2 * kd), lora_qkv, (o_rows, parts, lw.n_adapters)).view(T, qd)
         o_main = torch.empty_like(hidden) if trace is not None else None
         # B row-major: each workgroup reads the 16 consecutive B rows of its columns
         lo = fused_ops.LoraUp(None, 0, lw.lora["o"][1], scale, a)
-        # the norm's sums of squares from o_proj's epilogue only past the
-        # prologue's 8 tokens: the prologue forming them itself is faster
-        # (gate/up at 4 tokens 34.5 vs 36.5 us: normalizing in the main loop
-        # repeats the work in every wave)
-        sq = torch.empty((T, -(-h // 16)), dtype=torch.float32, device=x.device) if T > 8 else None
+        sq = _sq_buffer(cfg, T, hidden.device)
         linear_shuffled_add(attn, lw.shuffled["o"], h, hidden, lo, parts, ids, out=o_main, sq_out=sq)
-        o = PartialOutput(o_main, parts) if trace is not None else None
-        x2 = torch.empty_like(x) if trace is not None else None
+        if trace is not None:
+            for name, value in (("attn", attn), ("o", PartialOutput(o_main, parts)), ("hidden_mid", hidden)):
+                trace(name, value)
+        x2 = torch.empty_like(hidden) if trace is not None else None
         gu = linear_shuffled_norm(hidden, lw.post_norm, cfg.rms_eps, lw.shuffled["gate_up"], x2, sq=sq)
-    elif qkv_attend is not None and not isinstance(qkv, SplitOutput):
-        attn = qkv_attend(_cols(qkv, qd + 2 * kd), lora_qkv).view(qkv.shape[0], qd)
     else:
-        q = fused_ops.qk_norm_rope_append(
-            _cols(qkv, qd + 2 * kd), lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None,
-            positions, page_id, page_offset, layer_cache, num_qo_heads=cfg.num_qo_heads,
-            num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=page_size,
-            rope_theta=cfg.rope_theta, eps=cfg.rms_eps, lora=lora_qkv, adapter_ids=ids)
-        attn = attend(q).view(q.shape[0], qd)
-    if not fused:
+        if qkv_attend is not None and not isinstance(qkv, SplitOutput):
+            attn = qkv_attend(_cols(qkv, qd + 2 * kd), lora_qkv).view(T, qd)
+        else:
+            q = fused_ops.qk_norm_rope_append(
+                _cols(qkv, qd + 2 * kd), lw.q_norm if cfg.qk_norm else None, lw.k_norm if cfg.qk_norm else None,
+                positions, page_id, page_offset, layer_cache, num_qo_heads=cfg.num_qo_heads,
+                num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim, page_size=page_size,
+                rope_theta=cfg.rope_theta, eps=cfg.rms_eps, lora=lora_qkv, adapter_ids=ids)
+            attn = attend(q).view(T, qd)
         o = _project(attn, lw, "o")
         x2 = fused_ops.add_rmsnorm(hidden, _cols(o, h), lw.post_norm, cfg.rms_eps, lora=lw.up("o", o, scale, a),
                                    adapter_ids=ids)
+        if trace is not None:
+            for name, value in (("attn", attn), ("o", o), ("hidden_mid", hidden)):
+                trace(name, value)
         gu = _project(x2, lw, "gate_up")
-    act = fused_ops.silu_mul(gu[:, : 2 * I], lora=(lw.up("gate", gu, scale, a), lw.up("up", gu, scale, a)),
-                             adapter_ids=ids)
+    if trace is not None:
+        trace("x2", x2)
+        trace("gate_up", gu)
+    lora_gu = (lw.up("gate", gu, scale, a), lw.up("up", gu, scale, a))
+    if fused and _fused_down(cfg, lw):
+        parts_d = LoraPartials(torch.empty((T, -(-I // 512), r), dtype=torch.float32, device=hidden.device))
+        d_rows = lora_a_rows(lw.shuffled["down"], lw.y_offset["down"], r, a)
+        act = fused_ops.silu_mul(gu[:, : 2 * I], lora=lora_gu, adapter_ids=ids, down_shrink=(d_rows, parts_d))
+        before = hidden.clone() if trace is not None else None
+        d_main = torch.empty_like(hidden) if trace is not None else None
+        sq = _sq_buffer(cfg, T, hidden.device)
+        ld = fused_ops.LoraUp(None, 0, lw.lora["down"][1], scale, a)
+        linear_shuffled_add(act, lw.shuffled["down"], h, hidden, ld, parts_d, ids, out=d_main, sq_out=sq)
+        if trace is not None:
+            down = PartialOutput(d_main, parts_d)
+            trace("act", act)
+            trace("down", down)
+            return FusedPending(sq, before, down)
+        return FusedPending(sq)
+    act = fused_ops.silu_mul(gu[:, : 2 * I], lora=lora_gu, adapter_ids=ids)
     d = _project(act, lw, "down")
     if trace is not None:
-        for name, value in (("attn", attn), ("o", o), ("hidden_mid", hidden), ("x2", x2), ("gate_up", gu),
-                            ("act", act), ("down", d)):
-            trace(name, value)
+        trace("act", act)
+        trace("down", d)
     return d, lw.up("down", d, scale, a)
 
 
-def _fused_post_attention(cfg: DecoderConfig, lw: LayerWeights, x: torch.Tensor) -> bool:
-    """Whether a decode layer runs its post-attention add + RMSNorm fused
-    away: the decode-sized shuffled GEMMs for o_proj and gate/up, rank 8 or
-    16, at most 16 tokens (up to 8 with the hidden size a multiple of 512,
-    the RMSNorm prologue forms the sums of squares itself; beyond, o_proj's
-    epilogue hands them over)."""
-    T = x.shape[0]
-    prologue = T <= 8 and T * cfg.hidden <= 32768 and cfg.hidden % 512 == 0
-    return (FUSE_POST_ATTENTION_NORM and T <= 16 and (prologue or T > 8) and cfg.hidden % 32 == 0
-            and cfg.hidden <= 8192 and cfg.lora_rank in (8, 16) and "o" in lw.shuffled and "gate_up" in lw.shuffled
-            and lw.y_offset["o"] == cfg.hidden)
+class FusedPending:
+    """A layer's down_proj output already added, with its LoRA delta, into
+    the residual stream (linear_shuffled_add).  ``sq``: the stream's sums of
+    squares per 16 columns for the next RMSNorm (None: the norm's prologue
+    forms them).  Under a stage trace also the stream before that add
+    (``hidden_before``) and the projection's output (``down``)."""
+
+    def __init__(self, sq, hidden_before=None, down=None) -> None:
+        self.sq, self.hidden_before, self.down = sq, hidden_before, down
+
+
+def _norm_prologue(cfg: DecoderConfig, T: int) -> bool:
+    """The RMSNorm GEMM forms the sums of squares itself (up to 8 tokens,
+    hidden a multiple of 512): faster than taking them from the producing
+    GEMM (gate/up at 4 tokens 34.5 vs 36.5 us: normalizing in the main
+    loop repeats the work in every wave)."""
+    return T <= 8 and T * cfg.hidden <= 32768 and cfg.hidden % 512 == 0
+
+
+def _sq_buffer(cfg: DecoderConfig, T: int, device):
+    """The residual's sums of squares a producing GEMM hands to the next
+    RMSNorm GEMM, when that one does not form them itself."""
+    if _norm_prologue(cfg, T):
+        return None
+    return torch.empty((T, -(-cfg.hidden // 16)), dtype=torch.float32, device=device)
+
+
+def _fused_norms(cfg: DecoderConfig, lw: LayerWeights, T: int) -> bool:
+    """Whether a decode layer of T tokens fuses its add + RMSNorm launches
+    away: the decode-sized shuffled GEMMs for q/k/v, o_proj and gate/up,
+    LoRA rank 8 or 16, at most 16 tokens."""
+    return (FUSE_NORMS and T <= 16 and cfg.hidden % 32 == 0 and cfg.hidden <= 8192 and cfg.lora_rank in (8, 16)
+            and all(p in lw.shuffled for p in ("qkv", "o", "gate_up")) and lw.y_offset["o"] == cfg.hidden)
+
+
+def _fused_down(cfg: DecoderConfig, lw: LayerWeights) -> bool:
+    """down_proj's delta and residual add in its GEMM as well (its shrink in
+    SiLU*up)."""
+    return (FUSE_DOWN_NORM and "down" in lw.shuffled and lw.y_offset["down"] == cfg.hidden
+            and cfg.intermediate % 32 == 0 and cfg.intermediate <= 8192 * 4)
 
 
 def _final_norm(weights: "DecoderWeights", hidden: torch.Tensor, pending, ids: torch.Tensor) -> torch.Tensor:
+    if isinstance(pending, FusedPending):
+        return fused_ops.rmsnorm(hidden, weights.final_norm, weights.cfg.rms_eps)
     prev_out, prev_up = pending
     return fused_ops.add_rmsnorm(hidden, _cols(prev_out, weights.cfg.hidden), weights.final_norm,
                                  weights.cfg.rms_eps, lora=prev_up, adapter_ids=ids)
@@ -715,8 +788,12 @@ def decode_step_static(weights: DecoderWeights, pool: PagedKVPool, backend: Page
                                       backend, ctx)
     trace = STAGE_TRACE
     if trace is not None:
-        trace("final_hidden_in", hidden)
-        trace("final_down", pending[0])
+        if isinstance(pending, FusedPending):  # the last down_proj is in hidden already
+            trace("final_hidden_in", pending.hidden_before)
+            trace("final_down", pending.down)
+        else:
+            trace("final_hidden_in", hidden)
+            trace("final_down", pending[0])
     x = _final_norm(weights, hidden, pending, ctx.adapter_ids)
     logits = weights.logits(x)
     # greedy (sampling.py:8-15); the pick also becomes the next step's input token

@@ -186,9 +186,13 @@ def add_rmsnorm(residual: torch.Tensor, x: "torch.Tensor | SplitOutput", weight:
 
 
 def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None, *,
-             lora: Sequence[LoraUp] | None = None, adapter_ids: torch.Tensor | None = None) -> torch.Tensor:
+             lora: Sequence[LoraUp] | None = None, adapter_ids: torch.Tensor | None = None,
+             down_shrink=None) -> torch.Tensor:
     """``silu(gate) * up`` of a packed ``[T, 2*inter]`` row block; with ``lora``
-    (gate, up) the modules' LoRA deltas are added first (pl_silu_mul_lora)."""
+    (gate, up) the modules' LoRA deltas are added first (pl_silu_mul_lora).
+    ``down_shrink`` = (``_lib.LoraARows`` of down_proj, ``linear.LoraPartials``
+    [T, ceil(inter / 512), rank]): the kernel also writes down_proj's LoRA
+    shrink partials of the output (pl_silu_mul_lora_shrink)."""
     _rows2d(gate_up, "gate_up")
     inter = gate_up.shape[1] // 2
     if gate_up.shape[1] != 2 * inter:
@@ -196,6 +200,19 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None, *,
     out = torch.empty((gate_up.shape[0], inter), dtype=gate_up.dtype, device=gate_up.device) if out is None else out
     lib = _lib.load()
     rows = gate_up.shape[0]
+    if down_shrink is not None:
+        if lora is None or len(lora) != 2:
+            raise ValueError("the down_proj shrink comes with the gate / up LoRA")
+        arr, ids, n = _lora_args(lora, adapter_ids, rows)
+        a_rows, parts = down_shrink
+        if parts.partials.shape[0] != rows:
+            raise ValueError("down_proj partials must have one row per token")
+        p = parts.struct()
+        _lib.check(lib.pl_silu_mul_lora_shrink(gate_up.data_ptr(), gate_up.stride(0), arr, ids, n, out.data_ptr(),
+                                               out.stride(0), rows, inter, ctypes.byref(a_rows), ctypes.byref(p),
+                                               _lib.dtype_code(gate_up.dtype), _lib.stream_handle(gate_up.device)),
+                   "pl_silu_mul_lora_shrink")
+        return out
     if lora is not None:
         if len(lora) != 2:
             raise ValueError("lora must be (gate, up)")

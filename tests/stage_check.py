@@ -12,8 +12,9 @@ greedy token.
 Bar: 2e-3 + one bf16 rounding of the output (2^-8 relative); where a stage
 rounds an intermediate before its output (the module output + LoRA delta
 before the head norm and RoPE or the SiLU, the delta before the residual
-add), also one rounding of that intermediate carried to the output (2^-8
-times the magnitude the intermediate contributes to each output element).
+add, y formed from partial sums before the up-projection), also one
+rounding of that intermediate carried to the output (2^-8 times the
+magnitude the intermediate contributes to each output element).
 
 The adapter's A/B may be given (``adapter``: {(layer, module): (A, B)}), so
 the oracle works from the values a caller bound rather than from the
@@ -168,8 +169,14 @@ def stage_check(w, pool, reqs, first, dev, slot=0, adapter=None):
     # o_proj: base rows and the LoRA A rows' intermediate (side planes or columns)
     attn2 = attn.reshape(B, qd)
     o_out = L0["o"]
+    o_yc = 0.0
     if isinstance(o_out, dict):
+        # y from partial sums: the kernel rounds their fp32 sum, one rounding
+        # of y carried through B; the module output, rounded from a value
+        # that differs by that much, may then round to the neighbouring
+        # value: a second rounding of it (|o_main| stands for |o_mod|)
         o_main, o_y = _f(o_out["main"]), o_out["y"]
+        o_yc = s * (np.abs(o_y) @ np.abs(AB("o")[1]).T) + np.abs(o_main)
     elif isinstance(o_out, tuple):
         o_main, o_y = _f(o_out[0]), _f(o_out[1])[:, slot * r: (slot + 1) * r]
     else:
@@ -178,7 +185,7 @@ def stage_check(w, pool, reqs, first, dev, slot=0, adapter=None):
     worst["o_shrink"] = check("o_shrink", o_y, ol.linear(attn2, AB("o")[0]))
     # residual add of o + its delta, post-attention RMSNorm (norm.py:27-57)
     o_mod = ol.round_bf16(o_main + ol.up_projection(o_y, AB("o")[1], s))
-    worst["o_residual"] = check("o_residual", _f(L0["hidden_mid"]), hid + o_mod, np.abs(o_mod))
+    worst["o_residual"] = check("o_residual", _f(L0["hidden_mid"]), hid + o_mod, np.abs(o_mod) + o_yc)
     worst["post_norm"] = check("post_norm", _f(L0["x2"]), of.rmsnorm(_f(L0["hidden_mid"]), _f(lw.post_norm), eps))
     # gate/up GEMM, SiLU(gate) * up with both deltas (packed_ops.py:168-239)
     x2 = _f(L0["x2"])
@@ -194,16 +201,24 @@ def stage_check(w, pool, reqs, first, dev, slot=0, adapter=None):
     # down_proj, whose delta lands in layer 1's input add + RMSNorm
     act = _f(L0["act"])
     d_out = L0["down"]
-    if isinstance(d_out, tuple):
+    d_yc = 0.0
+    if isinstance(d_out, dict):
+        d_main, d_y = _f(d_out["main"]), d_out["y"]
+        d_yc = s * (np.abs(d_y) @ np.abs(AB("down")[1]).T) + np.abs(d_main)
+    elif isinstance(d_out, tuple):
         d_main, d_y = _f(d_out[0]), _f(d_out[1])[:, slot * r: (slot + 1) * r]
     else:
         d_main, d_y = _f(d_out)[:, : cfg.hidden], _f(d_out)[:, ycols("down")]
     worst["down_gemm"] = check("down_gemm", d_main, ol.linear(act, _f(lw.w_down)))
     worst["down_shrink"] = check("down_shrink", d_y, ol.linear(act, AB("down")[0]))
     d_mod = ol.round_bf16(d_main + ol.up_projection(d_y, AB("down")[1], s))
-    worst["down_residual"] = check("down_residual", _f(L1["hidden"]), _f(L1["hidden_in"]) + d_mod, np.abs(d_mod))
+    if "hidden" in L1:  # the add in layer 1's input add+RMSNorm
+        h_before, h_after = _f(L1["hidden_in"]), _f(L1["hidden"])
+    else:  # the add in down_proj's GEMM: layer 1 starts from the complete stream
+        h_before, h_after = _f(L0["hidden_mid"]), _f(L1["hidden_in"])
+    worst["down_residual"] = check("down_residual", h_after, h_before + d_mod, np.abs(d_mod) + d_yc)
     worst["next_input_norm"] = check("next_input_norm", _f(L1["x"]),
-                                     of.rmsnorm(_f(L1["hidden"]), _f(w.layers[1].input_norm), eps))
+                                     of.rmsnorm(h_after, _f(w.layers[1].input_norm), eps))
     worst.update(final_stages(w, rec.final, AB, slot))
     print("[stage check] err/bound: " + ", ".join(f"{k} {v:.2f}" for k, v in worst.items()), flush=True)
     return worst
@@ -219,7 +234,11 @@ def final_stages(w, F, AB, slot):
     last = cfg.num_layers - 1
     worst = {}
     d_out = F["final_down"]
-    if isinstance(d_out, tuple):
+    d_yc = 0.0
+    if isinstance(d_out, dict):
+        d_main, d_y = _f(d_out["main"]), d_out["y"]
+        d_yc = s * (np.abs(d_y) @ np.abs(AB("down", last)[1]).T) + np.abs(d_main)
+    elif isinstance(d_out, tuple):
         d_main, d_y = _f(d_out[0]), _f(d_out[1])[:, slot * r: (slot + 1) * r]
     else:
         lw = w.layers[last]
@@ -227,7 +246,7 @@ def final_stages(w, F, AB, slot):
         d_main, d_y = _f(d_out)[:, : cfg.hidden], _f(d_out)[:, c: c + r]
     d_mod = ol.round_bf16(d_main + ol.up_projection(d_y, AB("down", last)[1], s))
     worst["final_residual"] = check("final_residual", _f(F["final_hidden"]), _f(F["final_hidden_in"]) + d_mod,
-                                    np.abs(d_mod))
+                                    np.abs(d_mod) + d_yc)
     worst["final_norm"] = check("final_norm", _f(F["final_x"]),
                                 of.rmsnorm(_f(F["final_hidden"]), _f(w.final_norm), eps))
     # lm_head over the whole vocabulary in float64, 16384 rows at a time

@@ -319,17 +319,20 @@ def test_folded_qkv_matches_separate_epilogue(gpu_device, monkeypatch):
     assert torch.allclose(cf.float(), cs.float(), atol=0.05, rtol=0.02)
 
 
-def test_fused_post_attention_matches_add_rmsnorm(gpu_device, monkeypatch):
-    """The post-attention add + RMSNorm fused away (o_proj's shrink in the
-    merge, o_proj + delta + residual add in one GEMM, the norm in the
-    gate/up GEMM's prologue) against the add+RMSNorm kernel between separate
-    projections: the same logits to within the roundings that move (y's sum
-    order, the norm's sum of squares), the same greedy tokens, and the
-    appended K/V of layer 0 bit for bit (computed before the fused part)."""
+@pytest.mark.parametrize("fuse", ["post_attention", "both"])
+def test_fused_norms_match_add_rmsnorm(gpu_device, monkeypatch, fuse):
+    """The add + RMSNorm launches fused away (o_proj's shrink in the merge,
+    down_proj's in SiLU*up, each projection + delta + residual add in one
+    GEMM, the norms in the q/k/v and gate/up GEMMs' prologues) against the
+    add+RMSNorm kernels between separate projections: the same logits to
+    within the roundings that move (y's sum order, the norms' sums of
+    squares), the same greedy tokens, and the appended K/V of layer 0 bit for
+    bit (computed before any fused part)."""
     from pagelora_amd import decoder
     out = []
-    for fuse in (True, False):
-        monkeypatch.setattr(decoder, "FUSE_POST_ATTENTION_NORM", fuse)
+    for on in (True, False):
+        monkeypatch.setattr(decoder, "FUSE_NORMS", on)
+        monkeypatch.setattr(decoder, "FUSE_DOWN_NORM", on and fuse == "both")
         w, pool, reqs, first, _ = _setup128(gpu_device)
         out.append(_eager_step(w, pool, reqs, first, [0, 1, 1], gpu_device) + (pool.cache.clone(),))
     (lf, tf, cf), (ls, ts, cs) = out

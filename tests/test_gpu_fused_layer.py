@@ -256,3 +256,39 @@ def test_oshrink_rejects_a_skipped_merge(gpu_device):
         _lib.PL_DTYPE_BF16, be._plan["target_items"], _lib.PL_DECODE_SKIP_MERGE, be.workspace_buffer.data_ptr(),
         be.workspace_buffer.numel(), ctypes.byref(rows), ctypes.byref(p), None)
     assert st == _lib.PL_ERR_INVALID
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 4, 9])
+@pytest.mark.parametrize("rank,down_rank", [(16, 16), (8, 16), (16, 8)])
+@pytest.mark.parametrize("inter,bound", [(12288, 1), (12288, -1), (1056, -1)])
+def test_silu_shrink_matches_plain_silu(gpu_device, dtype, rows, rank, down_rank, inter, bound):
+    """SiLU*up with down_proj's LoRA shrink (pl_silu_mul_lora_shrink): its
+    output bit for bit against pl_silu_mul_lora, and the partial sums (one
+    per 512 columns) against the float64 product of that output with the
+    row's adapter's A rows."""
+    n_ad = 2
+    g = torch.Generator().manual_seed(rows * 13 + rank + down_rank + inter)
+    gu = (torch.randn((rows, 2 * inter + 2 * n_ad * rank), generator=g)).to(dtype).to(gpu_device)
+    Bg = (torch.randn((n_ad, inter, rank), generator=g) * 0.05).to(dtype).to(gpu_device)
+    Bu = (torch.randn((n_ad, inter, rank), generator=g) * 0.05).to(dtype).to(gpu_device)
+    lora = (fused_ops.LoraUp(gu, 2 * inter, Bg, 2.0, bound), fused_ops.LoraUp(gu, 2 * inter + n_ad * rank, Bu, 2.0, bound))
+    ids = torch.tensor([(b % (n_ad + 1)) - 1 for b in range(rows)], dtype=torch.int32, device=gpu_device)
+    hidden = 256
+    Wd = (torch.randn((hidden + n_ad * down_rank, inter), generator=g) * 0.02).to(dtype)
+    sw = ShuffledWeight(Wd.to(gpu_device))
+    parts = LoraPartials(torch.full((rows, -(-inter // 512), down_rank), float("nan"), device=gpu_device))
+    act = fused_ops.silu_mul(gu[:, : 2 * inter], lora=lora, adapter_ids=ids,
+                             down_shrink=(lora_a_rows(sw, hidden, down_rank, bound), parts))
+    ref = fused_ops.silu_mul(gu[:, : 2 * inter], lora=lora, adapter_ids=ids)
+    torch.cuda.synchronize()
+    assert torch.equal(act, ref), "SiLU*up output differs with the down shrink"
+    A = _np(Wd[hidden:]).reshape(n_ad, down_rank, inter)
+    ids_h = ids.cpu().numpy() if bound < 0 else np.full(rows, bound)
+    got = parts.sum().cpu().numpy()
+    x = _np(act)
+    for b in range(rows):
+        a = ids_h[b] if 0 <= ids_h[b] < n_ad else 0
+        want = A[a] @ x[b]
+        bar = 1e-6 + 2e-5 * (np.abs(A[a]) @ np.abs(x[b]))
+        assert (np.abs(got[b] - want) <= bar).all(), f"row {b}: shrink partials off by {np.abs(got[b] - want).max():.3e}"
