@@ -1491,7 +1491,7 @@ __global__ __launch_bounds__(MT) void merge_kernel(
   if constexpr (OR > 0) {
     __syncthreads();
     // products of the A pieces with the stored output, summed over the LPT
-    // consecutive lanes of each rank (fixed butterfly order)
+    // consecutive lanes of each rank (DPP, fixed order)
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
       const int i = (int)threadIdx.x + j * MT;
@@ -1504,8 +1504,7 @@ __global__ __launch_bounds__(MT) void merge_kernel(
       float acc = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc = fmaf(s_ov[c][e], f[e], acc);
-#pragma unroll
-      for (int off = LPT / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+      acc = group_sum(acc, LPT == 16 ? 4 : LPT == 8 ? 3 : LPT == 4 ? 2 : LPT == 2 ? 1 : 0);
       if (c == 0 && i < NP) os.part[(int64_t)b * os.ld + (int64_t)(hq * DS + ds) * OR + r] = acc;
     }
   }

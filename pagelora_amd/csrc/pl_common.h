@@ -206,6 +206,28 @@ __device__ __forceinline__ float wave_sum(float x) {
   return (lane_value(x, 0) + lane_value(x, 16)) + (lane_value(x, 32) + lane_value(x, 48));
 }
 
+// All-reduce over aligned groups of 2^lg lanes (0 <= lg <= 6, wave
+// uniform) with DPP and lane reads, no LDS traffic; every lane of a group
+// gets the group's sum (lanes of one group may associate the terms in
+// different orders, each lane always the same way).
+__device__ __forceinline__ float group_sum(float x, int lg) {
+  if (lg >= 4) {
+    x = row16_sum(x);
+    if (lg == 4) return x;
+    const float r0 = lane_value(x, 0), r1 = lane_value(x, 16), r2 = lane_value(x, 32), r3 = lane_value(x, 48);
+    if (lg == 6) return (r0 + r1) + (r2 + r3);
+    return (threadIdx.x & 32) ? r2 + r3 : r0 + r1;
+  }
+  if (lg == 3) {
+    x += dpp_mov<0x141>(x);  // row_half_mirror: lane i of each 8 with lane 7 - i
+    x += dpp_mov<0x1b>(x);   // quad_perm [3,2,1,0]
+    return x + dpp_mov<0xb1>(x);  // quad_perm [1,0,3,2]
+  }
+  if (lg >= 1) x += dpp_mov<0xb1>(x);  // quad_perm [1,0,3,2]
+  if (lg == 2) x += dpp_mov<0x4e>(x);  // quad_perm [2,3,0,1]
+  return x;
+}
+
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // exp2 on the hardware transcendental unit (v_exp_f32).

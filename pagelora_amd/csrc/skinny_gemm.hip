@@ -466,8 +466,8 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_normsq_kernel(
 // to a power of two, p >= parts reading as 0) over the tile's tokens, one
 // float4 of ranks 4q .. 4q+3 per f, YPT of them per thread.  They are loaded
 // before the weights and summed while the first batch of weight blocks is in
-// flight: a butterfly over min(G, 64) lanes, then the per-wave slices of
-// groups wider than a wave in order through LDS.
+// flight: over min(G, 64) lanes with DPP (group_sum), then the per-wave
+// slices of groups wider than a wave in order through LDS.
 constexpr int kAddMaxYPT = 4;
 
 template <typename T, int R, int YPT>
@@ -553,12 +553,7 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
     for (int c = 0; c < YPT; ++c) {
       const float m = yon[c] ? 1.f : 0.f;
       float4 v = make_float4(yv[c].x * m, yv[c].y * m, yv[c].z * m, yv[c].w * m);
-      for (int off = 1; off < (1 << lgw); off <<= 1) {
-        v.x += __shfl_xor(v.x, off);
-        v.y += __shfl_xor(v.y, off);
-        v.z += __shfl_xor(v.z, off);
-        v.w += __shfl_xor(v.w, off);
-      }
+      v = make_float4(group_sum(v.x, lgw), group_sum(v.y, lgw), group_sum(v.z, lgw), group_sum(v.w, lgw));
       const int f = threadIdx.x + c * kThreads;
       const int p = f & (G - 1), tq = f >> lg;
       if ((p & ((1 << lgw) - 1)) == 0 && tq < nt * Q) s_y[tq * slices + (p >> lgw)] = v;
