@@ -188,7 +188,14 @@ __host__ __device__ constexpr int norm_lds_bytes(int nt, int K) {
   return nt * (K + kNormRowPad) * 2 + K * 2 > kRedBytes ? nt * (K + kNormRowPad) * 2 + K * 2 : kRedBytes;
 }
 
-template <typename T, int PPT>
+// HOLD: the rows stay in registers across the first barrier (no LDS copy of
+// the raw rows) and only the first batch of weights is preloaded: faster
+// for a grid that fits the chip at once (q/k/v at 4 tokens: 12.7 vs 13.5
+// us), where a second preloaded batch costs registers that the raw-row LDS
+// copy makes room for; a grid of several rounds (gate/up) overlaps the
+// prologue with other workgroups' streams and keeps the two-batch preload
+// (34.1 vs 35.6 us).
+template <typename T, int PPT, bool HOLD>
 __global__ __launch_bounds__(kThreads) void shuffled_gemm_norm_kernel(
     const T* __restrict__ x, int64_t ldx, int tokens, int K, const T* __restrict__ nw, float eps,
     const T* __restrict__ Ws, int N, T* __restrict__ out, int64_t ldo, T* __restrict__ xn_out, int64_t ldxn) {
@@ -229,8 +236,11 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_norm_kernel(
   u32x4 b[kUnroll], b1[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) b[u] = __builtin_nontemporal_load(wb + min(sb + u, ksteps - 1) * kWave);
+  if constexpr (!HOLD) {
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) b1[u] = __builtin_nontemporal_load(wb + min(sb + kUnroll + u, ksteps - 1) * kWave);
+    for (int u = 0; u < kUnroll; ++u)
+      b1[u] = __builtin_nontemporal_load(wb + min(sb + kUnroll + u, ksteps - 1) * kWave);
+  }
   __builtin_amdgcn_sched_barrier(0);
   // unconditional (threads past the K / 8 pieces rewrite piece 0 with its
   // own value): a store under a test drags its load below the weights'
@@ -238,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_norm_kernel(
 #pragma unroll
   for (int c = 0; c < PPT; ++c) {
     const int j = threadIdx.x + c * kThreads;
-    if (j < pieces) {
+    if (!HOLD && j < pieces) {
       const int tt = j / rp, cc = j - tt * rp;
       *reinterpret_cast<uint4*>(xs + tt * Kp + cc * 8) = hv[c];
     }
@@ -255,17 +265,14 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_norm_kernel(
   }
   __syncthreads();
   const int slices = rp / kWave;  // per row
-  // one piece at a time: the weight batches are live here, and two pieces'
-  // temporaries at once would raise the kernel's register count
-#pragma unroll 1
-  for (int c = 0; c < PPT; ++c) {
+  auto normalize_piece = [&](int c, const uint4& held) {
     const int j = threadIdx.x + c * kThreads;
     if (j < pieces) {
       const int tt = j / rp, cc = j - tt * rp;
       float tot = 0.f;
       for (int s = 0; s < slices; ++s) tot += s_ss[tt * slices + s];
       const float rstd = rsqrtf(tot / (float)K + eps);
-      const uint4 hw = *reinterpret_cast<const uint4*>(xs + tt * Kp + cc * 8), ww = sw8[cc];
+      const uint4 hw = HOLD ? held : *reinterpret_cast<const uint4*>(xs + tt * Kp + cc * 8), ww = sw8[cc];
       auto norm2 = [&](uint32_t h2, uint32_t w2) {
         float f0, f1, w0, w1;
         unpack2<T>(h2, f0, f1);
@@ -277,6 +284,17 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_norm_kernel(
       if (xn_out != nullptr && blockIdx.x == 0)
         *reinterpret_cast<uint4*>(xn_out + (int64_t)(t0 + tt) * ldxn + cc * 8) = o;
     }
+  };
+  if constexpr (HOLD) {
+    // the held rows: unrolled, so they stay in registers (a loop index into
+    // them would place them in scratch memory)
+#pragma unroll
+    for (int c = 0; c < PPT; ++c) normalize_piece(c, hv[c]);
+  } else {
+    // one piece at a time: the weight batches are live here, and two
+    // pieces' temporaries at once would raise the kernel's register count
+#pragma unroll 1
+    for (int c = 0; c < PPT; ++c) normalize_piece(c, hv[0]);
   }
   __syncthreads();
 
@@ -292,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_norm_kernel(
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[u], b[u], acc);
     s += kUnroll;
-    if (s + kUnroll <= se) {
+    if (!HOLD && s + kUnroll <= se) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) a[u] = *reinterpret_cast<const u32x4*>(xr + (s + u) * 32);
 #pragma unroll
@@ -784,13 +802,20 @@ extern "C" int pl_linear_shuffled_side(const void* x, int64_t ldx, int num_token
   return ok();
 }
 
+constexpr int kGemmCUs = 256;  // MI355X
+
 template <typename T, int PPT>
 static void launch_norm_gemm(const void* x, int64_t ldx, int num_tokens, int K, const void* nw, float eps,
                              const void* Ws, int N, void* out, int64_t ldo, void* xn, int64_t ldxn, hipStream_t s) {
   const int nt = std::min(num_tokens, 16);
   const dim3 grid((N + 15) / 16, (num_tokens + 15) / 16);
-  hipLaunchKernelGGL((shuffled_gemm_norm_kernel<T, PPT>), grid, dim3(kThreads), norm_lds_bytes(nt, K), s,
-                     (const T*)x, ldx, num_tokens, K, (const T*)nw, eps, (const T*)Ws, N, (T*)out, ldo, (T*)xn, ldxn);
+  // two workgroups per CU: a grid of at most that many runs in one round
+  if ((int64_t)grid.x * grid.y <= 2 * kGemmCUs)
+    hipLaunchKernelGGL((shuffled_gemm_norm_kernel<T, PPT, true>), grid, dim3(kThreads), norm_lds_bytes(nt, K), s,
+                       (const T*)x, ldx, num_tokens, K, (const T*)nw, eps, (const T*)Ws, N, (T*)out, ldo, (T*)xn, ldxn);
+  else
+    hipLaunchKernelGGL((shuffled_gemm_norm_kernel<T, PPT, false>), grid, dim3(kThreads), norm_lds_bytes(nt, K), s,
+                       (const T*)x, ldx, num_tokens, K, (const T*)nw, eps, (const T*)Ws, N, (T*)out, ldo, (T*)xn, ldxn);
 }
 
 template <typename T>
