@@ -486,9 +486,15 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_normsq_kernel(
 // before the weights and summed while the first batch of weight blocks is in
 // flight: over min(G, 64) lanes with DPP (group_sum), then the per-wave
 // slices of groups wider than a wave in order through LDS.
+//
+// NB > 0: every wave has exactly NB batches of weight blocks (K = 16 * 4 *
+// NB * 32) and the grid is at most one workgroup per CU, so a wave may hold
+// 128 registers: two batches are kept in flight (the next but one is issued
+// after each batch's MFMAs) instead of one.  NB == 0: any K, one batch at a
+// time, at most 64 registers.
 constexpr int kAddMaxYPT = 4;
 
-template <typename T, int R, int YPT>
+template <typename T, int R, int YPT, int NB>
 __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
     const T* __restrict__ x, int64_t ldx, int tokens, int K, const T* __restrict__ Ws, int N,
     T* __restrict__ res, int64_t ldr, LoraUp lora, const float* __restrict__ yp, int64_t ldyp, int parts, int lg,
@@ -552,13 +558,18 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
     const int nc = min(nb * 16 + col, N - 1);
     bpc = *lora_b_piece<T, R>(lora, a_ok_ld ? a_raw : 0, nc & ~7, nc & 7, kb);
   }
-  u32x4 b[kUnroll], a[kUnroll];
+  constexpr int NQ = NB > 0 ? NB : 1;
+  u32x4 b[NQ][kUnroll], a[NQ][kUnroll];
+  auto issue = [&](int q, int s0) {
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int s = min(sb + u, ksteps - 1);
-    b[u] = __builtin_nontemporal_load(wb + s * kWave);
-    a[u] = *reinterpret_cast<const u32x4*>(xr + s * 32);
-  }
+    for (int u = 0; u < kUnroll; ++u) {
+      const int s = min(s0 + u, ksteps - 1);
+      b[q][u] = __builtin_nontemporal_load(wb + s * kWave);
+      a[q][u] = *reinterpret_cast<const u32x4*>(xr + s * 32);
+    }
+  };
+  issue(0, sb);
+  if constexpr (NB > 1) issue(1, sb + kUnroll);
   s_res[ri] = to_float<T>(rv_ld);
   if constexpr (R > 0) {
     constexpr int KB = R / 8;
@@ -579,25 +590,33 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
   }
 
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  int s = sb;
-  if (s + kUnroll <= se) {
+  if constexpr (NB > 0) {
+    // batch i + 2 reuses batch i's registers once its MFMAs have read them
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[u], b[u], acc);
-    s += kUnroll;
-  }
-  for (; s + kUnroll <= se; s += kUnroll) {
+    for (int i = 0; i < NB; ++i) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) b[u] = __builtin_nontemporal_load(wb + (s + u) * kWave);
+      for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[i][u], b[i][u], acc);
+      if (i + 2 < NB) issue(i + 2, sb + (i + 2) * kUnroll);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    int s = sb;
+    if (s + kUnroll <= se) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) a[u] = *reinterpret_cast<const u32x4*>(xr + (s + u) * 32);
-    __builtin_amdgcn_sched_barrier(0);
+      for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[0][u], b[0][u], acc);
+      s += kUnroll;
+    }
+    for (; s + kUnroll <= se; s += kUnroll) {
+      issue(0, s);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[u], b[u], acc);
-  }
-  for (; s < se; ++s) {
-    const u32x4 bb = __builtin_nontemporal_load(wb + s * kWave);
-    const u32x4 aa = *reinterpret_cast<const u32x4*>(xr + s * 32);
-    acc = mfma32<T>(aa, bb, acc);
+      for (int u = 0; u < kUnroll; ++u) acc = mfma32<T>(a[0][u], b[0][u], acc);
+    }
+    for (; s < se; ++s) {
+      const u32x4 bb = __builtin_nontemporal_load(wb + s * kWave);
+      const u32x4 aa = *reinterpret_cast<const u32x4*>(xr + s * 32);
+      acc = mfma32<T>(aa, bb, acc);
+    }
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) s_red[wave][((lane / 16) * 4 + i) * 16 + lr] = acc[i];
@@ -903,9 +922,19 @@ static void launch_add_gemm(const void* x, int64_t ldx, int num_tokens, int K, c
                             int64_t ldr, const LoraUp& lu, const pl_lora_partials* yp, int lg, const int32_t* ids,
                             int na, void* out, int64_t ldo, float* sq, int64_t ldsq, hipStream_t s) {
   const dim3 grid((N + 15) / 16, (num_tokens + 15) / 16);
-  hipLaunchKernelGGL((shuffled_gemm_add_kernel<T, R, YPT>), grid, dim3(kThreads), 0, s, (const T*)x, ldx,
-                     num_tokens, K, (const T*)Ws, N, (T*)res, ldr, lu, yp ? yp->partials : nullptr,
-                     yp ? yp->ld : 0, yp ? yp->parts : 0, lg, ids, na, (T*)out, ldo, sq, ldsq);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, (const T*)x, ldx, num_tokens, K, (const T*)Ws, N,
+                       (T*)res, ldr, lu, yp ? yp->partials : nullptr, yp ? yp->ld : 0, yp ? yp->parts : 0, lg, ids,
+                       na, (T*)out, ldo, sq, ldsq);
+  };
+  // two batches in flight per wave where the grid is one workgroup per CU
+  // and K splits into whole batches per wave (o_proj 4096, down_proj 12288)
+  const int ksteps = K / 32;
+  const int nb = ksteps % (kWaves * kUnroll) == 0 ? ksteps / (kWaves * kUnroll) : 0;
+  const bool one_round = (int64_t)grid.x * grid.y <= kGemmCUs;
+  if (one_round && nb == 2) go(shuffled_gemm_add_kernel<T, R, YPT, 2>);
+  else if (one_round && nb == 6) go(shuffled_gemm_add_kernel<T, R, YPT, 6>);
+  else go(shuffled_gemm_add_kernel<T, R, YPT, 0>);
 }
 
 template <typename T>

@@ -140,30 +140,43 @@ def _add_case(gpu_device, dtype, tokens, rank, parts, n_ad, bound, layout, n=409
 @pytest.mark.parametrize("rank", [8, 16])
 @pytest.mark.parametrize("mode", ["ids", "bound", "chunk8"])
 def test_add_gemm(gpu_device, dtype, tokens, parts, rank, mode):
+    _check_add_gemm(gpu_device, dtype, tokens, parts, rank, mode)
+
+
+# K = 12288 (down_proj: six weight batches per wave, two in flight), a K that
+# splits into no whole batches per wave, and a grid of more than one
+# workgroup per CU (both take the one-batch loop)
+@pytest.mark.parametrize("n,k", [(4096, 12288), (4096, 4608), (5120, 4096), (64, 12288)])
+def test_add_gemm_shapes(gpu_device, n, k):
+    _check_add_gemm(gpu_device, torch.bfloat16, 4, 24, 16, "bound", n=n, k=k)
+
+
+def _check_add_gemm(gpu_device, dtype, tokens, parts, rank, mode, n=4096, k=4096):
     n_ad = 2
     bound = 1 if mode == "bound" else -1
     x, W, B, yp, hid, ids, sw, lora = _add_case(gpu_device, dtype, tokens, rank, parts, n_ad, bound,
-                                                "chunk8" if mode == "chunk8" else "rows")
+                                                "chunk8" if mode == "chunk8" else "rows", n=n, k=k)
     res = hid.to(gpu_device)
     base = torch.empty_like(res)
     ids_d = ids.to(gpu_device)
-    sq = torch.full((tokens, 260), float("nan"), device=gpu_device)
-    linear_shuffled_add(x.to(gpu_device), sw, 4096, res, lora, LoraPartials(yp.to(gpu_device)),
+    nblk = (n + 15) // 16
+    sq = torch.full((tokens, nblk + 4), float("nan"), device=gpu_device)
+    linear_shuffled_add(x.to(gpu_device), sw, n, res, lora, LoraPartials(yp.to(gpu_device)),
                         ids_d if bound < 0 else None, out=base, sq_out=sq)
-    ref = linear_shuffled(x.to(gpu_device), sw)[:, :4096]
+    ref = linear_shuffled(x.to(gpu_device), sw)[:, :n]
     torch.cuda.synchronize()
     assert torch.equal(base, ref), "base output differs from pl_linear_shuffled"
     # the squares of the stored residual per 16 columns (fp32 sums of 16 terms)
-    r64 = _np(res).reshape(tokens, 256, 16)
+    r64 = _np(res).reshape(tokens, nblk, 16)
     sq_want = (r64 ** 2).sum(axis=2)
-    sq_got = sq[:, :256].double().cpu().numpy()
+    sq_got = sq[:, :nblk].double().cpu().numpy()
     assert (np.abs(sq_got - sq_want) <= 1e-5 * sq_want + 1e-30).all(), "sums of squares"
-    assert torch.isnan(sq[:, 256:]).all(), "sq_out written past its blocks"
+    assert torch.isnan(sq[:, nblk:]).all(), "sq_out written past its blocks"
     rel = REL[dtype]
     y = yp.double().sum(dim=1).numpy()
     ok_id = np.array([bound] * tokens) if bound >= 0 else ids.numpy()
-    want = np.empty((tokens, 4096))
-    carry = np.empty((tokens, 4096))
+    want = np.empty((tokens, n))
+    carry = np.empty((tokens, n))
     b_base = _np(base)
     for t in range(tokens):
         a = ok_id[t]
