@@ -53,6 +53,23 @@ template <> __device__ __forceinline__ f32x4 mfma32<f16_t>(u32x4 a, u32x4 b, f32
                                                 0);
 }
 
+// The cross-wave sum of one cell of a workgroup's 16-token x 16-column tile
+// (s_red[wave][token * 16 + column]): lane l of wave w takes token
+// 4 * w + l / 16 and column l % 16, so at most four waves work and at four
+// tokens one wave finishes the tile in one pass (one wave looping over the
+// cells measured 0.4-0.5 us slower per launch at 4 tokens).  Lanes past the
+// tile's nt tokens sum token 0's cell and return false.
+__device__ __forceinline__ bool tile_cell_sum(const float (*s_red)[256], int wave, int lane, int nt, int& tl,
+                                              float& sum) {
+  tl = wave * 4 + lane / 16;
+  const bool live = tl < nt;
+  const int cell = (live ? tl : 0) * 16 + lane % 16;
+  sum = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) sum += s_red[w][cell];
+  return live;
+}
+
 // One thread per 16-byte piece of the shuffled buffer (N_pad x K elements).
 __global__ void shuffle_kernel(const uint16_t* __restrict__ W, int64_t ldw, int N, int K, uint16_t* __restrict__ Ws,
                                int64_t pieces) {
@@ -145,25 +162,20 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_kernel(const T* __rest
 #pragma unroll
   for (int i = 0; i < 4; ++i) s_red[wave][((lane / 16) * 4 + i) * 16 + lr] = acc[i];
   __syncthreads();
-  if (wave == 0) {
-    const int n = nb * 16 + lr;
-    const float bv = (!PARTIAL && !side && bias != nullptr && n < N) ? to_float<T>(bias[n]) : 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int cell = ((lane / 16) * 4 + i) * 16 + lr;
-      float sum = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) sum += s_red[w][cell];
-      const int tr = t0 + (lane / 16) * 4 + i;
-      if (n < N && tr < tokens) {
-        if (PARTIAL)
-          partial[(int64_t)blockIdx.z * plane_stride + (int64_t)tr * ldp + n] = sum;
-        else if (side)
-          partial[(int64_t)zs * plane_stride + (int64_t)tr * ldp + (n - main_tiles * 16)] = sum;
-        else
-          out[(int64_t)tr * ldo + n] = from_float<T>(sum + bv);
-      }
-    }
+  const int nt = min(16, tokens - t0);
+  if (wave * 4 >= nt) return;
+  const int n = nb * 16 + lr;
+  const float bv = (!PARTIAL && !side && bias != nullptr && n < N) ? to_float<T>(bias[n]) : 0.f;
+  int tl;
+  float sum;
+  if (tile_cell_sum(s_red, wave, lane, nt, tl, sum) && n < N) {
+    const int tr = t0 + tl;
+    if (PARTIAL)
+      partial[(int64_t)blockIdx.z * plane_stride + (int64_t)tr * ldp + n] = sum;
+    else if (side)
+      partial[(int64_t)zs * plane_stride + (int64_t)tr * ldp + (n - main_tiles * 16)] = sum;
+    else
+      out[(int64_t)tr * ldo + n] = from_float<T>(sum + bv);
   }
 }
 
@@ -337,18 +349,11 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_norm_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) s_red[wave][((lane / 16) * 4 + i) * 16 + lr] = acc[i];
   __syncthreads();
-  if (wave == 0) {
-    const int n = nb * 16 + lr;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int cell = ((lane / 16) * 4 + i) * 16 + lr;
-      float sum = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) sum += s_red[w][cell];
-      const int tr = t0 + (lane / 16) * 4 + i;
-      if (n < N && tr < tokens) out[(int64_t)tr * ldo + n] = from_float<T>(sum);
-    }
-  }
+  if (wave * 4 >= nt) return;
+  const int n = nb * 16 + lr;
+  int tl;
+  float sum;
+  if (tile_cell_sum(s_red, wave, lane, nt, tl, sum) && n < N) out[(int64_t)(t0 + tl) * ldo + n] = from_float<T>(sum);
 }
 
 // ------------------------------------ norm from the producer's squares ---
@@ -463,18 +468,11 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_normsq_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) s_red[wave][((lane / 16) * 4 + i) * 16 + lr] = acc[i];
   __syncthreads();
-  if (wave == 0) {
-    const int n = nb * 16 + lr;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int cell = ((lane / 16) * 4 + i) * 16 + lr;
-      float sum = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) sum += s_red[w][cell];
-      const int tr = t0 + (lane / 16) * 4 + i;
-      if (n < N && tr < tokens) out[(int64_t)tr * ldo + n] = from_float<T>(sum);
-    }
-  }
+  if (wave * 4 >= nt) return;
+  const int n = nb * 16 + lr;
+  int tl;
+  float sum;
+  if (tile_cell_sum(s_red, wave, lane, nt, tl, sum) && n < N) out[(int64_t)(t0 + tl) * ldo + n] = from_float<T>(sum);
 }
 
 // --------------------------------------------- residual + LoRA epilogue ---
@@ -485,7 +483,10 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_normsq_kernel(
 // float4 of ranks 4q .. 4q+3 per f, YPT of them per thread.  They are loaded
 // before the weights and summed while the first batch of weight blocks is in
 // flight: over min(G, 64) lanes with DPP (group_sum), then the per-wave
-// slices of groups wider than a wave in order through LDS.
+// slices of groups wider than a wave in order through LDS.  The epilogue
+// gives every (token, column) cell its own lane (tile_cell_sum): one wave
+// looping over the tokens cost 1.1 us more per launch at o_proj's and
+// down_proj's shapes.
 //
 // NB > 0: every wave has exactly NB batches of weight blocks (K = 16 * 4 *
 // NB * 32) and the grid is at most one workgroup per CU, so a wave may hold
@@ -505,7 +506,6 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
   // (t, q) group x slice: at most YPT * kThreads / kWave entries (G <= 64:
   // one slice per group, nt * Q <= 64 groups; G > 64: nt * Q * G / 64)
   __shared__ float4 s_y[R > 0 ? kAddMaxYPT * kThreads / kWave : 1];
-  __shared__ uint4 s_yr[R > 0 ? 16 * (R / 8) : 1];  // y rounded to T: token tl's ranks 8k .. at tl * R/8 + k
   // the epilogue's inputs, loaded with the partials: the residual tile and
   // the B pieces of the workgroup's 16 columns (token tl, column c, ranks 8k ..)
   __shared__ float s_res[16 * 16];
@@ -621,12 +621,20 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) s_red[wave][((lane / 16) * 4 + i) * 16 + lr] = acc[i];
   __syncthreads();
-  if (wave != 0) return;
+  if (wave * 4 >= nt) return;
+  int tl;
+  float sum;
+  const bool live = tile_cell_sum(s_red, wave, lane, nt, tl, sum);
+  const int tr = t0 + tl, tc = live ? tl : 0;
+  const int cell = tc * 16 + lr;
+  float xa = through<T>(sum);
   if constexpr (R > 0) {
-    // y of (token, 8 ranks): the wave slices in order, rounded to T (the
-    // lanes' LDS writes and the reads below are one wave's, in order)
-    if (lane < nt * (R / 8)) {
-      const int g0 = lane * 2;  // the two quads of ranks 8k ..
+    // y of the token, 8 ranks per piece: the wave slices in order, rounded to T
+    constexpr int KB = R / 8;
+    float d = 0.f;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      const int g0 = (tc * KB + k) * 2;  // the two quads of ranks 8k ..
       float4 lo = s_y[g0 * slices], hi = s_y[(g0 + 1) * slices];
 #pragma unroll 1
       for (int sl = 1; sl < slices; ++sl) {
@@ -634,39 +642,24 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
         lo.x += l2.x; lo.y += l2.y; lo.z += l2.z; lo.w += l2.w;
         hi.x += h2.x; hi.y += h2.y; hi.z += h2.z; hi.w += h2.w;
       }
-      s_yr[lane] = make_uint4(pack2<T>(lo.x, lo.y), pack2<T>(lo.z, lo.w), pack2<T>(hi.x, hi.y), pack2<T>(hi.z, hi.w));
+      const uint4 yr = make_uint4(pack2<T>(lo.x, lo.y), pack2<T>(lo.z, lo.w), pack2<T>(hi.x, hi.y), pack2<T>(hi.z, hi.w));
+      d = dot8<T>(yr, s_b[cell * KB + k], d);
     }
+    d *= lora.scale;
+    xa = through<T>(xa + (s_ok[tc] ? d : -0.f));
   }
+  const T v = from_float<T>(s_res[cell] + xa);
   const int n = nb * 16 + lr;
-#pragma unroll 1
-  for (int i = 0; i < 4; ++i) {
-    const int tl = (lane / 16) * 4 + i, tr = t0 + tl;
-    if (tl >= nt) break;  // uniform per 16-lane group
-    const int cell = tl * 16 + lr;
-    float sum = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) sum += s_red[w][cell];
-    float xa = through<T>(sum);
-    if constexpr (R > 0) {
-      constexpr int KB = R / 8;
-      float d = 0.f;
-#pragma unroll
-      for (int k = 0; k < KB; ++k) d = dot8<T>(s_yr[tl * KB + k], s_b[cell * KB + k], d);
-      d *= lora.scale;
-      xa = through<T>(xa + (s_ok[tl] ? d : -0.f));
-    }
-    const T v = from_float<T>(s_res[cell] + xa);
-    if (n < N) {
-      res[(int64_t)tr * ldr + n] = v;
-      if (out != nullptr) out[(int64_t)tr * ldo + n] = from_float<T>(sum);
-    }
-    if (sq_out != nullptr) {
-      // the squares of the stored residual over the block's columns (the 16
-      // lanes of this token's group), for the next RMSNorm
-      const float vf = n < N ? to_float<T>(v) : 0.f;
-      const float q = row16_sum(vf * vf);
-      if (lr == 0) sq_out[(int64_t)tr * ldsq + nb] = q;
-    }
+  if (live && n < N) {
+    res[(int64_t)tr * ldr + n] = v;
+    if (out != nullptr) out[(int64_t)tr * ldo + n] = from_float<T>(sum);
+  }
+  if (sq_out != nullptr) {
+    // the squares of the stored residual over the block's columns (the 16
+    // lanes of this token's group), for the next RMSNorm
+    const float vf = n < N ? to_float<T>(v) : 0.f;
+    const float q = row16_sum(vf * vf);
+    if (live && lr == 0) sq_out[(int64_t)tr * ldsq + nb] = q;
   }
 }
 
