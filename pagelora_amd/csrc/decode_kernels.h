@@ -891,6 +891,26 @@ __device__ __forceinline__ void prefix_wave(const DirectScan& sc, const Direct& 
   const int pg_a = uniform(indices[min(ip0 + tok0 / page_size, last_idx)]);
   const int pg_b = uniform(indices[min(ip0 + (tok0 + 16) / page_size, last_idx)]);
   __builtin_amdgcn_sched_barrier(0);
+  // ---- K (A operand: token l % 16 of each block, dims 8 (l/16) + 32 jj) and
+  // V (token rows l/16 + 4 s of the 32, dims 8 (l % 16) ..) of the 32 tokens,
+  // issued before q is formed (a wave past the prefix reads chunk 0's)
+  auto tok_addr = [&](int t) -> int64_t {  // element offset of token t of the item, kv head h
+    const int tt = tok0 + t;
+    int64_t pg = (tt - tok0) < 16 ? pg_a : pg_b;
+    pg = pg < 0 ? 0 : (pg >= num_pages ? num_pages - 1 : pg);
+    return pg * page_stride + (int64_t)(tt % page_size) * token_stride + (int64_t)h * head_stride;
+  };
+  uint32_t kw[2][4][4];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const T* kp = kc + tok_addr(blk * 16 + col) + 8 * rg;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const uint4 t = *reinterpret_cast<const uint4*>(kp + 32 * jj);
+      kw[blk][jj][0] = t.x; kw[blk][jj][1] = t.y; kw[blk][jj][2] = t.z; kw[blk][jj][3] = t.w;
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   {
     float v[8];
     head_finish<T, R>(qin, x, 0, col, qin.q_norm_w != nullptr, true, R > 0, v);
@@ -908,24 +928,6 @@ __device__ __forceinline__ void prefix_wave(const DirectScan& sc, const Direct& 
     for (int jj = 0; jj < 4; ++jj) {
       const uint4 t = s_q[qrow][lane % 4][4 * jj + lane / 16];
       qb[jj][0] = t.x; qb[jj][1] = t.y; qb[jj][2] = t.z; qb[jj][3] = t.w;
-    }
-  }
-  // ---- K (A operand: token l % 16 of each block, dims 8 (l/16) + 32 jj) and
-  // V (token rows l/16 + 4 s of the 32, dims 8 (l % 16) ..) of the 32 tokens
-  auto tok_addr = [&](int t) -> int64_t {  // element offset of token t of the item, kv head h
-    const int tt = tok0 + t;
-    int64_t pg = (tt - tok0) < 16 ? pg_a : pg_b;
-    pg = pg < 0 ? 0 : (pg >= num_pages ? num_pages - 1 : pg);
-    return pg * page_stride + (int64_t)(tt % page_size) * token_stride + (int64_t)h * head_stride;
-  };
-  uint32_t kw[2][4][4];
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk) {
-    const T* kp = kc + tok_addr(blk * 16 + col) + 8 * rg;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const uint4 t = *reinterpret_cast<const uint4*>(kp + 32 * jj);
-      kw[blk][jj][0] = t.x; kw[blk][jj][1] = t.y; kw[blk][jj][2] = t.z; kw[blk][jj][3] = t.w;
     }
   }
   uint4 vr[8];
