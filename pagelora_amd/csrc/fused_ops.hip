@@ -479,27 +479,50 @@ __global__ __launch_bounds__(kWave) void silu_mul_shrink_kernel(const T* __restr
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = g[i] / (1.f + expf(-g[i])) * u[i];
   if (live) store_row8<T>(out + row * ldo + chunk * 8, o);
-  // the shrink of the stored values
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = live ? through<T>(o[i]) : 0.f;
+  // the shrink of the stored values: their 16-bit pairs (the same rounding as
+  // the store; idle lanes zero) against the A pieces on v_dot2
+  uint4 ov = make_uint4(pack2_hw<T>(o[0], o[1]), pack2_hw<T>(o[2], o[3]), pack2_hw<T>(o[4], o[5]),
+                        pack2_hw<T>(o[6], o[7]));
+  if (!live) ov = make_uint4(0u, 0u, 0u, 0u);
   float p[OR];
 #pragma unroll
-  for (int r = 0; r < OR; ++r) {
-    float f[8];
-    unpack2<T>(ap[r].x, f[0], f[1]);
-    unpack2<T>(ap[r].y, f[2], f[3]);
-    unpack2<T>(ap[r].z, f[4], f[5]);
-    unpack2<T>(ap[r].w, f[6], f[7]);
-    float acc = 0.f;
+  for (int r = 0; r < OR; ++r) p[r] = dot8<T>(ov, ap[r], 0.f);
+  // Transposed reduction: each step pairs lanes with DPP and halves the
+  // values a lane holds (it keeps one of each pair and adds its partner's),
+  // until lane i of every 16-lane row holds rank rank_of(i) summed over the
+  // row; then the rows are summed.
+  const int lr = lane % 16;
+  float x;
+  {
+    float w8[OR / 2];
+    const bool s3 = lr & 8;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc = fmaf(o[i], f[i], acc);
-    p[r] = wave_sum(acc);
-  }
-  if (lane == 0) {
-    float* dst = ds.part + (int64_t)row * ds.ldp + (int64_t)blockIdx.x * OR;
+    for (int k = 0; k < OR / 2; ++k)
+      w8[k] = (s3 ? p[2 * k + 1] : p[2 * k]) + dpp_mov<0x128>(s3 ? p[2 * k] : p[2 * k + 1]);  // row_ror:8: lane ^ 8
+    float w4[OR / 4];
+    const bool s2 = lr & 4;
 #pragma unroll
-    for (int r = 0; r < OR; r += 4) *reinterpret_cast<float4*>(dst + r) = make_float4(p[r], p[r + 1], p[r + 2], p[r + 3]);
+    for (int k = 0; k < OR / 4; ++k)  // row_half_mirror: lane ^ 7 (the same bit 3)
+      w4[k] = (s2 ? w8[2 * k + 1] : w8[2 * k]) + dpp_mov<0x141>(s2 ? w8[2 * k] : w8[2 * k + 1]);
+    float w2[OR / 8];
+    const bool s1 = lr & 2;
+#pragma unroll
+    for (int k = 0; k < OR / 8; ++k)  // quad_perm [2,3,0,1]: lane ^ 2
+      w2[k] = (s1 ? w4[2 * k + 1] : w4[2 * k]) + dpp_mov<0x4e>(s1 ? w4[2 * k] : w4[2 * k + 1]);
+    const bool s0 = lr & 1;
+    if constexpr (OR == 16)  // quad_perm [1,0,3,2]: lane ^ 1
+      x = (s0 ? w2[1] : w2[0]) + dpp_mov<0xb1>(s0 ? w2[0] : w2[1]);
+    else
+      x = w2[0] + dpp_mov<0xb1>(w2[0]);
   }
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  // lane i of row 0 holds rank 8 (i&1) + 4 ((i>>1)&1) + 2 ((i>>2)&1) + (i>>3)
+  // (OR == 8: 4 ((i>>1)&1) + 2 ((i>>2)&1) + (i>>3), lanes i and i ^ 1 alike)
+  const int rk = OR == 16 ? 8 * (lr & 1) + 4 * ((lr >> 1) & 1) + 2 * ((lr >> 2) & 1) + (lr >> 3)
+                          : 4 * ((lr >> 1) & 1) + 2 * ((lr >> 2) & 1) + (lr >> 3);
+  if (lane < 16 && (OR == 16 || (lane & 1) == 0))
+    ds.part[(int64_t)row * ds.ldp + (int64_t)blockIdx.x * OR + rk] = x;
 }
 
 // R > 0: the q, k and v modules' up-projections (rank R); their columns are

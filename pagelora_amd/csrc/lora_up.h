@@ -25,13 +25,24 @@ struct LoraUp {
 
 // The 16-byte piece kb (ranks 8kb .. 8kb+7) of B[a][c0 + i] (c0 % 8 == 0 in
 // the chunked layout: chunk c0 / 8 is lane l of block j).  The layout flag
-// is wave-uniform: the two addresses are a select, not a branch.
+// is wave-uniform: the piece is a per-lane base (a select of the two
+// layouts' addresses, shared by every piece of the same columns) plus a
+// uniform step, so a lane's 8 x R/8 pieces cost one base and a scalar
+// offset each.
+template <typename T, int R>
+__device__ __forceinline__ const T* lora_b_base(const LoraUp& m, int a, int c0) {
+  const int64_t rows = ((int64_t)a * m.out_features + c0) * R;
+  const int nblk = (m.out_features + 511) / 512, ch = c0 / 8;
+  const int64_t chunk = ((((int64_t)a * nblk + (ch >> 6)) * 8 * (R / 8)) * 64 + (ch & 63)) * 8;
+  return (const T*)m.B + (m.b_chunk8 ? chunk : rows);
+}
+template <int R>
+__device__ __forceinline__ int lora_b_step(const LoraUp& m, int i, int kb) {
+  return m.b_chunk8 ? (i * (R / 8) + kb) * 512 : i * R + kb * 8;
+}
 template <typename T, int R>
 __device__ __forceinline__ const uint4* lora_b_piece(const LoraUp& m, int a, int c0, int i, int kb) {
-  const int64_t rows = ((int64_t)a * m.out_features + c0 + i) * R + kb * 8;
-  const int nblk = (m.out_features + 511) / 512, ch = c0 / 8;
-  const int64_t chunk = (((((int64_t)a * nblk + (ch >> 6)) * 8 + i) * (R / 8) + kb) * 64 + (ch & 63)) * 8;
-  return reinterpret_cast<const uint4*>((const T*)m.B + (m.b_chunk8 ? chunk : rows));
+  return reinterpret_cast<const uint4*>(lora_b_base<T, R>(m, a, c0) + lora_b_step<R>(m, i, kb));
 }
 
 // One token's rank-space intermediate y[t, a, :], kept packed (R/8 x 16 B).
