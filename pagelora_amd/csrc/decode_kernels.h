@@ -1185,61 +1185,71 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
       const bool a_ok = R > 0 && a_in >= 0 && a_in < qin.n_adapters;
       const int a_ld = a_ok ? a_in : 0;
       const int qh = h * G + row;
-      head_lora_load<T, R>(qin, b, 0, qh * D, col, a_ld, hq_in);
-      __builtin_amdgcn_sched_barrier(0);
-      float v[8];
-      head_finish<T, R>(qin, hq_in, 0, col, qin.q_norm_w != nullptr, true, a_ok, v);
-      const uint32_t w4[4] = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
-                              pack2<T>(v[6], v[7])};
-      if constexpr (WaveT::kMfmaScores) {
-        // B operand: head lane % 4, dims 32 j + 8 (lane / 16) .. = the
-        // 8-dim slice 4 j + lane / 16 of row group lane % 4
-#pragma unroll
-        for (int j = 0; j < WaveT::NS; ++j)
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-            st.qb[j][k] = (uint32_t)__shfl((int)w4[k], (lane % 4) * LPT + 4 * j + lane / 16);
-      } else {
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int k = 0; k < 4; ++k) st.q[g][k] = (uint32_t)__shfl((int)w4[k], g * LPT + col);
-      }
-      if (flags & 2) {
-        const int mod = is_k ? 1 : 2;
-        head_lora_load<T, R>(qin, b, mod, h * D, col, a_ld, hkv_in);
-        __builtin_amdgcn_sched_barrier(0);
-        head_finish<T, R>(qin, hkv_in, mod, col, is_k & (qin.k_norm_w != nullptr), is_k, a_ok,
-                          v);  // rows 2, 3 compute v again; unused
-        const uint32_t kv4[4] = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
-                                 pack2<T>(v[6], v[7])};
-        if (row < 2 && slot_ok) {
-          T* dst = const_cast<T*>(is_k ? kc : vc) + pg * page_stride + off * token_stride +
-                   (int64_t)h * head_stride + col * 8;
-          *reinterpret_cast<uint4*>(dst) = make_uint4(kv4[0], kv4[1], kv4[2], kv4[3]);
-        }
-        // A slot at the row's last token (where a decode step appends) is
-        // the item's token ntok - 1: attend over the computed k / v there.
-        // The store above is not waited for: nothing in this launch reads
-        // the slot from memory then.
-        const int lst = last_raw < 1 ? 1 : (last_raw > page_size ? page_size : last_raw);
-        const int t = ntok - 1, tt = t - (t / kBlockTokens) * kBlockTokens;
-        nt.blk = (slot_ok & (off == lst - 1) & (ntok > 0)) ? t / kBlockTokens : -1;
-        nt.pg = (int)pg;  // the block must also come from the slot's page
-        nt.s = tt / WaveT::TPI;
-        nt.row = tt - nt.s * WaveT::TPI;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          nt.k[k] = (uint32_t)__shfl((int)kv4[k], col);        // row group 0
-          nt.v[k] = (uint32_t)__shfl((int)kv4[k], LPT + col);  // row group 1
-        }
+      const int mod = is_k ? 1 : 2;
+      auto form_q = [&]() {
+        float v[8];
+        head_finish<T, R>(qin, hq_in, 0, col, qin.q_norm_w != nullptr, true, a_ok, v);
+        const uint32_t w4[4] = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
+                                pack2<T>(v[6], v[7])};
         if constexpr (WaveT::kMfmaScores) {
-          nt.klane = WaveT::k_lane_of(tt);
+          // B operand: head lane % 4, dims 32 j + 8 (lane / 16) .. = the
+          // 8-dim slice 4 j + lane / 16 of row group lane % 4
 #pragma unroll
           for (int j = 0; j < WaveT::NS; ++j)
 #pragma unroll
-            for (int k = 0; k < 4; ++k) nt.kq[j][k] = (uint32_t)__shfl((int)kv4[k], 4 * j + lane / 16);
+            for (int k = 0; k < 4; ++k)
+              st.qb[j][k] = (uint32_t)__shfl((int)w4[k], (lane % 4) * LPT + 4 * j + lane / 16);
+        } else {
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) st.q[g][k] = (uint32_t)__shfl((int)w4[k], g * LPT + col);
         }
+      };
+      if (!(flags & 2)) {
+        head_lora_load<T, R>(qin, b, 0, qh * D, col, a_ld, hq_in);
+        __builtin_amdgcn_sched_barrier(0);
+        form_q();
+        return;
+      }
+      // The item holding the row's last page: the new token's k / v LoRA rows
+      // go out right after q's (q's products wait only for the loads before
+      // them), one round trip for both.
+      head_lora_load<T, R>(qin, b, 0, qh * D, col, a_ld, hq_in);
+      head_lora_load<T, R>(qin, b, mod, h * D, col, a_ld, hkv_in);
+      __builtin_amdgcn_sched_barrier(0);
+      form_q();
+      float v[8];
+      head_finish<T, R>(qin, hkv_in, mod, col, is_k & (qin.k_norm_w != nullptr), is_k, a_ok,
+                        v);  // rows 2, 3 compute v again; unused
+      const uint32_t kv4[4] = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
+                               pack2<T>(v[6], v[7])};
+      if (row < 2 && slot_ok) {
+        T* dst = const_cast<T*>(is_k ? kc : vc) + pg * page_stride + off * token_stride +
+                 (int64_t)h * head_stride + col * 8;
+        *reinterpret_cast<uint4*>(dst) = make_uint4(kv4[0], kv4[1], kv4[2], kv4[3]);
+      }
+      // A slot at the row's last token (where a decode step appends) is
+      // the item's token ntok - 1: attend over the computed k / v there.
+      // The store above is not waited for: nothing in this launch reads
+      // the slot from memory then.
+      const int lst = last_raw < 1 ? 1 : (last_raw > page_size ? page_size : last_raw);
+      const int t = ntok - 1, tt = t - (t / kBlockTokens) * kBlockTokens;
+      nt.blk = (slot_ok & (off == lst - 1) & (ntok > 0)) ? t / kBlockTokens : -1;
+      nt.pg = (int)pg;  // the block must also come from the slot's page
+      nt.s = tt / WaveT::TPI;
+      nt.row = tt - nt.s * WaveT::TPI;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        nt.k[k] = (uint32_t)__shfl((int)kv4[k], col);        // row group 0
+        nt.v[k] = (uint32_t)__shfl((int)kv4[k], LPT + col);  // row group 1
+      }
+      if constexpr (WaveT::kMfmaScores) {
+        nt.klane = WaveT::k_lane_of(tt);
+#pragma unroll
+        for (int j = 0; j < WaveT::NS; ++j)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) nt.kq[j][k] = (uint32_t)__shfl((int)kv4[k], 4 * j + lane / 16);
       }
     };
     stream_blocks_fused<T>(st, kc, vc, page_stride, token_stride, ln, indices, pbeg, page_size,
