@@ -62,8 +62,8 @@ inline int ok() {
   } while (0)
 
 // --------------------------------------------------------- element types ---
-// Storage types.  bf16 is kept as raw 16-bit words: every conversion below is
-// written out so the rounding is explicit (round-to-nearest-even).
+// Storage types.  bf16 is kept as raw 16-bit words; every conversion below
+// rounds to nearest even.
 struct bf16_t { uint16_t x; };
 typedef _Float16 f16_t;
 
@@ -78,18 +78,19 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) {
 __device__ __forceinline__ float bf16_hi(uint32_t w) {
   return __uint_as_float(w & 0xffff0000u);
 }
-// Round to nearest even; a NaN stays a (quiet) NaN.  Written as a select, not
-// a branch: on wave-uniform values a branch becomes a scalar jump that splits
-// the block and keeps loads after it from being issued early.
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t qnan = (u >> 16) | 0x40u;
-  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? qnan : rne);
-}
-
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round to nearest even with the hardware conversion (v_cvt_pk_bf16_f32, one
+// instruction per pair): the bits of (u + 0x7fff + ((u >> 16) & 1)) >> 16
+// for every non-NaN float u; a NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  return (uint16_t)f32x2_to_bf16x2_bits(f, f);
+}
 
 __device__ __forceinline__ float h_lo(uint32_t w) {
   half2_t h = __builtin_bit_cast(half2_t, w);
@@ -141,7 +142,7 @@ template <> __device__ __forceinline__ float to_float<bf16_t>(bf16_t v) {
 // Pack two floats into one 32-bit word of two T (16-bit types only).
 template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
 template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float a, float b) {
-  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+  return f32x2_to_bf16x2_bits(a, b);
 }
 template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
   half2_t h;
@@ -150,11 +151,8 @@ template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
-// pack2 through the hardware round-to-nearest-even conversion
-// (v_cvt_pk_bf16_f32 for bf16): the same bits as pack2 for every non-NaN
-// value in one instruction per pair; a NaN stays a NaN (its payload bits may
-// differ).
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// pack2 by the hardware conversion for both types (bf16's pack2 is that
+// conversion too).
 template <typename T> __device__ __forceinline__ uint32_t pack2_hw(float a, float b);
 template <> __device__ __forceinline__ uint32_t pack2_hw<bf16_t>(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
