@@ -883,8 +883,8 @@ int pl_decode_run_qkv_oshrink(
  * pl_silu_mul_lora that also forms down_proj's LoRA shrink: the stored
  * output act (down_proj's input), times the same columns of the row's
  * adapter's A rows (down_lora_a, in_features = inter, binding the gate / up
- * modules' adapter), as fp32 partial sums down_lora_y with one part per 512
- * columns (parts = ceil(inter / 512); ld a multiple of 4), for
+ * modules' adapter), as fp32 partial sums down_lora_y with one part per 256
+ * columns (parts = ceil(inter / 256); ld a multiple of 4), for
  * pl_linear_shuffled_add.  16-bit dtypes, gate / up rank up to 16, down rank
  * 8 or 16, inter a multiple of 32.  No counterpart in the reference: it
  * computes the first F.linear of down_proj's LoRALinear.forward delta

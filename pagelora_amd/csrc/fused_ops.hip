@@ -420,14 +420,17 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const T* __restrict_
   store_row8<T>(out + row * ldo + chunk * 8, o);
 }
 
-// silu_mul_kernel (one wave per workgroup, LoRA rank R on gate / up) that
-// also forms down_proj's LoRA shrink: the product of the stored output (the
-// down projection's input) with the same columns of the row's adapter's
-// down A rows, read from the shuffled [W_down; A_down] weight (adapter a's
-// rank r is row a_row0 + a * OR + r), summed over the wave's 512 columns in
-// a fixed order and written as one partial per workgroup:
+// SiLU*up with gate / up's LoRA rank-R up-projection (one wave per
+// workgroup, 4 columns per lane: 256 per wave, twice the waves of the 8-column
+// silu_mul_kernel, which at decode sizes is one wave per CU) that also forms
+// down_proj's LoRA shrink: the product of the stored output (the down
+// projection's input) with the same columns of the row's adapter's down A
+// rows, read from the shuffled [W_down; A_down] weight (adapter a's rank r is
+// row a_row0 + a * OR + r), summed over the wave's 256 columns in a fixed
+// order and written as one partial per workgroup:
 // part[row * ldp + blockIdx.x * OR + r].  An adapter outside [0,
 // n_adapters) gives adapter 0's products (the consumer does not apply them).
+constexpr int kShrinkCols = 4;  // columns per lane
 struct DownShrink {
   const void* A;
   int ksteps;  // inter / 32
@@ -442,51 +445,75 @@ __global__ __launch_bounds__(kWave) void silu_mul_shrink_kernel(const T* __restr
                                                                 LoraUp lu, const int32_t* __restrict__ ids,
                                                                 int n_adapters, DownShrink ds) {
   static_assert(R > 0 && R <= 16 && (OR == 8 || OR == 16), "gate / up rank up to 16, down rank 8 or 16");
+  constexpr int C = kShrinkCols;
   const int row = blockIdx.y;
   const int lane = threadIdx.x;
   const int chunk_raw = blockIdx.x * kWave + lane;
-  const bool live = chunk_raw * 8 < inter;
-  const int chunk = live ? chunk_raw : inter / 8 - 1;  // idle lanes redo the last chunk, contributing nothing
+  const bool live = chunk_raw * C < inter;
+  const int c0 = (live ? chunk_raw : inter / C - 1) * C;  // idle lanes redo the last columns, contributing nothing
   const int a = lg.adapter >= 0 ? lg.adapter : ids[row];
   const bool a_ok = a >= 0 && a < n_adapters;
   const int a_ld = a_ok ? a : 0;
-  float g[8], u[8], o[8];
-  load_row8<T>(gu + row * ldg + chunk * 8, g);
-  load_row8<T>(gu + row * ldg + inter + chunk * 8, u);
+  float g[C], u[C], o[C];
+  const uint2 gw = *reinterpret_cast<const uint2*>(gu + row * ldg + c0);
+  const uint2 uw = *reinterpret_cast<const uint2*>(gu + row * ldg + inter + c0);
   LoraRow<R> yg, yu;
   load_y<T, R>(lg, row, a_ld, yg);
   load_y<T, R>(lu, row, a_ld, yu);
-  // the down A pieces: ranks 0 .. OR-1 of columns chunk*8 .. +8 (OR
-  // consecutive 16-byte pieces of one shuffled block when a_row0 + a*OR is
-  // a multiple of 16)
-  uint4 ap[OR];
+  // gate's and up's B pieces of the lane's 4 columns: one base per module
+  // (the 8-column group's, moved to its second half for c0 % 8 == 4) and
+  // the uniform steps of the columns and rank pieces
+  constexpr int KB = R >= 16 ? 2 : 1;
+  uint4 bg[C][KB], bu[C][KB];
   {
-    const int k = chunk * 8;
+    const int half = c0 & 7;
+    const T* gb = lora_b_base<T, R>(lg, a_ld, c0 - half) + (half ? lora_b_step<R>(lg, half, 0) : 0);
+    const T* ub = lora_b_base<T, R>(lu, a_ld, c0 - half) + (half ? lora_b_step<R>(lu, half, 0) : 0);
+#pragma unroll
+    for (int i = 0; i < C; ++i)
+#pragma unroll
+      for (int k = 0; k < KB; ++k) {
+        bg[i][k] = *reinterpret_cast<const uint4*>(gb + lora_b_step<R>(lg, i, k));
+        bu[i][k] = *reinterpret_cast<const uint4*>(ub + lora_b_step<R>(lu, i, k));
+      }
+  }
+  // the down A half-pieces: ranks 0 .. OR-1 of columns c0 .. c0+3 (8 bytes of
+  // the 16-byte piece that holds 8 consecutive columns of a rank)
+  uint2 ap[OR];
+  {
 #pragma unroll
     for (int r = 0; r < OR; ++r) {
       const int64_t n = (int64_t)ds.a_row0 + (int64_t)a_ld * OR + r;
-      const int64_t e = (((n / 16) * ds.ksteps + k / 32) * 64 + ((k % 32) / 8) * 16 + n % 16) * 8;
-      ap[r] = *reinterpret_cast<const uint4*>((const T*)ds.A + e);
+      const int64_t e = (((n / 16) * ds.ksteps + c0 / 32) * 64 + ((c0 % 32) / 8) * 16 + n % 16) * 8 + (c0 % 8);
+      ap[r] = *reinterpret_cast<const uint2*>((const T*)ds.A + e);
     }
   }
-  float dg[8], du[8];
-  lora_delta8_pair<T, R>(lg, lu, a_ld, chunk * 8, yg, yu, dg, du);
+  __builtin_amdgcn_sched_barrier(0);
+  unpack2<T>(gw.x, g[0], g[1]);
+  unpack2<T>(gw.y, g[2], g[3]);
+  unpack2<T>(uw.x, u[0], u[1]);
+  unpack2<T>(uw.y, u[2], u[3]);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    g[i] = through<T>(g[i] + (a_ok ? dg[i] : -0.f));
-    u[i] = through<T>(u[i] + (a_ok ? du[i] : -0.f));
+  for (int i = 0; i < C; ++i) {
+    float dg = 0.f, du = 0.f;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      dg = dot8<T>(yg.v[k], bg[i][k], dg);
+      du = dot8<T>(yu.v[k], bu[i][k], du);
+    }
+    g[i] = through<T>(g[i] + (a_ok ? dg * lg.scale : -0.f));
+    u[i] = through<T>(u[i] + (a_ok ? du * lu.scale : -0.f));
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = g[i] / (1.f + expf(-g[i])) * u[i];
-  if (live) store_row8<T>(out + row * ldo + chunk * 8, o);
-  // the shrink of the stored values: their 16-bit pairs (the same rounding as
-  // the store; idle lanes zero) against the A pieces on v_dot2
-  uint4 ov = make_uint4(pack2_hw<T>(o[0], o[1]), pack2_hw<T>(o[2], o[3]), pack2_hw<T>(o[4], o[5]),
-                        pack2_hw<T>(o[6], o[7]));
-  if (!live) ov = make_uint4(0u, 0u, 0u, 0u);
+  for (int i = 0; i < C; ++i) o[i] = g[i] / (1.f + expf(-g[i])) * u[i];
+  // the stored values' 16-bit pairs (idle lanes zero) against the A pieces
+  // on v_dot2
+  uint2 ov = make_uint2(pack2_hw<T>(o[0], o[1]), pack2_hw<T>(o[2], o[3]));
+  if (live) *reinterpret_cast<uint2*>(out + row * ldo + c0) = ov;
+  if (!live) ov = make_uint2(0u, 0u);
   float p[OR];
 #pragma unroll
-  for (int r = 0; r < OR; ++r) p[r] = dot8<T>(ov, ap[r], 0.f);
+  for (int r = 0; r < OR; ++r) p[r] = dot2<T>(ov.y, ap[r].y, dot2<T>(ov.x, ap[r].x, 0.f));
   // Transposed reduction: each step pairs lanes with DPP and halves the
   // values a lane holds (it keeps one of each pair and adds its partner's),
   // until lane i of every 16-lane row holds rank rank_of(i) summed over the
@@ -997,10 +1024,10 @@ extern "C" int pl_silu_mul_lora_shrink(const void* gate_up, int64_t ldg, const p
     return fail(PL_ERR_INVALID, "down_proj A rows: a 16-byte aligned shuffled weight %d wide (got %d) whose %d rows "
                 "hold rows a_row0 (%d) .. + %d adapters x rank %d", inter, da.in_features, da.out_features, da.a_row0,
                 num_adapters, da.rank);
-  const int parts = (inter / 8 + kWave - 1) / kWave;
+  const int parts = (inter / kShrinkCols + kWave - 1) / kWave;
   if (!dy.partials || (uintptr_t)dy.partials % 16 || dy.rank != da.rank || dy.parts != parts ||
       dy.ld < (int64_t)parts * dy.rank || dy.ld % 4)
-    return fail(PL_ERR_INVALID, "down_proj partials: rank %d, %d parts per row (one per 512 columns), ld >= %d and a "
+    return fail(PL_ERR_INVALID, "down_proj partials: rank %d, %d parts per row (one per 256 columns), ld >= %d and a "
                 "multiple of 4, 16-byte aligned", da.rank, parts, parts * da.rank);
   const DownShrink dsh{da.shuffled, inter / 32, da.a_row0, dy.partials, dy.ld};
   hipStream_t s = (hipStream_t)stream;

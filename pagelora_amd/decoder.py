@@ -648,7 +648,7 @@ def _layer(cfg: DecoderConfig, lw: LayerWeights, scale: float, hidden: torch.Ten
         trace("gate_up", gu)
     lora_gu = (lw.up("gate", gu, scale, a), lw.up("up", gu, scale, a))
     if fused and _fused_down(cfg, lw):
-        parts_d = LoraPartials(torch.empty((T, -(-I // 512), r), dtype=torch.float32, device=hidden.device))
+        parts_d = LoraPartials(torch.empty((T, -(-I // 256), r), dtype=torch.float32, device=hidden.device))
         d_rows = lora_a_rows(lw.shuffled["down"], lw.y_offset["down"], r, a)
         act = fused_ops.silu_mul(gu[:, : 2 * I], lora=lora_gu, adapter_ids=ids, down_shrink=(d_rows, parts_d))
         before = hidden.clone() if trace is not None else None

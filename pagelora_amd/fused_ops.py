@@ -191,7 +191,7 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None, *,
     """``silu(gate) * up`` of a packed ``[T, 2*inter]`` row block; with ``lora``
     (gate, up) the modules' LoRA deltas are added first (pl_silu_mul_lora).
     ``down_shrink`` = (``_lib.LoraARows`` of down_proj, ``linear.LoraPartials``
-    [T, ceil(inter / 512), rank]): the kernel also writes down_proj's LoRA
+    [T, ceil(inter / 256), rank]): the kernel also writes down_proj's LoRA
     shrink partials of the output (pl_silu_mul_lora_shrink)."""
     _rows2d(gate_up, "gate_up")
     inter = gate_up.shape[1] // 2

@@ -278,7 +278,7 @@ def test_oshrink_rejects_a_skipped_merge(gpu_device):
 def test_silu_shrink_matches_plain_silu(gpu_device, dtype, rows, rank, down_rank, inter, bound):
     """SiLU*up with down_proj's LoRA shrink (pl_silu_mul_lora_shrink): its
     output bit for bit against pl_silu_mul_lora, and the partial sums (one
-    per 512 columns) against the float64 product of that output with the
+    per 256 columns) against the float64 product of that output with the
     row's adapter's A rows."""
     n_ad = 2
     g = torch.Generator().manual_seed(rows * 13 + rank + down_rank + inter)
@@ -290,7 +290,7 @@ def test_silu_shrink_matches_plain_silu(gpu_device, dtype, rows, rank, down_rank
     hidden = 256
     Wd = (torch.randn((hidden + n_ad * down_rank, inter), generator=g) * 0.02).to(dtype)
     sw = ShuffledWeight(Wd.to(gpu_device))
-    parts = LoraPartials(torch.full((rows, -(-inter // 512), down_rank), float("nan"), device=gpu_device))
+    parts = LoraPartials(torch.full((rows, -(-inter // 256), down_rank), float("nan"), device=gpu_device))
     act = fused_ops.silu_mul(gu[:, : 2 * inter], lora=lora, adapter_ids=ids,
                              down_shrink=(lora_a_rows(sw, hidden, down_rank, bound), parts))
     ref = fused_ops.silu_mul(gu[:, : 2 * inter], lora=lora, adapter_ids=ids)
