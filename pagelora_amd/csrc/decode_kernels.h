@@ -513,11 +513,12 @@ __device__ __forceinline__ void stream_blocks(WaveT& st, const T* __restrict__ k
   // first_page / second_page: the page ids of blocks blk0 and blk0 + 1
   // (clamped to the item, as page_of does), read by the caller in an earlier
   // round trip, so the loop's first loads wait on no scalar load
-  auto load_at = [&](int blk, int64_t page, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
+  const int last_page = (int)min(num_pages, (int64_t)INT32_MAX) - 1;  // 32-bit: scalar compares
+  auto load_at = [&](int blk, int page, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
     const int t0 = blk * kBlockTokens;
     const int tip = t0 - (t0 / page_size) * page_size;
-    page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);  // stay inside the pool
-    const int64_t base = page * page_stride + (int64_t)tip * token_stride;
+    page = page < 0 ? 0 : min(page, last_page);  // stay inside the pool
+    const int64_t base = (int64_t)page * page_stride + (int64_t)tip * token_stride;
     const T* kp = kc + base + ln.k_off;
     const T* vp = vc + base + ln.v_off;
 #pragma unroll
@@ -536,30 +537,35 @@ __device__ __forceinline__ void stream_blocks(WaveT& st, const T* __restrict__ k
   // of the loads: headline 746.5 -> 743 us, 64 x 2K GQA-4 114.2 -> 113.2 us;
   // entering the loop with both buffers in flight instead was 1-10% slower.)
   int pid_next = second_page;
-  for (int i = blk0; i < blk1; i += 2) {
-    // Prefetch the next block before consuming this one.  The index is
-    // clamped instead of branched on so the load count is the same on
-    // every path (a re-load of the last block hits in cache).
+  auto consume = [&](int blk, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
+    if ((blk + 1) * kBlockTokens <= ntok)
+      st.template consume<false>(kw, vw, scale_log2, row, kBlockTokens);
+    else
+      st.template consume<true>(kw, vw, scale_log2, row, ntok - blk * kBlockTokens);
+  };
+  // Pairs of blocks, then the odd last one.  The loop has one exit: a break
+  // between the halves gives the compiler a path from the first half's
+  // loads back to the loop head, where it then waits for every load in
+  // flight before reusing their registers (one block in flight, not two).
+  int i = blk0;
+  for (; i + 1 < blk1; i += 2) {
+    // Prefetch the next block before consuming this one.  The second load's
+    // index is clamped instead of branched on so the load count is the same
+    // on every path (a re-load of the last block hits in cache).
     const int p1 = pid_next;
     pid_next = page_of(i + 2);
-    load_at(min(i + 1, blk1 - 1), p1, kb, vb);
+    load_at(i + 1, p1, kb, vb);
     // keep the scheduler from pulling the consume (and its waits on this
     // block's data) above the prefetch
     __builtin_amdgcn_sched_barrier(0);
-    if ((i + 1) * kBlockTokens <= ntok)
-      st.template consume<false>(ka, va, scale_log2, row, kBlockTokens);
-    else
-      st.template consume<true>(ka, va, scale_log2, row, ntok - i * kBlockTokens);
-    if (i + 1 >= blk1) break;
+    consume(i, ka, va);
     const int p2 = pid_next;
     pid_next = page_of(i + 3);
     load_at(min(i + 2, blk1 - 1), p2, ka, va);
     __builtin_amdgcn_sched_barrier(0);
-    if ((i + 2) * kBlockTokens <= ntok)
-      st.template consume<false>(kb, vb, scale_log2, row, kBlockTokens);
-    else
-      st.template consume<true>(kb, vb, scale_log2, row, ntok - (i + 1) * kBlockTokens);
+    consume(i + 1, kb, vb);
   }
+  if (i < blk1) consume(i, ka, va);
 }
 
 // stream_blocks for pages whose size is not a multiple of 16 tokens (1, 2,
@@ -634,23 +640,25 @@ __device__ __forceinline__ void stream_blocks_small(WaveT& st, const T* __restri
   fetch_ids(0, wa);
   fetch_ids(min(1, nblk - 1), wb);
   load_at(wa, ka, va);
-  for (int i = 0; i < nblk; i += 2) {
+  auto consume = [&](int blk, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
+    if ((blk + 1) * kBlockTokens <= ntok)
+      st.template consume<false>(kw, vw, scale_log2, row, kBlockTokens);
+    else
+      st.template consume<true>(kw, vw, scale_log2, row, ntok - blk * kBlockTokens);
+  };
+  // pairs of blocks, then the odd last one: one loop exit, as in stream_blocks
+  int i = 0;
+  for (; i + 1 < nblk; i += 2) {
     fetch_ids(min(i + 2, nblk - 1), wa);  // block i's loads are issued: wa is free
-    load_at(wb, kb, vb);                  // block i + 1 (a re-load of the last block past the end)
+    load_at(wb, kb, vb);                  // block i + 1
     __builtin_amdgcn_sched_barrier(0);
-    if ((i + 1) * kBlockTokens <= ntok)
-      st.template consume<false>(ka, va, scale_log2, row, kBlockTokens);
-    else
-      st.template consume<true>(ka, va, scale_log2, row, ntok - i * kBlockTokens);
-    if (i + 1 >= nblk) break;
+    consume(i, ka, va);
     fetch_ids(min(i + 3, nblk - 1), wb);
-    load_at(wa, ka, va);  // block i + 2
+    load_at(wa, ka, va);  // block i + 2 (a re-load of the last block past the end)
     __builtin_amdgcn_sched_barrier(0);
-    if ((i + 2) * kBlockTokens <= ntok)
-      st.template consume<false>(kb, vb, scale_log2, row, kBlockTokens);
-    else
-      st.template consume<true>(kb, vb, scale_log2, row, ntok - (i + 1) * kBlockTokens);
+    consume(i + 1, kb, vb);
   }
+  if (i < nblk) consume(i, ka, va);
 }
 
 // The new token's K and V of a wave's kv head, as registers to splice into
@@ -678,11 +686,12 @@ __device__ __forceinline__ void stream_blocks_fused(WaveT& st, const T* __restri
   constexpr int NS = WaveT::NS, W = WaveT::W;
   static_assert(W == 4, "16-bit types: 4 words per lane per token");
   using L8 = Lane8<T>;
-  auto load_at = [&](int blk, int64_t page, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
+  const int last_page = (int)min(num_pages, (int64_t)INT32_MAX) - 1;  // 32-bit: scalar compares
+  auto load_at = [&](int blk, int page, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
     const int t0 = blk * kBlockTokens;
     const int tip = t0 - (t0 / page_size) * page_size;
-    page = page < 0 ? 0 : (page >= num_pages ? num_pages - 1 : page);  // stay inside the pool
-    const int64_t base = page * page_stride + (int64_t)tip * token_stride;
+    page = page < 0 ? 0 : min(page, last_page);  // stay inside the pool
+    const int64_t base = (int64_t)page * page_stride + (int64_t)tip * token_stride;
     const T* kp = kc + base + ln.k_off;
     const T* vp = vc + base + ln.v_off;
 #pragma unroll
@@ -715,27 +724,28 @@ __device__ __forceinline__ void stream_blocks_fused(WaveT& st, const T* __restri
   load_at(blk0, pa, ka, va);
   int pid_next = second_page;
   hook();
-  for (int i = blk0; i < blk1; i += 2) {
+  auto consume = [&](int blk, int page, uint32_t (&kw)[NS][W], uint32_t (&vw)[NS][W]) {
+    splice(blk, page, kw, vw);
+    if ((blk + 1) * kBlockTokens <= ntok)
+      st.template consume<false>(kw, vw, scale_log2, row, kBlockTokens);
+    else
+      st.template consume<true>(kw, vw, scale_log2, row, ntok - blk * kBlockTokens);
+  };
+  // pairs of blocks, then the odd last one: one loop exit, as in stream_blocks
+  int i = blk0;
+  for (; i + 1 < blk1; i += 2) {
     pb = pid_next;
     pid_next = page_of(i + 2);
-    load_at(min(i + 1, blk1 - 1), pb, kb, vb);
+    load_at(i + 1, pb, kb, vb);
     __builtin_amdgcn_sched_barrier(0);
-    splice(i, pa, ka, va);
-    if ((i + 1) * kBlockTokens <= ntok)
-      st.template consume<false>(ka, va, scale_log2, row, kBlockTokens);
-    else
-      st.template consume<true>(ka, va, scale_log2, row, ntok - i * kBlockTokens);
-    if (i + 1 >= blk1) break;
+    consume(i, pa, ka, va);
     pa = pid_next;
     pid_next = page_of(i + 3);
     load_at(min(i + 2, blk1 - 1), pa, ka, va);
     __builtin_amdgcn_sched_barrier(0);
-    splice(i + 1, pb, kb, vb);
-    if ((i + 2) * kBlockTokens <= ntok)
-      st.template consume<false>(kb, vb, scale_log2, row, kBlockTokens);
-    else
-      st.template consume<true>(kb, vb, scale_log2, row, ntok - (i + 1) * kBlockTokens);
+    consume(i + 1, pb, kb, vb);
   }
+  if (i < blk1) consume(i, pa, ka, va);
 }
 
 // Inputs of the decode run with the q/k/v epilogue folded in
@@ -888,22 +898,29 @@ __device__ __forceinline__ void prefix_wave(const DirectScan& sc, const Direct& 
   const int ip0 = __builtin_amdgcn_readfirstlane(sc.ip);
   const int tok0 = (live ? j : 0) * kPrefixTokens;
   const int last_idx = dir.capacity > 0 ? dir.capacity - 1 : 0;  // page reads stay inside the indices buffer
-  const int pg_a = uniform(indices[min(ip0 + tok0 / page_size, last_idx)]);
-  const int pg_b = uniform(indices[min(ip0 + (tok0 + 16) / page_size, last_idx)]);
+  const int psh = page_size == 16 ? 4 : 5;  // log2 of the page size (16 or 32 tokens)
+  const int pg_a = uniform(indices[min(ip0 + (tok0 >> psh), last_idx)]);
+  const int pg_b = uniform(indices[min(ip0 + ((tok0 + 16) >> psh), last_idx)]);
   __builtin_amdgcn_sched_barrier(0);
   // ---- K (A operand: token l % 16 of each block, dims 8 (l/16) + 32 jj) and
   // V (token rows l/16 + 4 s of the 32, dims 8 (l % 16) ..) of the 32 tokens,
   // issued before q is formed (a wave past the prefix reads chunk 0's)
-  auto tok_addr = [&](int t) -> int64_t {  // element offset of token t of the item, kv head h
-    const int tt = tok0 + t;
-    int64_t pg = (tt - tok0) < 16 ? pg_a : pg_b;
-    pg = pg < 0 ? 0 : (pg >= num_pages ? num_pages - 1 : pg);
-    return pg * page_stride + (int64_t)(tt % page_size) * token_stride + (int64_t)h * head_stride;
+  // the item's two 16-token halves (pages of 16 or 32 tokens here, and tok0
+  // a multiple of 32): rows 0.. of page pg_a, then rows 0.. of page pg_b
+  // (16-token pages) or rows 16.. of page pg_a (32-token pages).  Element
+  // offset of row r of half hf, kv head h: uniform bases, one per half.
+  auto page_off = [&](int pg) -> int64_t {
+    const int64_t pc = pg < 0 ? 0 : (pg >= num_pages ? num_pages - 1 : pg);
+    return pc * page_stride + (int64_t)h * head_stride;
   };
+  const int64_t half0 = page_off(pg_a);
+  const int64_t half1 = page_size == 16 ? page_off(pg_b) : half0 + 16 * token_stride;
+  auto tok_addr = [&](int hf, int64_t row_off) -> int64_t { return (hf ? half1 : half0) + row_off; };
   uint32_t kw[2][4][4];
+  const int64_t col_off = (int64_t)col * token_stride;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
-    const T* kp = kc + tok_addr(blk * 16 + col) + 8 * rg;
+    const T* kp = kc + tok_addr(blk, col_off) + 8 * rg;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const uint4 t = *reinterpret_cast<const uint4*>(kp + 32 * jj);
@@ -932,7 +949,8 @@ __device__ __forceinline__ void prefix_wave(const DirectScan& sc, const Direct& 
   }
   uint4 vr[8];
 #pragma unroll
-  for (int s2 = 0; s2 < 8; ++s2) vr[s2] = *reinterpret_cast<const uint4*>(vc + tok_addr(rg + 4 * s2) + 8 * col);
+  for (int s2 = 0; s2 < 8; ++s2)
+    vr[s2] = *reinterpret_cast<const uint4*>(vc + tok_addr(s2 >= 4, (int64_t)(rg + 4 * (s2 & 3)) * token_stride) + 8 * col);
   // ---- S^T and the softmax of each column over the 32 tokens
   f32x4 sacc[2];
 #pragma unroll
