@@ -891,17 +891,21 @@ __device__ __forceinline__ void prefix_wave(const DirectScan& sc, const Direct& 
   const int hq_form = h * G + rg;
   const int a_ld = R > 0 ? qin.m[0].adapter : 0;  // the bound adapter (the host requires one)
   const int qb_row = min(wv, nrows - 1);
-  HeadIn<T, R> x;
-  head_base_load<T, R>(qin, qb_row, hq_form, col, (const T*)qin.q_norm_w, x);
-  head_lora_load<T, R>(qin, qb_row, 0, hq_form * D, col, a_ld, x);
-  // the item's pages: tokens j*32 .. of row 0's list (every row's, up to the prefix)
+  // the item's pages: tokens j*32 .. of row 0's list (every row's, up to the
+  // prefix).  Issued before q's loads: loads complete in order, so the K
+  // loads below then wait for the page ids alone.
   const int ip0 = __builtin_amdgcn_readfirstlane(sc.ip);
   const int tok0 = (live ? j : 0) * kPrefixTokens;
   const int last_idx = dir.capacity > 0 ? dir.capacity - 1 : 0;  // page reads stay inside the indices buffer
   const int psh = page_size == 16 ? 4 : 5;  // log2 of the page size (16 or 32 tokens)
-  const int pg_a = uniform(indices[min(ip0 + (tok0 >> psh), last_idx)]);
-  const int pg_b = uniform(indices[min(ip0 + ((tok0 + 16) >> psh), last_idx)]);
+  const int pid_a = indices[min(ip0 + (tok0 >> psh), last_idx)];
+  const int pid_b = indices[min(ip0 + ((tok0 + 16) >> psh), last_idx)];
   __builtin_amdgcn_sched_barrier(0);
+  HeadIn<T, R> x;
+  head_base_load<T, R>(qin, qb_row, hq_form, col, (const T*)qin.q_norm_w, x);
+  head_lora_load<T, R>(qin, qb_row, 0, hq_form * D, col, a_ld, x);
+  __builtin_amdgcn_sched_barrier(0);
+  const int pg_a = uniform(pid_a), pg_b = uniform(pid_b);
   // ---- K (A operand: token l % 16 of each block, dims 8 (l/16) + 32 jj) and
   // V (token rows l/16 + 4 s of the 32, dims 8 (l % 16) ..) of the 32 tokens,
   // issued before q is formed (a wave past the prefix reads chunk 0's)
