@@ -671,18 +671,19 @@ struct NewToken {
   uint32_t kq[4][4];    // load j holding dims 32 j + 8 (l / 16) ..
 };
 
-// stream_blocks for the folded q/k/v epilogue: `hook` runs once the first
+// stream_blocks for the folded q/k/v epilogue: `pre` issues loads ahead of
+// the first block's, `hook` runs once the first
 // block's loads are in flight (it forms q, and for the item holding the
 // row's last page the new token's k / v, filling `nt`), and the new token's
 // K/V rows are taken from `nt` rather than from memory, so no load waits on
 // the append's stores.
-template <typename T, class WaveT, class Hook>
+template <typename T, class WaveT, class Pre, class Hook>
 __device__ __forceinline__ void stream_blocks_fused(WaveT& st, const T* __restrict__ kc, const T* __restrict__ vc,
                                                     int64_t page_stride, int64_t token_stride, const KvLanes& ln,
                                                     const int32_t* __restrict__ indices, int pbeg, int page_size,
                                                     int64_t num_pages, int ntok, int blk0, int blk1,
                                                     float scale_log2, int row, int first_page, int second_page,
-                                                    Hook&& hook, const NewToken& nt) {
+                                                    Pre&& pre, Hook&& hook, const NewToken& nt) {
   constexpr int NS = WaveT::NS, W = WaveT::W;
   static_assert(W == 4, "16-bit types: 4 words per lane per token");
   using L8 = Lane8<T>;
@@ -715,6 +716,7 @@ __device__ __forceinline__ void stream_blocks_fused(WaveT& st, const T* __restri
       }
     }
   };
+  pre();
   if (blk1 <= blk0) {
     hook();
     return;
@@ -1198,15 +1200,23 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
     // holding the row's last page, the new token's k (row group 0: + LoRA,
     // k-norm, RoPE) and v (row group 1: + LoRA) of this kv head, stored into
     // its slot and spliced into the block that holds it.
+    // the adapter: blended with bit operations, so the id's load is not
+    // moved under a test of the uniform adapter
+    const uint32_t per_row = (uint32_t)(qin.m[0].adapter >> 31);  // all ones: per-row ids
+    const int a_in = (int)(((uint32_t)qin.m[0].adapter & ~per_row) | ((uint32_t)id_raw & per_row));
+    const bool a_ok = R > 0 && a_in >= 0 && a_in < qin.n_adapters;
+    const int a_ld = a_ok ? a_in : 0;
+    const int qh = h * G + row;
+    // q's LoRA rows: without a shared prefix (long rows) they go out before
+    // the first block's loads, so q's products wait for them alone (loads
+    // complete in order), not for the block (1 x 32K +0.4%); in a
+    // shared-prefix launch after them (4 rows -0.3% the other way)
+    auto q_lora = [&]() { head_lora_load<T, R>(qin, b, 0, qh * D, col, a_ld, hq_in); };
+    auto pre = [&]() {
+      if constexpr (!PREFIX) q_lora();
+    };
     auto hook = [&]() {
       const bool slot_ok = (pg >= 0) & (pg < num_pages) & (off >= 0) & (off < page_size);
-      // the adapter: blended with bit operations, so the id's load is not
-      // moved under a test of the uniform adapter
-      const uint32_t per_row = (uint32_t)(qin.m[0].adapter >> 31);  // all ones: per-row ids
-      const int a_in = (int)(((uint32_t)qin.m[0].adapter & ~per_row) | ((uint32_t)id_raw & per_row));
-      const bool a_ok = R > 0 && a_in >= 0 && a_in < qin.n_adapters;
-      const int a_ld = a_ok ? a_in : 0;
-      const int qh = h * G + row;
       const int mod = is_k ? 1 : 2;
       auto form_q = [&]() {
         float v[8];
@@ -1228,8 +1238,8 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
             for (int k = 0; k < 4; ++k) st.q[g][k] = (uint32_t)__shfl((int)w4[k], g * LPT + col);
         }
       };
+      if constexpr (PREFIX) q_lora();
       if (!(flags & 2)) {
-        head_lora_load<T, R>(qin, b, 0, qh * D, col, a_ld, hq_in);
         __builtin_amdgcn_sched_barrier(0);
         form_q();
         return;
@@ -1237,7 +1247,6 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
       // The item holding the row's last page: the new token's k / v LoRA rows
       // go out right after q's (q's products wait only for the loads before
       // them), one round trip for both.
-      head_lora_load<T, R>(qin, b, 0, qh * D, col, a_ld, hq_in);
       head_lora_load<T, R>(qin, b, mod, h * D, col, a_ld, hkv_in);
       __builtin_amdgcn_sched_barrier(0);
       form_q();
@@ -1275,7 +1284,7 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
       }
     };
     stream_blocks_fused<T>(st, kc, vc, page_stride, token_stride, ln, indices, pbeg, page_size,
-                                 num_pages, ntok, 0, nblk, scale_log2, row, first_page, second_page, hook, nt);
+                                 num_pages, ntok, 0, nblk, scale_log2, row, first_page, second_page, pre, hook, nt);
   } else if constexpr (SMALL) {
     const int64_t v_fix = (int64_t)hk * head_stride + col * 8;
     int k_tok = -1;
