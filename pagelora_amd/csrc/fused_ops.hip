@@ -460,6 +460,7 @@ __global__ __launch_bounds__(kWave) void silu_mul_shrink_kernel(const T* __restr
   LoraRow<R> yg, yu;
   load_y<T, R>(lg, row, a_ld, yg);
   load_y<T, R>(lu, row, a_ld, yu);
+  __builtin_amdgcn_sched_barrier(0);  // y (scalar loads) out before the B and A pieces
   // gate's and up's B pieces of the lane's 4 columns: one base per module
   // (the 8-column group's, moved to its second half for c0 % 8 == 4) and
   // the uniform steps of the columns and rank pieces
@@ -509,7 +510,10 @@ __global__ __launch_bounds__(kWave) void silu_mul_shrink_kernel(const T* __restr
   // the stored values' 16-bit pairs (idle lanes zero) against the A pieces
   // on v_dot2
   uint2 ov = make_uint2(pack2_hw<T>(o[0], o[1]), pack2_hw<T>(o[2], o[3]));
-  if (live) *reinterpret_cast<uint2*>(out + row * ldo + c0) = ov;
+  // every lane stores (an idle lane rewrites the last 4 columns with the
+  // bits their own lane stores): under a test, the compiler sinks the
+  // gate / up loads into it, behind every B and A load
+  *reinterpret_cast<uint2*>(out + row * ldo + c0) = ov;
   if (!live) ov = make_uint2(0u, 0u);
   float p[OR];
 #pragma unroll
