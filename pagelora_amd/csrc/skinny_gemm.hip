@@ -556,16 +556,17 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
   // unconditional, so no load waits under a test)
   const int ri = min((int)threadIdx.x, nt * 16 - 1);
   const T rv_ld = res[(int64_t)(t0 + ri / 16) * ldr + min(nb * 16 + ri % 16, N - 1)];
-  [[maybe_unused]] uint4 bpc;
-  [[maybe_unused]] int a_ok_ld = 0;
+  // The token's adapter id: an unconditional load (a bound adapter reads a
+  // dummy word of the weight), so no load sits under a test: a test would
+  // make the compiler wait for every load in flight where the paths join,
+  // the weights' first batch included.  The B piece it addresses goes out
+  // after the weights' first batches, and reaches LDS after the main loop.
+  [[maybe_unused]] int id_ld = 0;
   if constexpr (R > 0) {
     constexpr int KB = R / 8;
     const int bi = min((int)threadIdx.x, nt * 16 * KB - 1);
-    const int tl = bi / (16 * KB), col = (bi / KB) % 16, kb = bi % KB;
-    const int a_raw = lora.adapter >= 0 ? lora.adapter : ids[t0 + tl];
-    a_ok_ld = (a_raw >= 0) & (a_raw < n_adapters);
-    const int nc = min(nb * 16 + col, N - 1);
-    bpc = *lora_b_piece<T, R>(lora, a_ok_ld ? a_raw : 0, nc & ~7, nc & 7, kb);
+    const int tl = bi / (16 * KB);
+    id_ld = *(lora.adapter >= 0 ? reinterpret_cast<const int32_t*>(Ws) : ids + t0 + tl);
   }
   constexpr int NQ = NB > 0 ? NB : 1;
   u32x4 b[NQ][kUnroll], a[NQ][kUnroll];
@@ -583,11 +584,17 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
   };
   issue(0, NB > 0 ? 0 : sb);
   if constexpr (NB > 1) issue(1, kUnroll);
+  __builtin_amdgcn_sched_barrier(0);  // every weight and x load of the first batches out first
   s_res[ri] = to_float<T>(rv_ld);
+  [[maybe_unused]] uint4 bpc;
   if constexpr (R > 0) {
     constexpr int KB = R / 8;
     const int bi = min((int)threadIdx.x, nt * 16 * KB - 1);
-    s_b[bi] = bpc;
+    const int col = (bi / KB) % 16, kb = bi % KB;
+    const int a_raw = lora.adapter >= 0 ? lora.adapter : id_ld;
+    const int a_ok_ld = (a_raw >= 0) & (a_raw < n_adapters);
+    const int nc = min(nb * 16 + col, N - 1);
+    bpc = *lora_b_piece<T, R>(lora, a_ok_ld ? a_raw : 0, nc & ~7, nc & 7, kb);
     if (bi % (16 * KB) == 0) s_ok[bi / (16 * KB)] = a_ok_ld;
   }
   if constexpr (R > 0) {
@@ -631,6 +638,7 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
       acc = mfma32<T>(aa, bb, acc);
     }
   }
+  if constexpr (R > 0) s_b[min((int)threadIdx.x, nt * 16 * (R / 8) - 1)] = bpc;
 #pragma unroll
   for (int i = 0; i < 4; ++i) s_red[wave][((lane / 16) * 4 + i) * 16 + lr] = acc[i];
   __syncthreads();
