@@ -1418,6 +1418,13 @@ __global__ __launch_bounds__(MT) void merge_kernel(
   constexpr int kMinItems = OR > 0 ? 1 : 2;
   __shared__ float s_m[NWV][LPT], s_w[NWV][LPT], s_a[NWV][LPT][8];
   __shared__ float s_ov[OR > 0 ? LPT : 1][8];
+  // the partials' addresses are read with the first arguments (held in
+  // scalar registers): left to their first use, they come from another
+  // cache line of the arguments, a round trip after the row's range
+  uint64_t plse_u = (uint64_t)(uintptr_t)part_lse, po_u = (uint64_t)(uintptr_t)part_o;
+  asm volatile("" : "+s"(plse_u), "+s"(po_u));
+  part_lse = gptr<const float*>(plse_u);
+  part_o = gptr<const float*>(po_u);
   const int pair = blockIdx.x / DS, ds = blockIdx.x % DS;
   if (pair >= batch * num_qo_heads) return;
   const int b = pair / num_qo_heads;
