@@ -1079,6 +1079,15 @@ __global__ __launch_bounds__(kWave * waves_per_wg<FUSED>()) void decode_kernel(
   using L8 = Lane8<T>;
 
   static_assert(!PREFIX || FUSED, "prefix items are built into the folded q/k/v kernel");
+  // One word of each cache line of the arguments, read first and dropped:
+  // every line is then in the scalar cache before the code reads its fields
+  // (otherwise each line first read later costs a round trip there).  In
+  // the shared-prefix instantiation only: the plain folded kernel's register
+  // allocation came out worse with it (1 x 32K -1.5%).
+  if constexpr (PREFIX) {
+    asm volatile("" ::"s"(q), "s"(indices), "s"(num_pages), "s"(qin.ld), "s"(qin.m[0].ldy),
+                 "s"(qin.m[1].y_offset), "s"(qin.m[2].B), "s"(dir.capacity));
+  }
   // the prefix workgroups' V tiles (one 8 KB tile per wave) and q (4 rows x 4 heads)
   __shared__ uint32_t s_pv[PREFIX ? waves_per_wg<FUSED>() : 1][PREFIX ? kPrefixTokens * 64 : 1];
   __shared__ uint4 s_q[PREFIX ? kPrefixMaxRows : 1][4][16];
