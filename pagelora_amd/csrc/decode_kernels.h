@@ -672,8 +672,8 @@ struct NewToken {
 };
 
 // stream_blocks for the folded q/k/v epilogue: `pre` issues loads ahead of
-// the first block's, `hook` runs once the first
-// block's loads are in flight (it forms q, and for the item holding the
+// the first block's, and `hook` runs once the first block's loads are in
+// flight (it forms q, and for the item holding the
 // row's last page the new token's k / v, filling `nt`), and the new token's
 // K/V rows are taken from `nt` rather than from memory, so no load waits on
 // the append's stores.

@@ -513,8 +513,9 @@ __global__ __launch_bounds__(kThreads) void shuffled_gemm_add_kernel(
   // (t, q) group x slice: at most YPT * kThreads / kWave entries (G <= 64:
   // one slice per group, nt * Q <= 64 groups; G > 64: nt * Q * G / 64)
   __shared__ float4 s_y[R > 0 ? kAddMaxYPT * kThreads / kWave : 1];
-  // the epilogue's inputs, loaded with the partials: the residual tile and
-  // the B pieces of the workgroup's 16 columns (token tl, column c, ranks 8k ..)
+  // the epilogue's inputs: the residual tile (loaded with the partials) and
+  // the B pieces of the workgroup's 16 columns (token tl, column c, ranks
+  // 8k ..; loaded after the weights' first batches)
   __shared__ float s_res[16 * 16];
   __shared__ uint4 s_b[R > 0 ? 16 * 16 * (R / 8) : 1];
   __shared__ int s_ok[16];
